@@ -1,0 +1,104 @@
+/* r9k.h -- C-ABI of libr9k.so, the gfx950 (MI355X) kernels of r9700-stack's quantized-MoE hot path.
+ *
+ * Drop-in for the symbols the reference's Python binds with ctypes (r9700_vllm/kernels/moe.py:22-57,
+ * r9700_vllm/moe/route.py:40-52, r9700_vllm/kernels/moe.py:557-571): same names, same argument lists (pointers are
+ * raw device addresses passed as `long`, sizes as `int`), same meaning, 0 on success and a negative (GEMMs, quant)
+ * or nonzero (route, sum) code on a bad shape. Every call is ONE asynchronous launch group on `stream`
+ * (a hipStream_t); nothing allocates, frees or synchronises, so calls are HIP-graph capturable. The caller owns
+ * every buffer.
+ *
+ * Layouts that differ from the reference (the layout is the kernel's, produced by r9700_vllm/kernels/moe.py):
+ *   wq  [E][N*K/2 bytes]: per 16-row column tile, 1 KB per 128-K tile = one 16x16x128 scaled-MFMA B operand
+ *       (permute_fragments). Same size as the checkpoint codes, so weight prep stays in place.
+ *   ws  [E][(K/32 + 1) * N bytes]: e8m0 exponents in the kernel's fragment order + the per-row max (pack_scales).
+ * Knobs that only meant something on gfx1201 (WV, SK, NPW, the LDS-A and fold bits of MT, wref) are accepted and
+ * ignored; the routing-block contract is honoured: blk = 16 * (MT & 7) rows at decode, r9k_moe_prefill_bm(cfg)
+ * rows in the prefill entry.
+ */
+#ifndef R9K_H
+#define R9K_H
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Grouped MXFP4 x fp8 GEMM, decode family. Replaces kernels/r9k_moe_mxfp4a8.hip:631-638 (r9k_moe_mxfp4a8).
+ * out[r, n] = bf16((sum_k A[r / a_row_div, k] * W_e[n, k]) * (As[r / a_row_div] * topk_w[r])) for every routed
+ * flat row r of the align tables (sorted_ids / expert_ids / ntpp, blocks of 16 * (MT & 7) rows).
+ * a e4m3 [Ma][K]; as fp32 [Ma]; wq / ws as above (ws_estride = bytes per expert of ws); c bf16 [numel][N];
+ * topk_w fp32 [numel] or 0. Errors: -1 N % 16, -2 K % 32, -3 bad argument, -5/-7 bad MT, -6 launch error. */
+int r9k_moe_mxfp4a8(long a, long as, long wq, long ws, long wref, long c, long sorted_ids, long expert_ids,
+                    long ntpp, long topk_w, long ws_estride, long wref_estride, int max_blocks, int numel,
+                    int a_row_div, int K, int N, int WV, int SK, int NPW, int MT, long stream);
+
+/* Prefill entry of the same GEMM. Replaces kernels/r9k_moe_mxfp4a8.hip:1227-1230 (r9k_moe_4bit_prefill).
+ * nv: 0 MXFP4 (2, the reference's folded MXFP4, is the same data here); 1 NVFP4 and 3 fp8 weights return -8.
+ * Tables built with blk = r9k_moe_prefill_bm(cfg). -7 unknown cfg, -2 K % r9k_moe_prefill_bk(cfg). */
+int r9k_moe_4bit_prefill(int nv, long a, long as, long wq, long ws, long wref, long c, long sorted_ids,
+                         long expert_ids, long ntpp, long topk_w, long ws_estride, long wref_estride, int max_blocks,
+                         int numel, int a_row_div, int K, int N, int cfg, long stream);
+
+/* Rows per routing block / K granularity of a prefill cfg (-1: no such cfg).
+ * Replace kernels/r9k_moe_mxfp4a8.hip:1196-1203. */
+int r9k_moe_prefill_bm(int cfg);
+int r9k_moe_prefill_bk(int cfg);
+
+/* Rows per M tile (16); the reference's Python asserts it. Replaces kernels/r9k_moe_mxfp4a8.hip:557. */
+int r9k_moe_block(void);
+
+/* 0: no folded-exponent kernels (the scaled MFMA applies the block exponents). Replaces :558. */
+int r9k_fold_supported(void);
+
+/* Per-row dynamic fp8 quant: x bf16 [M][K] (row stride ld) -> q e4m3fn [M][K], s fp32 [M] (amax / 448).
+ * Replaces kernels/r9k_moe_mxfp4a8.hip:1745-1757. -3 bad shape, -6 launch error. */
+int r9k_quant_rows_fp8(long x, long q, long s, int M, int K, int ld, long stream);
+
+/* The same plus g[row] = bf16(sigmoid(bf16(x[row] . wg))) as fp32 (shared-expert gate); tiled != 0 (the gfx1201
+ * fragment-tiled store) returns -3. Replaces kernels/r9k_moe_mxfp4a8.hip:1770-1781. */
+int r9k_quant_rows_fp8_gate(long x, long q, long s, long wg, long g, int M, int K, int ld, int tiled, long stream);
+
+/* silu(gate) * up + per-row fp8 quant: gu bf16 [M][2I] -> q e4m3fn [M][I], s fp32 [M].
+ * Replaces kernels/r9k_moe_mxfp4a8.hip:550-555. */
+int r9k_silu_mul_quant_fp8(long gu, long q, long s, int M, int I, long stream);
+
+/* Softmax top-k routing + align tables in one call: logits bf16 [M][E] (row stride ldl) -> weights fp32 [M][topk],
+ * ids int32 [M][topk], sorted_ids int32 [capacity], expert_ids int32 [capacity / blk], ntpp int32 [1]
+ * (capacity = ceil((M*topk + E*(blk-1)) / blk) * blk). scratch: 2E+1 int32 (reference contract; unused here).
+ * Tables in canonical order (rows ascending within each expert). Returns 0, 1 for an unsupported shape
+ * (E > 1024, topk > 16, blk not a power of two), else the HIP error. Replaces kernels/r9k_moe_route.hip:217-233. */
+int r9k_moe_route(long logits, int ldl, long weights, long ids, long sorted_ids, long expert_ids, long ntpp,
+                  long scratch, int M, int E, int topk, int renorm, int blk, long stream);
+int r9k_moe_route_max_experts(void);   /* 1024; replaces r9k_moe_route.hip:235 */
+int r9k_moe_route_max_topk(void);      /* 16;   replaces r9k_moe_route.hip:236 */
+
+/* Weighted top-k sum: out[m, n] = bf16(sum_j down[m, j, n] (+ shared[m, n])), fp32, j ascending, one rounding.
+ * down bf16 [M][topk][N] contiguous, shared [M][N] (row stride ld_shared) or 0, out row stride ld_out; N % 8 == 0.
+ * Replaces kernels/r9k_moe_sum.hip:62-69. */
+int r9k_moe_sum(long down, long shared, long out, int M, int topk, int N, long ld_shared, long ld_out, long stream);
+
+/* --- entry points with no reference C symbol ------------------------------------------------------------------ */
+
+/* Routing only (the role of vLLM's topk_softmax behind the stock FusedTopKRouter, which the reference calls when
+ * its fused router is off: r9700_vllm/moe/route.py:159-163). Same numerics as r9k_moe_route. 0 / 1 / HIP error. */
+int r9k_moe_topk(long logits, int ldl, long weights, long ids, int M, int E, int topk, int renorm, long stream);
+
+/* Align tables only, from ids int32 [numel] (the role of vLLM's moe_align_block_size, called at
+ * r9700_vllm/moe/experts.py:172 of the reference). ids outside [0, E) are left out. scratch: at least
+ * r9k_moe_align_scratch_ints(numel, E) int32, zero at the first call (the kernels leave it zero). */
+int r9k_moe_align(long ids, int numel, int E, int blk, long sorted_ids, long expert_ids, long ntpp, long scratch,
+                  long scratch_ints, long stream);
+long r9k_moe_align_scratch_ints(int numel, int E);
+
+/* Load-time NVFP4 -> MXFP4 with MSE-searched block exponents (the reference does this with torch:
+ * r9700_vllm/quant/nvfp4.py:39-90). packed u8 [N][K/2], s16 e4m3 [N][K/16], row_div fp32 [N] -> out_packed u8
+ * [N][K/2], out_e8m0 u8 [N][K/32] (checkpoint layout). -2 K % 32, -3 bad pointer / alignment, -6 launch error. */
+int r9k_nvfp4_to_mxfp4(long packed, long s16, long row_div, long out_packed, long out_e8m0, int N, int K, long stream);
+
+/* The same MSE search on fp32 weights [N][K] (r9700_vllm/quant/nvfp4.py:54-75, quantize_mxfp4_search). */
+int r9k_quantize_mxfp4_search(long w, long out_packed, long out_e8m0, int N, int K, long stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* R9K_H */

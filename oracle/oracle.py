@@ -1,0 +1,288 @@
+"""CPU oracle for the quantized-MoE hot path -- TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import this module, and only as the
+checker (or, in bench.py, as the timed CPU baseline). The product (r9700-stack_amd/) never imports it.
+
+Integer / byte parts come from liboracle.so (oracle/r9k_oracle.c, built by oracle/Makefile): fp8 and bf16
+encodes, per-row quant, routing ids, align tables, the top-k sum, NVFP4 -> MXFP4. The floating-point parts are the
+reference's own dequant-then-matmul restated in torch on the CPU (tests/test_moe_mxfp4.py:16-72 and
+kernels/r9k_moe_mxfp4a8.hip:469-482 of the reference fix the math and the rounding points): each GEMM output row is
+bf16(acc * (As * topk_w)) with acc = dequant(A row) . dequant(W row) accumulated in fp64.
+
+Parity status per function (what pins it; tests/test_oracle_*.py):
+  e4m3 encode, quant_rows_fp8      torch float8_e4m3fn cast (library routine), exhaustive over bf16 inputs
+  bf16 encode                      torch bfloat16 cast (library routine)
+  silu_mul_quant_fp8               torch silu in fp32 (tolerance) + torch cast of the same products (exact)
+  route                            torch.softmax + stable sort (ids exact, weights 2e-6), degenerate-row rules
+  align                            numpy stable argsort restatement + the reference test's table invariants
+  moe_sum                          sequential fp32 loop + exactly-representable sums vs torch
+  nvfp4 dequant / search           E2M1 closed form, brute-force nearest value and exponent, the reference
+                                   test's error-floor criterion, fp32-log2 agreement on all NVFP4-derivable maxima
+  gemm / layer                     pure-Python dot products on tiny inputs
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+import torch
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+_SO = os.path.join(HERE, "_build", "liboracle.so")
+_L = None
+
+E2M1 = np.array([0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0, -0.0, -0.5, -1.0, -1.5, -2.0, -3.0, -4.0, -6.0],
+                dtype=np.float64)
+
+
+def build() -> str:
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+    return _SO
+
+
+def lib() -> ctypes.CDLL:
+    global _L
+    if _L is None:
+        if not os.path.exists(_SO):
+            build()
+        L = ctypes.CDLL(_SO)
+        P = ctypes.c_void_p
+        i, l, f = ctypes.c_int, ctypes.c_long, ctypes.c_float
+        L.or_f32_to_bf16.restype = ctypes.c_uint16
+        L.or_f32_to_bf16.argtypes = [f]
+        L.or_f32_to_e4m3.restype = ctypes.c_uint8
+        L.or_f32_to_e4m3.argtypes = [f]
+        L.or_e4m3_value.restype = ctypes.c_double
+        L.or_e4m3_value.argtypes = [ctypes.c_uint8]
+        L.or_f32_to_e4m3_array.argtypes = [P, P, l]
+        L.or_quant_rows_fp8.argtypes = [P, i, i, l, P, P]
+        L.or_silu_mul_quant_fp8.argtypes = [P, i, i, P, P, P]
+        L.or_moe_route.restype = i
+        L.or_moe_route.argtypes = [P, l, i, i, i, i, P, P]
+        L.or_moe_align.restype = i
+        L.or_moe_align.argtypes = [P, l, i, i, P, P, P]
+        L.or_capacity.restype = l
+        L.or_capacity.argtypes = [l, i, i]
+        L.or_moe_sum.argtypes = [P, P, P, i, i, i, l, l]
+        L.or_e2m1_encode.restype = ctypes.c_uint8
+        L.or_e2m1_encode.argtypes = [f]
+        L.or_exp_no_clip.restype = i
+        L.or_exp_no_clip.argtypes = [f]
+        L.or_dequant_nvfp4.argtypes = [P, P, P, i, i, P]
+        L.or_quantize_mxfp4_search.argtypes = [P, i, i, P, P]
+        L.or_nvfp4_to_mxfp4.argtypes = [P, P, P, i, i, P, P]
+        _L = L
+    return _L
+
+
+def _p(a: np.ndarray):
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def bf16_bits(x: torch.Tensor) -> np.ndarray:
+    """bf16 tensor (any device) -> uint16 numpy bits."""
+    return np.ascontiguousarray(x.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16))
+
+
+def bits_to_bf16(b: np.ndarray) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(b).view(np.int16)).view(torch.bfloat16)
+
+
+def bf16_to_f32(b: np.ndarray) -> np.ndarray:
+    return (b.astype(np.uint32) << 16).view(np.float32)
+
+
+_E4M3 = None
+
+
+def e4m3_table() -> np.ndarray:
+    """float64 value of every e4m3fn byte (NaN for 0x7f / 0xff)."""
+    global _E4M3
+    if _E4M3 is None:
+        L = lib()
+        _E4M3 = np.array([L.or_e4m3_value(b) for b in range(256)], dtype=np.float64)
+    return _E4M3
+
+
+def f32_to_e4m3(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    q = np.empty(x.shape, dtype=np.uint8)
+    lib().or_f32_to_e4m3_array(_p(x), _p(q), x.size)
+    return q
+
+
+def f32_to_bf16(x: np.ndarray) -> np.ndarray:
+    L = lib()
+    flat = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    return np.array([L.or_f32_to_bf16(float(v)) for v in flat], dtype=np.uint16).reshape(np.shape(x))
+
+
+# ------------------------------------------------------------------------------------------ activations
+def quant_rows_fp8(x: torch.Tensor):
+    """bf16 [M, K] -> (q uint8 [M, K], s float32 [M])."""
+    xb = bf16_bits(x)
+    M, K = xb.shape
+    q = np.empty((M, K), dtype=np.uint8)
+    s = np.empty((M,), dtype=np.float32)
+    lib().or_quant_rows_fp8(_p(xb), M, K, K, _p(q), _p(s))
+    return q, s
+
+
+def silu_mul_quant_fp8(gu: torch.Tensor):
+    """bf16 [M, 2I] -> (q uint8 [M, I], s float32 [M], act float32 [M, I])."""
+    gb = bf16_bits(gu)
+    M, I2 = gb.shape
+    I = I2 // 2
+    q = np.empty((M, I), dtype=np.uint8)
+    s = np.empty((M,), dtype=np.float32)
+    act = np.empty((M, I), dtype=np.float32)
+    lib().or_silu_mul_quant_fp8(_p(gb), M, I, _p(q), _p(s), _p(act))
+    return q, s, act
+
+
+# ------------------------------------------------------------------------------------- routing and tables
+def route(logits: torch.Tensor, topk: int, renorm: bool):
+    """bf16 [M, E] -> (w float32 [M, topk], ids int32 [M, topk])."""
+    lb = bf16_bits(logits)
+    M, E = lb.shape
+    w = np.empty((M, topk), dtype=np.float32)
+    ids = np.empty((M, topk), dtype=np.int32)
+    rc = lib().or_moe_route(_p(lb), E, M, E, topk, 1 if renorm else 0, _p(w), _p(ids))
+    if rc:
+        raise ValueError(f"or_moe_route rejected M={M} E={E} topk={topk}")
+    return w, ids
+
+
+def capacity(numel: int, E: int, blk: int) -> int:
+    return int(lib().or_capacity(numel, E, blk))
+
+
+def align(ids: np.ndarray, E: int, blk: int):
+    """ids int [numel] -> (sorted_ids [cap], expert_ids [cap/blk], ntpp [1]) int32, canonical order."""
+    flat = np.ascontiguousarray(np.asarray(ids).reshape(-1), dtype=np.int32)
+    numel = flat.size
+    cap = capacity(numel, E, blk)
+    s = np.empty(cap, dtype=np.int32)
+    e = np.empty(cap // blk, dtype=np.int32)
+    n = np.empty(1, dtype=np.int32)
+    lib().or_moe_align(_p(flat), numel, E, blk, _p(s), _p(e), _p(n))
+    return s, e, n
+
+
+def moe_sum(down: torch.Tensor, shared: torch.Tensor | None = None) -> np.ndarray:
+    """bf16 [M, topk, N] (+ bf16 [M, N]) -> uint16 bf16 bits [M, N]."""
+    db = bf16_bits(down)
+    M, topk, N = db.shape
+    out = np.empty((M, N), dtype=np.uint16)
+    sb = bf16_bits(shared) if shared is not None else None
+    lib().or_moe_sum(_p(db), _p(sb) if sb is not None else None, _p(out), M, topk, N, N, N)
+    return out
+
+
+# ------------------------------------------------------------------------------------------- NVFP4 / MXFP4
+def dequant_nvfp4(packed: np.ndarray, s16: np.ndarray, row_div: np.ndarray) -> np.ndarray:
+    packed = np.ascontiguousarray(packed, dtype=np.uint8)
+    s16 = np.ascontiguousarray(s16, dtype=np.uint8)
+    row_div = np.ascontiguousarray(row_div, dtype=np.float32)
+    N, Kh = packed.shape
+    out = np.empty((N, Kh * 2), dtype=np.float32)
+    lib().or_dequant_nvfp4(_p(packed), _p(s16), _p(row_div), N, Kh * 2, _p(out))
+    return out
+
+
+def quantize_mxfp4_search(w: np.ndarray):
+    """fp32 [N, K] -> (packed uint8 [N, K/2], e8m0 uint8 [N, K/32])."""
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    N, K = w.shape
+    p = np.empty((N, K // 2), dtype=np.uint8)
+    e = np.empty((N, K // 32), dtype=np.uint8)
+    lib().or_quantize_mxfp4_search(_p(w), N, K, _p(p), _p(e))
+    return p, e
+
+
+def nvfp4_to_mxfp4(packed: np.ndarray, s16: np.ndarray, row_div: np.ndarray):
+    packed = np.ascontiguousarray(packed, dtype=np.uint8)
+    s16 = np.ascontiguousarray(s16, dtype=np.uint8)
+    row_div = np.ascontiguousarray(row_div, dtype=np.float32)
+    N, Kh = packed.shape
+    p = np.empty((N, Kh), dtype=np.uint8)
+    e = np.empty((N, Kh * 2 // 32), dtype=np.uint8)
+    lib().or_nvfp4_to_mxfp4(_p(packed), _p(s16), _p(row_div), N, Kh * 2, _p(p), _p(e))
+    return p, e
+
+
+def mxfp4_dequant(packed: torch.Tensor, e8m0: torch.Tensor, dtype=torch.float64) -> torch.Tensor:
+    """[..., N, K/2] codes + [..., N, K/32] exponents -> [..., N, K] values E2M1[c] * 2^(e - 127)
+    (the reference tests' mx_deq: tests/test_fold_mxfp4.py:36-39, tests/test_prefill_4bit.py:19-22)."""
+    lut = torch.tensor(E2M1, dtype=dtype)
+    p = packed.to(torch.int64)
+    c = torch.stack((p & 15, p >> 4), dim=-1).reshape(*p.shape[:-1], p.shape[-1] * 2)
+    v = lut[c].reshape(*c.shape[:-1], -1, 32)
+    sc = torch.exp2(e8m0.to(dtype) - 127.0).unsqueeze(-1)
+    return (v * sc).reshape(c.shape)
+
+
+def e4m3_dequant(q: np.ndarray, dtype=torch.float64) -> torch.Tensor:
+    return torch.from_numpy(e4m3_table()[np.asarray(q, dtype=np.uint8)]).to(dtype)
+
+
+# ------------------------------------------------------------------------------------------ GEMM / layer
+def grouped_gemm(aq: np.ndarray, a_s: np.ndarray, w_deq: dict, expert_of_row: np.ndarray, a_row_div: int,
+                 topk_w: np.ndarray | None = None, rows: np.ndarray | None = None) -> np.ndarray:
+    """bf16 bits [R, N] of out[r] = bf16((deq(aq[r // a_row_div]) . W[e_r]^T) * (a_s[r // a_row_div] * topk_w[r]))
+    for the routed rows `rows` (default all). w_deq: expert -> float64 [N, K] dequantized weight. The scale product
+    order and the single bf16 rounding follow kernels/r9k_moe_mxfp4a8.hip:478-481 of the reference."""
+    rows = np.arange(expert_of_row.size) if rows is None else np.asarray(rows)
+    N = next(iter(w_deq.values())).shape[0]
+    out = np.zeros((rows.size, N), dtype=np.uint16)
+    eor = expert_of_row[rows]
+    for e in np.unique(eor):
+        sel = np.nonzero(eor == e)[0]
+        r = rows[sel]
+        a = e4m3_dequant(aq[r // a_row_div])                          # [n, K] fp64
+        acc = (a @ w_deq[int(e)].T).to(torch.float32)                 # fp64 accumulation, then the fp32 result
+        sc = torch.from_numpy(a_s[r // a_row_div].astype(np.float32))
+        if topk_w is not None:
+            sc = sc * torch.from_numpy(topk_w[r].astype(np.float32))
+        v = (acc * sc[:, None]).to(torch.bfloat16)
+        out[sel] = bf16_bits(v)
+    return out
+
+
+def moe_layer(x: torch.Tensor, logits: torch.Tensor, w13: tuple, w2: tuple, topk: int, renorm: bool = True,
+              tokens: np.ndarray | None = None, route_out=None) -> dict:
+    """The whole layer on the CPU: route -> per-token fp8 quant -> gate_up -> silu*up + quant -> down (router weight
+    folded) -> top-k sum. w13 = (packed [E, 2I, H/2], e8m0 [E, 2I, H/32]) and w2 = (packed [E, H, I/2],
+    e8m0 [E, H, I/32]) uint8 tensors in checkpoint layout. `tokens` restricts the math to those tokens (the routing
+    and the quant are per token, so any subset is exact). Returns every intermediate as numpy."""
+    T, H = x.shape
+    w, ids = route_out if route_out is not None else route(logits, topk, renorm)
+    tok = np.arange(T) if tokens is None else np.asarray(tokens)
+    rows = (tok[:, None] * topk + np.arange(topk)[None, :]).reshape(-1)
+    xq, xs = quant_rows_fp8(x)
+    flat_ids = ids.reshape(-1)
+    need = np.unique(flat_ids[rows])
+    p13, e13 = w13
+    p2, e2 = w2
+    W13 = {int(e): mxfp4_dequant(p13[int(e)], e13[int(e)]) for e in need}
+    gate_up = grouped_gemm(xq, xs, W13, flat_ids, topk, None, rows)                     # [R, 2I] bf16 bits
+    aq, a_s, _ = silu_mul_quant_fp8(bits_to_bf16(gate_up))
+    del W13
+    W2 = {int(e): mxfp4_dequant(p2[int(e)], e2[int(e)]) for e in need}
+    # down: the A row of routed row rows[i] is aq[i]; fold the router weight
+    R = rows.size
+    down = np.zeros((R, W2[int(need[0])].shape[0]), dtype=np.uint16)
+    eor = flat_ids[rows]
+    tw = w.reshape(-1)[rows]
+    for e in np.unique(eor):
+        sel = np.nonzero(eor == e)[0]
+        a = e4m3_dequant(aq[sel])
+        acc = (a @ W2[int(e)].T).to(torch.float32)
+        sc = torch.from_numpy(a_s[sel]) * torch.from_numpy(tw[sel].astype(np.float32))
+        down[sel] = bf16_bits((acc * sc[:, None]).to(torch.bfloat16))
+    out = moe_sum(bits_to_bf16(down.reshape(tok.size, topk, -1)))
+    return dict(w=w, ids=ids, xq=xq, xs=xs, rows=rows, gate_up=gate_up, aq=aq, a_s=a_s, down=down, out=out,
+                tokens=tok)

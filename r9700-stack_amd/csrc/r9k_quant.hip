@@ -1,0 +1,219 @@
+// r9k_quant.hip -- per-row dynamic fp8 (OCP e4m3fn) quantisation for the MoE hot path on gfx950.
+//
+//   r9k_quant_rows_fp8       x bf16 [M, K] (row stride ld) -> q e4m3fn [M, K], s fp32 [M]
+//   r9k_quant_rows_fp8_gate  the same, plus g[row] = bf16(sigmoid(bf16(x[row] . wg))) (shared-expert gate)
+//   r9k_silu_mul_quant_fp8   gu bf16 [M, 2I] (gate | up) -> silu(gate) * up quantised per row: q [M, I], s [M]
+//
+// Numerics (kernels/r9k_moe_mxfp4a8.hip:1729-1741 and :517-548 of the reference define them):
+//   amax = max(max_k |x_k|, 1e-12);  inv = 448 / amax  (IEEE fp32 division);  q_k = e4m3_rne(x_k * inv);
+//   s = amax / 448.  x_k * inv <= 448 * (1 + 2^-23) always rounds to 448 at most, so no NaN code appears.
+// The fp32 -> e4m3 encode is the explicit RNE bit routine in r9k_common.h, so the bytes are the bytes torch's
+// float8_e4m3fn cast produces for the same fp32 products.
+//
+// One workgroup of QT threads per row. The vectorised path keeps the row in registers (one HBM read): each
+// thread owns up to QR chunks of 8 bf16 (16 bytes). Rows that do not fit (K > QT * 8 * QR) or are not
+// 16-byte aligned take the two-pass scalar kernel. Rows are independent, so M up to the grid limit is fine.
+#include "r9k_common.h"
+
+namespace {
+
+using namespace r9k;
+
+constexpr int QT = 256;     // threads per row
+constexpr int QR = 4;       // 16-byte chunks per thread kept in registers: K <= 8192 on the vectorised path
+
+__device__ __forceinline__ float lo16(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float hi16(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+__device__ __forceinline__ uint32_t pack4_e4m3(float a, float b, float c, float d) {
+  return f32_to_e4m3(a) | (f32_to_e4m3(b) << 8) | (f32_to_e4m3(c) << 16) | (f32_to_e4m3(d) << 24);
+}
+
+template <bool GATE>
+__global__ void __launch_bounds__(QT) quant_rows_vec_kernel(const uint16_t* __restrict__ x, uint8_t* __restrict__ q,
+                                                            float* __restrict__ s, int K, long ld,
+                                                            const uint16_t* __restrict__ wg, float* __restrict__ g) {
+  __shared__ float sh[QT / WAVE];
+  __shared__ float shd[QT / WAVE];
+  const int row = blockIdx.x, tid = threadIdx.x, nvec = K / 8;
+  const uint4* xr = reinterpret_cast<const uint4*>(x + (size_t)row * ld);
+  uint4 v[QR];
+  float m = 0.f, dot = 0.f;
+#pragma unroll
+  for (int i = 0; i < QR; i++) {
+    const int c = tid + i * QT;
+    v[i] = c < nvec ? xr[c] : make_uint4(0u, 0u, 0u, 0u);
+    const uint32_t w[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+#pragma unroll
+    for (int j = 0; j < 4; j++) m = fmaxf(m, fmaxf(fabsf(lo16(w[j])), fabsf(hi16(w[j]))));
+    if constexpr (GATE) {
+      if (c < nvec) {
+        const uint4 gw = reinterpret_cast<const uint4*>(wg)[c];
+        const uint32_t u[4] = {gw.x, gw.y, gw.z, gw.w};
+#pragma unroll
+        for (int j = 0; j < 4; j++) dot += lo16(w[j]) * lo16(u[j]) + hi16(w[j]) * hi16(u[j]);
+      }
+    }
+  }
+  const float rmax = block_max<QT>(m, sh);
+  if constexpr (GATE) {
+    dot = wave_sum(dot);
+    if (tid % WAVE == 0) shd[tid / WAVE] = dot;
+    __syncthreads();
+    if (tid == 0) {
+      float d = 0.f;
+#pragma unroll
+      for (int i = 0; i < QT / WAVE; i++) d += shd[i];
+      const float logit = bf2f(f2bf(d));                       // the router-style bf16 GEMM output
+      g[row] = bf2f(f2bf(1.f / (1.f + expf(-logit))));           // bf16 sigmoid
+    }
+  }
+  const float amax = fmaxf(rmax, 1e-12f);
+  const float inv = 448.f / amax;
+  if (tid == 0) s[row] = amax / 448.f;
+  uint2* qr = reinterpret_cast<uint2*>(q + (size_t)row * K);
+#pragma unroll
+  for (int i = 0; i < QR; i++) {
+    const int c = tid + i * QT;
+    if (c >= nvec) break;
+    const uint32_t lo = pack4_e4m3(lo16(v[i].x) * inv, hi16(v[i].x) * inv, lo16(v[i].y) * inv, hi16(v[i].y) * inv);
+    const uint32_t hi = pack4_e4m3(lo16(v[i].z) * inv, hi16(v[i].z) * inv, lo16(v[i].w) * inv, hi16(v[i].w) * inv);
+    qr[c] = make_uint2(lo, hi);
+  }
+}
+
+// Two-pass fallback for any K / ld / alignment: max pass, then a quantise pass that re-reads the row.
+template <bool GATE>
+__global__ void __launch_bounds__(QT) quant_rows_scalar_kernel(const uint16_t* __restrict__ x, uint8_t* __restrict__ q,
+                                                               float* __restrict__ s, int K, long ld,
+                                                               const uint16_t* __restrict__ wg, float* __restrict__ g) {
+  __shared__ float sh[QT / WAVE];
+  __shared__ float shd[QT / WAVE];
+  const int row = blockIdx.x, tid = threadIdx.x;
+  const uint16_t* xr = x + (size_t)row * ld;
+  float m = 0.f, dot = 0.f;
+  for (int k = tid; k < K; k += QT) {
+    const float v = bf2f(xr[k]);
+    m = fmaxf(m, fabsf(v));
+    if constexpr (GATE) dot += v * bf2f(wg[k]);
+  }
+  const float rmax = block_max<QT>(m, sh);
+  if constexpr (GATE) {
+    dot = wave_sum(dot);
+    if (tid % WAVE == 0) shd[tid / WAVE] = dot;
+    __syncthreads();
+    if (tid == 0) {
+      float d = 0.f;
+#pragma unroll
+      for (int i = 0; i < QT / WAVE; i++) d += shd[i];
+      const float logit = bf2f(f2bf(d));
+      g[row] = bf2f(f2bf(1.f / (1.f + expf(-logit))));
+    }
+  }
+  const float amax = fmaxf(rmax, 1e-12f);
+  const float inv = 448.f / amax;
+  if (tid == 0) s[row] = amax / 448.f;
+  uint8_t* qr = q + (size_t)row * K;
+  for (int k = tid; k < K; k += QT) qr[k] = (uint8_t)f32_to_e4m3(bf2f(xr[k]) * inv);
+}
+
+// silu(g) * u with g, u the stored bf16 values, evaluated as (g / (1 + exp(-g))) * u in fp32.
+__device__ __forceinline__ float silu_mul(float gv, float uv) { return gv / (1.f + expf(-gv)) * uv; }
+
+// One row per workgroup; each thread keeps its activations (I <= QT * 8 * QR) in registers between the max pass
+// and the store pass. Larger I recomputes the activation in the store pass.
+__global__ void __launch_bounds__(QT) silu_mul_quant_kernel(const uint16_t* __restrict__ gu, uint8_t* __restrict__ q,
+                                                            float* __restrict__ s, int I, int vec) {
+  __shared__ float sh[QT / WAVE];
+  const int row = blockIdx.x, tid = threadIdx.x;
+  const uint16_t* gr = gu + (size_t)row * 2 * I;
+  const uint16_t* ur = gr + I;
+  float m = 0.f;
+  float a[QR][8];
+  if (vec) {
+    const int nvec = I / 8;
+#pragma unroll
+    for (int i = 0; i < QR; i++) {
+      const int c = tid + i * QT;
+#pragma unroll
+      for (int j = 0; j < 8; j++) a[i][j] = 0.f;
+      if (c < nvec) {
+        const uint4 gv = reinterpret_cast<const uint4*>(gr)[c];
+        const uint4 uv = reinterpret_cast<const uint4*>(ur)[c];
+        const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w}, uw[4] = {uv.x, uv.y, uv.z, uv.w};
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          a[i][2 * j] = silu_mul(lo16(gw[j]), lo16(uw[j]));
+          a[i][2 * j + 1] = silu_mul(hi16(gw[j]), hi16(uw[j]));
+        }
+#pragma unroll
+        for (int j = 0; j < 8; j++) m = fmaxf(m, fabsf(a[i][j]));
+      }
+    }
+  } else {
+    for (int k = tid; k < I; k += QT) m = fmaxf(m, fabsf(silu_mul(bf2f(gr[k]), bf2f(ur[k]))));
+  }
+  const float amax = fmaxf(block_max<QT>(m, sh), 1e-12f);
+  const float inv = 448.f / amax;
+  if (tid == 0) s[row] = amax / 448.f;
+  uint8_t* qr = q + (size_t)row * I;
+  if (vec) {
+    const int nvec = I / 8;
+#pragma unroll
+    for (int i = 0; i < QR; i++) {
+      const int c = tid + i * QT;
+      if (c >= nvec) break;
+      const uint32_t lo = pack4_e4m3(a[i][0] * inv, a[i][1] * inv, a[i][2] * inv, a[i][3] * inv);
+      const uint32_t hi = pack4_e4m3(a[i][4] * inv, a[i][5] * inv, a[i][6] * inv, a[i][7] * inv);
+      reinterpret_cast<uint2*>(qr)[c] = make_uint2(lo, hi);
+    }
+  } else {
+    for (int k = tid; k < I; k += QT) qr[k] = (uint8_t)f32_to_e4m3(silu_mul(bf2f(gr[k]), bf2f(ur[k])) * inv);
+  }
+}
+
+bool vec_ok(long x, long q, int K, long ld) {
+  return K % 8 == 0 && ld % 8 == 0 && (x & 15) == 0 && (q & 7) == 0 && K <= QT * 8 * QR;
+}
+
+}  // namespace
+
+// Reference: kernels/r9k_moe_mxfp4a8.hip:1745-1757 (r9k_quant_rows_fp8). 0 on success, -3 bad shape, -6 launch error.
+extern "C" int r9k_quant_rows_fp8(long x, long q, long s, int M, int K, int ld, long stream) {
+  if (M <= 0) return 0;
+  if (K <= 0 || ld < K || !x || !q || !s) return -3;
+  const hipStream_t st = (hipStream_t)stream;
+  if (vec_ok(x, q, K, ld))
+    hipLaunchKernelGGL(quant_rows_vec_kernel<false>, dim3(M), dim3(QT), 0, st, (const uint16_t*)x, (uint8_t*)q,
+                       (float*)s, K, (long)ld, (const uint16_t*)nullptr, (float*)nullptr);
+  else
+    hipLaunchKernelGGL(quant_rows_scalar_kernel<false>, dim3(M), dim3(QT), 0, st, (const uint16_t*)x, (uint8_t*)q,
+                       (float*)s, K, (long)ld, (const uint16_t*)nullptr, (float*)nullptr);
+  return hipGetLastError() == hipSuccess ? 0 : -6;
+}
+
+// Reference: kernels/r9k_moe_mxfp4a8.hip:1770-1781. The fragment-tiled store (tiled != 0) belongs to the gfx12
+// A-tiled prefill kernel, which this library does not carry: tiled != 0 returns -3.
+extern "C" int r9k_quant_rows_fp8_gate(long x, long q, long s, long wg, long g, int M, int K, int ld, int tiled,
+                                       long stream) {
+  if (M <= 0) return 0;
+  if (tiled || K <= 0 || ld < K || !x || !q || !s || !wg || !g) return -3;
+  const hipStream_t st = (hipStream_t)stream;
+  if (vec_ok(x, q, K, ld) && (wg & 15) == 0)
+    hipLaunchKernelGGL(quant_rows_vec_kernel<true>, dim3(M), dim3(QT), 0, st, (const uint16_t*)x, (uint8_t*)q,
+                       (float*)s, K, (long)ld, (const uint16_t*)wg, (float*)g);
+  else
+    hipLaunchKernelGGL(quant_rows_scalar_kernel<true>, dim3(M), dim3(QT), 0, st, (const uint16_t*)x, (uint8_t*)q,
+                       (float*)s, K, (long)ld, (const uint16_t*)wg, (float*)g);
+  return hipGetLastError() == hipSuccess ? 0 : -6;
+}
+
+// Reference: kernels/r9k_moe_mxfp4a8.hip:550-555. gu contiguous [M, 2I] bf16.
+extern "C" int r9k_silu_mul_quant_fp8(long gu, long q, long s, int M, int I, long stream) {
+  if (M <= 0) return 0;
+  if (I <= 0 || !gu || !q || !s) return -3;
+  const int vec = (gu & 15) == 0 && (q & 7) == 0 && I % 8 == 0 && I <= QT * 8 * QR;
+  hipLaunchKernelGGL(silu_mul_quant_kernel, dim3(M), dim3(QT), 0, (hipStream_t)stream, (const uint16_t*)gu,
+                     (uint8_t*)q, (float*)s, I, vec);
+  return hipGetLastError() == hipSuccess ? 0 : -6;
+}

@@ -1,0 +1,535 @@
+"""Python bindings for libr9k's grouped MXFP4 x FP8 MoE GEMM and its companion kernels (gfx950 / CDNA4).
+
+Mirrors r9700_vllm/kernels/moe.py of the reference (same names, argument meaning and RuntimeError on a negative
+return code). Weights come from a compressed-tensors ``mxfp4-pack-quantized`` checkpoint: per expert
+``weight_packed [N, K/2] uint8`` (element 2i in the low nibble, 2i+1 in the high nibble, e2m1 codes) and
+``weight_scale [N, K/32] uint8`` (E8M0). ``prepare_mxfp4_weights`` converts them once at load to the layout the
+gfx950 kernels read (see ``permute_fragments`` / ``pack_scales``): one 16x16x128 scaled-MFMA B operand per 1 KB,
+plus its 64 exponent bytes. Everything here launches on torch's current stream and never synchronises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from dataclasses import dataclass
+
+import torch
+
+GROUP = 32
+MOE_BLOCK = 16
+KTILE = 128          # K per scaled MFMA (16x16x128): one fragment-order weight tile is 16 rows x 128 K = 1 KB
+
+_LIB = None
+
+
+def _lib_path() -> str:
+    return os.environ.get("R9K_LIB") or os.path.join(os.path.dirname(__file__), "libr9k.so")
+
+
+def lib() -> ctypes.CDLL:
+    """The kernel library (lazy, process-global). Raises OSError when libr9k.so is missing: there is no fallback."""
+    global _LIB
+    if _LIB is None:
+        L = ctypes.CDLL(_lib_path())
+        i, l = ctypes.c_int, ctypes.c_long
+        L.r9k_moe_mxfp4a8.restype = i
+        L.r9k_moe_mxfp4a8.argtypes = [l] * 12 + [i] * 9 + [l]
+        L.r9k_moe_4bit_prefill.restype = i
+        L.r9k_moe_4bit_prefill.argtypes = [i] + [l] * 12 + [i] * 6 + [l]
+        L.r9k_moe_prefill_bm.restype = i
+        L.r9k_moe_prefill_bm.argtypes = [i]
+        L.r9k_moe_prefill_bk.restype = i
+        L.r9k_moe_prefill_bk.argtypes = [i]
+        L.r9k_quant_rows_fp8.restype = i
+        L.r9k_quant_rows_fp8.argtypes = [l] * 3 + [i] * 3 + [l]
+        L.r9k_silu_mul_quant_fp8.restype = i
+        L.r9k_silu_mul_quant_fp8.argtypes = [l] * 3 + [i] * 2 + [l]
+        L.r9k_quant_rows_fp8_gate.restype = i
+        L.r9k_quant_rows_fp8_gate.argtypes = [l] * 5 + [i] * 4 + [l]
+        L.r9k_moe_sum.restype = i
+        L.r9k_moe_sum.argtypes = [l] * 3 + [i] * 3 + [l] * 3
+        L.r9k_moe_topk.restype = i
+        L.r9k_moe_topk.argtypes = [l, i, l, l, i, i, i, i, l]
+        L.r9k_moe_align.restype = i
+        L.r9k_moe_align.argtypes = [l, i, i, i, l, l, l, l, l, l]
+        L.r9k_moe_align_scratch_ints.restype = l
+        L.r9k_moe_align_scratch_ints.argtypes = [i, i]
+        L.r9k_nvfp4_to_mxfp4.restype = i
+        L.r9k_nvfp4_to_mxfp4.argtypes = [l] * 5 + [i] * 2 + [l]
+        L.r9k_quantize_mxfp4_search.restype = i
+        L.r9k_quantize_mxfp4_search.argtypes = [l] * 3 + [i] * 2 + [l]
+        L.r9k_fold_supported.restype = i
+        assert L.r9k_moe_block() == MOE_BLOCK
+        _LIB = L
+    return _LIB
+
+
+def fold_supported() -> bool:
+    L = lib()
+    return hasattr(L, "r9k_fold_supported") and bool(L.r9k_fold_supported())
+
+
+def atiled_supported() -> bool:
+    """The gfx1201 fragment-tiled-activation prefill kernel has no gfx950 counterpart here."""
+    return hasattr(lib(), "r9k_moe_4bit_prefill_at")
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _check(rc: int, what: str) -> None:
+    if rc:
+        raise RuntimeError(f"{what} failed ({rc})")
+
+
+@dataclass
+class Mxfp4Experts:
+    wq: torch.Tensor    # [E, N/16 * K/16 * 32] int32: fragment order (permute_fragments)
+    wsr: torch.Tensor   # [E, K/32 + 1, N] uint8: exponents in fragment order (pack_scales), last row = per-row max
+    N: int
+    K: int
+    fold: bool = False  # folded-exponent kernels: not used on gfx950 (the scaled MFMA applies the exponents)
+
+    @property
+    def estride(self) -> int:
+        return (self.K // GROUP + 1) * self.N
+
+
+@dataclass
+class Nvfp4Experts:
+    """Native NVFP4 (e2m1 + e4m3 scale per 16 + fp32 global per row); not served by the gfx950 library."""
+    wq: torch.Tensor
+    ws: torch.Tensor
+    wg: torch.Tensor
+    N: int
+    K: int
+
+
+def prepare_nvfp4_weights(packed: torch.Tensor, scale16: torch.Tensor, row_mult: torch.Tensor) -> Nvfp4Experts:
+    """packed [E, N, K/2] u8, scale16 [E, N, K/16] e4m3, row_mult [E, N] fp32 -> Nvfp4Experts (fragment-order codes,
+    scales transposed to [E, K/16, N]). The layout is kept for API parity; moe_gemm refuses it on gfx950."""
+    E, N, Kh = packed.shape
+    K = Kh * 2
+    assert N % 16 == 0 and K % 32 == 0, (N, K)
+    assert scale16.shape == (E, N, K // 16), (scale16.shape, (E, N, K // 16))
+    ws = scale16.view(torch.uint8).transpose(1, 2).contiguous()
+    return Nvfp4Experts(permute_fragments(packed.view(torch.uint8)), ws,
+                        row_mult.float().reshape(E, N).contiguous(), N, K)
+
+
+def permute_fragments(packed: torch.Tensor) -> torch.Tensor:
+    """[E, N, K/2] uint8 checkpoint order -> [E, N*K/8] int32 fragment order (same bytes, same size).
+
+    Column tile nt (16 rows) occupies 8*K bytes. Its K-tile kt (128 K) is 1 KB at kt*1024: lane l = g*16 + r of the
+    V_MFMA_SCALE_F32_16X16X128_F8F6F4 B operand holds row nt*16 + r, K elements kt*128 + g*32 .. +32, i.e. the 16
+    checkpoint bytes W[nt*16 + r, kt*64 + g*16 .. +16], at l*16. A last partial K-tile (K % 128 = 32*G) keeps only
+    its G groups (lanes l < 16*G), 256*G bytes."""
+    E, N, Kh = packed.shape
+    K = Kh * 2
+    assert N % 16 == 0 and K % GROUP == 0, (N, K)
+    nt, nkf, G = N // 16, K // KTILE, (K % KTILE) // GROUP
+    w = packed.reshape(E, nt, 16, Kh)
+    parts = []
+    if nkf:
+        f = w[..., : nkf * 64].reshape(E, nt, 16, nkf, 4, 16).permute(0, 1, 3, 4, 2, 5)   # [E, nt, kt, g, r, 16]
+        parts.append(f.reshape(E, nt, nkf * 1024))
+    if G:
+        t = w[..., nkf * 64:].reshape(E, nt, 16, G, 16).permute(0, 1, 3, 2, 4)              # [E, nt, g, r, 16]
+        parts.append(t.reshape(E, nt, G * 256))
+    out = parts[0] if len(parts) == 1 else torch.cat(parts, dim=2)
+    return out.reshape(E, -1).contiguous().view(torch.int32)
+
+
+def unpermute_fragments(wq: torch.Tensor, N: int, K: int) -> torch.Tensor:
+    """Inverse of permute_fragments: [E, N*K/8] int32 -> [E, N, K/2] uint8."""
+    E = wq.shape[0]
+    nt, nkf, G = N // 16, K // KTILE, (K % KTILE) // GROUP
+    b = wq.contiguous().view(torch.uint8).reshape(E, nt, 8 * K)
+    parts = []
+    if nkf:
+        f = b[..., : nkf * 1024].reshape(E, nt, nkf, 4, 16, 16).permute(0, 1, 4, 2, 3, 5)  # [E, nt, r, kt, g, 16]
+        parts.append(f.reshape(E, nt, 16, nkf * 64))
+    if G:
+        t = b[..., nkf * 1024:].reshape(E, nt, G, 16, 16).permute(0, 1, 3, 2, 4)            # [E, nt, r, g, 16]
+        parts.append(t.reshape(E, nt, 16, G * 16))
+    out = parts[0] if len(parts) == 1 else torch.cat(parts, dim=3)
+    return out.reshape(E, N, K // 2).contiguous()
+
+
+def prepare_mxfp4_weights(packed: torch.Tensor, scale: torch.Tensor) -> Mxfp4Experts:
+    E, N, Kh = packed.shape
+    K = Kh * 2
+    assert N % 16 == 0 and K % GROUP == 0, (N, K)
+    assert scale.shape == (E, N, K // GROUP), (scale.shape, (E, N, K // GROUP))
+    return Mxfp4Experts(permute_fragments(packed.view(torch.uint8)), pack_scales(scale), N, K)
+
+
+def pack_scales(scale: torch.Tensor) -> torch.Tensor:
+    """[E, N, K/32] E8M0 -> [E, K/32 + 1, N] uint8: the first (K/32)*N bytes of each expert are the exponents in
+    the kernels' fragment order, the last N bytes the per-row maximum exponent.
+
+    Column tile nt owns 16*K/32 bytes at nt*16*K/32. Full super-steps q of 4 K-tiles (16 blocks) are 256 bytes:
+    lane l = g*16 + r has the dword at q*256 + l*4 whose byte j is the exponent of row r, block 16q + 4j + g
+    (K-tile 4q + j, group g) -- one scale operand a K-tile. The K-tiles after the last full super-step are 64
+    bytes each, lane l's byte at l (a partial last tile 16*G bytes)."""
+    scale = scale.view(torch.uint8)
+    E, N, KB = scale.shape
+    nt, nq, tb = N // 16, KB // 16, KB % 16
+    s = scale.reshape(E, nt, 16, KB)                                                     # [E, nt, r, kb]
+    parts = []
+    if nq:
+        q = s[..., : nq * 16].reshape(E, nt, 16, nq, 4, 4).permute(0, 1, 3, 5, 2, 4)     # [E, nt, q, g, r, j]
+        parts.append(q.reshape(E, nt, nq * 256))
+    if tb:
+        ntt = (tb + 3) // 4
+        t = torch.zeros((E, nt, 16, ntt * 4), dtype=torch.uint8, device=scale.device)
+        t[..., :tb] = s[..., nq * 16:]
+        t = t.reshape(E, nt, 16, ntt, 4).permute(0, 1, 3, 4, 2).reshape(E, nt, ntt * 64)  # [E, nt, t, g, r]
+        parts.append(t[..., : tb * 16])
+    body = parts[0] if len(parts) == 1 else torch.cat(parts, dim=2)
+    out = torch.empty((E, KB + 1, N), dtype=torch.uint8, device=scale.device)
+    out.view(E, -1)[:, : KB * N].copy_(body.reshape(E, KB * N))
+    out[:, KB] = scale.max(dim=2).values
+    return out
+
+
+def unpack_scales(wsr: torch.Tensor) -> torch.Tensor:
+    """Inverse of pack_scales: [E, K/32 + 1, N] -> [E, N, K/32] uint8 exponents."""
+    E, KB1, N = wsr.shape
+    KB = KB1 - 1
+    nt, nq, tb = N // 16, KB // 16, KB % 16
+    body = wsr.reshape(E, -1)[:, : KB * N].reshape(E, nt, 16 * KB)
+    parts = []
+    if nq:
+        q = body[..., : nq * 256].reshape(E, nt, nq, 4, 16, 4).permute(0, 1, 4, 2, 5, 3)   # [E, nt, r, q, j, g]
+        parts.append(q.reshape(E, nt, 16, nq * 16))
+    if tb:
+        t = body[..., nq * 256:]
+        ntt = (tb + 3) // 4
+        pad = torch.zeros((E, nt, ntt * 64), dtype=torch.uint8, device=wsr.device)
+        pad[..., : tb * 16] = t
+        t = pad.reshape(E, nt, ntt, 4, 16).permute(0, 1, 4, 2, 3).reshape(E, nt, 16, ntt * 4)
+        parts.append(t[..., :tb])
+    out = parts[0] if len(parts) == 1 else torch.cat(parts, dim=3)
+    return out.reshape(E, N, KB).contiguous()
+
+
+# ------------------------------------------------------------------------------------ folded-exponent MXFP4
+# The reference folds each block's E8M0 into its gfx1201 e2m1 -> e4m3 unpack. The gfx950 scaled MFMA consumes the
+# block exponents directly, so folding is never selected (fold_supported() is False) and fold_decide() returns
+# False without looking. fold_stats stays available for inspecting a checkpoint's exponent spread.
+FOLD_EXACT, FOLD_REACH = 8, 12
+FOLD_MODE = os.environ.get("R9K_FOLD", "0").lower()
+
+
+@dataclass
+class FoldStats:
+    blocks: int
+    hist: list            # hist[d] = blocks with d = ref - block exponent (d clamped to 0..16)
+    max_d: int
+    K: int = 0
+
+    @property
+    def p_inexact(self) -> float:
+        return sum(self.hist[FOLD_EXACT + 1:]) / max(1, self.blocks)
+
+    @property
+    def p_flush(self) -> float:
+        return sum(self.hist[FOLD_REACH + 1:]) / max(1, self.blocks)
+
+    @property
+    def mean_d(self) -> float:
+        return sum(d * n for d, n in enumerate(self.hist)) / max(1, self.blocks)
+
+
+def fold_stats(wsr: torch.Tensor, chunk: int = 64 << 20) -> FoldStats:
+    """Distribution of d = row maximum exponent - block exponent over a pack_scales tensor, chunked by expert."""
+    E, nb1, N = wsr.shape
+    hist = torch.zeros(17, dtype=torch.int64)
+    step = max(1, chunk // (nb1 * N))
+    for e0 in range(0, E, step):
+        w = wsr[e0:e0 + step]
+        blocks = unpack_scales(w).to(torch.int16)                 # [e, N, KB]
+        d = (w[:, -1, :].to(torch.int16).unsqueeze(-1) - blocks).clamp_(0, 16)
+        hist += torch.bincount(d.reshape(-1).cpu(), minlength=17)
+    h = hist.tolist()
+    return FoldStats(E * (nb1 - 1) * N, h, max(i for i, n in enumerate(h) if n) if any(h) else 0, (nb1 - 1) * GROUP)
+
+
+def fold_decide(wsr: torch.Tensor, name: str = "", log=None) -> bool:
+    """Always False on gfx950 (no folded kernels); kept so weight prep reads like the reference's."""
+    return False
+
+
+# ------------------------------------------------------------------------------------------ activations
+def quant_rows_fp8(x: torch.Tensor, tiled: bool = False):
+    """bf16 [M, K] -> (e4m3fn [M, K], fp32 [M]) with a per-row dynamic scale (amax / 448)."""
+    assert x.dtype == torch.bfloat16 and x.dim() == 2 and x.stride(1) == 1
+    if tiled:
+        raise RuntimeError("quant_rows_fp8(tiled=True): the fragment-tiled layout is a gfx1201 A-tiled-kernel format")
+    M, K = x.shape
+    s = torch.empty((M,), dtype=torch.float32, device=x.device)
+    q = torch.empty((M, K), dtype=torch.float8_e4m3fn, device=x.device)
+    if M == 0:
+        return q, s
+    rc = lib().r9k_quant_rows_fp8(x.data_ptr(), q.data_ptr(), s.data_ptr(), M, K, x.stride(0), _stream())
+    if rc:
+        raise RuntimeError(f"r9k_quant_rows_fp8 failed ({rc}) M={M} K={K}")
+    return q, s
+
+
+def quant_rows_fp8_gate(x: torch.Tensor, wg: torch.Tensor, tiled: bool = False):
+    """quant_rows_fp8 plus the shared expert's gate in the same launch: (q, s, g) with g [M] fp32 =
+    bf16(sigmoid(bf16(x @ wg)))."""
+    assert x.dtype == torch.bfloat16 and x.dim() == 2 and x.stride(1) == 1
+    assert wg.dtype == torch.bfloat16 and wg.is_contiguous() and wg.numel() == x.shape[1]
+    if tiled:
+        raise RuntimeError("quant_rows_fp8_gate(tiled=True): not available on gfx950")
+    M, K = x.shape
+    s = torch.empty((M,), dtype=torch.float32, device=x.device)
+    g = torch.empty((M,), dtype=torch.float32, device=x.device)
+    q = torch.empty((M, K), dtype=torch.float8_e4m3fn, device=x.device)
+    if M == 0:
+        return q, s, g
+    rc = lib().r9k_quant_rows_fp8_gate(x.data_ptr(), q.data_ptr(), s.data_ptr(), wg.data_ptr(), g.data_ptr(), M, K,
+                                       x.stride(0), 0, _stream())
+    if rc:
+        raise RuntimeError(f"r9k_quant_rows_fp8_gate failed ({rc}) M={M} K={K}")
+    return q, s, g
+
+
+def silu_mul_quant_fp8(gu: torch.Tensor):
+    """bf16 [M, 2I] (gate | up) -> (e4m3fn [M, I], fp32 [M]): silu(gate) * up with a per-row dynamic scale."""
+    assert gu.dtype == torch.bfloat16 and gu.is_contiguous() and gu.shape[1] % 2 == 0
+    M, I2 = gu.shape
+    q = torch.empty((M, I2 // 2), dtype=torch.float8_e4m3fn, device=gu.device)
+    s = torch.empty((M,), dtype=torch.float32, device=gu.device)
+    if M == 0:
+        return q, s
+    rc = lib().r9k_silu_mul_quant_fp8(gu.data_ptr(), q.data_ptr(), s.data_ptr(), M, I2 // 2, _stream())
+    if rc:
+        raise RuntimeError(f"r9k_silu_mul_quant_fp8 failed ({rc})")
+    return q, s
+
+
+# ------------------------------------------------------------------------------------------------ GEMMs
+# Prefill tile table: cfg -> (rows per routing block BM, columns BN). The kernel is the source of truth for BM
+# (prefill_block() asks it); the cfg indices keep the reference's BM per index.
+PREFILL_TILES = {0: (256, 64), 1: (256, 128), 2: (128, 128), 3: (128, 64), 4: (128, 64), 5: (256, 32),
+                 6: (64, 64), 7: (256, 128), 8: (256, 128), 9: (256, 128), 10: (128, 128), 11: (64, 64),
+                 12: (256, 128), 13: (128, 128), 14: (64, 64), 15: (64, 128), 16: (256, 128), 17: (64, 128),
+                 18: (64, 64), 19: (64, 128)}
+PREFILL_MIN_M = int(os.environ.get("R9K_PREFILL_MIN_M", "128"))
+PREFILL_DEFAULT = int(os.environ.get("R9K_PREFILL_CFG", "12"))
+PREFILL_DEFAULT_SMALL = int(os.environ.get("R9K_PREFILL_CFG_SMALL", "10"))
+
+
+def prefill_block(cfg: int) -> int:
+    """Rows per routing block (moe_align_block_size block) of prefill tile `cfg`."""
+    bm = lib().r9k_moe_prefill_bm(cfg)
+    if bm <= 0:
+        raise ValueError(f"unknown prefill cfg {cfg}")
+    return bm
+
+
+def prefill_bk(cfg: int) -> int:
+    """K granularity of prefill tile `cfg`: the kernel needs K % BK == 0."""
+    bk = lib().r9k_moe_prefill_bk(cfg)
+    if bk <= 0:
+        raise ValueError(f"unknown prefill cfg {cfg}")
+    return bk
+
+
+def is_prefill_cfg(cfg) -> bool:
+    return bool(cfg) and cfg[0] == "P"
+
+
+def is_atiled_cfg(cfg) -> bool:
+    return bool(cfg) and cfg[0] == "A"
+
+
+def pick_atiled(N: int, K: int, M: int, fold: bool = True):
+    """The gfx1201 A-tiled kernel is not part of the gfx950 library: never selected."""
+    return None
+
+
+def moe_gemm(a_q: torch.Tensor, a_s: torch.Tensor, w: Mxfp4Experts, out: torch.Tensor,
+             sorted_ids: torch.Tensor, expert_ids: torch.Tensor, ntpp: torch.Tensor, numel: int,
+             a_row_div: int, topk_w: torch.Tensor | None = None, WV: int = 2, SK: int = 4, NPW: int = 2,
+             num_experts: int | None = None, MT: int = 1, ldsa: bool = False, prefill: int | None = None,
+             a_tiled: bool = False, fuse: int = 0):
+    """out[r, :] = dequant(a_q[r // a_row_div]) @ W[expert(r)]^T (* topk_w[r]) for every routed flat row r.
+
+    sorted_ids/expert_ids must come from an align with block_size 16*MT (or prefill_block(prefill)). WV/SK/NPW/ldsa
+    are the reference's gfx1201 launch knobs and are accepted but not used: the gfx950 kernel picks its own split.
+    The grid covers at most ceil(numel/BLK) + min(numel, E) blocks -- the most an align can fill with numel routed
+    rows over E experts -- so the launch stays graph-capturable."""
+    if fuse:
+        raise RuntimeError("moe_gemm(fuse=...) is not available in this build")
+    if a_tiled:
+        raise RuntimeError("moe_gemm(a_tiled=True) is a gfx1201 kernel format")
+    if isinstance(w, Nvfp4Experts):
+        raise RuntimeError("native NVFP4 experts are not served on gfx950: convert with quant.nvfp4.nvfp4_to_mxfp4")
+    E = num_experts if num_experts is not None else w.wq.shape[0]
+    assert out.dtype == torch.bfloat16 and out.shape[1] == w.N and a_q.shape[1] == w.K and out.is_contiguous()
+    assert a_q.is_contiguous() and a_s.dtype == torch.float32
+    if topk_w is not None:
+        assert topk_w.dtype == torch.float32 and topk_w.is_contiguous()
+    tw = topk_w.data_ptr() if topk_w is not None else 0
+    wsr = w.wsr
+    if prefill is not None:
+        blk = prefill_block(prefill)
+        max_blocks = min(expert_ids.numel(), (numel + blk - 1) // blk + min(numel, E))
+        rc = lib().r9k_moe_4bit_prefill(
+            2 if w.fold else 0, a_q.data_ptr(), a_s.data_ptr(), w.wq.data_ptr(), wsr.data_ptr(),
+            wsr.data_ptr() + (w.K // GROUP) * w.N, out.data_ptr(), sorted_ids.data_ptr(), expert_ids.data_ptr(),
+            ntpp.data_ptr(), tw, w.estride, w.estride, max_blocks, numel, a_row_div, w.K, w.N, prefill, _stream())
+        if rc:
+            raise RuntimeError(f"r9k_moe_4bit_prefill failed ({rc}) N={w.N} K={w.K} cfg={prefill}")
+        return out
+    blk = MOE_BLOCK * MT
+    max_blocks = min(expert_ids.numel(), (numel + blk - 1) // blk + min(numel, E))
+    rc = lib().r9k_moe_mxfp4a8(
+        a_q.data_ptr(), a_s.data_ptr(), w.wq.data_ptr(), wsr.data_ptr(), wsr.data_ptr() + (w.K // GROUP) * w.N,
+        out.data_ptr(), sorted_ids.data_ptr(), expert_ids.data_ptr(), ntpp.data_ptr(), tw,
+        w.estride, w.estride, max_blocks, numel, a_row_div, w.K, w.N, WV, SK, NPW,
+        MT | (8 if ldsa and MT > 1 else 0), _stream())
+    if rc:
+        raise RuntimeError(f"r9k_moe_mxfp4a8 failed ({rc}) N={w.N} K={w.K} MT={MT}")
+    return out
+
+
+def pick_cfg(N: int, K: int, group: int = GROUP, M: int | None = None, kind: str | None = None,
+             fold: bool = False) -> tuple:
+    """A (WV, SK, NPW) tuple for the decode kernel, or ("P", cfg) for the prefill entry at M >= PREFILL_MIN_M.
+    The tuple's values are the reference's gfx1201 knobs (ignored by the gfx950 kernel, which sizes its own split);
+    they are still returned legal for the shape so callers written against the reference keep working."""
+    if kind and M:
+        from .tuned import lookup
+        t = lookup(kind, N, K, M)
+        if t:
+            return t
+        if M >= PREFILL_MIN_M and K % prefill_bk(PREFILL_DEFAULT) == 0:
+            return ("P", PREFILL_DEFAULT if M >= 512 else PREFILL_DEFAULT_SMALL)
+    for WV, SK, NPW in ((2, 4, 2), (4, 2, 1), (2, 5, 2), (4, 1, 1)):
+        if K % (SK * group) == 0 and (K >= 1024 or SK <= 2):
+            return WV, SK, NPW
+    return 4, 1, 1
+
+
+def legal_cfg(cfg: tuple, N: int, K: int, group: int = GROUP) -> tuple:
+    """cfg's (WV, SK, NPW) if legal for this shape (K % (SK*group) == 0), else pick_cfg's."""
+    WV, SK, NPW = cfg[:3]
+    if K % (SK * group) == 0 and WV * SK * 32 <= 1024:
+        return WV, SK, NPW
+    return pick_cfg(N, K, group)[:3]
+
+
+def pick_mt(numel: int, num_experts: int) -> int:
+    """M tiles per routing block from the host-known row count: rows per touched expert >= 32 -> 4, >= 16 -> 2."""
+    per = numel / max(1, min(num_experts, numel))
+    return 4 if per >= 32 else (2 if per >= 16 else 1)
+
+
+MOE_PREFILL_CFG = int(os.environ.get("R9K_MOE_PREFILL_CFG", "17"))
+MOE_PREFILL_CFG_GATE_UP = int(os.environ.get("R9K_MOE_PREFILL_CFG1", "17"))
+
+
+def pick_moe_prefill(MT: int, K_down: int, gate_up: bool = False) -> int | None:
+    """Prefill tile for the routed-MoE GEMMs of a step whose routing block is 16*MT rows (None: the decode kernel).
+    Both GEMMs must share the block size, so one align table serves both."""
+    cfg = MOE_PREFILL_CFG_GATE_UP if gate_up else MOE_PREFILL_CFG
+    if cfg < 0 or 16 * MT != prefill_block(cfg) or K_down % prefill_bk(cfg):
+        return None
+    return cfg
+
+
+# ------------------------------------------------------------------------------------- routing and sum
+def moe_sum(down: torch.Tensor, shared: torch.Tensor | None, out: torch.Tensor) -> torch.Tensor:
+    """out[M, N] = sum over top-k of down[M, topk, N] (+ shared[M, N]) in fp32, one bf16 rounding."""
+    M, topk, N = down.shape
+    assert down.is_contiguous() and out.shape == (M, N) and out.dtype == torch.bfloat16 and out.stride(1) == 1
+    rc = lib().r9k_moe_sum(down.data_ptr(), shared.data_ptr() if shared is not None else 0, out.data_ptr(), M, topk,
+                           N, shared.stride(0) if shared is not None else 0, out.stride(0), _stream())
+    if rc:
+        raise RuntimeError(f"r9k_moe_sum failed ({rc}) M={M} topk={topk} N={N}")
+    return out
+
+
+def capacity(numel: int, num_experts: int, blk: int) -> int:
+    """sorted_ids length for `numel` routed rows (moe_align_block_size's sizing)."""
+    cap = numel + num_experts * (blk - 1)
+    return (cap + blk - 1) // blk * blk
+
+
+_ALIGN_SCRATCH: dict = {}
+
+
+def _align_scratch(device: torch.device, n: int) -> torch.Tensor:
+    key = (device.type, device.index)
+    t = _ALIGN_SCRATCH.get(key)
+    if t is None or t.numel() < n:
+        t = torch.zeros(max(n, 1 << 16), dtype=torch.int32, device=device)   # zero once; the kernels leave it zero
+        _ALIGN_SCRATCH[key] = t
+    return t
+
+
+def moe_align(topk_ids: torch.Tensor, block: int, num_experts: int, expert_map: torch.Tensor | None = None):
+    """GPU moe_align_block_size: (sorted_ids [cap], expert_ids [cap/block], ntpp [1]) int32, rows ascending within
+    each expert (align_block_size_ref's canonical order). expert_map (global -> local id, -1 = not here) is
+    applied first; rows of experts outside [0, num_experts) are left out of the tables."""
+    ids = topk_ids.reshape(-1)
+    if expert_map is not None:
+        ids = expert_map[ids.long()]
+    ids = ids.to(torch.int32).contiguous()
+    numel = ids.numel()
+    dev = ids.device
+    cap = capacity(numel, num_experts, block)
+    sorted_ids = torch.empty(cap, dtype=torch.int32, device=dev)
+    expert_ids = torch.empty(cap // block, dtype=torch.int32, device=dev)
+    ntpp = torch.empty(1, dtype=torch.int32, device=dev)
+    L = lib()
+    n = L.r9k_moe_align_scratch_ints(numel, num_experts)
+    scratch = _align_scratch(dev, n)
+    rc = L.r9k_moe_align(ids.data_ptr(), numel, num_experts, block, sorted_ids.data_ptr(), expert_ids.data_ptr(),
+                         ntpp.data_ptr(), scratch.data_ptr(), scratch.numel(), _stream())
+    if rc:
+        raise RuntimeError(f"r9k_moe_align failed ({rc}) numel={numel} E={num_experts} block={block}")
+    return sorted_ids, expert_ids, ntpp
+
+
+def moe_topk(logits: torch.Tensor, topk: int, renorm: bool):
+    """Softmax top-k routing (stock FusedTopKRouter's outputs): logits [M, E] bf16 -> (w fp32 [M, topk],
+    ids int32 [M, topk]), descending probability, ties to the lower expert index."""
+    assert logits.dtype == torch.bfloat16 and logits.dim() == 2 and logits.stride(1) == 1
+    M, E = logits.shape
+    w = torch.empty((M, topk), dtype=torch.float32, device=logits.device)
+    ids = torch.empty((M, topk), dtype=torch.int32, device=logits.device)
+    if M == 0:
+        return w, ids
+    rc = lib().r9k_moe_topk(logits.data_ptr(), logits.stride(0), w.data_ptr(), ids.data_ptr(), M, E, topk,
+                            1 if renorm else 0, _stream())
+    if rc:
+        raise RuntimeError(f"r9k_moe_topk failed ({rc}) M={M} E={E} topk={topk}")
+    return w, ids
+
+
+def align_block_size_ref(topk_ids: torch.Tensor, num_experts: int, block: int = MOE_BLOCK):
+    """Pure-torch equivalent of moe_align_block_size (tests and host-side table builds): pads each expert's rows
+    to a multiple of `block`, pad value = numel. Returns (sorted_ids, expert_ids, ntpp) sized to capacity."""
+    flat = topk_ids.flatten().to(torch.int64).cpu()
+    numel = flat.numel()
+    cap = capacity(numel, num_experts, block)
+    sorted_ids = torch.full((cap,), numel, dtype=torch.int32)
+    expert_ids = torch.full((cap // block,), -1, dtype=torch.int32)
+    pos = 0
+    for e in range(num_experts):
+        rows = (flat == e).nonzero().flatten()
+        if rows.numel() == 0:
+            continue
+        n = (rows.numel() + block - 1) // block * block
+        sorted_ids[pos:pos + rows.numel()] = rows.to(torch.int32)
+        expert_ids[pos // block:(pos + n) // block] = e
+        pos += n
+    return sorted_ids, expert_ids, torch.tensor([pos], dtype=torch.int32)

@@ -1,0 +1,164 @@
+"""R9700Mxfp4Experts: the fused-MoE experts backed by libr9k's grouped MXFP4 x FP8 GEMM on gfx950.
+
+Mirrors the reference's r9700_vllm/moe/experts.py (class name, apply() signature, in-place output). With vLLM
+installed it is a vLLM modular fused-MoE experts class; without it, the same class works standalone
+(``R9700Mxfp4Experts.standalone(w13_scale, w2_scale)``), which is how the tests and bench.py drive it.
+
+Layer weights (set by weight prep, quant/ct.py or kernels/moe.prepare_mxfp4_weights):
+  w13_weight        [E, N1*K1/8] int32   fragment order (N1 = 2*I, K1 = hidden)
+  w2_weight         [E, N2*K2/8] int32                  (N2 = hidden, K2 = I)
+  w13_weight_scale  [E, K1/32 + 1, N1]  uint8  exponents in fragment order + per-row max (last row)
+  w2_weight_scale   [E, K2/32 + 1, N2]  uint8
+Flow per call (reference experts.py:149-251): align tables (from the router, else the GPU align) -> per-token fp8
+quant -> grouped gate_up GEMM -> silu(g)*u + per-row fp8 quant -> grouped down GEMM with the router weight in the
+epilogue -> top-k sum into `output`. Six launches on torch's current stream, no host synchronisation, so a call can
+be captured in a HIP graph.
+"""
+from __future__ import annotations
+
+import os
+
+import torch
+
+from .._compat import vllm_available
+from ..kernels import moe as K
+from . import route
+
+ZERO_DOWN = os.environ.get("R9K_MOE_ZERO_DOWN", "0") == "1"
+
+
+def r9k_available() -> bool:
+    """ROCm torch with a gfx950 device and the kernel library loadable."""
+    try:
+        if not torch.cuda.is_available() or torch.version.hip is None:
+            return False
+        arch = torch.cuda.get_device_properties(torch.cuda.current_device()).gcnArchName
+        if not arch.startswith("gfx950"):
+            return False
+        K.lib()
+        return True
+    except Exception:
+        return False
+
+
+def _experts_base():
+    if vllm_available():
+        try:
+            import vllm.model_executor.layers.fused_moe.modular_kernel as mk
+            return mk.FusedMoEExpertsModular
+        except Exception:
+            pass
+
+    class _StandaloneExperts:
+        """Base used when vLLM is not installed: holds the two scale tensors the modular kernel would supply."""
+
+        def __init__(self, moe_config=None, quant_config=None, max_num_tokens=None, num_dispatchers=None):
+            self.moe_config = moe_config
+            self.quant_config = quant_config
+            self.w1_scale = getattr(quant_config, "w1_scale", None)
+            self.w2_scale = getattr(quant_config, "w2_scale", None)
+
+    return _StandaloneExperts
+
+
+class R9700Mxfp4Experts(_experts_base()):
+
+    @classmethod
+    def standalone(cls, w1_scale: torch.Tensor, w2_scale: torch.Tensor) -> "R9700Mxfp4Experts":
+        """An experts object outside vLLM over pack_scales-layout scale tensors."""
+        obj = cls.__new__(cls)
+        obj.w1_scale = w1_scale
+        obj.w2_scale = w2_scale
+        return obj
+
+    @staticmethod
+    def activation_format():
+        import vllm.model_executor.layers.fused_moe.modular_kernel as mk
+        return mk.FusedMoEActivationFormat.Standard
+
+    def finalize_weight_and_reduce_impl(self):
+        from vllm.model_executor.layers.fused_moe.topk_weight_and_reduce import TopKWeightAndReduceNoOP
+        return TopKWeightAndReduceNoOP()
+
+    @staticmethod
+    def _supports_current_device() -> bool:
+        return r9k_available()
+
+    @staticmethod
+    def _supports_no_act_and_mul() -> bool:
+        return False
+
+    @staticmethod
+    def _supports_quant_scheme(weight_key, activation_key) -> bool:
+        return activation_key is None
+
+    @staticmethod
+    def _supports_activation(activation) -> bool:
+        return str(getattr(activation, "name", activation)).lower() == "silu"
+
+    @staticmethod
+    def _supports_parallel_config(moe_parallel_config) -> bool:
+        return not (getattr(moe_parallel_config, "use_fi_nvl_two_sided_kernels", False)
+                    or getattr(moe_parallel_config, "use_fi_nvl_one_sided_kernels", False))
+
+    fold = (False, False)
+
+    def _dims(self, ws: torch.Tensor) -> tuple[int, int]:
+        """(N, K) of one GEMM from its pack_scales tensor [E, K/32 + 1, N]."""
+        return ws.shape[2], (ws.shape[1] - 1) * K.GROUP
+
+    def process_weights_after_loading(self, layer) -> None:
+        sup = getattr(super(), "process_weights_after_loading", None)
+        if sup is not None:
+            sup(layer)
+        self.fold = (False, False)
+
+    def moe_problem_size(self, a1, w1, w2, topk_ids):
+        N1, _ = self._dims(self.w1_scale)
+        return w1.size(0), a1.size(0), N1 // 2, a1.size(-1), topk_ids.size(1)
+
+    def workspace_shapes(self, M, N, K_, topk, global_num_experts, local_num_experts, expert_tokens_meta,
+                         activation):
+        # only the output buffer comes from the modular kernel's workspace; intermediates are allocated per call
+        return ((M, K_), (1,), (M, K_))
+
+    def apply(self, output, hidden_states, w1, w2, topk_weights, topk_ids, activation, global_num_experts,
+              expert_map, a1q_scale, a2_scale, workspace13, workspace2, expert_tokens_meta,
+              apply_router_weight_on_input):
+        assert not apply_router_weight_on_input, "R9700Mxfp4Experts: router weight on input not supported"
+        assert hidden_states.dtype == torch.bfloat16 and hidden_states.is_contiguous()
+        N1, K1 = self._dims(self.w1_scale)
+        N2, K2 = self._dims(self.w2_scale)
+        M, topk = hidden_states.shape[0], topk_ids.shape[1]
+        E = w1.shape[0]
+        if global_num_experts == -1:
+            global_num_experts = E
+        numel = M * topk
+        dev = hidden_states.device
+        if M == 0:
+            return
+
+        MT = K.pick_mt(numel, global_num_experts)
+        blk = K.MOE_BLOCK * MT
+        pf_down = K.pick_moe_prefill(MT, K2)
+        pf_gate = K.pick_moe_prefill(MT, K1, gate_up=True)
+        tabs = route.take(getattr(self, "r9k_layer", None), topk_ids, blk, numel) if expert_map is None else None
+        if tabs is None:
+            tabs = K.moe_align(topk_ids, blk, E, expert_map)
+        sid, eid, ntpp = tabs
+        W1 = K.Mxfp4Experts(w1, self.w1_scale, N1, K1)
+        W2 = K.Mxfp4Experts(w2, self.w2_scale, N2, K2)
+
+        xq, xs = K.quant_rows_fp8(hidden_states)
+        gate_up = torch.empty((numel, N1), dtype=torch.bfloat16, device=dev)
+        K.moe_gemm(xq, xs, W1, gate_up, sid, eid, ntpp, numel, topk, None, num_experts=E, MT=MT, prefill=pf_gate)
+        aq, as_ = K.silu_mul_quant_fp8(gate_up)
+        # Rows no table places (experts on other ranks under an expert map) must not feed moe_sum garbage.
+        if expert_map is not None or ZERO_DOWN:
+            down = torch.zeros((numel, N2), dtype=torch.bfloat16, device=dev)
+        else:
+            down = torch.empty((numel, N2), dtype=torch.bfloat16, device=dev)
+        tw = topk_weights.reshape(-1).to(torch.float32).contiguous()
+        K.moe_gemm(aq, as_, W2, down, sid, eid, ntpp, numel, 1, tw, num_experts=E, MT=MT, prefill=pf_down)
+        K.moe_sum(down.view(M, topk, N2), None, output)
+        return output

@@ -1,0 +1,190 @@
+"""MoE routing in one launch at decode widths (libr9k r9k_moe_route): softmax top-k, renormalisation and the
+moe_align_block_size tables together. Mirrors the reference's r9700_vllm/moe/route.py (same names and contract).
+
+The router (``R9kTopKRouter``, a ``FusedTopKRouter`` whose ``_compute_routing`` runs ``torch.ops.r9700.moe_route``)
+leaves the tables on the ``RoutedExperts`` object it shares with ``R9700Mxfp4Experts``, whose apply() then skips its
+own align. Rows above ``MAX_ROWS`` take the top-k kernel plus the multi-workgroup align instead.
+
+Numerics: fp32 softmax; ids ordered by logit (the probability order), ties to the lower expert index; weights
+p / sum (renorm over the selection). The tables are in canonical order (rows ascending within each expert).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from dataclasses import dataclass
+
+import torch
+
+from .._compat import get_logger, register_custom_op
+from ..kernels import moe as KM
+
+logger = get_logger(__name__)
+
+MAX_ROWS = int(os.environ.get("R9K_MOE_ROUTE_MAX_ROWS", "256"))
+_L = None
+_DONE = False
+_LIB = torch.library.Library("r9700", "FRAGMENT")
+
+
+def lib():
+    global _L
+    if _L is None:
+        L = KM.lib()
+        if not hasattr(L, "r9k_moe_route"):
+            raise RuntimeError("libr9k.so has no r9k_moe_route (rebuild r9700-stack_amd)")
+        L.r9k_moe_route.restype = ctypes.c_int
+        L.r9k_moe_route.argtypes = [ctypes.c_long, ctypes.c_int] + [ctypes.c_long] * 6 + [ctypes.c_int] * 5 \
+            + [ctypes.c_long]
+        L.r9k_moe_route_max_experts.restype = ctypes.c_int
+        L.r9k_moe_route_max_topk.restype = ctypes.c_int
+        _L = L
+    return _L
+
+
+def available() -> bool:
+    try:
+        lib()
+        return True
+    except Exception:
+        return False
+
+
+def capacity(numel: int, num_experts: int, blk: int) -> int:
+    """sorted_ids length for `numel` routed rows, as moe_align_block_size sizes it."""
+    return KM.capacity(numel, num_experts, blk)
+
+
+def scratch_ints(E: int) -> int:
+    """int32 count of the routing scratch of the reference contract (counts[E], cursor[E], arrive). The gfx950
+    kernel keeps that state in LDS and never touches it; the size is kept so callers allocate as before."""
+    return 2 * E + 1
+
+
+def moe_route(logits: torch.Tensor, topk: int, renorm: bool, blk: int, sorted_ids: torch.Tensor,
+              expert_ids: torch.Tensor, ntpp: torch.Tensor, scratch: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """logits [M, E] bf16 -> (weights fp32 [M, topk], ids int32 [M, topk]); fills the first capacity(M*topk)
+    entries of sorted_ids / expert_ids and ntpp[0]."""
+    M, E = logits.shape
+    w = torch.empty((M, topk), dtype=torch.float32, device=logits.device)
+    ids = torch.empty((M, topk), dtype=torch.int32, device=logits.device)
+    rc = lib().r9k_moe_route(logits.data_ptr(), logits.stride(0), w.data_ptr(), ids.data_ptr(),
+                             sorted_ids.data_ptr(), expert_ids.data_ptr(), ntpp.data_ptr(), scratch.data_ptr(),
+                             M, E, topk, 1 if renorm else 0, blk, torch.cuda.current_stream().cuda_stream)
+    if rc:
+        raise RuntimeError(f"r9k_moe_route failed ({rc}) M={M} E={E} topk={topk} blk={blk}")
+    return w, ids
+
+
+def _moe_route_fake(logits: torch.Tensor, topk: int, renorm: bool, blk: int, sorted_ids: torch.Tensor,
+                    expert_ids: torch.Tensor, ntpp: torch.Tensor, scratch: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    M = logits.shape[0]
+    return (logits.new_empty((M, topk), dtype=torch.float32), logits.new_empty((M, topk), dtype=torch.int32))
+
+
+def register() -> None:
+    global _DONE
+    if _DONE:
+        return
+    register_custom_op(_LIB, "moe_route", moe_route, ["sorted_ids", "expert_ids", "ntpp", "scratch"],
+                       _moe_route_fake)
+    _DONE = True
+
+
+@dataclass
+class Tables:
+    """Routing tables for one call, keyed by the topk_ids tensor the router returned with them."""
+    ids: torch.Tensor
+    sorted_ids: torch.Tensor
+    expert_ids: torch.Tensor
+    ntpp: torch.Tensor
+    blk: int
+    numel: int
+
+    def matches(self, topk_ids: torch.Tensor, blk: int, numel: int) -> bool:
+        return (self.ids.data_ptr() == topk_ids.data_ptr() and self.ids.shape == topk_ids.shape
+                and self.blk == blk and self.numel == numel)
+
+
+def _fits(logits: torch.Tensor, topk: int, E: int) -> bool:
+    L = lib()
+    return (logits.dim() == 2 and logits.dtype == torch.bfloat16 and logits.stride(1) == 1
+            and 1 <= logits.shape[0] <= MAX_ROWS and logits.shape[1] == E and E <= L.r9k_moe_route_max_experts()
+            and 1 <= topk <= min(E, L.r9k_moe_route_max_topk()))
+
+
+def make_router(stock, routed_experts):
+    """An R9kTopKRouter standing in for a stock FusedTopKRouter (softmax scoring, no EPLB). Needs vLLM."""
+    from vllm.model_executor.layers.fused_moe.router.fused_topk_router import FusedTopKRouter
+
+    class R9kTopKRouter(FusedTopKRouter):
+        def __init__(self):
+            super().__init__(top_k=stock.top_k, global_num_experts=stock.global_num_experts,
+                             scoring_func=stock.scoring_func, renormalize=stock.renormalize,
+                             eplb_state=stock.eplb_state)
+            self.capture_fn = getattr(stock, "capture_fn", None)
+            self._routing_replay_out = getattr(stock, "_routing_replay_out", None)
+            self.routed_experts = routed_experts
+            self._bufs: dict = {}
+            # allocate at construction, outside any graph-capture memory-profiling pass
+            if torch.cuda.is_available():
+                self._buffers(torch.device("cuda", torch.cuda.current_device()), stock.global_num_experts)
+
+        def _buffers(self, device: torch.device, E: int):
+            b = self._bufs.get(device)
+            if b is None:
+                cap = max(capacity(m * self.top_k, E, 16 * KM.pick_mt(m * self.top_k, E))
+                          for m in range(1, MAX_ROWS + 1))
+                b = (torch.empty(cap, dtype=torch.int32, device=device),
+                     torch.empty(cap // 16, dtype=torch.int32, device=device),
+                     torch.zeros(1, dtype=torch.int32, device=device),
+                     torch.zeros(scratch_ints(E), dtype=torch.int32, device=device))
+                self._bufs[device] = b
+            return b
+
+        def _compute_routing(self, hidden_states, router_logits, indices_type, *, input_ids=None):
+            E = self.global_num_experts
+            if indices_type not in (None, torch.int32) or not _fits(router_logits, self.top_k, E):
+                self.routed_experts._r9k_tables = None
+                return super()._compute_routing(hidden_states, router_logits, indices_type, input_ids=input_ids)
+            M = router_logits.shape[0]
+            numel = M * self.top_k
+            blk = KM.MOE_BLOCK * KM.pick_mt(numel, E)
+            sorted_ids, expert_ids, ntpp, scratch = self._buffers(router_logits.device, E)
+            w, ids = torch.ops.r9700.moe_route(router_logits, self.top_k, self.renormalize, blk, sorted_ids,
+                                               expert_ids, ntpp, scratch)
+            self.routed_experts._r9k_tables = Tables(ids, sorted_ids, expert_ids, ntpp, blk, numel)
+            return w, ids
+
+    return R9kTopKRouter()
+
+
+def take(layer, topk_ids: torch.Tensor, blk: int, numel: int):
+    """The tables the router left for this call on the RoutedExperts `layer`, or None."""
+    t = getattr(layer, "_r9k_tables", None)
+    if t is None or not t.matches(topk_ids, blk, numel):
+        return None
+    return t.sorted_ids, t.expert_ids, t.ntpp
+
+
+def install(model: torch.nn.Module) -> int:
+    """Replace the router of every MoE runner under `model` that routes by plain softmax top-k.
+    R9K_MOE_ROUTE=stock skips."""
+    if os.environ.get("R9K_MOE_ROUTE", "stock") != "r9k" or not available():
+        return 0
+    register()
+    n = 0
+    for name, mod in model.named_modules():
+        router = getattr(mod, "router", None)
+        re_ = getattr(mod, "routed_experts", None)
+        if router is None or re_ is None or type(router).__name__ != "FusedTopKRouter":
+            continue
+        if getattr(router, "scoring_func", None) != "softmax" or getattr(router, "eplb_state", None) is not None:
+            logger.warning("r9700: fused MoE routing skipped for %s", name)
+            continue
+        mod.router = make_router(router, re_)
+        n += 1
+    if n:
+        logger.info("r9700: fused MoE routing (softmax top-k + align in one launch, <= %d rows) on %d runners",
+                    MAX_ROWS, n)
+    return n

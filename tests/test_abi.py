@@ -1,0 +1,59 @@
+"""The C-ABI library loads and exports every symbol include/r9k.h declares, and shape errors come back as the
+documented return codes before anything touches a GPU (CPU only: no kernel launches)."""
+import ctypes
+import os
+import re
+
+from r9700_vllm.kernels import moe as K
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_symbols():
+    src = open(os.path.join(ROOT, "include", "r9k.h")).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return re.findall(r"^\s*(?:int|long)\s+(r9k_\w+)\s*\(", src, flags=re.M)
+
+
+def test_header_symbols_exported():
+    names = declared_symbols()
+    assert len(names) >= 18, names
+    L = ctypes.CDLL(K._lib_path())
+    missing = [n for n in names if not hasattr(L, n)]
+    assert not missing, missing
+
+
+def test_python_binding_contract():
+    L = K.lib()
+    assert L.r9k_moe_block() == 16
+    assert L.r9k_fold_supported() == 0
+    assert L.r9k_moe_route_max_experts() == 1024 and L.r9k_moe_route_max_topk() == 16
+    assert K.prefill_block(17) == 64 and L.r9k_moe_prefill_bm(20) == -1 and L.r9k_moe_prefill_bk(-1) == -1
+
+
+def test_shape_errors_before_launch():
+    L = K.lib()
+    z = 0
+    # N % 16, K % 32, bad MT (the reference's -1 / -2 / -7)
+    assert L.r9k_moe_mxfp4a8(1, 1, 1, 1, 1, 1, 1, 1, 1, z, 0, 0, 4, 16, 1, 64, 17, 2, 4, 2, 1, z) == -1
+    assert L.r9k_moe_mxfp4a8(1, 1, 1, 1, 1, 1, 1, 1, 1, z, 0, 0, 4, 16, 1, 48, 16, 2, 4, 2, 1, z) == -2
+    assert L.r9k_moe_mxfp4a8(1, 1, 1, 1, 1, 1, 1, 1, 1, z, 0, 0, 4, 16, 1, 64, 16, 2, 4, 2, 3, z) == -7
+    assert L.r9k_moe_4bit_prefill(0, 1, 1, 1, 1, 1, 1, 1, 1, 1, z, 0, 0, 4, 16, 1, 64, 16, 99, z) == -7
+    assert L.r9k_moe_4bit_prefill(3, 1, 1, 1, 1, 1, 1, 1, 1, 1, z, 0, 0, 4, 16, 1, 64, 16, 17, z) == -8
+    assert L.r9k_moe_4bit_prefill(1, 1, 1, 1, 1, 1, 1, 1, 1, 1, z, 0, 0, 4, 16, 1, 64, 16, 17, z) == -8
+    # route: topk > 16, E > 1024, blk not a power of two (the reference returns 1)
+    assert L.r9k_moe_route(1, 64, 1, 1, 1, 1, 1, 1, 1, 64, 17, 1, 16, z) == 1
+    assert L.r9k_moe_route(1, 2048, 1, 1, 1, 1, 1, 1, 1, 2048, 8, 1, 16, z) == 1
+    assert L.r9k_moe_route(1, 64, 1, 1, 1, 1, 1, 1, 1, 64, 8, 1, 24, z) == 1
+    assert L.r9k_moe_topk(1, 64, 1, 1, 1, 64, 65, 1, z) == 1
+    assert L.r9k_moe_align(1, 100000, 64, 64, 1, 1, 1, 1, 1, z) == 1          # scratch too small
+    assert L.r9k_moe_align_scratch_ints(4096, 64) == 1
+    assert L.r9k_moe_align_scratch_ints(65536, 288) == 1 + 32 * 288
+    # sum: N % 8
+    assert L.r9k_moe_sum(16, 0, 16, 1, 8, 12, 0, 12, z) == 1
+    # quant: nothing to do for M == 0; tiled gate refused
+    assert L.r9k_quant_rows_fp8(1, 1, 1, 0, 64, 64, z) == 0
+    assert L.r9k_quant_rows_fp8_gate(16, 16, 16, 16, 16, 1, 64, 64, 1, z) == -3
+    # converter: K % 32
+    assert L.r9k_nvfp4_to_mxfp4(16, 16, 16, 16, 16, 4, 48, z) == -2
+    assert L.r9k_quantize_mxfp4_search(16, 16, 16, 4, 40, z) == -2

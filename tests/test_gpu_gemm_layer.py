@@ -1,0 +1,191 @@
+"""GPU parity: the grouped MXFP4 x fp8 GEMM (decode and prefill entries), the dense MXFP4 linear, the NVFP4 ->
+MXFP4 converter and the whole MoE layer (R9700Mxfp4Experts.apply), through the C-ABI against the CPU oracle.
+
+Float outputs are held to the north-star tolerance (norm ratio <= 1e-2, cosine >= 0.9999) and, tighter, to what
+fp32 accumulation order can explain (rel <= 2e-3); converter outputs and routing ids are bit-exact."""
+import numpy as np
+import pytest
+import torch
+
+from helpers import bf16_bits_to_f64, cosine, make_experts, rel_err
+from oracle import oracle as O
+from r9700_vllm import ops
+from r9700_vllm.kernels import moe as K
+from r9700_vllm.moe.experts import R9700Mxfp4Experts
+from r9700_vllm.quant import nvfp4 as NV
+
+pytestmark = pytest.mark.gpu
+
+
+def gemm_case(dev, E, M, topk, N, Kd, seed, MT=1, prefill=None, down=False):
+    g = torch.Generator().manual_seed(seed)
+    packed, e8 = make_experts(E, N, Kd, g)
+    W = K.prepare_mxfp4_weights(packed.to(dev), e8.to(dev))
+    numel = M * topk
+    rows_a = numel if down else M
+    x = (torch.randn(rows_a, Kd, generator=g) * 0.5).to(torch.bfloat16)
+    ids = torch.stack([torch.randperm(E, generator=g)[:topk] for _ in range(M)]).to(torch.int32)
+    tw = torch.rand(numel, generator=g).float() if down else None
+    blk = K.prefill_block(prefill) if prefill is not None else 16 * MT
+    sid, eid, ntpp = (t.to(dev) for t in K.align_block_size_ref(ids, E, blk))
+    xq, xs = K.quant_rows_fp8(x.to(dev))
+    out = torch.full((numel, N), float("nan"), dtype=torch.bfloat16, device=dev)
+    K.moe_gemm(xq, xs, W, out, sid, eid, ntpp, numel, 1 if down else topk, tw.to(dev) if down else None,
+               num_experts=E, MT=MT, prefill=prefill)
+    qo, so = O.quant_rows_fp8(x)
+    Wd = {e: O.mxfp4_dequant(packed[e], e8[e]) for e in range(E)}
+    ref = O.grouped_gemm(qo, so, Wd, ids.reshape(-1).numpy(), 1 if down else topk,
+                         tw.numpy() if down else None)
+    got = O.bf16_bits(out)
+    assert not np.isnan(bf16_bits_to_f64(got).numpy()).any(), "a routed row was not written"
+    r, c = rel_err(bf16_bits_to_f64(got), bf16_bits_to_f64(ref)), cosine(bf16_bits_to_f64(got), bf16_bits_to_f64(ref))
+    exact = (got == ref).mean()
+    print(f"gemm E={E} M={M} k={topk} N={N} K={Kd} MT={MT} pf={prefill} down={down}: rel {r:.2e} cos {c:.7f} "
+          f"exact {exact:.4f}", flush=True)
+    assert r < 2e-3 and c > 0.99999 and exact > 0.97
+
+
+@pytest.mark.parametrize("E,M,topk,N,Kd", [(8, 1, 2, 1024, 2048), (32, 4, 8, 1024, 2048), (64, 16, 8, 2048, 512),
+                                           (288, 64, 8, 1024, 2048), (8, 3, 2, 48, 1024), (8, 3, 2, 2560, 320),
+                                           (8, 5, 3, 320, 160), (4, 6, 2, 64, 544), (4, 2, 2, 32, 32)])
+@pytest.mark.parametrize("down", [False, True])
+def test_grouped_gemm_decode(dev, E, M, topk, N, Kd, down):
+    gemm_case(dev, E, M, topk, N, Kd, seed=E * 100 + M + N, down=down)
+
+
+@pytest.mark.parametrize("MT", [2, 4])
+@pytest.mark.parametrize("N,Kd", [(640, 2560), (2560, 320), (1024, 2048)])
+def test_grouped_gemm_multitile(dev, MT, N, Kd):
+    gemm_case(dev, 16, 200, 4, N, Kd, seed=MT + N, MT=MT)
+    gemm_case(dev, 16, 200, 4, Kd if Kd % 16 == 0 else N, N if N % 32 == 0 else Kd, seed=MT + N + 1, MT=MT, down=True)
+
+
+@pytest.mark.parametrize("cfg", [17, 10, 12, 6])
+def test_grouped_gemm_prefill_entry(dev, cfg):
+    gemm_case(dev, 16, 600, 4, 1040, 1024, seed=cfg, prefill=cfg)
+    gemm_case(dev, 16, 600, 4, 512, 320, seed=cfg + 50, prefill=cfg, down=True)
+
+
+@pytest.mark.parametrize("M,N,Kd", [(16, 1024, 2048), (1, 17408, 5120), (4, 1024, 5120), (300, 512, 1024)])
+def test_dense_mxfp4_linear(dev, M, N, Kd):
+    """BASELINE config 1 (and small slices of config 4): identity routing tables through ops.mxfp4_linear."""
+    g = torch.Generator().manual_seed(M + N)
+    packed, e8 = make_experts(1, N, Kd, g)
+    W = K.prepare_mxfp4_weights(packed.to(dev), e8.to(dev))
+    x = torch.randn(M, Kd, generator=g).to(torch.bfloat16)
+    out = ops.mxfp4_linear(x.to(dev), W.wq, W.wsr, N, Kd)
+    qo, so = O.quant_rows_fp8(x)
+    ref = O.grouped_gemm(qo, so, {0: O.mxfp4_dequant(packed[0], e8[0])}, np.zeros(M, dtype=np.int32), 1)
+    got = O.bf16_bits(out)
+    r = rel_err(bf16_bits_to_f64(got), bf16_bits_to_f64(ref))
+    assert r < 2e-3 and cosine(bf16_bits_to_f64(got), bf16_bits_to_f64(ref)) > 0.99999
+
+
+def test_nvfp4_to_mxfp4_config4_bit_exact(dev):
+    """BASELINE config 4 full shape: [17408, 5120] NVFP4 (uniform codes, s16 = e4m3(|N(0,1)| * 0.05), global 1)."""
+    g = torch.Generator().manual_seed(20261201 + 4000)
+    N, Kd = 17408, 5120
+    p16 = torch.randint(0, 256, (N, Kd // 2), generator=g, dtype=torch.int32).to(torch.uint8)
+    s16 = (torch.randn(N, Kd // 16, generator=g).abs() * 0.05).to(torch.float8_e4m3fn)
+    div = torch.ones(N)
+    pm, em = NV.nvfp4_to_mxfp4(p16.to(dev), s16.to(dev), div.to(dev))
+    po, eo = O.nvfp4_to_mxfp4(p16.numpy(), s16.view(torch.uint8).numpy(), div.numpy())
+    assert np.array_equal(pm.cpu().numpy(), po)
+    assert np.array_equal(em.cpu().numpy(), eo)
+
+
+def test_nvfp4_to_mxfp4_row_divisors_and_host_input(dev):
+    """Per-row global divisors (a fused gate_up with two shards) and host-resident input (chunked device copies)."""
+    g = torch.Generator().manual_seed(9)
+    N, Kd = 512, 2560
+    w = torch.randn(N, Kd, generator=g) * 0.02
+    gd = torch.where(torch.arange(N) < N // 2, torch.tensor(3000.0), torch.tensor(7000.0))
+    x = w.reshape(N, Kd // 16, 16)
+    s16 = (x.abs().amax(-1) / 6.0 * gd[:, None]).clamp(min=2 ** -9).to(torch.float8_e4m3fn)
+    v = x * gd[:, None, None] / s16.float().unsqueeze(-1)
+    code = (torch.bucketize(v.abs(), NV._MID).to(torch.uint8) | ((v < 0).to(torch.uint8) << 3)).reshape(N, Kd)
+    p16 = code[:, 0::2] | (code[:, 1::2] << 4)
+    pm, em = NV.nvfp4_to_mxfp4(p16, s16, gd, rows_per_chunk=200)          # CPU tensors in, CPU tensors out
+    po, eo = O.nvfp4_to_mxfp4(p16.numpy(), s16.view(torch.uint8).numpy(), gd.numpy())
+    assert pm.device.type == "cpu" and np.array_equal(pm.numpy(), po) and np.array_equal(em.numpy(), eo)
+
+
+def test_quantize_mxfp4_search_bit_exact(dev):
+    g = torch.Generator().manual_seed(12)
+    w = torch.randn(1024, 2048, generator=g) * torch.exp(torch.randn(1024, 1, generator=g))
+    w[0, :64] = 0.0
+    pm, em = NV.quantize_mxfp4_search(w.to(dev))
+    po, eo = O.quantize_mxfp4_search(w.numpy())
+    assert np.array_equal(pm.cpu().numpy(), po) and np.array_equal(em.cpu().numpy(), eo)
+
+
+# --------------------------------------------------------------------------------------------------- layer
+def make_layer(dev, E, H, I, seed, lo=118, hi=126):
+    """MXFP4 layer weights drawn on the GPU (seeded), plus their checkpoint-layout copies for the oracle."""
+    g = torch.Generator(device=dev).manual_seed(seed)
+    p13 = torch.randint(0, 256, (E, 2 * I, H // 2), generator=g, device=dev, dtype=torch.int32).to(torch.uint8)
+    e13 = torch.randint(lo, hi + 1, (E, 2 * I, H // 32), generator=g, device=dev, dtype=torch.int32).to(torch.uint8)
+    p2 = torch.randint(0, 256, (E, H, I // 2), generator=g, device=dev, dtype=torch.int32).to(torch.uint8)
+    e2 = torch.randint(lo, hi + 1, (E, H, I // 32), generator=g, device=dev, dtype=torch.int32).to(torch.uint8)
+    W13 = K.prepare_mxfp4_weights(p13, e13)
+    W2 = K.prepare_mxfp4_weights(p2, e2)
+    return (p13, e13), (p2, e2), W13, W2
+
+
+def run_layer(dev, E, H, I, T, topk, seed, tokens=None, zipf=False, lo=118, hi=126):
+    (p13, e13), (p2, e2), W13, W2 = make_layer(dev, E, H, I, seed, lo, hi)
+    g = torch.Generator().manual_seed(seed + 1)
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    logits = torch.randn(T, E, generator=g)
+    if zipf:
+        rank = torch.randperm(E, generator=g).float() + 1
+        logits = logits - 1.1 * torch.log(rank)[None, :]
+    logits = logits.to(torch.bfloat16)
+    w, ids = K.moe_topk(logits.to(dev), topk, True)
+    ex = R9700Mxfp4Experts.standalone(W13.wsr, W2.wsr)
+    out = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
+    ex.apply(out, x.to(dev), W13.wq, W2.wq, w, ids, "silu", E, None, None, None, None, None, None, False)
+    torch.cuda.synchronize()
+    ro = O.route(logits, topk, True)
+    assert np.array_equal(ids.cpu().numpy(), ro[1]), "routing ids"
+    need = np.unique(ro[1][tokens] if tokens is not None else ro[1])
+    sub = lambda p: {int(e): p[int(e)].cpu() for e in need}                         # only touched experts
+    c13 = (_Lazy(sub(p13)), _Lazy(sub(e13)))
+    c2 = (_Lazy(sub(p2)), _Lazy(sub(e2)))
+    ref = O.moe_layer(x, logits, c13, c2, topk, True, tokens=tokens, route_out=ro)
+    got = O.bf16_bits(out)[ref["tokens"]]
+    a, b = bf16_bits_to_f64(got), bf16_bits_to_f64(ref["out"])
+    r, c = rel_err(a, b), cosine(a, b)
+    print(f"layer E={E} H={H} I={I} T={T} sampled={None if tokens is None else len(tokens)}: rel {r:.2e} "
+          f"cos {c:.7f}", flush=True)
+    assert r < 1e-2 and c >= 0.9999
+
+
+class _Lazy:
+    """Dict-backed stand-in for an [E, ...] tensor: the oracle only indexes touched experts."""
+
+    def __init__(self, d):
+        self.d = d
+
+    def __getitem__(self, e):
+        return self.d[int(e)]
+
+
+@pytest.mark.parametrize("T", [1, 8, 16, 64])
+def test_layer_config2_decode(dev, T):
+    run_layer(dev, 288, 2048, 512, T, 8, seed=20261201 + 2000 + T)
+
+
+def test_layer_config3_prefill_sampled(dev):
+    tokens = np.random.default_rng(3).choice(8192, 96, replace=False)
+    run_layer(dev, 288, 2048, 512, 8192, 8, seed=20261201 + 3000 + 8192, tokens=np.sort(tokens))
+
+
+@pytest.mark.parametrize("T", [1, 32])
+def test_layer_config5_skewed(dev, T):
+    run_layer(dev, 384, 4096, 2048, T, 8, seed=20261201 + 5000 + T, zipf=True, lo=116, hi=126)
+
+
+def test_layer_config5_skewed_4096_sampled(dev):
+    tokens = np.sort(np.random.default_rng(5).choice(4096, 32, replace=False))
+    run_layer(dev, 384, 4096, 2048, 4096, 8, seed=20261201 + 5000 + 4096, tokens=tokens, zipf=True, lo=116, hi=126)

@@ -1,0 +1,183 @@
+"""GPU parity: per-row fp8 quant, SiLU-gating quant, routing + align tables, top-k sum -- through the C-ABI against
+the CPU oracle. Integer outputs (fp8 codes and scales, ids, tables, bf16 sums) bit-exact; router weights within
+2e-6 (tests/test_moe_route_r9k.py:78 of the reference)."""
+import numpy as np
+import pytest
+import torch
+
+from helpers import check_tables
+from oracle import oracle as O
+from r9700_vllm.kernels import moe as K
+from r9700_vllm.moe import route
+
+pytestmark = pytest.mark.gpu
+
+
+def u8(t: torch.Tensor) -> np.ndarray:
+    return t.view(torch.uint8).cpu().numpy()
+
+
+@pytest.mark.parametrize("M,Kd,scale", [(1, 2048, 1.0), (64, 2048, 1.0), (8192, 2048, 1.0), (16, 5120, 3.0),
+                                        (4, 4096, 1e-4), (5, 96, 1.0), (3, 100, 1.0), (2, 9000, 1.0)])
+def test_quant_rows_fp8_bit_exact(dev, M, Kd, scale):
+    print(f"quant M={M} K={Kd}", flush=True)
+    g = torch.Generator().manual_seed(M + Kd)
+    x = (torch.randn(M, Kd, generator=g) * scale).to(torch.bfloat16)
+    q, s = K.quant_rows_fp8(x.to(dev))
+    qo, so = O.quant_rows_fp8(x)
+    assert np.array_equal(u8(q), qo)
+    assert np.array_equal(s.cpu().numpy().view(np.uint32), so.view(np.uint32))
+
+
+def test_quant_rows_fp8_strided_and_edge_rows(dev):
+    base = torch.zeros(4, 80)
+    base[1, 3], base[1, 4] = 3.0e38, -1.0
+    base[2] = torch.linspace(-1e-3, 1e-3, 80)
+    base[2, 0] = 5.0
+    base[3], base[3, 7] = -1e-30, 1.0
+    xb = base.to(torch.bfloat16)
+    xd = xb.to(dev)[:, :64]                      # row stride 80 > K = 64
+    q, s = K.quant_rows_fp8(xd)
+    qo, so = O.quant_rows_fp8(xb[:, :64].contiguous())
+    assert np.array_equal(u8(q), qo) and np.array_equal(s.cpu().numpy(), so)
+
+
+def test_quant_rows_fp8_gate(dev):
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(37, 2048, generator=g).to(torch.bfloat16)
+    wg = (torch.randn(2048, generator=g) * 0.02).to(torch.bfloat16)
+    q, s, gate = K.quant_rows_fp8_gate(x.to(dev), wg.to(dev))
+    qo, so = O.quant_rows_fp8(x)
+    assert np.array_equal(u8(q), qo) and np.array_equal(s.cpu().numpy(), so)
+    ref = torch.sigmoid((x.float() @ wg.float()).to(torch.bfloat16).float()).to(torch.bfloat16).float()
+    assert (gate.cpu() - ref).abs().max().item() <= 2 ** -8        # one bf16 ulp of a value in (0, 1)
+
+
+@pytest.mark.parametrize("M,I,scale", [(37, 320, 2.0), (512, 512, 1.0), (64, 2048, 1.0), (3, 100, 1.0)])
+def test_silu_mul_quant_fp8(dev, M, I, scale):
+    g = torch.Generator().manual_seed(M * I)
+    gu = (torch.randn(M, 2 * I, generator=g) * scale).to(torch.bfloat16)
+    q, s = K.silu_mul_quant_fp8(gu.to(dev))
+    qo, so, act = O.silu_mul_quant_fp8(gu)
+    # exp() may differ by an fp32 ulp between the device and libm: codes may move by one step at a rounding edge
+    qd = u8(q)
+    same = (qd == qo).mean()
+    assert same >= 0.999, same
+    assert np.all(np.abs(O.e4m3_table()[qd] - O.e4m3_table()[qo])[qd != qo] <= np.abs(O.e4m3_table()[qo])[qd != qo] / 8 + 2 ** -9)
+    assert np.allclose(s.cpu().numpy(), so, rtol=1e-6, atol=0)
+    deq = O.e4m3_table()[qd] * s.cpu().numpy()[:, None]
+    gf, uf = gu.float()[:, :I], gu.float()[:, I:]
+    ref = (torch.nn.functional.silu(gf) * uf).numpy()
+    assert np.linalg.norm(deq - ref) / np.linalg.norm(ref) < 6e-2      # the reference's quant round-trip gate
+
+
+@pytest.mark.parametrize("M,E,topk,blk", [(1, 288, 8, 16), (8, 288, 8, 16), (16, 288, 8, 16), (64, 288, 8, 16),
+                                          (37, 512, 10, 32), (256, 384, 8, 64), (5, 48, 6, 16), (300, 100, 10, 16)])
+@pytest.mark.parametrize("renorm", [True, False])
+def test_moe_route_fused(dev, M, E, topk, blk, renorm):
+    print(f"route M={M} E={E} topk={topk} blk={blk} renorm={renorm}", flush=True)
+    g = torch.Generator().manual_seed(M * 7 + E)
+    logits = torch.randn(M, E, generator=g).to(torch.bfloat16)
+    numel = M * topk
+    cap = route.capacity(numel, E, blk)
+    guard = 64
+    s_ = torch.full((cap + guard,), -9, dtype=torch.int32, device=dev)
+    e_ = torch.full((cap // blk + guard,), -9, dtype=torch.int32, device=dev)
+    n_ = torch.zeros(1, dtype=torch.int32, device=dev)
+    scratch = torch.zeros(route.scratch_ints(E), dtype=torch.int32, device=dev)
+    w, ids = route.moe_route(logits.to(dev), topk, renorm, blk, s_[:cap], e_[:cap // blk], n_, scratch)
+    wo, ido = O.route(logits, topk, renorm)
+    assert np.array_equal(ids.cpu().numpy(), ido)
+    assert np.abs(w.cpu().numpy() - wo).max() < 2e-6
+    so, eo, no = O.align(ido, E, blk)
+    s_h, e_h = s_.cpu().numpy(), e_.cpu().numpy()
+    assert np.array_equal(s_h[:cap], so) and np.array_equal(e_h[:cap // blk], eo) and n_.item() == no[0]
+    assert np.all(s_h[cap:] == -9) and np.all(e_h[cap // blk:] == -9), "wrote past the tables"
+    assert not scratch.any()
+    check_tables(so, eo, no, ido, blk, numel, E)
+
+
+def test_moe_route_degenerate_rows(dev):
+    """NaN, +-inf, all-equal and -3e38 rows, E not a multiple of 64 (tests/test_moe_route_r9k.py:84-104)."""
+    for Ed in (512, 100, 48):
+        M, tk = 24, 10
+        g = torch.Generator().manual_seed(Ed)
+        x = torch.randn(M, Ed, generator=g) * 2
+        x[0] = float("nan"); x[1, :5] = float("nan"); x[2] = float("inf"); x[3] = float("-inf"); x[4] = 0.0
+        x[5] = 1.0; x[6, ::2] = float("inf"); x[7] = -3e38
+        x = x.to(torch.bfloat16)
+        blk = 16
+        cap = route.capacity(M * tk, Ed, blk)
+        s_ = torch.full((cap + 64,), -9, dtype=torch.int32, device=dev)
+        e_ = torch.full((cap // blk + 64,), -9, dtype=torch.int32, device=dev)
+        n_ = torch.zeros(1, dtype=torch.int32, device=dev)
+        sc = torch.zeros(route.scratch_ints(Ed), dtype=torch.int32, device=dev)
+        w, ids = route.moe_route(x.to(dev), tk, True, blk, s_[:cap], e_[:cap // blk], n_, sc)
+        wo, ido = O.route(x, tk, True)
+        assert np.array_equal(ids.cpu().numpy(), ido)
+        assert np.isfinite(w.cpu().numpy()).all() and np.abs(w.cpu().numpy() - wo).max() < 2e-6
+        assert bool((s_[cap:] == -9).all()) and bool((e_[cap // blk:] == -9).all())
+        check_tables(s_[:cap].cpu().numpy(), e_[:cap // blk].cpu().numpy(), n_.cpu().numpy(), ido, blk, M * tk, Ed)
+
+
+def test_moe_route_large_m_path(dev):
+    """numel above the one-workgroup limit: top-k kernel + single-workgroup table launch."""
+    M, E, topk, blk = 1024, 288, 8, 64
+    g = torch.Generator().manual_seed(5)
+    logits = torch.randn(M, E, generator=g).to(torch.bfloat16)
+    cap = route.capacity(M * topk, E, blk)
+    s_ = torch.empty(cap, dtype=torch.int32, device=dev)
+    e_ = torch.empty(cap // blk, dtype=torch.int32, device=dev)
+    n_ = torch.zeros(1, dtype=torch.int32, device=dev)
+    w, ids = route.moe_route(logits.to(dev), topk, True, blk, s_, e_, n_,
+                             torch.zeros(route.scratch_ints(E), dtype=torch.int32, device=dev))
+    wo, ido = O.route(logits, topk, True)
+    so, eo, no = O.align(ido, E, blk)
+    assert np.array_equal(ids.cpu().numpy(), ido) and np.abs(w.cpu().numpy() - wo).max() < 2e-6
+    assert np.array_equal(s_.cpu().numpy(), so) and np.array_equal(e_.cpu().numpy(), eo) and n_.item() == no[0]
+
+
+@pytest.mark.parametrize("T,E,topk,blk,zipf", [(8192, 288, 8, 64, False), (4096, 384, 8, 64, True),
+                                               (256, 384, 8, 16, True), (3000, 64, 4, 128, False)])
+def test_topk_and_align_multiblock(dev, T, E, topk, blk, zipf):
+    print(f"topk+align T={T} E={E} blk={blk} zipf={zipf}", flush=True)
+    g = torch.Generator().manual_seed(T + E)
+    logits = torch.randn(T, E, generator=g)
+    if zipf:
+        rank = torch.randperm(E, generator=g).float() + 1
+        logits = logits - 1.1 * torch.log(rank)[None, :]
+    logits = logits.to(torch.bfloat16)
+    w, ids = K.moe_topk(logits.to(dev), topk, True)
+    wo, ido = O.route(logits, topk, True)
+    assert np.array_equal(ids.cpu().numpy(), ido) and np.abs(w.cpu().numpy() - wo).max() < 2e-6
+    for rep in range(2):                                  # the second call reuses the (self-cleaning) scratch
+        s_, e_, n_ = K.moe_align(ids, blk, E)
+        so, eo, no = O.align(ido, E, blk)
+        assert np.array_equal(s_.cpu().numpy(), so) and np.array_equal(e_.cpu().numpy(), eo)
+        assert n_.item() == no[0]
+    sc = K._ALIGN_SCRATCH[(dev.type, dev.index)]
+    assert sc[0].item() == 0
+
+
+def test_align_skips_foreign_experts(dev):
+    """Ids mapped to -1 (an expert map: experts on another rank) are left out of the tables."""
+    g = torch.Generator().manual_seed(3)
+    ids = torch.stack([torch.randperm(16, generator=g)[:4] for _ in range(40)]).to(torch.int32)
+    emap = torch.tensor([i if i < 10 else -1 for i in range(16)], dtype=torch.int32)
+    s_, e_, n_ = K.moe_align(ids.to(dev), 16, 10, emap.to(dev))
+    mapped = emap[ids.long()].numpy()
+    so, eo, no = O.align(mapped, 10, 16)
+    assert np.array_equal(s_.cpu().numpy(), so) and np.array_equal(e_.cpu().numpy(), eo) and n_.item() == no[0]
+
+
+@pytest.mark.parametrize("M,topk,N", [(1, 8, 2048), (64, 8, 2048), (37, 10, 2560), (8192, 8, 2048), (3, 4, 320)])
+def test_moe_sum_bit_exact(dev, M, topk, N):
+    g = torch.Generator().manual_seed(M + N)
+    down = (torch.randn(M, topk, N, generator=g) * 0.5).to(torch.bfloat16)
+    shared = (torch.randn(M, N, generator=g) * 0.5).to(torch.bfloat16)
+    out = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+    K.moe_sum(down.to(dev), None, out)
+    assert np.array_equal(O.bf16_bits(out), O.moe_sum(down))
+    out2 = torch.empty(M, N + 16, dtype=torch.bfloat16, device=dev)[:, :N]          # strided output rows
+    K.moe_sum(down.to(dev), shared.to(dev), out2)
+    assert np.array_equal(O.bf16_bits(out2), O.moe_sum(down, shared))

@@ -1,0 +1,81 @@
+"""Host-side logic of the package (CPU only, no kernel launches): the gfx950 weight layouts and their inverses,
+table sizing and the tile-selection helpers that mirror the reference's kernels/moe.py."""
+import numpy as np
+import pytest
+import torch
+
+from helpers import make_experts
+from r9700_vllm.kernels import moe as K
+
+
+@pytest.mark.parametrize("N,Kd", [(16, 128), (32, 2048), (48, 320), (64, 160), (16, 32), (32, 544)])
+def test_permute_fragments_lane_layout(N, Kd):
+    g = torch.Generator().manual_seed(N + Kd)
+    packed, _ = make_experts(2, N, Kd, g)
+    wq = K.permute_fragments(packed)
+    assert wq.dtype == torch.int32 and wq.shape == (2, N * Kd // 8)
+    b = wq.view(torch.uint8).reshape(2, -1)
+    nkf, G = Kd // 128, (Kd % 128) // 32
+    for e in range(2):
+        for nt in range(N // 16):
+            base = nt * 8 * Kd
+            for kt in range(nkf + (1 if G else 0)):
+                groups = 4 if kt < nkf else G
+                for lane in range(16 * groups):
+                    gg, r = lane >> 4, lane & 15
+                    got = b[e, base + kt * 1024 + lane * 16: base + kt * 1024 + lane * 16 + 16]
+                    want = packed[e, nt * 16 + r, kt * 64 + gg * 16: kt * 64 + gg * 16 + 16]
+                    assert torch.equal(got, want)
+    assert torch.equal(K.unpermute_fragments(wq, N, Kd), packed)
+
+
+@pytest.mark.parametrize("N,Kd", [(16, 128), (32, 2048), (48, 320), (64, 160), (16, 32), (32, 544), (16, 512)])
+def test_pack_scales_lane_layout(N, Kd):
+    g = torch.Generator().manual_seed(N * Kd)
+    _, e8 = make_experts(2, N, Kd, g, 0, 255)
+    wsr = K.pack_scales(e8)
+    KB = Kd // 32
+    assert wsr.shape == (2, KB + 1, N)
+    body = wsr.reshape(2, -1)
+    nq = KB // 16
+    for e in range(2):
+        for nt in range(N // 16):
+            base = nt * 16 * KB
+            for kb in range(KB):
+                kt, gg = kb // 4, kb % 4
+                for r in range(16):
+                    lane = gg * 16 + r
+                    off = (kt // 4) * 256 + lane * 4 + (kt % 4) if kt < 4 * nq else nq * 256 + (kt - 4 * nq) * 64 + lane
+                    assert body[e, base + off] == e8[e, nt * 16 + r, kb]
+        assert torch.equal(wsr[e, KB], e8[e].max(dim=1).values)
+    assert torch.equal(K.unpack_scales(wsr), e8)
+
+
+def test_fold_stats_on_packed_layout():
+    g = torch.Generator().manual_seed(0)
+    _, e8 = make_experts(3, 32, 512, g, 118, 126)
+    st = K.fold_stats(K.pack_scales(e8))
+    d = (e8.max(dim=2, keepdim=True).values.int() - e8.int()).clamp(0, 16)
+    assert st.hist == torch.bincount(d.reshape(-1), minlength=17).tolist()
+    assert not K.fold_decide(K.pack_scales(e8))
+
+
+def test_capacity_and_pick_mt():
+    assert K.capacity(512, 288, 16) == (512 + 288 * 15 + 15) // 16 * 16
+    assert K.pick_mt(8, 288) == 1 and K.pick_mt(65536, 288) == 4 and K.pick_mt(288 * 20, 288) == 2
+
+
+def test_prefill_cfg_table_from_library():
+    for cfg, (bm, _) in K.PREFILL_TILES.items():
+        assert K.prefill_block(cfg) == bm
+        assert K.prefill_bk(cfg) == 32
+    assert K.pick_moe_prefill(4, 512) == 17 and K.pick_moe_prefill(1, 512) is None
+    with pytest.raises(ValueError):
+        K.prefill_block(99)
+
+
+def test_align_block_size_ref_canonical():
+    ids = torch.tensor([[3, 1], [1, 0], [3, 2]])
+    s, e, n = K.align_block_size_ref(ids, 4, 4)
+    assert n.item() == 16 and s[:16].tolist() == [3, 6, 6, 6, 1, 2, 6, 6, 5, 6, 6, 6, 0, 4, 6, 6]
+    assert e[:4].tolist() == [0, 1, 2, 3] and (e[4:] == -1).all()

@@ -1,0 +1,65 @@
+"""Pins the oracle's top-k sum and dequant-then-matmul GEMM (CPU only).
+
+moe_sum: a sequential fp32 loop (kernels/r9k_moe_sum.hip:37-55 of the reference) and, where every partial sum is
+exact, torch's own bf16 sum. GEMM: pure-Python dot products on tiny inputs against oracle.grouped_gemm, and the
+MXFP4 dequant against the E2M1 x 2^(e - 127) closed form (the reference tests' mx_deq)."""
+import numpy as np
+import torch
+
+from helpers import make_experts
+from oracle import oracle as O
+
+
+def test_moe_sum_sequential_loop():
+    g = torch.Generator().manual_seed(0)
+    down = (torch.randn(3, 8, 64, generator=g) * 0.5).to(torch.bfloat16)
+    shared = (torch.randn(3, 64, generator=g) * 0.5).to(torch.bfloat16)
+    for sh in (None, shared):
+        got = O.moe_sum(down, sh)
+        d = down.float().numpy()
+        for m in range(3):
+            for n in range(64):
+                acc = np.float32(0)
+                for j in range(8):
+                    acc = np.float32(acc + d[m, j, n])
+                if sh is not None:
+                    acc = np.float32(acc + sh.float().numpy()[m, n])
+                ref = torch.tensor([acc]).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)[0]
+                assert got[m, n] == ref
+
+
+def test_moe_sum_exact_sums_match_torch():
+    g = torch.Generator().manual_seed(1)
+    down = (torch.randint(-64, 64, (5, 8, 256), generator=g).float() / 16).to(torch.bfloat16)
+    ref = down.float().sum(1).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(O.moe_sum(down), ref)
+
+
+def test_mxfp4_dequant_closed_form():
+    p = torch.tensor([[[0x10, 0xf7] + [0] * 14]], dtype=torch.uint8)          # codes 0,1,7,15, then zeros
+    e = torch.tensor([[[127]]], dtype=torch.uint8)
+    v = O.mxfp4_dequant(p, e)[0, 0]
+    assert v[:4].tolist() == [0.0, 0.5, 6.0, -6.0]
+    e = torch.tensor([[[120]]], dtype=torch.uint8)
+    assert O.mxfp4_dequant(p, e)[0, 0, 2].item() == 6.0 * 2.0 ** -7
+
+
+def test_grouped_gemm_python_loop():
+    g = torch.Generator().manual_seed(2)
+    E, N, K, T, k = 3, 16, 64, 4, 2
+    packed, e8 = make_experts(E, N, K, g, 120, 130)
+    W = {e: O.mxfp4_dequant(packed[e], e8[e]) for e in range(E)}
+    x = torch.randn(T, K, generator=g).to(torch.bfloat16)
+    xq, xs = O.quant_rows_fp8(x)
+    ids = np.array([[0, 2], [1, 0], [2, 1], [0, 1]], dtype=np.int32)
+    tw = np.array([0.25, 0.75, 0.5, 0.5, 0.1, 0.9, 0.6, 0.4], dtype=np.float32)
+    out = O.grouped_gemm(xq, xs, W, ids.reshape(-1), k, tw)
+    tab = O.e4m3_table()
+    for r in range(T * k):
+        t, e = r // k, int(ids.reshape(-1)[r])
+        for n in range(N):
+            acc = sum(tab[xq[t, kk]] * float(W[e][n, kk]) for kk in range(K))
+            sc = np.float32(np.float32(xs[t]) * np.float32(tw[r]))
+            v = np.float32(np.float32(acc) * sc)
+            ref = torch.tensor([v]).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)[0]
+            assert out[r, n] == ref
