@@ -214,15 +214,22 @@ def nvfp4_to_mxfp4(packed: np.ndarray, s16: np.ndarray, row_div: np.ndarray):
     return p, e
 
 
+_LUT2 = None
+
+
 def mxfp4_dequant(packed: torch.Tensor, e8m0: torch.Tensor, dtype=torch.float64) -> torch.Tensor:
     """[..., N, K/2] codes + [..., N, K/32] exponents -> [..., N, K] values E2M1[c] * 2^(e - 127)
-    (the reference tests' mx_deq: tests/test_fold_mxfp4.py:36-39, tests/test_prefill_4bit.py:19-22)."""
-    lut = torch.tensor(E2M1, dtype=dtype)
-    p = packed.to(torch.int64)
-    c = torch.stack((p & 15, p >> 4), dim=-1).reshape(*p.shape[:-1], p.shape[-1] * 2)
-    v = lut[c].reshape(*c.shape[:-1], -1, 32)
+    (the reference tests' mx_deq: tests/test_fold_mxfp4.py:36-39, tests/test_prefill_4bit.py:19-22). One gather
+    through a byte -> (even, odd) value table; exact in fp32 for exponent bytes below 253."""
+    global _LUT2
+    if _LUT2 is None:
+        b = np.arange(256)
+        _LUT2 = torch.from_numpy(np.stack([E2M1[b & 15], E2M1[b >> 4]], axis=1))     # [256, 2] float64
+    v = _LUT2.to(dtype)[packed.to(torch.int64)]                                       # [..., N, K/2, 2]
+    shape = (*packed.shape[:-1], packed.shape[-1] * 2)
+    v = v.reshape(*packed.shape[:-1], -1, 32)
     sc = torch.exp2(e8m0.to(dtype) - 127.0).unsqueeze(-1)
-    return (v * sc).reshape(c.shape)
+    return (v * sc).reshape(shape)
 
 
 def e4m3_dequant(q: np.ndarray, dtype=torch.float64) -> torch.Tensor:
@@ -230,59 +237,55 @@ def e4m3_dequant(q: np.ndarray, dtype=torch.float64) -> torch.Tensor:
 
 
 # ------------------------------------------------------------------------------------------ GEMM / layer
-def grouped_gemm(aq: np.ndarray, a_s: np.ndarray, w_deq: dict, expert_of_row: np.ndarray, a_row_div: int,
-                 topk_w: np.ndarray | None = None, rows: np.ndarray | None = None) -> np.ndarray:
+def grouped_gemm(aq: np.ndarray, a_s: np.ndarray, w_deq, expert_of_row: np.ndarray, a_row_div: int,
+                 topk_w: np.ndarray | None = None, rows: np.ndarray | None = None,
+                 acc_dtype=torch.float64) -> np.ndarray:
     """bf16 bits [R, N] of out[r] = bf16((deq(aq[r // a_row_div]) . W[e_r]^T) * (a_s[r // a_row_div] * topk_w[r]))
-    for the routed rows `rows` (default all). w_deq: expert -> float64 [N, K] dequantized weight. The scale product
-    order and the single bf16 rounding follow kernels/r9k_moe_mxfp4a8.hip:478-481 of the reference."""
+    for the routed rows `rows` (default all). w_deq: expert -> dequantized [N, K] weight (a dict or a callable,
+    evaluated one expert at a time). acc_dtype: fp64 (exact products, the GEMM parity tests) or fp32 (the
+    fp32-accumulated layer reference). The scale product order and the single bf16 rounding follow
+    kernels/r9k_moe_mxfp4a8.hip:478-481 of the reference."""
+    get = w_deq if callable(w_deq) else (lambda e: w_deq[e])
     rows = np.arange(expert_of_row.size) if rows is None else np.asarray(rows)
-    N = next(iter(w_deq.values())).shape[0]
-    out = np.zeros((rows.size, N), dtype=np.uint16)
     eor = expert_of_row[rows]
+    out = None
     for e in np.unique(eor):
         sel = np.nonzero(eor == e)[0]
         r = rows[sel]
-        a = e4m3_dequant(aq[r // a_row_div])                          # [n, K] fp64
-        acc = (a @ w_deq[int(e)].T).to(torch.float32)                 # fp64 accumulation, then the fp32 result
+        W = get(int(e)).to(acc_dtype)
+        if out is None:
+            out = np.zeros((rows.size, W.shape[0]), dtype=np.uint16)
+        a = e4m3_dequant(aq[r // a_row_div], acc_dtype)
+        acc = (a @ W.T).to(torch.float32)
         sc = torch.from_numpy(a_s[r // a_row_div].astype(np.float32))
         if topk_w is not None:
             sc = sc * torch.from_numpy(topk_w[r].astype(np.float32))
-        v = (acc * sc[:, None]).to(torch.bfloat16)
-        out[sel] = bf16_bits(v)
+        out[sel] = bf16_bits((acc * sc[:, None]).to(torch.bfloat16))
     return out
 
 
 def moe_layer(x: torch.Tensor, logits: torch.Tensor, w13: tuple, w2: tuple, topk: int, renorm: bool = True,
-              tokens: np.ndarray | None = None, route_out=None) -> dict:
+              tokens: np.ndarray | None = None, route_out=None, acc_dtype=torch.float32) -> dict:
     """The whole layer on the CPU: route -> per-token fp8 quant -> gate_up -> silu*up + quant -> down (router weight
     folded) -> top-k sum. w13 = (packed [E, 2I, H/2], e8m0 [E, 2I, H/32]) and w2 = (packed [E, H, I/2],
-    e8m0 [E, H, I/32]) uint8 tensors in checkpoint layout. `tokens` restricts the math to those tokens (the routing
-    and the quant are per token, so any subset is exact). Returns every intermediate as numpy."""
+    e8m0 [E, H, I/32]) uint8, in checkpoint layout and indexable by expert. `tokens` restricts the math to those
+    tokens (routing and quant are per token, so any subset is exact). Returns every intermediate as numpy."""
     T, H = x.shape
     w, ids = route_out if route_out is not None else route(logits, topk, renorm)
     tok = np.arange(T) if tokens is None else np.asarray(tokens)
     rows = (tok[:, None] * topk + np.arange(topk)[None, :]).reshape(-1)
     xq, xs = quant_rows_fp8(x)
     flat_ids = ids.reshape(-1)
-    need = np.unique(flat_ids[rows])
     p13, e13 = w13
     p2, e2 = w2
-    W13 = {int(e): mxfp4_dequant(p13[int(e)], e13[int(e)]) for e in need}
-    gate_up = grouped_gemm(xq, xs, W13, flat_ids, topk, None, rows)                     # [R, 2I] bf16 bits
+    deq13 = lambda e: mxfp4_dequant(p13[e], e13[e], torch.float32)
+    deq2 = lambda e: mxfp4_dequant(p2[e], e2[e], torch.float32)
+    gate_up = grouped_gemm(xq, xs, deq13, flat_ids, topk, None, rows, acc_dtype)          # [R, 2I] bf16 bits
     aq, a_s, _ = silu_mul_quant_fp8(bits_to_bf16(gate_up))
-    del W13
-    W2 = {int(e): mxfp4_dequant(p2[int(e)], e2[int(e)]) for e in need}
-    # down: the A row of routed row rows[i] is aq[i]; fold the router weight
-    R = rows.size
-    down = np.zeros((R, W2[int(need[0])].shape[0]), dtype=np.uint16)
-    eor = flat_ids[rows]
+    # down: the A row of routed row rows[i] is aq[i]; the router weight folds into the epilogue
     tw = w.reshape(-1)[rows]
-    for e in np.unique(eor):
-        sel = np.nonzero(eor == e)[0]
-        a = e4m3_dequant(aq[sel])
-        acc = (a @ W2[int(e)].T).to(torch.float32)
-        sc = torch.from_numpy(a_s[sel]) * torch.from_numpy(tw[sel].astype(np.float32))
-        down[sel] = bf16_bits((acc * sc[:, None]).to(torch.bfloat16))
+    local = np.arange(rows.size)
+    down = grouped_gemm(aq, a_s, deq2, flat_ids[rows], 1, tw, local, acc_dtype)
     out = moe_sum(bits_to_bf16(down.reshape(tok.size, topk, -1)))
     return dict(w=w, ids=ids, xq=xq, xs=xs, rows=rows, gate_up=gate_up, aq=aq, a_s=a_s, down=down, out=out,
                 tokens=tok)

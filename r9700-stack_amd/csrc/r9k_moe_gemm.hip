@@ -11,6 +11,10 @@
 // B = e2m1 weights with their e8m0 block exponent fed as the B scale: the hardware applies the MXFP4 block scale
 // exactly, so there is no per-group fp32 rescaling in the inner loop (the reference's gfx1201 kernel needs one)
 // and no exponent folding. The per-token fp32 scale As (and the router weight) are applied in the epilogue.
+// Operand layout of that instruction (measured on gfx950): output row r = lane % 16 of A, column c = lane % 16 of
+// B, g = lane / 16. The fp4 B operand holds K = 32g .. 32g+31 of column c in nibbles 0..31 (low nibble first), and
+// lane's scale byte scales that 32-block. The fp8 A operand splits K in halves: bytes 0..15 hold K = 16g .. 16g+15,
+// bytes 16..31 hold K = 64 + 16g .. +15 of row r. C: lane holds column lane % 16, rows 4g .. 4g+3.
 //
 // Weight layout (per expert, produced by kernels/moe.py permute_fragments / pack_scales):
 //   codes  : N/16 column tiles of 16 rows x K/2 bytes (8K bytes each). Within a column tile, K-tile kt (128 K) is
@@ -78,14 +82,16 @@ __global__ void __launch_bounds__(WAVE * SK) moe_mxfp4_kernel(
   const int nkt = (K + KT - 1) / KT, nkt_full = K / KT, tail_groups = (K % KT) / GROUP;
   const int KB = K / GROUP, nq = KB / 16;
 
-  // A row byte offsets of this lane's row in each M tile (+ its K group)
+  // A row byte offsets of this lane's row in each M tile (+ its 16-byte K chunk of the low half)
   size_t aoff[MT];
 #pragma unroll
   for (int i = 0; i < MT; i++) {
     int fr = sorted_ids[row0 + i * 16 + r];
     if (fr >= numel || fr < 0) fr = first;
-    aoff[i] = (size_t)(fr / a_row_div) * K + g * GROUP;
+    aoff[i] = (size_t)(fr / a_row_div) * K + g * 16;
   }
+  // a partial last K-tile (K % 128 = 32 * G) holds K < 32G: the A halves at 16g and 64 + 16g are live below it
+  const bool a_lo_tail = g < 2 * tail_groups, a_hi_tail = g < 2 * tail_groups - 4;
   const uint8_t* __restrict__ We = Wq + (size_t)e * wq_estride;
   const uint8_t* __restrict__ Se = Ws + (size_t)e * ws_estride;
   const uint8_t* wbase[NPW];
@@ -128,15 +134,14 @@ __global__ void __launch_bounds__(WAVE * SK) moe_mxfp4_kernel(
           sb[u][j] = E8M0_ONE;
         }
       }
+      const bool full = k < nkt_full;
+      const bool lo_ok = live && (full || a_lo_tail), hi_ok = live && (full || a_hi_tail);
 #pragma unroll
       for (int i = 0; i < MT; i++) {
-        if (lane_ok) {
-          const uint4* ap = reinterpret_cast<const uint4*>(A + aoff[i] + (size_t)k * KT);
-          const uint4 a0 = ap[0], a1 = ap[1];
-          af[u][i] = (v8i){(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w, (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
-        } else {
-          af[u][i] = (v8i){0, 0, 0, 0, 0, 0, 0, 0};
-        }
+        const uint8_t* ap = A + aoff[i] + (size_t)k * KT;
+        const uint4 a0 = lo_ok ? *reinterpret_cast<const uint4*>(ap) : make_uint4(0u, 0u, 0u, 0u);
+        const uint4 a1 = hi_ok ? *reinterpret_cast<const uint4*>(ap + 64) : make_uint4(0u, 0u, 0u, 0u);
+        af[u][i] = (v8i){(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w, (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
       }
     }
 #pragma unroll
