@@ -1,0 +1,294 @@
+"""Benchmark of the quantized MoE layer on one MI355X (BASELINE.json metric: MoE-layer tokens/s + HBM GB/s at decode,
+MXFP4 TFLOPS at prefill).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+
+A step is one MoE layer forward over one batch of synthetic tokens: fused routing (softmax top-8 + align tables) ->
+per-token fp8 quant -> grouped gate_up GEMM -> SiLU*up + fp8 quant -> grouped down GEMM (router weight folded) ->
+top-k sum, six launches on one stream. The headline `value` is BASELINE config 2 (E=288 experts, hidden 2048,
+expert intermediate 512, top-8) at T=64 tokens, the bandwidth-bound decode point; T = 1, 8, 16 and the config 3
+prefill (T=8192) are reported beside it.
+
+Method: weights and inputs are resident in HBM before timing. Steps run as HIP-graph replays that cycle through
+COPIES independent weight copies (> 2x the 256 MB Infinity Cache per cycle), so weight bytes come from HBM, not from
+a cache warmed by the previous step. The dominant kernel (the gate_up GEMM) is also launched on its own, bracketed by
+HIP events on the stream it runs on, for the roofline figure. The CPU baseline is the oracle's dequant-then-matmul
+layer (oracle/, the reference's torch CPU path restated) timed on this host on a bounded sample.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (os.path.join(ROOT, "r9700-stack_amd"), ROOT):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+import numpy as np
+import torch
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
+FP8_PEAK_TFLOPS = 5000.0       # dense fp8 MFMA
+FP4_PEAK_TFLOPS = 10100.0      # dense fp4 / fp6 MFMA
+COPIES = 4
+SEED = 20261201
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-prefill", action="store_true", help="skip the T=8192 prefill line")
+    return ap.parse_args()
+
+
+class Layer:
+    """One MoE layer's MXFP4 weights in COPIES independent HBM copies (kernel layout), plus copy 0 in checkpoint
+    layout for the CPU baseline."""
+
+    def __init__(self, E, H, I, dev, lo=118, hi=126, copies=COPIES, seed=SEED):
+        from r9700_vllm.kernels import moe as K
+        g = torch.Generator(device=dev).manual_seed(seed)
+        rnd = lambda shape, a, b: torch.randint(a, b + 1, shape, generator=g, device=dev, dtype=torch.int32).to(torch.uint8)
+        self.p13, self.e13 = rnd((E, 2 * I, H // 2), 0, 255), rnd((E, 2 * I, H // 32), lo, hi)
+        self.p2, self.e2 = rnd((E, H, I // 2), 0, 255), rnd((E, H, I // 32), lo, hi)
+        W13 = K.prepare_mxfp4_weights(self.p13, self.e13)
+        W2 = K.prepare_mxfp4_weights(self.p2, self.e2)
+        self.W13 = [W13] + [K.Mxfp4Experts(W13.wq.clone(), W13.wsr.clone(), W13.N, W13.K) for _ in range(copies - 1)]
+        self.W2 = [W2] + [K.Mxfp4Experts(W2.wq.clone(), W2.wsr.clone(), W2.N, W2.K) for _ in range(copies - 1)]
+        self.E, self.H, self.I = E, H, I
+
+    def bytes_per_expert(self) -> int:
+        H, I = self.H, self.I
+        return 2 * I * H // 2 + 2 * I * H // 32 + H * I // 2 + H * I // 32
+
+
+class Step:
+    """The layer forward for T tokens, graph-capturable: fused routing when the decode router path applies
+    (T * topk <= 4096 rows, as R9kTopKRouter), otherwise top-k + the in-apply align."""
+
+    def __init__(self, layer: Layer, T: int, topk: int, dev, seed: int):
+        from r9700_vllm.kernels import moe as K
+        from r9700_vllm.moe import route
+        from r9700_vllm.moe.experts import R9700Mxfp4Experts
+        self.K, self.route = K, route
+        self.layer, self.T, self.topk, self.dev = layer, T, topk, dev
+        g = torch.Generator().manual_seed(seed)
+        self.x_cpu = torch.randn(T, layer.H, generator=g).to(torch.bfloat16)
+        self.logits_cpu = torch.randn(T, layer.E, generator=g).to(torch.bfloat16)
+        self.x = self.x_cpu.to(dev)
+        self.logits = self.logits_cpu.to(dev)
+        self.out = torch.empty(T, layer.H, dtype=torch.bfloat16, device=dev)
+        self.numel = T * topk
+        self.fused = self.numel <= 4096 and T <= route.MAX_ROWS
+        E = layer.E
+        self.blk = K.MOE_BLOCK * K.pick_mt(self.numel, E)
+        cap = route.capacity(self.numel, E, self.blk)
+        self.sid = torch.empty(cap, dtype=torch.int32, device=dev)
+        self.eid = torch.empty(cap // self.blk, dtype=torch.int32, device=dev)
+        self.ntpp = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.scratch = torch.zeros(route.scratch_ints(E), dtype=torch.int32, device=dev)
+        self.experts = [R9700Mxfp4Experts.standalone(w13.wsr, w2.wsr) for w13, w2 in zip(layer.W13, layer.W2)]
+
+        class _Routed:
+            _r9k_tables = None
+        self.routed = _Routed()
+        for ex in self.experts:
+            ex.r9k_layer = self.routed
+
+    def __call__(self, c: int):
+        K, route, L = self.K, self.route, self.layer
+        if self.fused:
+            w, ids = route.moe_route(self.logits, self.topk, True, self.blk, self.sid, self.eid, self.ntpp,
+                                     self.scratch)
+            self.routed._r9k_tables = route.Tables(ids, self.sid, self.eid, self.ntpp, self.blk, self.numel)
+        else:
+            w, ids = K.moe_topk(self.logits, self.topk, True)
+            self.routed._r9k_tables = None
+        self.experts[c].apply(self.out, self.x, L.W13[c].wq, L.W2[c].wq, w, ids, "silu", L.E, None, None, None,
+                              None, None, None, False)
+        self.w, self.ids = w, ids
+        return self.out
+
+
+def graph_time(step: Step, steps: int, warmup: int):
+    """ms per step over `steps` steps replayed from a HIP graph that cycles the weight copies."""
+    copies = len(step.layer.W13)
+    for i in range(max(2, warmup)):
+        step(i % copies)
+    torch.cuda.synchronize()
+    ref = step(copies - 1).clone()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for c in range(copies):
+            step(c)
+    for _ in range(max(1, warmup // copies)):
+        g.replay()
+    torch.cuda.synchronize()
+    if not torch.equal(step.out, ref):
+        raise RuntimeError("graph replay output differs from the eager step")
+    reps = max(1, steps // copies)
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0.record()
+    for _ in range(reps):
+        g.replay()
+    t1.record()
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / (reps * copies)
+    return ms, reps * copies
+
+
+def gate_up_kernel_time(step: Step, reps: int = 40):
+    """Average duration (ms) of the gate_up GEMM launch alone, HIP events on its stream, rotating weight copies.
+    Returns (ms, algorithmic bytes per launch, flops per launch, experts touched)."""
+    K, L = step.K, step.layer
+    step(0)
+    torch.cuda.synchronize()
+    ids = step.ids
+    E = L.E
+    tabs = K.moe_align(ids, step.blk, E)
+    xq, xs = K.quant_rows_fp8(step.x)
+    N1, K1 = 2 * L.I, L.H
+    out = torch.empty(step.numel, N1, dtype=torch.bfloat16, device=step.dev)
+    MT = step.blk // K.MOE_BLOCK
+    pf = K.pick_moe_prefill(MT, K1, gate_up=True)
+    copies = len(L.W13)
+
+    def launch(c):
+        K.moe_gemm(xq, xs, L.W13[c], out, *tabs, step.numel, step.topk, None, num_experts=E, MT=MT, prefill=pf)
+
+    for i in range(8):
+        launch(i % copies)
+    torch.cuda.synchronize()
+    s = torch.cuda.current_stream()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+    for i, (a, b) in enumerate(evs):
+        a.record(s)
+        launch(i % copies)
+        b.record(s)
+    torch.cuda.synchronize()
+    ms = float(np.mean([a.elapsed_time(b) for a, b in evs]))
+    touched = int(torch.unique(ids).numel())
+    nbytes = touched * (N1 * K1 // 2 + N1 * K1 // 32) + step.T * K1 + step.T * 4 + step.numel * N1 * 2
+    flops = 2 * step.numel * N1 * K1
+    return ms, nbytes, flops, touched
+
+
+def layer_bytes(step: Step) -> tuple[int, int]:
+    """Algorithmic bytes of one layer step (touched-expert weights + x + logits + out) and experts touched."""
+    touched = int(torch.unique(step.ids).numel())
+    L, T = step.layer, step.T
+    return touched * L.bytes_per_expert() + T * L.H * 2 + T * L.E * 2 + T * L.H * 2, touched
+
+
+def cpu_baseline(step: Step, budget_s: float = 10.0) -> dict:
+    """The oracle's CPU layer (route, quant, per-expert dequant + fp32 matmul, SiLU quant, down, sum) on this host's
+    cores, on the first tokens of the same workload; tokens/s."""
+    from oracle import oracle as O
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    L = step.layer
+    T = step.T
+    x, logits = step.x_cpu, step.logits_cpu
+    ids = O.route(logits, step.topk, True)[1]
+    need = np.unique(ids)
+    p13 = {int(e): L.p13[int(e)].cpu() for e in need}
+    e13 = {int(e): L.e13[int(e)].cpu() for e in need}
+    p2 = {int(e): L.p2[int(e)].cpu() for e in need}
+    e2 = {int(e): L.e2[int(e)].cpu() for e in need}
+    n, t0 = 0, time.perf_counter()
+    while True:
+        O.moe_layer(x, logits, (p13, e13), (p2, e2), step.topk, True)
+        n += 1
+        el = time.perf_counter() - t0
+        if el > budget_s or n >= 30:
+            break
+    return {"value": round(n * T / el, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"{n} full layer forward(s) of the T={T} workload (E={L.E}, H={L.H}, I={L.I}, top-{step.topk}),"
+                      f" oracle dequant-then-matmul in fp32 on {threads} host threads, {el:.1f} s"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build runs no multi-GPU path (asked for --gpus {args.gpus})",
+              file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+    dev = torch.device("cuda", 0)
+    from r9700_vllm.kernels import moe as K
+    K.lib()
+    topk = 8
+    t_build = time.perf_counter()
+    layer = Layer(288, 2048, 512, dev)
+    print(f"# weights ready ({COPIES} copies, {time.perf_counter() - t_build:.1f} s)", file=sys.stderr, flush=True)
+
+    sweep = {}
+    main_step = None
+    for T in (1, 8, 16, 64):
+        st = Step(layer, T, topk, dev, SEED + 2000 + T)
+        ms, n = graph_time(st, args.steps, args.warmup)
+        nbytes, touched = layer_bytes(st)
+        sweep[str(T)] = {"ms_per_step": round(ms, 5), "tokens_per_s": round(T / (ms * 1e-3), 1),
+                         "experts_touched": touched, "layer_GBps": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                         "hbm_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        print(f"# T={T}: {ms * 1e3:.1f} us/layer, {sweep[str(T)]['layer_GBps']} GB/s over {touched} experts",
+              file=sys.stderr, flush=True)
+        if T == 64:
+            main_step, main_ms, main_n = st, ms, n
+
+    k_ms, k_bytes, k_flops, k_touched = gate_up_kernel_time(main_step)
+    k_gbs = k_bytes / (k_ms * 1e-3) / 1e9
+    print(f"# gate_up GEMM alone: {k_ms * 1e3:.1f} us, {k_gbs:.0f} GB/s", file=sys.stderr, flush=True)
+
+    prefill = None
+    if not args.no_prefill:
+        pl = Step(layer, 8192, topk, dev, SEED + 3000 + 8192)
+        ms, n = graph_time(pl, max(8, args.steps // 10), max(4, args.warmup // 4))
+        flops = 6 * 8192 * topk * layer.H * layer.I
+        tf = flops / (ms * 1e-3) / 1e12
+        prefill = {"workload": "cfg3 prefill T=8192", "ms_per_step": round(ms, 4), "tokens_per_s": round(8192 / (ms * 1e-3)),
+                   "TFLOPS": round(tf, 1), "frac_fp4_peak": round(tf / FP4_PEAK_TFLOPS, 4),
+                   "frac_fp8_peak": round(tf / FP8_PEAK_TFLOPS, 4), "steps": n}
+        print(f"# prefill T=8192: {ms:.3f} ms/layer, {tf:.1f} TFLOPS", file=sys.stderr, flush=True)
+
+    cpu = None if args.no_cpu else cpu_baseline(main_step)
+    line = {
+        "metric": "MoE-layer tokens/s + HBM GB/s (decode) / MXFP4 TFLOPS (prefill), 1 GPU",
+        "value": sweep["64"]["tokens_per_s"],
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": main_n,
+        "warmup": args.warmup,
+        "ms_per_step": sweep["64"]["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp8e4m3 x mxfp4 (fp32 accumulate)",
+        "data": "synthetic (seeded random e2m1 codes, e8m0 in [118,126], N(0,1) tokens and router logits)",
+        "config": {"workload": "cfg2 decode MoE layer: E=288, hidden 2048, intermediate 512, top-8, T=64 tokens",
+                   "tokens": 64, "experts": 288, "hidden": 2048, "intermediate": 512, "topk": 8,
+                   "weight_copies_rotated": COPIES},
+        "roofline": {"bound": "hbm", "kernel": "r9k_moe_mxfp4a8 gate_up (T=64)", "achieved": round(k_gbs, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(k_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": None, "kernel_us": round(k_ms * 1e3, 2), "bytes_per_launch": k_bytes},
+        "cpu_baseline": cpu,
+        "decode_sweep": sweep,
+        "prefill": prefill,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

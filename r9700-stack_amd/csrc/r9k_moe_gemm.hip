@@ -33,6 +33,8 @@
 // are clamped to the block's first row for the loads and dropped at the store.
 #include "r9k_common.h"
 
+#include <cstdlib>
+
 namespace {
 
 using namespace r9k;
@@ -51,19 +53,24 @@ __device__ __forceinline__ u32x4 ld16(const uint8_t* p) {
   else return *reinterpret_cast<const u32x4*>(p);
 }
 template <bool NTL>
-__device__ __forceinline__ uint32_t ld4(const uint8_t* p) {
-  if constexpr (NTL) return __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(p));
-  else return *reinterpret_cast<const uint32_t*>(p);
+__device__ __forceinline__ uint32_t ld1(const uint8_t* p) {
+  if constexpr (NTL) return __builtin_nontemporal_load(p);
+  else return *p;
 }
 
-template <int MT, int NPW, int SK>
+// One workgroup: 16*MT routed rows x NPW column tiles; SK waves split the K-tiles (SK > 1: partial tiles summed
+// through LDS). Each wave walks its K range in batches of U K-tiles: all loads of a batch (U*NPW weight tiles,
+// U*NPW scale bytes, U*MT*2 activation chunks) are issued back to back with no branch or use in between, then the
+// U*NPW*MT MFMAs run. Addresses are clamped instead of branched around (a lane past a partial K-tile, or a batch
+// slot past the wave's range, re-reads a valid location and its operand is zeroed by select), so the compiler
+// never has to drain the memory queue inside a batch.
+template <int MT, int NPW, int SK, int U>
 __global__ void __launch_bounds__(WAVE * SK) moe_mxfp4_kernel(
     const uint8_t* __restrict__ A, const float* __restrict__ As, const uint8_t* __restrict__ Wq,
     const uint8_t* __restrict__ Ws, uint16_t* __restrict__ C, const int* __restrict__ sorted_ids,
     const int* __restrict__ expert_ids, const int* __restrict__ ntpp, const float* __restrict__ topk_w,
     long wq_estride, long ws_estride, int numel, int a_row_div, int K, int N, int blk, int subs) {
   constexpr int BLK = 16 * MT;
-  constexpr int U = MT == 1 ? 4 : (MT == 2 ? 2 : 1);      // K-tiles whose loads are issued together
   constexpr bool NTL = MT == 1;                            // decode: every weight byte is read once
   extern __shared__ float red[];
 
@@ -71,37 +78,39 @@ __global__ void __launch_bounds__(WAVE * SK) moe_mxfp4_kernel(
   if (rb * blk >= ntpp[0]) return;
   const int e = expert_ids[rb];
   if (e < 0) return;
-  const int first = sorted_ids[rb * blk];
-  if (first < 0 || first >= numel) return;
   const int row0 = rb * blk + sub * BLK;
-  if (sorted_ids[row0] >= numel) return;                   // padding sits at the end of a block
+  const int first = sorted_ids[rb * blk];
+  if (first < 0 || first >= numel || sorted_ids[row0] >= numel) return;   // padding sits at the end of a block
 
   const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
   const int g = lane >> 4, r = lane & 15;
   const int NT = N / 16;
-  const int nkt = (K + KT - 1) / KT, nkt_full = K / KT, tail_groups = (K % KT) / GROUP;
+  const int nkt = (K + KT - 1) / KT, nkt_full = K / KT, tg = (K % KT) / GROUP;
   const int KB = K / GROUP, nq = KB / 16;
 
-  // A row byte offsets of this lane's row in each M tile (+ its 16-byte K chunk of the low half)
-  size_t aoff[MT];
+  // per-lane operand offsets that stay valid on a partial last K-tile (only lanes/halves below K are live there)
+  const int lane_b_tail = g < tg ? lane : r;                          // B lanes of the partial tile: lanes < 16 * tg
+  const int a_lo_tail = g < 2 * tg ? 16 * g : 0;                     // A low half  (K 16g .. 16g + 15)
+  const int a_hi_tail = g < 2 * tg - 4 ? 64 + 16 * g : 0;            // A high half (K 64 + 16g ..)
+  const bool b_live_tail = g < tg, lo_live_tail = g < 2 * tg, hi_live_tail = g < 2 * tg - 4;
+
+  size_t arow[MT];
 #pragma unroll
   for (int i = 0; i < MT; i++) {
     int fr = sorted_ids[row0 + i * 16 + r];
     if (fr >= numel || fr < 0) fr = first;
-    aoff[i] = (size_t)(fr / a_row_div) * K + g * 16;
+    arow[i] = (size_t)(fr / a_row_div) * K;
   }
-  // a partial last K-tile (K % 128 = 32 * G) holds K < 32G: the A halves at 16g and 64 + 16g are live below it
-  const bool a_lo_tail = g < 2 * tail_groups, a_hi_tail = g < 2 * tail_groups - 4;
   const uint8_t* __restrict__ We = Wq + (size_t)e * wq_estride;
   const uint8_t* __restrict__ Se = Ws + (size_t)e * ws_estride;
-  const uint8_t* wbase[NPW];
-  const uint8_t* sbase[NPW];
+  const uint8_t* wtile[NPW];
+  const uint8_t* stile[NPW];
 #pragma unroll
   for (int j = 0; j < NPW; j++) {
     int nt = blockIdx.x * NPW + j;
     nt = nt < NT ? nt : NT - 1;                            // out-of-range tiles compute a copy, never stored
-    wbase[j] = We + (size_t)nt * (size_t)(8 * K) + lane * 16;
-    sbase[j] = Se + (size_t)nt * (size_t)(16 * KB);
+    wtile[j] = We + (size_t)nt * (size_t)(8 * K);
+    stile[j] = Se + (size_t)nt * (size_t)(16 * KB);
   }
 
   v4f acc[NPW][MT];
@@ -112,102 +121,134 @@ __global__ void __launch_bounds__(WAVE * SK) moe_mxfp4_kernel(
 
   const int kt0 = wave * nkt / SK, kt1 = (wave + 1) * nkt / SK;
   for (int kt = kt0; kt < kt1; kt += U) {
-    v8i af[U][MT];
     u32x4 bf[U][NPW];
     uint32_t sb[U][NPW];
+    uint4 alo[U][MT], ahi[U][MT];
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const int k = min(kt + u, kt1 - 1);
+      const bool full = k < nkt_full;
+      const int bl = full ? lane : lane_b_tail;
+      const int soff = k < 4 * nq ? (k >> 2) * 256 + lane * 4 + (k & 3) : nq * 256 + (k - 4 * nq) * 64 + bl;
+#pragma unroll
+      for (int j = 0; j < NPW; j++) {
+        bf[u][j] = ld16<NTL>(wtile[j] + (size_t)k * 1024 + bl * 16);
+        sb[u][j] = ld1<NTL>(stile[j] + soff);
+      }
+      const int olo = full ? 16 * g : a_lo_tail, ohi = full ? 64 + 16 * g : a_hi_tail;
+#pragma unroll
+      for (int i = 0; i < MT; i++) {
+        const uint8_t* ap = A + arow[i] + (size_t)k * KT;
+        alo[u][i] = *reinterpret_cast<const uint4*>(ap + olo);
+        ahi[u][i] = *reinterpret_cast<const uint4*>(ap + ohi);
+      }
+    }
 #pragma unroll
     for (int u = 0; u < U; u++) {
       const int k = kt + u;
-      const bool live = k < kt1;
-      const bool lane_ok = live && (k < nkt_full || g < tail_groups);
-#pragma unroll
-      for (int j = 0; j < NPW; j++) {
-        if (lane_ok) {
-          bf[u][j] = ld16<NTL>(wbase[j] + (size_t)k * 1024);
-          if (k < 4 * nq) {
-            sb[u][j] = (ld4<NTL>(sbase[j] + (k >> 2) * 256 + lane * 4) >> (8 * (k & 3))) & 0xffu;
-          } else {
-            sb[u][j] = sbase[j][nq * 256 + (k - 4 * nq) * 64 + lane];
-          }
-        } else {
-          bf[u][j] = (u32x4){0u, 0u, 0u, 0u};
-          sb[u][j] = E8M0_ONE;
-        }
-      }
-      const bool full = k < nkt_full;
-      const bool lo_ok = live && (full || a_lo_tail), hi_ok = live && (full || a_hi_tail);
-#pragma unroll
-      for (int i = 0; i < MT; i++) {
-        const uint8_t* ap = A + aoff[i] + (size_t)k * KT;
-        const uint4 a0 = lo_ok ? *reinterpret_cast<const uint4*>(ap) : make_uint4(0u, 0u, 0u, 0u);
-        const uint4 a1 = hi_ok ? *reinterpret_cast<const uint4*>(ap + 64) : make_uint4(0u, 0u, 0u, 0u);
-        af[u][i] = (v8i){(int)a0.x, (int)a0.y, (int)a0.z, (int)a0.w, (int)a1.x, (int)a1.y, (int)a1.z, (int)a1.w};
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < U; u++) {
-      if (kt + u < kt1) {
+      if (k < kt1) {
+        const bool full = k < nkt_full;
+        const bool bl = full || b_live_tail, lo = full || lo_live_tail, hi = full || hi_live_tail;
 #pragma unroll
         for (int j = 0; j < NPW; j++) {
-          const v8i b = (v8i){(int)bf[u][j].x, (int)bf[u][j].y, (int)bf[u][j].z, (int)bf[u][j].w, 0, 0, 0, 0};
+          const v8i b = bl ? (v8i){(int)bf[u][j].x, (int)bf[u][j].y, (int)bf[u][j].z, (int)bf[u][j].w, 0, 0, 0, 0}
+                           : (v8i){0, 0, 0, 0, 0, 0, 0, 0};
+          const int sc = bl ? (int)sb[u][j] : E8M0_ONE;
 #pragma unroll
-          for (int i = 0; i < MT; i++)
-            acc[j][i] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(af[u][i], b, acc[j][i], 0, 4, 0, E8M0_ONE,
-                                                                          0, (int)sb[u][j]);
+          for (int i = 0; i < MT; i++) {
+            const uint4 l = lo ? alo[u][i] : make_uint4(0u, 0u, 0u, 0u);
+            const uint4 h = hi ? ahi[u][i] : make_uint4(0u, 0u, 0u, 0u);
+            const v8i a = (v8i){(int)l.x, (int)l.y, (int)l.z, (int)l.w, (int)h.x, (int)h.y, (int)h.z, (int)h.w};
+            acc[j][i] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, acc[j][i], 0, 4, 0, E8M0_ONE, 0, sc);
+          }
         }
       }
     }
   }
 
-  // C layout of a 16x16 tile: lane l holds column l % 16, rows 4 * (l / 16) + q. Partials to LDS as [row][col].
+  if constexpr (SK == 1) {
+    // C layout of a 16x16 tile: lane holds column lane % 16, rows 4g .. 4g + 3: store straight from registers
 #pragma unroll
-  for (int j = 0; j < NPW; j++)
+    for (int i = 0; i < MT; i++)
 #pragma unroll
-    for (int i = 0; i < MT; i++) {
-      float* t = red + (size_t)((wave * NPW + j) * MT + i) * 256;
+      for (int q = 0; q < 4; q++) {
+        const int fr = sorted_ids[row0 + i * 16 + 4 * g + q];
+        if (fr < 0 || fr >= numel) continue;
+        float sc = As[fr / a_row_div];
+        if (topk_w) sc *= topk_w[fr];
 #pragma unroll
-      for (int q = 0; q < 4; q++) t[(4 * g + q) * 16 + r] = acc[j][i][q];
+        for (int j = 0; j < NPW; j++) {
+          const int n = (blockIdx.x * NPW + j) * 16 + r;
+          if (n < N) C[(size_t)fr * N + n] = f2bf(acc[j][i][q] * sc);
+        }
+      }
+  } else {
+    // partial tiles to LDS as [row][col], then each thread sums SK partials of some outputs
+#pragma unroll
+    for (int j = 0; j < NPW; j++)
+#pragma unroll
+      for (int i = 0; i < MT; i++) {
+        float* t = red + (size_t)((wave * NPW + j) * MT + i) * 256;
+#pragma unroll
+        for (int q = 0; q < 4; q++) t[(4 * g + q) * 16 + r] = acc[j][i][q];
+      }
+    __syncthreads();
+    constexpr int TOT = NPW * MT * 256;
+    for (int idx = tid; idx < TOT; idx += WAVE * SK) {
+      const int col = idx & 15, row = (idx >> 4) & 15, ti = idx >> 8;   // ti = j * MT + i
+      const int j = ti / MT, i = ti - j * MT;
+      const int n = (blockIdx.x * NPW + j) * 16 + col;
+      if (n >= N) continue;
+      const int fr = sorted_ids[row0 + i * 16 + row];
+      if (fr < 0 || fr >= numel) continue;
+      float v = 0.f;
+#pragma unroll
+      for (int s = 0; s < SK; s++) v += red[(size_t)s * TOT + idx];
+      float sc = As[fr / a_row_div];
+      if (topk_w) sc *= topk_w[fr];
+      C[(size_t)fr * N + n] = f2bf(v * sc);
     }
-  __syncthreads();
-  constexpr int TOT = NPW * MT * 256;
-  for (int idx = tid; idx < TOT; idx += WAVE * SK) {
-    const int col = idx & 15, row = (idx >> 4) & 15, ti = idx >> 8;   // ti = j * MT + i
-    const int j = ti / MT, i = ti - j * MT;
-    const int n = (blockIdx.x * NPW + j) * 16 + col;
-    if (n >= N) continue;
-    const int fr = sorted_ids[row0 + i * 16 + row];
-    if (fr < 0 || fr >= numel) continue;
-    float v = 0.f;
-#pragma unroll
-    for (int s = 0; s < SK; s++) v += red[(size_t)s * TOT + idx];
-    float sc = As[fr / a_row_div];
-    if (topk_w) sc *= topk_w[fr];
-    C[(size_t)fr * N + n] = f2bf(v * sc);
   }
 }
 
-struct Pick { int MT, NPW, SK; };
+struct Pick { int MT, NPW, SK, U; };
 
-// Launch shape for the decode-family kernel: SK waves split K (up to 4 K-tiles a wave at long K), NPW column tiles
-// a wave. Chosen from the host-known shape only, so a call stays graph-capturable.
+int env_int(const char* name, int dflt) {
+  const char* v = getenv(name);
+  return v && *v ? atoi(v) : dflt;
+}
+
+// Launch shape for the decode-family kernel, from the host-known shape only (graph-capturable). Two column tiles a
+// wave. Long K (>= 8 K-tiles) splits over SK waves so that fewer dependent load batches sit on one wave: 4 while the
+// grid is small, 2 once it holds >= 12K waves' worth of tiles; short K stays in one wave (no LDS reduction), with
+// 4-tile load batches while the grid is small. Measured on MI355X over config-2 decode widths (T = 1..64).
+// R9K_GEMM_SK / R9K_GEMM_NPW / R9K_GEMM_U override (tuning sweeps).
 Pick pick(int MT, int N, int K, int max_blocks) {
   const int nkt = (K + KT - 1) / KT;
   const int NT = N / 16;
-  int SK = nkt >= 8 ? 4 : (nkt >= 2 ? 2 : 1);
-  int NPW = NT >= 4 ? 4 : 2;
-  if (MT >= 4) NPW = 2;
-  // few live blocks (single-token decode): more, smaller workgroups
-  if (max_blocks * ((NT + NPW - 1) / NPW) < 512 && NPW > 2) NPW = 2;
-  (void)N;
-  return {MT, NPW, SK};
+  int NPW = NT >= 2 ? 2 : 1;
+  const long tiles = (long)max_blocks * ((NT + NPW - 1) / NPW);
+  int SK, U;
+  if (nkt >= 8) {
+    SK = tiles >= 12288 ? 2 : 4;
+    U = SK == 2 ? 2 : 1;
+  } else {
+    SK = 1;
+    U = tiles >= 8192 ? 1 : 4;
+  }
+  if (MT >= 4) U = U > 2 ? 2 : U;
+  SK = env_int("R9K_GEMM_SK", SK);
+  NPW = env_int("R9K_GEMM_NPW", NPW);
+  U = env_int("R9K_GEMM_U", U);
+  return {MT, NPW, SK, U};
 }
 
-template <int MT, int NPW, int SK>
+template <int MT, int NPW, int SK, int U>
 int launch_one(dim3 grid, hipStream_t st, long a, long as, long wq, long ws, long c, long sorted_ids,
                long expert_ids, long ntpp, long topk_w, long wq_estride, long ws_estride, int numel, int a_row_div,
                int K, int N, int blk, int subs) {
-  const size_t smem = (size_t)SK * NPW * MT * 256 * sizeof(float);
-  hipLaunchKernelGGL((moe_mxfp4_kernel<MT, NPW, SK>), grid, dim3(WAVE * SK), smem, st, (const uint8_t*)a,
+  const size_t smem = SK > 1 ? (size_t)SK * NPW * MT * 256 * sizeof(float) : 0;
+  hipLaunchKernelGGL((moe_mxfp4_kernel<MT, NPW, SK, U>), grid, dim3(WAVE * SK), smem, st, (const uint8_t*)a,
                      (const float*)as, (const uint8_t*)wq, (const uint8_t*)ws, (uint16_t*)c, (const int*)sorted_ids,
                      (const int*)expert_ids, (const int*)ntpp, (const float*)topk_w, wq_estride, ws_estride, numel,
                      a_row_div, K, N, blk, subs);
@@ -229,17 +270,19 @@ int moe_dispatch(long a, long as, long wq, long ws, long c, long sorted_ids, lon
   const Pick p = pick(MT, N, K, max_blocks);
   const int subs = blk / (16 * MT);
   const long ny = (long)max_blocks * subs;
-  if (ny > 0x7fffffffL) return -3;
+  if (ny > 0x7fffffffL || p.NPW < 1) return -3;
   const dim3 grid((N / 16 + p.NPW - 1) / p.NPW, (unsigned)ny);
   const long wq_estride = (long)N * K / 2;
   const hipStream_t st = (hipStream_t)stream;
-#define L(MTv, NPWv, SKv)                                                                                   \
-  if (p.MT == MTv && p.NPW == NPWv && p.SK == SKv)                                                          \
-    return launch_one<MTv, NPWv, SKv>(grid, st, a, as, wq, ws, c, sorted_ids, expert_ids, ntpp, topk_w,     \
-                                      wq_estride, ws_estride, numel, a_row_div, K, N, blk, subs);
-#define LS(MTv, NPWv) L(MTv, NPWv, 1) L(MTv, NPWv, 2) L(MTv, NPWv, 4)
-  LS(1, 2) LS(1, 4) LS(2, 2) LS(2, 4) LS(4, 2)
+#define L(MTv, NPWv, SKv, Uv)                                                                               \
+  if (p.MT == MTv && p.NPW == NPWv && p.SK == SKv && p.U == Uv)                                             \
+    return launch_one<MTv, NPWv, SKv, Uv>(grid, st, a, as, wq, ws, c, sorted_ids, expert_ids, ntpp, topk_w, \
+                                          wq_estride, ws_estride, numel, a_row_div, K, N, blk, subs);
+#define LU(MTv, NPWv, SKv) L(MTv, NPWv, SKv, 1) L(MTv, NPWv, SKv, 2) L(MTv, NPWv, SKv, 4)
+#define LS(MTv, NPWv) LU(MTv, NPWv, 1) LU(MTv, NPWv, 2) LU(MTv, NPWv, 4)
+  LS(1, 1) LS(1, 2) LS(1, 4) LS(2, 1) LS(2, 2) LS(2, 4) LS(4, 1) LS(4, 2)
 #undef LS
+#undef LU
 #undef L
   return -5;
 }

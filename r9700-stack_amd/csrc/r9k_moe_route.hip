@@ -9,8 +9,8 @@
 //     +inf row, entries more than 87 below the row max): dead entries rank after every live one, among
 //     themselves by index, and get weight 0 -- the reference's rule for degenerate rows (:81-95).
 //   * weights: p = exp(x - max) / sum_row exp(x - max); renorm: w_k = p_k / sum_j p_j over the selection.
-// Keys are packed into 64 bits, (orderable fp32 bits of the logit << 32) | (~index), so one 64-bit wave max per
-// selected slot is the whole argmax, ties included.
+// Keys pack (valid, live, order-preserving bf16 logit, ~index) into 32 bits, so one DPP wave max per selected
+// slot is the whole argmax, ties included.
 //
 // Compaction (the moe_align_block_size tables, reference contract kernels/r9k_moe_route.hip:27-31 and
 // r9700_vllm/kernels/moe.py:574-592): each expert's routed flat rows (token * topk + j) padded to a multiple of blk,
@@ -41,9 +41,26 @@ constexpr int SMALL_MAX = 4096;   // routed rows handled by one workgroup (ids k
 constexpr int CH = 2048;          // routed rows per chunk in the multi-workgroup align
 constexpr int RW = 8;             // waves (rows) per block of the top-k kernel
 
-__device__ __forceinline__ uint32_t orderable(float x) {
-  const uint32_t u = __float_as_uint(x + 0.0f);     // -0 -> +0: equal logits must tie
-  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+// Max of a 32-bit key over the wave, returned as a wave-uniform (scalar) value: DPP within 16-lane rows (quad
+// swaps, row rotates by 4 and 8), then the four row results through v_readlane and a scalar max.
+__device__ __forceinline__ uint32_t wave_max_key(uint32_t v) {
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false));    // quad_perm [1,0,3,2]
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false));    // quad_perm [2,3,0,1]
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x124, 0xF, 0xF, false));   // row_ror:4
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x128, 0xF, 0xF, false));   // row_ror:8
+  const uint32_t a = __builtin_amdgcn_readlane(v, 0), b = __builtin_amdgcn_readlane(v, 16);
+  const uint32_t c = __builtin_amdgcn_readlane(v, 32), d = __builtin_amdgcn_readlane(v, 48);
+  return max(max(a, b), max(c, d));
+}
+
+// Selection key of an expert entry (0 = not selectable: taken, or past E):
+//   bit 27 valid | bit 26 live | bits 10..25 the bf16 logit made order-preserving (-0 folded onto +0) | 1023 - e
+// so the unsigned maximum is the live entry with the largest logit, ties to the lower index, then dead entries by
+// index. E <= 1024.
+__device__ __forceinline__ uint32_t route_key(uint16_t h, bool live, int e) {
+  uint32_t b = h == 0x8000u ? 0u : h;
+  const uint32_t ord = (b & 0x8000u) ? (~b & 0xffffu) : (b | 0x8000u);
+  return (1u << 27) | (live ? (1u << 26) | (ord << 10) : 0u) | (uint32_t)(1023 - e);
 }
 
 // One wave routes one row. Lane k < topk ends holding selection k. Writes w/ids (global) and optionally LDS ids.
@@ -51,53 +68,51 @@ template <int EPL>
 __device__ __forceinline__ void topk_row(const uint16_t* __restrict__ row, int E, int topk, bool renorm,
                                          float* __restrict__ w_out, int* __restrict__ id_out, short* lds_ids,
                                          int lane) {
-  float x[EPL];
+  uint16_t h[EPL];
   float mx = -INFINITY;
 #pragma unroll
   for (int i = 0; i < EPL; i++) {
     const int e = lane + WAVE * i;
-    x[i] = e < E ? bf2f(row[e]) : -INFINITY;
-    mx = fmaxf(mx, x[i]);
+    h[i] = e < E ? row[e] : (uint16_t)0xff80u;          // -inf for lanes past E
+    mx = fmaxf(mx, bf2f(h[i]));
   }
   mx = wave_max(mx);
   float ex[EPL];
-  uint64_t key[EPL];
+  uint32_t key[EPL];
   float s = 0.f;
 #pragma unroll
   for (int i = 0; i < EPL; i++) {
     const int e = lane + WAVE * i;
-    if (e < E) {
-      const float d = x[i] - mx;
-      const bool live = d >= -87.f;                  // false for NaN (NaN logit, or a +inf row)
-      ex[i] = live ? expf(d) : 0.f;
-      s += ex[i];
-      key[i] = ((uint64_t)(live ? orderable(x[i]) : 0u) << 32) | (uint32_t)(0xffffffffu - (uint32_t)e);
-    } else {
-      ex[i] = 0.f;
-      key[i] = 0;                                    // not an expert: never selected
-    }
+    const float d = bf2f(h[i]) - mx;
+    const bool live = d >= -87.f;                        // false for NaN (NaN logit, or a +inf row)
+    ex[i] = (e < E && live) ? expf(d) : 0.f;
+    s += ex[i];
+    key[i] = e < E ? route_key(h[i], live, e) : 0u;
   }
   s = wave_sum(s);
-  float wsel = 0.f;
+  float wsel = 0.f, tot = 0.f;
   int isel = 0;
   for (int k = 0; k < topk; k++) {
-    uint64_t b = key[0];
+    uint32_t b = key[0];
 #pragma unroll
-    for (int i = 1; i < EPL; i++) b = key[i] > b ? key[i] : b;
-    b = wave_max_u64(b);
-    const int idx = (int)(0xffffffffu - (uint32_t)b);
+    for (int i = 1; i < EPL; i++) b = max(b, key[i]);
+    b = wave_max_key(b);
+    const int idx = 1023 - (int)(b & 1023u);
+    const int owner = idx & (WAVE - 1), slot = idx / WAVE;
     float eb = 0.f;
 #pragma unroll
     for (int i = 0; i < EPL; i++)
-      if (lane + WAVE * i == idx) { eb = ex[i]; key[i] = 0; }
-    eb = __shfl(eb, idx & (WAVE - 1), WAVE);
-    if (lane == k) { wsel = eb; isel = idx; }
+      if (i == slot) eb = ex[i];
+    eb = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(eb), owner));
+#pragma unroll
+    for (int i = 0; i < EPL; i++)
+      if (i == slot && lane == owner) key[i] = 0u;
+    const float p = s > 0.f ? eb / s : 0.f;
+    tot += p;
+    if (lane == k) { wsel = p; isel = idx; }
   }
-  float p = s > 0.f ? wsel / s : 0.f;
-  if (renorm) {
-    const float tot = wave_sum(lane < topk ? p : 0.f);
-    p = tot > 0.f ? p / tot : 0.f;
-  }
+  float p = wsel;
+  if (renorm) p = tot > 0.f ? p / tot : 0.f;
   if (isel < 0 || isel >= E) isel = 0;               // unreachable (topk <= E); keeps every table write in range
   if (lane < topk) {
     w_out[lane] = p;
