@@ -38,6 +38,12 @@ int r9k_moe_4bit_prefill(int nv, long a, long as, long wq, long ws, long wref, l
                          long expert_ids, long ntpp, long topk_w, long ws_estride, long wref_estride, int max_blocks,
                          int numel, int a_row_div, int K, int N, int cfg, long stream);
 
+/* Native NVFP4 experts (kernels/r9k_moe_mxfp4a8.hip:641-647): not served on gfx950, returns -8 (NVFP4 checkpoints
+ * are converted to MXFP4 at load with r9k_nvfp4_to_mxfp4). Exported so the reference's bindings load. */
+int r9k_moe_nvfp4a8(long a, long as, long wq, long ws, long wg, long c, long sorted_ids, long expert_ids, long ntpp,
+                    long topk_w, long ws_estride, long wg_estride, int max_blocks, int numel, int a_row_div, int K,
+                    int N, int WV, int SK, int NPW, int MT, long stream);
+
 /* Rows per routing block / K granularity of a prefill cfg (-1: no such cfg).
  * Replace kernels/r9k_moe_mxfp4a8.hip:1196-1203. */
 int r9k_moe_prefill_bm(int cfg);
