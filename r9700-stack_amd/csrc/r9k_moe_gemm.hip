@@ -213,6 +213,12 @@ __global__ void __launch_bounds__(WAVE * SK) moe_mxfp4_kernel(
 
 struct Pick { int MT, NPW, SK, U; };
 
+// 1 when the environment variable is set to "0" (a switch turned off), else 0.
+int getenv_flag_off(const char* name) {
+  const char* v = getenv(name);
+  return v && v[0] == '0' ? 1 : 0;
+}
+
 int env_int(const char* name, int dflt) {
   const char* v = getenv(name);
   return v && *v ? atoi(v) : dflt;
@@ -300,6 +306,11 @@ constexpr int NPF = sizeof(kPf) / sizeof(kPf[0]);
 
 }  // namespace
 
+int r9k_prefill_launch(long a, long as, long wq, long ws, long c, long sorted_ids, long expert_ids, long ntpp,
+                       long topk_w, long ws_estride, int max_blocks, int numel, int a_row_div, int K, int N,
+                       long stream);
+int r9k_prefill_block_rows();
+
 // Reference: kernels/r9k_moe_mxfp4a8.hip:625-638 (r9k_moe_mxfp4a8). `wref`, WV, SK, NPW and the MT bits 3 (LDS-A)
 // and 4 (fold) are gfx1201 tuning / layout knobs with no meaning here and are ignored; MT & 7 in {1, 2, 4} sets the
 // routing block (16 * MT rows). ws_estride: bytes per expert of the scale tensor. 0 / negative error code.
@@ -324,6 +335,10 @@ extern "C" int r9k_moe_4bit_prefill(int nv, long a, long as, long wq, long ws, l
   if (cfg < 0 || cfg >= NPF) return -7;
   if (K % kPf[cfg].BK) return -2;
   if (nv != 0 && nv != 2) return -8;
+  // 256-row blocks with K a multiple of 128: the LDS-tiled 32x32x64 kernel (r9k_moe_prefill.hip)
+  if (kPf[cfg].BM == r9k_prefill_block_rows() && K % 128 == 0 && getenv_flag_off("R9K_PREFILL_LDS") == 0)
+    return r9k_prefill_launch(a, as, wq, ws, c, sorted_ids, expert_ids, ntpp, topk_w, ws_estride, max_blocks, numel,
+                              a_row_div, K, N, stream);
   const int rc = moe_dispatch(a, as, wq, ws, c, sorted_ids, expert_ids, ntpp, topk_w, ws_estride, max_blocks, numel,
                               a_row_div, K, N, 4, kPf[cfg].BM, stream);
   if (rc) return rc;

@@ -436,6 +436,20 @@ MOE_PREFILL_CFG = int(os.environ.get("R9K_MOE_PREFILL_CFG", "17"))
 MOE_PREFILL_CFG_GATE_UP = int(os.environ.get("R9K_MOE_PREFILL_CFG1", "17"))
 
 
+PREFILL_MOE_ROWS = int(os.environ.get("R9K_PREFILL_MOE_ROWS", "128"))
+MOE_PREFILL_CFG_BIG = int(os.environ.get("R9K_MOE_PREFILL_CFG_BIG", "12"))
+
+
+def pick_moe_prefill_block(numel: int, num_experts: int, K1: int, K2: int):
+    """(cfg, rows per routing block) for a routed layer whose touched experts average >= PREFILL_MOE_ROWS rows: the
+    256-row LDS-tiled kernel on the 32x32x64 scaled MFMA (both GEMMs' K multiples of 128), one block ~ one expert so
+    each weight tile streams from HBM once. None keeps the 16*MT-row decode-family blocks."""
+    per = numel / max(1, min(num_experts, numel))
+    if MOE_PREFILL_CFG_BIG < 0 or per < PREFILL_MOE_ROWS or K1 % 128 or K2 % 128:
+        return None
+    return MOE_PREFILL_CFG_BIG, prefill_block(MOE_PREFILL_CFG_BIG)
+
+
 def pick_moe_prefill(MT: int, K_down: int, gate_up: bool = False) -> int | None:
     """Prefill tile for the routed-MoE GEMMs of a step whose routing block is 16*MT rows (None: the decode kernel).
     Both GEMMs must share the block size, so one align table serves both."""

@@ -139,9 +139,14 @@ class R9700Mxfp4Experts(_experts_base()):
             return
 
         MT = K.pick_mt(numel, global_num_experts)
-        blk = K.MOE_BLOCK * MT
-        pf_down = K.pick_moe_prefill(MT, K2)
-        pf_gate = K.pick_moe_prefill(MT, K1, gate_up=True)
+        big = K.pick_moe_prefill_block(numel, global_num_experts, K1, K2)
+        if big is not None:                                  # prefill widths: one 256-row block ~ one expert
+            pf_gate = pf_down = big[0]
+            blk = big[1]
+        else:
+            blk = K.MOE_BLOCK * MT
+            pf_down = K.pick_moe_prefill(MT, K2)
+            pf_gate = K.pick_moe_prefill(MT, K1, gate_up=True)
         tabs = route.take(getattr(self, "r9k_layer", None), topk_ids, blk, numel) if expert_map is None else None
         if tabs is None:
             tabs = K.moe_align(topk_ids, blk, E, expert_map)

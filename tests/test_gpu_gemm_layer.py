@@ -60,10 +60,19 @@ def test_grouped_gemm_multitile(dev, MT, N, Kd):
     gemm_case(dev, 16, 200, 4, Kd if Kd % 16 == 0 else N, N if N % 32 == 0 else Kd, seed=MT + N + 1, MT=MT, down=True)
 
 
-@pytest.mark.parametrize("cfg", [17, 10, 12, 6])
+@pytest.mark.parametrize("cfg", [17, 10, 12, 6, 1])
 def test_grouped_gemm_prefill_entry(dev, cfg):
     gemm_case(dev, 16, 600, 4, 1040, 1024, seed=cfg, prefill=cfg)
     gemm_case(dev, 16, 600, 4, 512, 320, seed=cfg + 50, prefill=cfg, down=True)
+
+
+@pytest.mark.parametrize("E,M,topk,N,Kd", [(16, 1200, 4, 1024, 2048), (8, 900, 2, 2048, 512), (4, 300, 1, 272, 384),
+                                           (32, 2000, 8, 512, 256)])
+@pytest.mark.parametrize("down", [False, True])
+def test_grouped_gemm_prefill_256(dev, E, M, topk, N, Kd, down):
+    """256-row blocks with K % 128 == 0: the LDS-tiled 32x32x64 kernel (ragged expert sizes, padded M tiles,
+    a column block past N, one and several 256-row blocks per expert)."""
+    gemm_case(dev, E, M, topk, N, Kd, seed=E + M + N + Kd, prefill=12, down=down)
 
 
 @pytest.mark.parametrize("M,N,Kd", [(16, 1024, 2048), (1, 17408, 5120), (4, 1024, 5120), (300, 512, 1024)])
@@ -77,6 +86,24 @@ def test_dense_mxfp4_linear(dev, M, N, Kd):
     qo, so = O.quant_rows_fp8(x)
     ref = O.grouped_gemm(qo, so, {0: O.mxfp4_dequant(packed[0], e8[0])}, np.zeros(M, dtype=np.int32), 1)
     got = O.bf16_bits(out)
+    r = rel_err(bf16_bits_to_f64(got), bf16_bits_to_f64(ref))
+    assert r < 2e-3 and cosine(bf16_bits_to_f64(got), bf16_bits_to_f64(ref)) > 0.99999
+
+
+def test_dense_mxfp4_linear_config4_prefill_sampled(dev):
+    """BASELINE config 4 at M = 4096: [4096, 5120] x [17408, 5120]^T through ops.mxfp4_linear (256-row tiles), checked
+    on 48 sampled rows (rows are independent)."""
+    M, N, Kd = 4096, 17408, 5120
+    g = torch.Generator().manual_seed(4096)
+    packed, e8 = make_experts(1, N, Kd, g)
+    W = K.prepare_mxfp4_weights(packed.to(dev), e8.to(dev))
+    x = torch.randn(M, Kd, generator=g).to(torch.bfloat16)
+    out = ops.mxfp4_linear(x.to(dev), W.wq, W.wsr, N, Kd)
+    rows = np.sort(np.random.default_rng(0).choice(M, 48, replace=False))
+    qo, so = O.quant_rows_fp8(x)
+    Wd = O.mxfp4_dequant(packed[0], e8[0], torch.float32)
+    ref = O.grouped_gemm(qo, so, {0: Wd}, np.zeros(M, dtype=np.int32), 1, None, rows, acc_dtype=torch.float32)
+    got = O.bf16_bits(out)[rows]
     r = rel_err(bf16_bits_to_f64(got), bf16_bits_to_f64(ref))
     assert r < 2e-3 and cosine(bf16_bits_to_f64(got), bf16_bits_to_f64(ref)) > 0.99999
 
