@@ -21,9 +21,8 @@
 //            1 KB at kt * 1024: lane l = g * 16 + r holds row r, K elements kt*128 + g*32 .. +32 as 16 bytes at
 //            l * 16 -- exactly the B operand of one 16x16x128 MFMA, so a wave loads it as one contiguous 1 KB
 //            (global_load_dwordx4). A last partial K-tile (K % 128 = 32 * G) holds only lanes l < 16 * G.
-//   scales : N/16 column tiles of 16 * K/32 bytes. Full super-steps of 4 K-tiles are 256 bytes each: lane l's
-//            dword holds the exponents of its (row, group) for the 4 K-tiles, byte j = K-tile 4q + j. The K-tiles
-//            after the last full super-step are 64 bytes each (lane l's byte at l; a partial tile 16 * G bytes).
+//   scales : N/16 column tiles of 16 * K/32 bytes. K-tile kt is 64 bytes at kt * 64: lane l's byte at l is the
+//            exponent of its (row r, group g) -- the MFMA's B scale operand (a partial last tile 16 * G bytes).
 // One 16-row x 16-column MFMA tile therefore reads 1 KB of codes and 64 bytes of exponents, all coalesced.
 //
 // Work split: a workgroup owns 16*MT routed rows (MT M-tiles sharing every weight fragment) x NPW column tiles,
@@ -86,7 +85,7 @@ __global__ void __launch_bounds__(WAVE * SK) moe_mxfp4_kernel(
   const int g = lane >> 4, r = lane & 15;
   const int NT = N / 16;
   const int nkt = (K + KT - 1) / KT, nkt_full = K / KT, tg = (K % KT) / GROUP;
-  const int KB = K / GROUP, nq = KB / 16;
+  const int KB = K / GROUP;
 
   // per-lane operand offsets that stay valid on a partial last K-tile (only lanes/halves below K are live there)
   const int lane_b_tail = g < tg ? lane : r;                          // B lanes of the partial tile: lanes < 16 * tg
@@ -129,7 +128,7 @@ __global__ void __launch_bounds__(WAVE * SK) moe_mxfp4_kernel(
       const int k = min(kt + u, kt1 - 1);
       const bool full = k < nkt_full;
       const int bl = full ? lane : lane_b_tail;
-      const int soff = k < 4 * nq ? (k >> 2) * 256 + lane * 4 + (k & 3) : nq * 256 + (k - 4 * nq) * 64 + bl;
+      const int soff = k * 64 + bl;
 #pragma unroll
       for (int j = 0; j < NPW; j++) {
         bf[u][j] = ld16<NTL>(wtile[j] + (size_t)k * 1024 + bl * 16);

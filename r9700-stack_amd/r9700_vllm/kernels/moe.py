@@ -169,24 +169,18 @@ def pack_scales(scale: torch.Tensor) -> torch.Tensor:
     """[E, N, K/32] E8M0 -> [E, K/32 + 1, N] uint8: the first (K/32)*N bytes of each expert are the exponents in
     the kernels' fragment order, the last N bytes the per-row maximum exponent.
 
-    Column tile nt owns 16*K/32 bytes at nt*16*K/32. Full super-steps q of 4 K-tiles (16 blocks) are 256 bytes:
-    lane l = g*16 + r has the dword at q*256 + l*4 whose byte j is the exponent of row r, block 16q + 4j + g
-    (K-tile 4q + j, group g) -- one scale operand a K-tile. The K-tiles after the last full super-step are 64
-    bytes each, lane l's byte at l (a partial last tile 16*G bytes)."""
+    Column tile nt owns 16*K/32 bytes at nt*16*K/32. K-tile kt (128 K, four 32-blocks) is 64 bytes at kt*64: lane
+    l = g*16 + r has the exponent of row r, block 4*kt + g at byte l -- the scale operand of one MFMA tile, one byte
+    a lane. A partial last K-tile (K % 128 = 32*G) keeps its 16*G bytes."""
     scale = scale.view(torch.uint8)
     E, N, KB = scale.shape
-    nt, nq, tb = N // 16, KB // 16, KB % 16
+    nt, nkf, G = N // 16, KB // 4, KB % 4
     s = scale.reshape(E, nt, 16, KB)                                                     # [E, nt, r, kb]
     parts = []
-    if nq:
-        q = s[..., : nq * 16].reshape(E, nt, 16, nq, 4, 4).permute(0, 1, 3, 5, 2, 4)     # [E, nt, q, g, r, j]
-        parts.append(q.reshape(E, nt, nq * 256))
-    if tb:
-        ntt = (tb + 3) // 4
-        t = torch.zeros((E, nt, 16, ntt * 4), dtype=torch.uint8, device=scale.device)
-        t[..., :tb] = s[..., nq * 16:]
-        t = t.reshape(E, nt, 16, ntt, 4).permute(0, 1, 3, 4, 2).reshape(E, nt, ntt * 64)  # [E, nt, t, g, r]
-        parts.append(t[..., : tb * 16])
+    if nkf:
+        parts.append(s[..., : nkf * 4].reshape(E, nt, 16, nkf, 4).permute(0, 1, 3, 4, 2).reshape(E, nt, nkf * 64))
+    if G:
+        parts.append(s[..., nkf * 4:].permute(0, 1, 3, 2).reshape(E, nt, G * 16))    # [E, nt, g, r]
     body = parts[0] if len(parts) == 1 else torch.cat(parts, dim=2)
     out = torch.empty((E, KB + 1, N), dtype=torch.uint8, device=scale.device)
     out.view(E, -1)[:, : KB * N].copy_(body.reshape(E, KB * N))
@@ -198,19 +192,14 @@ def unpack_scales(wsr: torch.Tensor) -> torch.Tensor:
     """Inverse of pack_scales: [E, K/32 + 1, N] -> [E, N, K/32] uint8 exponents."""
     E, KB1, N = wsr.shape
     KB = KB1 - 1
-    nt, nq, tb = N // 16, KB // 16, KB % 16
+    nt, nkf, G = N // 16, KB // 4, KB % 4
     body = wsr.reshape(E, -1)[:, : KB * N].reshape(E, nt, 16 * KB)
     parts = []
-    if nq:
-        q = body[..., : nq * 256].reshape(E, nt, nq, 4, 16, 4).permute(0, 1, 4, 2, 5, 3)   # [E, nt, r, q, j, g]
-        parts.append(q.reshape(E, nt, 16, nq * 16))
-    if tb:
-        t = body[..., nq * 256:]
-        ntt = (tb + 3) // 4
-        pad = torch.zeros((E, nt, ntt * 64), dtype=torch.uint8, device=wsr.device)
-        pad[..., : tb * 16] = t
-        t = pad.reshape(E, nt, ntt, 4, 16).permute(0, 1, 4, 2, 3).reshape(E, nt, 16, ntt * 4)
-        parts.append(t[..., :tb])
+    if nkf:
+        q = body[..., : nkf * 64].reshape(E, nt, nkf, 4, 16).permute(0, 1, 4, 2, 3)         # [E, nt, r, kt, g]
+        parts.append(q.reshape(E, nt, 16, nkf * 4))
+    if G:
+        parts.append(body[..., nkf * 64:].reshape(E, nt, G, 16).permute(0, 1, 3, 2))        # [E, nt, r, g]
     out = parts[0] if len(parts) == 1 else torch.cat(parts, dim=3)
     return out.reshape(E, N, KB).contiguous()
 

@@ -37,7 +37,6 @@ def test_pack_scales_lane_layout(N, Kd):
     KB = Kd // 32
     assert wsr.shape == (2, KB + 1, N)
     body = wsr.reshape(2, -1)
-    nq = KB // 16
     for e in range(2):
         for nt in range(N // 16):
             base = nt * 16 * KB
@@ -45,7 +44,7 @@ def test_pack_scales_lane_layout(N, Kd):
                 kt, gg = kb // 4, kb % 4
                 for r in range(16):
                     lane = gg * 16 + r
-                    off = (kt // 4) * 256 + lane * 4 + (kt % 4) if kt < 4 * nq else nq * 256 + (kt - 4 * nq) * 64 + lane
+                    off = kt * 64 + lane
                     assert body[e, base + off] == e8[e, nt * 16 + r, kb]
         assert torch.equal(wsr[e, KB], e8[e].max(dim=1).values)
     assert torch.equal(K.unpack_scales(wsr), e8)
