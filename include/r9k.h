@@ -69,7 +69,8 @@ int r9k_silu_mul_quant_fp8(long gu, long q, long s, int M, int I, long stream);
 
 /* Softmax top-k routing + align tables in one call: logits bf16 [M][E] (row stride ldl) -> weights fp32 [M][topk],
  * ids int32 [M][topk], sorted_ids int32 [capacity], expert_ids int32 [capacity / blk], ntpp int32 [1]
- * (capacity = ceil((M*topk + E*(blk-1)) / blk) * blk). scratch: 2E+1 int32 (reference contract; unused here).
+ * (capacity = ceil((M*topk + E*(blk-1)) / blk) * blk). scratch: 2E+1 int32, zeroed once by the caller (reference contract);
+ * scratch[0] is the workgroups' arrival counter and is left zero. Calls sharing one scratch must not overlap.
  * Tables in canonical order (rows ascending within each expert). Returns 0, 1 for an unsupported shape
  * (E > 1024, topk > 16, blk not a power of two), else the HIP error. Replaces kernels/r9k_moe_route.hip:217-233. */
 int r9k_moe_route(long logits, int ldl, long weights, long ids, long sorted_ids, long expert_ids, long ntpp,
@@ -90,7 +91,8 @@ int r9k_moe_topk(long logits, int ldl, long weights, long ids, int M, int E, int
 
 /* Align tables only, from ids int32 [numel] (the role of vLLM's moe_align_block_size, called at
  * r9700_vllm/moe/experts.py:172 of the reference). ids outside [0, E) are left out. scratch: at least
- * r9k_moe_align_scratch_ints(numel, E) int32, zero at the first call (the kernels leave it zero). */
+ * r9k_moe_align_scratch_ints(numel, E) int32 of per-chunk histograms, rewritten by every call (no initial
+ * contents needed; calls sharing one scratch must not overlap). */
 int r9k_moe_align(long ids, int numel, int E, int blk, long sorted_ids, long expert_ids, long ntpp, long scratch,
                   long scratch_ints, long stream);
 long r9k_moe_align_scratch_ints(int numel, int E);

@@ -99,7 +99,7 @@ __global__ void __launch_bounds__(NTH) moe_prefill_kernel(
     const int row = p * 64 + (tid >> 3);
     int fr = rows[row];
     if (row >= nlive) fr = first;
-    const int piece = (tid & 7) ^ ((tid >> 3) & 7);            // row & 7 == (tid >> 3) & 7
+    const int piece = (tid & 7) ^ ((tid >> 3) & 7) ^ ((tid >> 6) & 1);            // row & 7 == (tid >> 3) & 7
     ga[p] = A + (size_t)(fr / a_row_div) * K + piece * 16;
   }
   const uint8_t* gb[2];
@@ -153,8 +153,8 @@ __global__ void __launch_bounds__(NTH) moe_prefill_kernel(
     const int row = wm * 64 + i * 32 + c32;
 #pragma unroll
     for (int ks = 0; ks < 2; ks++) {
-      aoff_lo[i][ks] = (row * 8 + ((4 * ks + g) ^ (row & 7))) * 16;
-      aoff_hi[i][ks] = (row * 8 + ((4 * ks + 2 + g) ^ (row & 7))) * 16;
+      aoff_lo[i][ks] = (row * 8 + ((4 * ks + g) ^ (row & 7) ^ ((row >> 3) & 1))) * 16;
+      aoff_hi[i][ks] = (row * 8 + ((4 * ks + 2 + g) ^ (row & 7) ^ ((row >> 3) & 1))) * 16;
     }
   }
 

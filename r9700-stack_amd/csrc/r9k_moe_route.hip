@@ -17,16 +17,19 @@
 // experts ascending, padding value numel; expert_ids[b] = expert of block b or -1 past the end; ntpp[0] = padded
 // total. Unlike the reference kernel (atomics: row order within an expert unspecified) the scatter here is STABLE:
 // rows ascend within each expert, which is exactly align_block_size_ref's canonical order, so the tables are
-// bit-exact against it. Stable ranks come from a wave64 match loop (ballot per distinct expert in the wave) plus
-// per-wave counts in LDS. The whole capacity (sorted_ids [cap], expert_ids [cap / blk], cap =
-// ceil((numel + E * (blk - 1)) / blk) * blk) is written, the tail with numel / -1.
+// bit-exact against it. The ids sit in LDS; after an LDS histogram and a scan of the block-padded counts, rows are
+// placed in rounds of one row per thread: a row's rank among equal ids of its wave comes from a branch-free compare
+// against all 64 lanes (v_readlane), earlier waves' rows from per-wave counts in LDS. The whole capacity (sorted_ids [cap], expert_ids [cap / blk], cap =
+// ceil((numel + E * (blk - 1)) / blk) * blk) is written, the tail with numel / -1. Barriers between phases wait for
+// LDS traffic only; global stores are never waited for inside a kernel (nothing reads them back).
 //
 // Entry points:
-//   r9k_moe_route   the reference's one-launch routing + tables (any M; numel <= 4096 in one workgroup and one
-//                   launch, larger as a top-k launch plus one single-workgroup table launch)
+//   r9k_moe_route   the reference's one-launch routing + tables (any M; numel <= 4096: one wave per row over
+//                   ceil(M / 8) workgroups, the last to arrive builds the tables; larger numel as a top-k launch plus
+//                   a single-workgroup table launch)
 //   r9k_moe_topk    routing only (the stock top-k router's role)
-//   r9k_moe_align   tables only from given ids (vLLM's moe_align_block_size role); large numel runs as a count
-//                   launch (the last block to arrive scans) plus a scatter launch, with caller scratch.
+//   r9k_moe_align   tables only from given ids (vLLM's moe_align_block_size role); large numel runs as a
+//                   per-chunk histogram launch plus a scatter launch (bases from the histograms), caller scratch.
 #include "r9k_common.h"
 
 namespace {
@@ -37,20 +40,51 @@ constexpr int MAX_E = 1024;       // experts
 constexpr int MAX_K = 16;         // top-k
 constexpr int AT = 1024;          // threads of an align / fused workgroup (16 waves)
 constexpr int AW = AT / WAVE;
-constexpr int SMALL_MAX = 4096;   // routed rows handled by one workgroup (ids kept in LDS)
+constexpr int SMALL_MAX = 4096;   // routed rows whose tables one workgroup builds
 constexpr int CH = 2048;          // routed rows per chunk in the multi-workgroup align
 constexpr int RW = 8;             // waves (rows) per block of the top-k kernel
+constexpr int FT = 512;           // threads of a fused routing workgroup (8 waves, one token row each)
+constexpr int FW = FT / WAVE;
 
-// Max of a 32-bit key over the wave, returned as a wave-uniform (scalar) value: DPP within 16-lane rows (quad
-// swaps, row rotates by 4 and 8), then the four row results through v_readlane and a scalar max.
+// Workgroup barrier that orders LDS traffic only (global stores stay in flight).
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+#define R9K_DPP(v, ctrl) (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(v), ctrl, 0xF, 0xF, false)
+
+// Wave-uniform max of a 32-bit key: DPP within 16-lane rows (quad swaps, row rotates by 4 and 8), then the four row
+// results through v_readlane and a scalar max.
 __device__ __forceinline__ uint32_t wave_max_key(uint32_t v) {
-  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false));    // quad_perm [1,0,3,2]
-  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false));    // quad_perm [2,3,0,1]
-  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x124, 0xF, 0xF, false));   // row_ror:4
-  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x128, 0xF, 0xF, false));   // row_ror:8
+  v = max(v, R9K_DPP(v, 0xB1));    // quad_perm [1,0,3,2]
+  v = max(v, R9K_DPP(v, 0x4E));    // quad_perm [2,3,0,1]
+  v = max(v, R9K_DPP(v, 0x124));   // row_ror:4
+  v = max(v, R9K_DPP(v, 0x128));   // row_ror:8
   const uint32_t a = __builtin_amdgcn_readlane(v, 0), b = __builtin_amdgcn_readlane(v, 16);
   const uint32_t c = __builtin_amdgcn_readlane(v, 32), d = __builtin_amdgcn_readlane(v, 48);
   return max(max(a, b), max(c, d));
+}
+
+// Wave-uniform fmaxf / sum of a float, same DPP pattern (the sum in a fixed order: deterministic).
+__device__ __forceinline__ float wave_max_dpp(float v) {
+  v = fmaxf(v, __uint_as_float(R9K_DPP(__float_as_uint(v), 0xB1)));
+  v = fmaxf(v, __uint_as_float(R9K_DPP(__float_as_uint(v), 0x4E)));
+  v = fmaxf(v, __uint_as_float(R9K_DPP(__float_as_uint(v), 0x124)));
+  v = fmaxf(v, __uint_as_float(R9K_DPP(__float_as_uint(v), 0x128)));
+  const float a = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), 0));
+  const float b = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), 16));
+  const float c = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), 32));
+  const float d = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), 48));
+  return fmaxf(fmaxf(a, b), fmaxf(c, d));
+}
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  v += __uint_as_float(R9K_DPP(__float_as_uint(v), 0xB1));
+  v += __uint_as_float(R9K_DPP(__float_as_uint(v), 0x4E));
+  v += __uint_as_float(R9K_DPP(__float_as_uint(v), 0x124));
+  v += __uint_as_float(R9K_DPP(__float_as_uint(v), 0x128));
+  const float a = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), 0));
+  const float b = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), 16));
+  const float c = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), 32));
+  const float d = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), 48));
+  return (a + b) + (c + d);
 }
 
 // Selection key of an expert entry (0 = not selectable: taken, or past E):
@@ -63,20 +97,25 @@ __device__ __forceinline__ uint32_t route_key(uint16_t h, bool live, int e) {
   return (1u << 27) | (live ? (1u << 26) | (ord << 10) : 0u) | (uint32_t)(1023 - e);
 }
 
-// One wave routes one row. Lane k < topk ends holding selection k. Writes w/ids (global) and optionally LDS ids.
+// Logits of one row for this lane: entry lane + 64 i, -inf past E.
 template <int EPL>
-__device__ __forceinline__ void topk_row(const uint16_t* __restrict__ row, int E, int topk, bool renorm,
-                                         float* __restrict__ w_out, int* __restrict__ id_out, short* lds_ids,
-                                         int lane) {
-  uint16_t h[EPL];
-  float mx = -INFINITY;
+__device__ __forceinline__ void load_row(const uint16_t* __restrict__ row, int E, int lane, uint16_t* h) {
 #pragma unroll
   for (int i = 0; i < EPL; i++) {
     const int e = lane + WAVE * i;
-    h[i] = e < E ? row[e] : (uint16_t)0xff80u;          // -inf for lanes past E
-    mx = fmaxf(mx, bf2f(h[i]));
+    h[i] = e < E ? row[e] : (uint16_t)0xff80u;
   }
-  mx = wave_max(mx);
+}
+
+// One wave routes one row from its preloaded logits. Lane k < topk ends holding selection k; writes w / ids
+// (global) and, when given, the ids to LDS.
+template <int EPL>
+__device__ __forceinline__ void topk_core(const uint16_t* h, int E, int topk, bool renorm, float* __restrict__ w_out,
+                                          int* __restrict__ id_out, short* lds_ids, int lane) {
+  float mx = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < EPL; i++) mx = fmaxf(mx, bf2f(h[i]));
+  mx = wave_max_dpp(mx);
   float ex[EPL];
   uint32_t key[EPL];
   float s = 0.f;
@@ -89,7 +128,7 @@ __device__ __forceinline__ void topk_row(const uint16_t* __restrict__ row, int E
     s += ex[i];
     key[i] = e < E ? route_key(h[i], live, e) : 0u;
   }
-  s = wave_sum(s);
+  s = wave_sum_dpp(s);
   float wsel = 0.f, tot = 0.f;
   int isel = 0;
   for (int k = 0; k < topk; k++) {
@@ -121,15 +160,27 @@ __device__ __forceinline__ void topk_row(const uint16_t* __restrict__ row, int E
   }
 }
 
-struct AlignLds {
-  int cnt[MAX_E];              // counts, then the running scatter cursor
+template <int NT>
+struct TabLds {
+  static constexpr int NW = NT / WAVE;
+  int cnt[MAX_E];              // rows per expert
   int offs[MAX_E];             // first padded position of each expert
-  uint8_t wcnt[AW][MAX_E];     // rows per (wave, expert) in the current 1024-row sub-chunk
-  int scan[AW];
+  int cursor[MAX_E];           // next slot of each expert during the placement
+  uint16_t wcnt[NW][MAX_E];    // rows per (wave, expert) in the current round of NT rows; zero between rounds
+  int scan[NW];
 };
 
-// Exclusive scan of the block-padded counts (one expert per thread, E <= AT): offs[], returns the padded total.
-__device__ __forceinline__ int padded_scan(AlignLds& sh, int E, int blk) {
+template <int NT>
+__device__ __forceinline__ void zero_counts(TabLds<NT>& sh, int E) {
+  for (int e = threadIdx.x; e < E; e += NT) sh.cnt[e] = 0;
+  uint32_t* p = reinterpret_cast<uint32_t*>(&sh.wcnt[0][0]);
+  for (int i = threadIdx.x; i < TabLds<NT>::NW * MAX_E / 2; i += NT) p[i] = 0u;
+}
+
+// Exclusive scan of the block-padded counts (one expert per thread, E <= NT): offs[], returns the padded total.
+template <int NT>
+__device__ __forceinline__ int padded_scan(TabLds<NT>& sh, int E, int blk) {
+  constexpr int NW = NT / WAVE;
   const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
   const int c = tid < E ? sh.cnt[tid] : 0;
   const int n = ((c + blk - 1) / blk) * blk;
@@ -140,113 +191,137 @@ __device__ __forceinline__ int padded_scan(AlignLds& sh, int E, int blk) {
     if (lane >= o) x += y;
   }
   if (lane == WAVE - 1) sh.scan[wave] = x;
-  __syncthreads();
+  lds_barrier();
   int wbase = 0, total = 0;
 #pragma unroll
-  for (int w = 0; w < AW; w++) {
+  for (int w = 0; w < NW; w++) {
     if (w < wave) wbase += sh.scan[w];
     total += sh.scan[w];
   }
   if (tid < E) sh.offs[tid] = wbase + x - n;
-  __syncthreads();
+  lds_barrier();
   return total;
 }
 
-// expert_ids / padding entries of every expert with rows, ntpp, and the capacity tail.
-__device__ __forceinline__ void write_layout(const int* cnt, const int* offs, int total, int numel, int E, int blk,
-                                             int* __restrict__ sorted_ids, int* __restrict__ expert_ids,
-                                             int* __restrict__ ntpp) {
+// Expert blocks and padding entries of the experts e < E with e % nshare == share, every expert's cursor at its
+// first slot plus `pre` (the calling thread's expert's rows in earlier chunks), and this share's part of the
+// capacity tail. Ends with an LDS barrier.
+template <int NT>
+__device__ __forceinline__ void write_layout(TabLds<NT>& sh, int E, int blk, int numel, int total, int pre,
+                                             int share, int nshare, int* __restrict__ sorted_ids,
+                                             int* __restrict__ expert_ids) {
   const int tid = threadIdx.x;
-  if (tid == 0) ntpp[0] = total;
   if (tid < E) {
-    const int c = cnt[tid];
-    if (c > 0) {
-      const int o = offs[tid], n = ((c + blk - 1) / blk) * blk;
+    const int c = sh.cnt[tid], o = sh.offs[tid];
+    sh.cursor[tid] = o + pre;
+    if (c > 0 && tid % nshare == share) {
+      const int n = ((c + blk - 1) / blk) * blk;
       for (int b = o / blk; b < (o + n) / blk; b++) expert_ids[b] = tid;
       for (int i = o + c; i < o + n; i++) sorted_ids[i] = numel;
     }
   }
   const long cap = ((long)numel + (long)E * (blk - 1) + blk - 1) / blk * blk;
-  for (long i = total + tid; i < cap; i += AT) sorted_ids[i] = numel;
-  for (long b = total / blk + tid; b < cap / blk; b += AT) expert_ids[b] = -1;
+  const long tail = cap - total, per = (tail + nshare - 1) / nshare;
+  const long i1 = min(cap, total + (long)(share + 1) * per);
+  for (long i = total + (long)share * per + tid; i < i1; i += NT) sorted_ids[i] = numel;
+  const long btail = tail / blk, bper = (btail + nshare - 1) / nshare;
+  const long b1 = min(cap / blk, total / blk + (long)(share + 1) * bper);
+  for (long b = total / blk + (long)share * bper + tid; b < b1; b += NT) expert_ids[b] = -1;
+  lds_barrier();
 }
 
-// Stable placement of rows [base, min(base + AT, end)) given the per-expert cursor in sh.cnt (advanced here).
-// ids_at(t) returns the expert of flat row t. Rows with an expert outside [0, E) are not placed.
-template <typename IdsAt>
-__device__ __forceinline__ void stable_subchunk(AlignLds& sh, int base, int end, int E, int* __restrict__ sorted_ids,
-                                                IdsAt ids_at) {
+// Stable placement of ids[base, base + NT) (LDS; -1 = not placed) at their experts' cursors: a lane's rank among
+// the equal ids of lower lanes in its wave comes from a 64-step compare against every lane's id (v_readlane, no
+// branch), the rows of earlier waves from the per-wave counts. Advances the cursors; leaves wcnt zero.
+template <int NT>
+__device__ __forceinline__ void stable_round(TabLds<NT>& sh, const short* ids, int base, int n, int row0, int E,
+                                             int* __restrict__ sorted_ids) {
+  constexpr int NW = NT / WAVE;
   const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
   const int t = base + tid;
-  const int e = t < end ? ids_at(t) : -1;
-  const bool valid = e >= 0 && e < E;
-  uint64_t pending = __ballot(valid);
-  int rank = 0;
-  while (pending) {
-    const int leader = __ffsll((unsigned long long)pending) - 1;
-    const int e0 = __shfl(e, leader, WAVE);
-    const uint64_t m = __ballot(valid && e == e0);
-    if (valid && e == e0) rank = __popcll(m & __lanemask_lt());
-    if (lane == leader) sh.wcnt[wave][e0] = (uint8_t)__popcll(m);
-    pending &= ~m;
-  }
-  __syncthreads();
-  if (valid) {
-    int pre = 0;
-    for (int w = 0; w < wave; w++) pre += sh.wcnt[w][e];
-    sorted_ids[sh.cnt[e] + pre + rank] = t;
-  }
-  __syncthreads();
-  if (tid < E) {
-    int tot = 0;
+  const int e = t < n ? ids[t] : -1;
+  int rank = 0, cw = 0;
+  if (base + wave * WAVE < n) {                                     // waves past the rows skip the compare loop
 #pragma unroll
-    for (int w = 0; w < AW; w++) { tot += sh.wcnt[w][tid]; sh.wcnt[w][tid] = 0; }
-    sh.cnt[tid] += tot;
+    for (int j = 0; j < WAVE; j++) {
+      const int m = __builtin_amdgcn_readlane(e, j) == e;
+      cw += m;
+      rank += j < lane ? m : 0;
+    }
   }
-  __syncthreads();
+  if (e >= 0 && rank == cw - 1) sh.wcnt[wave][e] = (uint16_t)cw;     // the last of its expert in this wave
+  lds_barrier();
+  if (e >= 0) {
+    int pos = sh.cursor[e] + rank;
+    for (int w = 0; w < wave; w++) pos += sh.wcnt[w][e];
+    sorted_ids[pos] = row0 + t;
+  }
+  lds_barrier();
+  if (tid < E) {
+    int add = 0;
+#pragma unroll
+    for (int w = 0; w < NW; w++) {
+      add += sh.wcnt[w][tid];
+      sh.wcnt[w][tid] = 0;
+    }
+    sh.cursor[tid] += add;
+  }
+  lds_barrier();
 }
 
-__device__ __forceinline__ void zero_wcnt(AlignLds& sh) {
-  uint32_t* p = reinterpret_cast<uint32_t*>(&sh.wcnt[0][0]);
-  for (int i = threadIdx.x; i < AW * MAX_E / 4; i += AT) p[i] = 0u;
-}
-
-// The whole table build in one workgroup: count, scan, layout, stable scatter (cursor starts at offs).
-template <typename IdsAt>
-__device__ void align_one_block(AlignLds& sh, int numel, int E, int blk, int* __restrict__ sorted_ids,
-                                int* __restrict__ expert_ids, int* __restrict__ ntpp, IdsAt ids_at) {
-  const int tid = threadIdx.x;
-  for (int e = tid; e < E; e += AT) sh.cnt[e] = 0;
-  zero_wcnt(sh);
-  __syncthreads();
-  for (int t = tid; t < numel; t += AT) {
-    const int e = ids_at(t);
-    if (e >= 0 && e < E) atomicAdd(&sh.cnt[e], 1);
+// The whole table build in one workgroup from ids in LDS (numel <= SMALL_MAX, -1 = skipped; zero_counts and a
+// barrier done by the caller): histogram, scan, layout and the stable placement.
+template <int NT>
+__device__ __forceinline__ void build_tables(TabLds<NT>& sh, const short* ids, int numel, int E, int blk,
+                                             int* __restrict__ sorted_ids, int* __restrict__ expert_ids,
+                                             int* __restrict__ ntpp) {
+  for (int t = threadIdx.x; t < numel; t += NT) {
+    const int e = ids[t];
+    if (e >= 0) atomicAdd(&sh.cnt[e], 1);
   }
-  __syncthreads();
+  lds_barrier();
   const int total = padded_scan(sh, E, blk);
-  write_layout(sh.cnt, sh.offs, total, numel, E, blk, sorted_ids, expert_ids, ntpp);
-  __syncthreads();
-  if (tid < E) sh.cnt[tid] = sh.offs[tid];
-  __syncthreads();
-  for (int base = 0; base < numel; base += AT) stable_subchunk(sh, base, numel, E, sorted_ids, ids_at);
+  if (threadIdx.x == 0) ntpp[0] = total;
+  write_layout(sh, E, blk, numel, total, 0, 0, 1, sorted_ids, expert_ids);
+  for (int base = 0; base < numel; base += NT) stable_round(sh, ids, base, numel, 0, E, sorted_ids);
 }
 
-// Fused routing + tables, one workgroup, numel <= SMALL_MAX (reference: r9k_moe_route_kernel, single-block path).
+// Fused routing + tables (reference: r9k_moe_route_kernel, kernels/r9k_moe_route.hip:67-210), numel <= SMALL_MAX:
+// one wave per token row over ceil(M / 8) workgroups of 8 waves (the rows' latency chains spread over CUs); the
+// last workgroup to arrive (counter `arrive`, zero at entry and left zero) reads all ids into LDS and builds the
+// tables. With one workgroup the ids go straight to LDS.
 template <int EPL>
-__global__ void __launch_bounds__(AT) route_fused_kernel(const uint16_t* __restrict__ logits, int ldl,
+__global__ void __launch_bounds__(FT) route_fused_kernel(const uint16_t* __restrict__ logits, int ldl,
                                                          float* __restrict__ weights, int* __restrict__ ids,
                                                          int* __restrict__ sorted_ids, int* __restrict__ expert_ids,
-                                                         int* __restrict__ ntpp, int M, int E, int topk, int renorm,
-                                                         int blk) {
-  __shared__ AlignLds sh;
+                                                         int* __restrict__ ntpp, int* __restrict__ arrive, int M,
+                                                         int E, int topk, int renorm, int blk) {
+  __shared__ TabLds<FT> sh;
   __shared__ short lids[SMALL_MAX];
+  __shared__ int s_last;
   const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
-  for (int r = wave; r < M; r += AW)
-    topk_row<EPL>(logits + (size_t)r * ldl, E, topk, renorm != 0, weights + (size_t)r * topk,
-                  ids + (size_t)r * topk, lids + r * topk, lane);
-  __syncthreads();
-  align_one_block(sh, M * topk, E, blk, sorted_ids, expert_ids, ntpp, [&](int t) { return (int)lids[t]; });
+  const int numel = M * topk;
+  const bool single = gridDim.x == 1;
+  zero_counts(sh, E);
+  for (int r = blockIdx.x * FW + wave; r < M; r += gridDim.x * FW) {
+    uint16_t h[EPL];
+    load_row<EPL>(logits + (size_t)r * ldl, E, lane, h);
+    topk_core<EPL>(h, E, topk, renorm != 0, weights + (size_t)r * topk, ids + (size_t)r * topk,
+                   single ? lids + r * topk : nullptr, lane);
+  }
+  if (!single) {
+    __threadfence();
+    __syncthreads();
+    if (threadIdx.x == 0) s_last = atomicAdd(arrive, 1) == (int)gridDim.x - 1;
+    __syncthreads();
+    if (!s_last) return;
+    __threadfence();
+    for (int t = threadIdx.x; t < numel; t += FT)                // ids of other workgroups: read past this CU's L1
+      lids[t] = (short)__hip_atomic_load(ids + t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  lds_barrier();
+  build_tables(sh, lids, numel, E, blk, sorted_ids, expert_ids, ntpp);
+  if (!single && threadIdx.x == 0) *arrive = 0;
 }
 
 template <int EPL>
@@ -255,77 +330,113 @@ __global__ void __launch_bounds__(RW * WAVE) topk_kernel(const uint16_t* __restr
                                                          int E, int topk, int renorm) {
   const int r = blockIdx.x * RW + threadIdx.x / WAVE;
   if (r >= M) return;
-  topk_row<EPL>(logits + (size_t)r * ldl, E, topk, renorm != 0, weights + (size_t)r * topk, ids + (size_t)r * topk,
-                nullptr, threadIdx.x % WAVE);
+  uint16_t h[EPL];
+  load_row<EPL>(logits + (size_t)r * ldl, E, threadIdx.x % WAVE, h);
+  topk_core<EPL>(h, E, topk, renorm != 0, weights + (size_t)r * topk, ids + (size_t)r * topk, nullptr,
+                 threadIdx.x % WAVE);
 }
 
-// Tables from ids in global memory, one workgroup (any numel; the multi-block path is faster above SMALL_MAX).
+// Tables from ids in global memory, one workgroup, numel <= SMALL_MAX.
 __global__ void __launch_bounds__(AT) align_single_kernel(const int* __restrict__ ids, int numel, int E, int blk,
                                                           int* __restrict__ sorted_ids, int* __restrict__ expert_ids,
                                                           int* __restrict__ ntpp) {
-  __shared__ AlignLds sh;
-  align_one_block(sh, numel, E, blk, sorted_ids, expert_ids, ntpp, [&](int t) { return ids[t]; });
-}
-
-// Multi-block align, pass 1: per-chunk histogram into scratch; the last chunk to arrive turns the histograms into
-// per-(chunk, expert) scatter bases and writes the layout. scratch = [arrive][nchunks x E]; arrive is zero at entry
-// and left zero.
-__global__ void __launch_bounds__(AT) align_count_kernel(const int* __restrict__ ids, int numel, int E, int blk,
-                                                         int* __restrict__ sorted_ids, int* __restrict__ expert_ids,
-                                                         int* __restrict__ ntpp, int* __restrict__ scratch) {
-  __shared__ AlignLds sh;
-  __shared__ int s_last;
-  const int tid = threadIdx.x, c = blockIdx.x, nch = gridDim.x;
-  int* const arrive = scratch;
-  int* const hist = scratch + 1;
-  for (int e = tid; e < E; e += AT) sh.cnt[e] = 0;
-  __syncthreads();
-  const int t0 = c * CH, t1 = min(numel, t0 + CH);
-  for (int t = t0 + tid; t < t1; t += AT) {
+  __shared__ TabLds<AT> sh;
+  __shared__ short lids[SMALL_MAX];
+  zero_counts(sh, E);
+  for (int t = threadIdx.x; t < numel; t += AT) {
     const int e = ids[t];
-    if (e >= 0 && e < E) atomicAdd(&sh.cnt[e], 1);
+    lids[t] = (short)(e >= 0 && e < E ? e : -1);
   }
-  __syncthreads();
-  for (int e = tid; e < E; e += AT) hist[(size_t)c * E + e] = sh.cnt[e];
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) s_last = (atomicAdd(arrive, 1) == nch - 1) ? 1 : 0;
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
-  // last block: totals, padded scan, per-chunk bases (in place), layout
-  int tot = 0;
-  if (tid < E)
-    for (int cc = 0; cc < nch; cc++)
-      tot += __hip_atomic_load(hist + (size_t)cc * E + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  if (tid < E) sh.cnt[tid] = tot;
-  __syncthreads();
-  const int total = padded_scan(sh, E, blk);
-  write_layout(sh.cnt, sh.offs, total, numel, E, blk, sorted_ids, expert_ids, ntpp);
-  if (tid < E) {
-    int run = sh.offs[tid];
-    for (int cc = 0; cc < nch; cc++) {
-      int* h = hist + (size_t)cc * E + tid;
-      const int v = __hip_atomic_load(h, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      *h = run;
-      run += v;
-    }
-  }
-  if (tid == 0) *arrive = 0;
+  lds_barrier();
+  build_tables(sh, lids, numel, E, blk, sorted_ids, expert_ids, ntpp);
 }
 
-// Multi-block align, pass 2: stable scatter of one chunk from its bases.
-__global__ void __launch_bounds__(AT) align_scatter_kernel(const int* __restrict__ ids, int numel, int E,
-                                                           int* __restrict__ sorted_ids,
-                                                           const int* __restrict__ scratch) {
-  __shared__ AlignLds sh;
+// Tables from ids in global memory for any numel in one workgroup without scratch (the reference route entry's
+// large-M path): count every id, scan, layout, then place chunk by chunk with each expert's cursor in a register.
+__global__ void __launch_bounds__(AT) align_big_single_kernel(const int* __restrict__ ids, int numel, int E, int blk,
+                                                              int* __restrict__ sorted_ids,
+                                                              int* __restrict__ expert_ids, int* __restrict__ ntpp) {
+  __shared__ TabLds<AT> sh;
+  __shared__ short lids[SMALL_MAX];
+  const int tid = threadIdx.x;
+  zero_counts(sh, E);
+  lds_barrier();
+  for (int t0 = 0; t0 < numel; t0 += 4 * AT) {
+    int v[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) v[u] = t0 + tid + u * AT < numel ? ids[t0 + tid + u * AT] : -1;
+#pragma unroll
+    for (int u = 0; u < 4; u++)
+      if (v[u] >= 0 && v[u] < E) atomicAdd(&sh.cnt[v[u]], 1);
+  }
+  lds_barrier();
+  const int total = padded_scan(sh, E, blk);
+  if (tid == 0) ntpp[0] = total;
+  write_layout(sh, E, blk, numel, total, 0, 0, 1, sorted_ids, expert_ids);
+  for (int c0 = 0; c0 < numel; c0 += SMALL_MAX) {
+    const int n = min(SMALL_MAX, numel - c0);
+    for (int t = tid; t < n; t += AT) {
+      const int e = ids[c0 + t];
+      lids[t] = (short)(e >= 0 && e < E ? e : -1);
+    }
+    lds_barrier();
+    for (int base = 0; base < n; base += AT) stable_round(sh, lids, base, n, c0, E, sorted_ids);
+  }
+}
+
+// Multi-block align, pass 1: per-chunk histogram of CH routed rows into hist[c * E + e] (every entry written).
+__global__ void __launch_bounds__(AT) align_count_kernel(const int* __restrict__ ids, int numel, int E,
+                                                         int* __restrict__ hist) {
+  __shared__ int cnt[MAX_E];
   const int tid = threadIdx.x, c = blockIdx.x;
-  const int* base = scratch + 1 + (size_t)c * E;
-  for (int e = tid; e < E; e += AT) sh.cnt[e] = base[e];
-  zero_wcnt(sh);
-  __syncthreads();
+  for (int e = tid; e < E; e += AT) cnt[e] = 0;
   const int t0 = c * CH, t1 = min(numel, t0 + CH);
-  for (int b = t0; b < t1; b += AT) stable_subchunk(sh, b, t1, E, sorted_ids, [&](int t) { return ids[t]; });
+  int v[CH / AT];
+#pragma unroll
+  for (int u = 0; u < CH / AT; u++) v[u] = t0 + tid + u * AT < t1 ? ids[t0 + tid + u * AT] : -1;
+  lds_barrier();
+#pragma unroll
+  for (int u = 0; u < CH / AT; u++)
+    if (v[u] >= 0 && v[u] < E) atomicAdd(&cnt[v[u]], 1);
+  lds_barrier();
+  for (int e = tid; e < E; e += AT) hist[(size_t)c * E + e] = cnt[e];
+}
+
+// Multi-block align, pass 2 (one workgroup per chunk): totals and this chunk's per-expert base from the histograms
+// (the previous launch's writes are visible), the padded scan, this chunk's share of the layout writes (expert
+// blocks of experts e = c, c + nch, ...; the capacity tail split by chunk), then the stable placement of its rows.
+__global__ void __launch_bounds__(AT) align_scatter_kernel(const int* __restrict__ ids, int numel, int E, int blk,
+                                                           int* __restrict__ sorted_ids, int* __restrict__ expert_ids,
+                                                           int* __restrict__ ntpp, const int* __restrict__ hist) {
+  __shared__ TabLds<AT> sh;
+  __shared__ short lids[CH];
+  const int tid = threadIdx.x, c = blockIdx.x, nch = gridDim.x;
+  const int t0 = c * CH, t1 = min(numel, t0 + CH), n = t1 - t0;
+  zero_counts(sh, E);
+  for (int t = tid; t < n; t += AT) {
+    const int e = ids[t0 + t];
+    lids[t] = (short)(e >= 0 && e < E ? e : -1);
+  }
+  int pre = 0;
+  if (tid < E) {
+    int tot = 0;
+    for (int c0 = 0; c0 < nch; c0 += 8) {                      // 8 independent loads in flight per thread
+      int v[8];
+#pragma unroll
+      for (int u = 0; u < 8; u++) v[u] = c0 + u < nch ? hist[(size_t)(c0 + u) * E + tid] : 0;
+#pragma unroll
+      for (int u = 0; u < 8; u++) {
+        tot += v[u];
+        pre += c0 + u < c ? v[u] : 0;
+      }
+    }
+    sh.cnt[tid] = tot;
+  }
+  lds_barrier();
+  const int total = padded_scan(sh, E, blk);
+  if (c == 0 && tid == 0) ntpp[0] = total;
+  write_layout(sh, E, blk, numel, total, pre, c, nch, sorted_ids, expert_ids);
+  for (int base = 0; base < n; base += AT) stable_round(sh, lids, base, n, t0, E, sorted_ids);
 }
 
 int epl_for(int E) {
@@ -352,6 +463,23 @@ int launch_topk(const uint16_t* logits, int ldl, float* w, int* ids, int M, int 
   return 0;
 }
 
+// Tables for numel routed rows from ids in global memory (any numel): one workgroup up to SMALL_MAX, else the
+// histogram + placement launches over CH-row chunks (hist: (numel / CH rounded up) * E int32).
+int launch_align(const int* ids, int numel, int E, int blk, int* sorted_ids, int* expert_ids, int* ntpp, int* hist,
+                 hipStream_t st) {
+  if (numel <= SMALL_MAX) {
+    hipLaunchKernelGGL(align_single_kernel, dim3(1), dim3(AT), 0, st, ids, numel, E, blk, sorted_ids, expert_ids,
+                       ntpp);
+    return 0;
+  }
+  if (!hist) return 1;
+  const int nch = (numel + CH - 1) / CH;
+  hipLaunchKernelGGL(align_count_kernel, dim3(nch), dim3(AT), 0, st, ids, numel, E, hist);
+  hipLaunchKernelGGL(align_scatter_kernel, dim3(nch), dim3(AT), 0, st, ids, numel, E, blk, sorted_ids, expert_ids,
+                     ntpp, (const int*)hist);
+  return 0;
+}
+
 bool route_args_ok(int M, int E, int topk, int blk) {
   return M >= 1 && E >= 1 && E <= MAX_E && topk >= 1 && topk <= MAX_K && topk <= E && blk >= 1 &&
          (blk & (blk - 1)) == 0;
@@ -360,20 +488,22 @@ bool route_args_ok(int M, int E, int topk, int blk) {
 }  // namespace
 
 // Reference: kernels/r9k_moe_route.hip:217-233. logits [M, E] bf16 (row stride ldl) -> weights fp32 [M, topk],
-// ids int32 [M, topk], and the align tables (first capacity(M * topk) entries). scratch (2E+1 int32) is part of the
-// reference contract; this implementation keeps its state in LDS and never touches it. Returns 0, 1 for an
-// unsupported shape, else the HIP error code.
+// ids int32 [M, topk], and the align tables (first capacity(M * topk) entries). scratch (2E+1 int32, zeroed once by
+// the caller, as in the reference contract): its first int is the workgroups' arrival counter, left zero; calls
+// that share one scratch must not overlap. numel > 4096 takes the top-k launch plus the single-workgroup table
+// launch. Returns 0, 1 for an unsupported shape, else the HIP error code.
 extern "C" int r9k_moe_route(long logits, int ldl, long weights, long ids, long sorted_ids, long expert_ids,
                              long ntpp, long scratch, int M, int E, int topk, int renorm, int blk, long stream) {
-  (void)scratch;
   if (!route_args_ok(M, E, topk, blk) || ldl < E) return 1;
   const hipStream_t st = (hipStream_t)stream;
   const long numel = (long)M * topk;
   if (numel <= SMALL_MAX) {
-#define RF(EPLV)                                                                                                    \
-  hipLaunchKernelGGL(route_fused_kernel<EPLV>, dim3(1), dim3(AT), 0, st, (const uint16_t*)logits, ldl,             \
-                     (float*)weights, (int*)ids, (int*)sorted_ids, (int*)expert_ids, (int*)ntpp, M, E, topk, renorm, \
-                     blk)
+    const int nblk = (M + FW - 1) / FW;
+    if (nblk > 1 && !scratch) return 1;
+#define RF(EPLV)                                                                                                  \
+  hipLaunchKernelGGL(route_fused_kernel<EPLV>, dim3(nblk), dim3(FT), 0, st, (const uint16_t*)logits, ldl,        \
+                     (float*)weights, (int*)ids, (int*)sorted_ids, (int*)expert_ids, (int*)ntpp, (int*)scratch, M, E, \
+                     topk, renorm, blk)
     switch (epl_for(E)) {
       case 2: RF(2); break;
       case 4: RF(4); break;
@@ -387,7 +517,7 @@ extern "C" int r9k_moe_route(long logits, int ldl, long weights, long ids, long 
   } else {
     if (numel > 0x7fffffffL) return 1;
     if (launch_topk((const uint16_t*)logits, ldl, (float*)weights, (int*)ids, M, E, topk, renorm, st)) return 1;
-    hipLaunchKernelGGL(align_single_kernel, dim3(1), dim3(AT), 0, st, (const int*)ids, (int)numel, E, blk,
+    hipLaunchKernelGGL(align_big_single_kernel, dim3(1), dim3(AT), 0, st, (const int*)ids, (int)numel, E, blk,
                        (int*)sorted_ids, (int*)expert_ids, (int*)ntpp);
   }
   return (int)hipGetLastError();
@@ -406,29 +536,21 @@ extern "C" int r9k_moe_topk(long logits, int ldl, long weights, long ids, int M,
   return (int)hipGetLastError();
 }
 
-// int32 count of the scratch r9k_moe_align needs for `numel` routed rows over E experts (zero it once; the kernels
-// leave it zero).
+// int32 count of the scratch r9k_moe_align needs for `numel` routed rows over E experts (per-chunk histograms,
+// rewritten by every call; no initial contents needed).
 extern "C" long r9k_moe_align_scratch_ints(int numel, int E) {
   if (numel <= SMALL_MAX) return 1;
-  return 1 + (long)((numel + CH - 1) / CH) * E;
+  return (long)((numel + CH - 1) / CH) * E;
 }
 
 // Tables only, from ids int32 [numel] (the stock moe_align_block_size role; ids outside [0, E) are skipped).
-// scratch: r9k_moe_align_scratch_ints(numel, E) int32, zero at the first call. 0 / 1 bad args / HIP error.
+// scratch: r9k_moe_align_scratch_ints(numel, E) int32 (histograms, any contents). 0 / 1 bad args / HIP error.
 extern "C" int r9k_moe_align(long ids, int numel, int E, int blk, long sorted_ids, long expert_ids, long ntpp,
                              long scratch, long scratch_ints, long stream) {
   if (numel < 1 || E < 1 || E > MAX_E || blk < 1 || (blk & (blk - 1))) return 1;
-  const hipStream_t st = (hipStream_t)stream;
-  if (numel <= SMALL_MAX) {
-    hipLaunchKernelGGL(align_single_kernel, dim3(1), dim3(AT), 0, st, (const int*)ids, numel, E, blk,
-                       (int*)sorted_ids, (int*)expert_ids, (int*)ntpp);
-  } else {
-    if (!scratch || scratch_ints < r9k_moe_align_scratch_ints(numel, E)) return 1;
-    const int nch = (numel + CH - 1) / CH;
-    hipLaunchKernelGGL(align_count_kernel, dim3(nch), dim3(AT), 0, st, (const int*)ids, numel, E, blk,
-                       (int*)sorted_ids, (int*)expert_ids, (int*)ntpp, (int*)scratch);
-    hipLaunchKernelGGL(align_scatter_kernel, dim3(nch), dim3(AT), 0, st, (const int*)ids, numel, E,
-                       (int*)sorted_ids, (const int*)scratch);
-  }
+  if (numel > SMALL_MAX && (!scratch || scratch_ints < r9k_moe_align_scratch_ints(numel, E))) return 1;
+  if (launch_align((const int*)ids, numel, E, blk, (int*)sorted_ids, (int*)expert_ids, (int*)ntpp, (int*)scratch,
+                   (hipStream_t)stream))
+    return 1;
   return (int)hipGetLastError();
 }

@@ -10,9 +10,10 @@
 // The fp32 -> e4m3 encode is the explicit RNE bit routine in r9k_common.h, so the bytes are the bytes torch's
 // float8_e4m3fn cast produces for the same fp32 products.
 //
-// One workgroup of QT threads per row. The vectorised path keeps the row in registers (one HBM read): each
-// thread owns up to QR chunks of 8 bf16 (16 bytes). Rows that do not fit (K > QT * 8 * QR) or are not
-// 16-byte aligned take the two-pass scalar kernel. Rows are independent, so M up to the grid limit is fine.
+// Rows up to 4096 elements run one wave per row (four rows a workgroup): each lane keeps R chunks of 8 bf16
+// (16 bytes) in registers (one HBM read) and the row maximum is a wave reduction, no LDS or barrier. Longer rows
+// take one workgroup of QT threads per row (QR chunks a thread), and rows that do not fit or are not 16-byte
+// aligned take the two-pass scalar kernel. Rows are independent, so M up to the grid limit is fine.
 #include "r9k_common.h"
 
 namespace {
@@ -27,6 +28,62 @@ __device__ __forceinline__ float hi16(uint32_t w) { return __uint_as_float(w & 0
 
 __device__ __forceinline__ uint32_t pack4_e4m3(float a, float b, float c, float d) {
   return f32_to_e4m3(a) | (f32_to_e4m3(b) << 8) | (f32_to_e4m3(c) << 16) | (f32_to_e4m3(d) << 24);
+}
+
+constexpr int WR = 4;       // rows (waves) per workgroup of the wave-per-row kernels
+
+// One wave per row, R 16-byte chunks per lane (K <= 512 * R).
+template <bool GATE, int R>
+__global__ void __launch_bounds__(WR * WAVE) quant_rows_wave_kernel(const uint16_t* __restrict__ x,
+                                                                    uint8_t* __restrict__ q, float* __restrict__ s,
+                                                                    int M, int K, long ld,
+                                                                    const uint16_t* __restrict__ wg,
+                                                                    float* __restrict__ g) {
+  const int row = blockIdx.x * WR + threadIdx.x / WAVE, lane = threadIdx.x % WAVE, nvec = K / 8;
+  if (row >= M) return;
+  const uint4* xr = reinterpret_cast<const uint4*>(x + (size_t)row * ld);
+  uint4 v[R];
+  float m = 0.f, dot = 0.f;
+#pragma unroll
+  for (int i = 0; i < R; i++) {
+    const int c = lane + i * WAVE;
+    v[i] = c < nvec ? xr[c] : make_uint4(0u, 0u, 0u, 0u);
+  }
+#pragma unroll
+  for (int i = 0; i < R; i++) {
+    const uint32_t w[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+#pragma unroll
+    for (int j = 0; j < 4; j++) m = fmaxf(m, fmaxf(fabsf(lo16(w[j])), fabsf(hi16(w[j]))));
+    if constexpr (GATE) {
+      const int c = lane + i * WAVE;
+      if (c < nvec) {
+        const uint4 gw = reinterpret_cast<const uint4*>(wg)[c];
+        const uint32_t u[4] = {gw.x, gw.y, gw.z, gw.w};
+#pragma unroll
+        for (int j = 0; j < 4; j++) dot += lo16(w[j]) * lo16(u[j]) + hi16(w[j]) * hi16(u[j]);
+      }
+    }
+  }
+  const float amax = fmaxf(wave_max(m), 1e-12f);
+  if constexpr (GATE) {
+    dot = wave_sum(dot);
+    if (lane == 0) {
+      const float logit = bf2f(f2bf(dot));                     // the router-style bf16 GEMM output
+      g[row] = bf2f(f2bf(1.f / (1.f + expf(-logit))));           // bf16 sigmoid
+    }
+  }
+  const float inv = 448.f / amax;
+  if (lane == 0) s[row] = amax / 448.f;
+  uint2* qr = reinterpret_cast<uint2*>(q + (size_t)row * K);
+#pragma unroll
+  for (int i = 0; i < R; i++) {
+    const int c = lane + i * WAVE;
+    if (c < nvec) {
+      const uint32_t lo = pack4_e4m3(lo16(v[i].x) * inv, hi16(v[i].x) * inv, lo16(v[i].y) * inv, hi16(v[i].y) * inv);
+      const uint32_t hi = pack4_e4m3(lo16(v[i].z) * inv, hi16(v[i].z) * inv, lo16(v[i].w) * inv, hi16(v[i].w) * inv);
+      qr[c] = make_uint2(lo, hi);
+    }
+  }
 }
 
 template <bool GATE>
@@ -120,6 +177,50 @@ __global__ void __launch_bounds__(QT) quant_rows_scalar_kernel(const uint16_t* _
 // silu(g) * u with g, u the stored bf16 values, evaluated as (g / (1 + exp(-g))) * u in fp32.
 __device__ __forceinline__ float silu_mul(float gv, float uv) { return gv / (1.f + expf(-gv)) * uv; }
 
+// One wave per row, R 16-byte chunks of gate and of up per lane (I <= 512 * R), activations kept in registers.
+template <int R>
+__global__ void __launch_bounds__(WR * WAVE) silu_mul_quant_wave_kernel(const uint16_t* __restrict__ gu,
+                                                                        uint8_t* __restrict__ q,
+                                                                        float* __restrict__ s, int M, int I) {
+  const int row = blockIdx.x * WR + threadIdx.x / WAVE, lane = threadIdx.x % WAVE, nvec = I / 8;
+  if (row >= M) return;
+  const uint4* gr = reinterpret_cast<const uint4*>(gu + (size_t)row * 2 * I);
+  const uint4* ur = reinterpret_cast<const uint4*>(gu + (size_t)row * 2 * I + I);
+  uint4 gv[R], uv[R];
+#pragma unroll
+  for (int i = 0; i < R; i++) {
+    const int c = lane + i * WAVE;
+    gv[i] = c < nvec ? gr[c] : make_uint4(0u, 0u, 0u, 0u);
+    uv[i] = c < nvec ? ur[c] : make_uint4(0u, 0u, 0u, 0u);
+  }
+  float a[R][8];
+  float m = 0.f;
+#pragma unroll
+  for (int i = 0; i < R; i++) {
+    const uint32_t gw[4] = {gv[i].x, gv[i].y, gv[i].z, gv[i].w}, uw[4] = {uv[i].x, uv[i].y, uv[i].z, uv[i].w};
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      a[i][2 * j] = silu_mul(lo16(gw[j]), lo16(uw[j]));
+      a[i][2 * j + 1] = silu_mul(hi16(gw[j]), hi16(uw[j]));
+    }
+#pragma unroll
+    for (int j = 0; j < 8; j++) m = fmaxf(m, fabsf(a[i][j]));      // zero padding lanes give silu(0) * 0 = 0
+  }
+  const float amax = fmaxf(wave_max(m), 1e-12f);
+  const float inv = 448.f / amax;
+  if (lane == 0) s[row] = amax / 448.f;
+  uint2* qr = reinterpret_cast<uint2*>(q + (size_t)row * I);
+#pragma unroll
+  for (int i = 0; i < R; i++) {
+    const int c = lane + i * WAVE;
+    if (c < nvec) {
+      const uint32_t lo = pack4_e4m3(a[i][0] * inv, a[i][1] * inv, a[i][2] * inv, a[i][3] * inv);
+      const uint32_t hi = pack4_e4m3(a[i][4] * inv, a[i][5] * inv, a[i][6] * inv, a[i][7] * inv);
+      qr[c] = make_uint2(lo, hi);
+    }
+  }
+}
+
 // One row per workgroup; each thread keeps its activations (I <= QT * 8 * QR) in registers between the max pass
 // and the store pass. Larger I recomputes the activation in the store pass.
 __global__ void __launch_bounds__(QT) silu_mul_quant_kernel(const uint16_t* __restrict__ gu, uint8_t* __restrict__ q,
@@ -176,6 +277,27 @@ bool vec_ok(long x, long q, int K, long ld) {
   return K % 8 == 0 && ld % 8 == 0 && (x & 15) == 0 && (q & 7) == 0 && K <= QT * 8 * QR;
 }
 
+// 16-byte chunks per lane of the wave-per-row kernels for a row of n elements (0: row too long).
+int wave_chunks(int n) {
+  const int c = (n / 8 + WAVE - 1) / WAVE;
+  return c <= 1 ? 1 : c <= 2 ? 2 : c <= 4 ? 4 : c <= 8 ? 8 : 0;
+}
+
+template <bool GATE>
+bool launch_wave(long x, long q, long s, long wg, long g, int M, int K, int ld, hipStream_t st) {
+  const dim3 grid((M + WR - 1) / WR), blk(WR * WAVE);
+  switch (wave_chunks(K)) {
+#define QW(RV)                                                                                                  \
+  case RV:                                                                                                      \
+    hipLaunchKernelGGL((quant_rows_wave_kernel<GATE, RV>), grid, blk, 0, st, (const uint16_t*)x, (uint8_t*)q,   \
+                       (float*)s, M, K, (long)ld, (const uint16_t*)wg, (float*)g);                             \
+    return true;
+    QW(1) QW(2) QW(4) QW(8)
+#undef QW
+    default: return false;
+  }
+}
+
 }  // namespace
 
 // Reference: kernels/r9k_moe_mxfp4a8.hip:1745-1757 (r9k_quant_rows_fp8). 0 on success, -3 bad shape, -6 launch error.
@@ -183,7 +305,8 @@ extern "C" int r9k_quant_rows_fp8(long x, long q, long s, int M, int K, int ld, 
   if (M <= 0) return 0;
   if (K <= 0 || ld < K || !x || !q || !s) return -3;
   const hipStream_t st = (hipStream_t)stream;
-  if (vec_ok(x, q, K, ld))
+  if (vec_ok(x, q, K, ld) && launch_wave<false>(x, q, s, 0, 0, M, K, ld, st)) {
+  } else if (vec_ok(x, q, K, ld))
     hipLaunchKernelGGL(quant_rows_vec_kernel<false>, dim3(M), dim3(QT), 0, st, (const uint16_t*)x, (uint8_t*)q,
                        (float*)s, K, (long)ld, (const uint16_t*)nullptr, (float*)nullptr);
   else
@@ -199,7 +322,8 @@ extern "C" int r9k_quant_rows_fp8_gate(long x, long q, long s, long wg, long g, 
   if (M <= 0) return 0;
   if (tiled || K <= 0 || ld < K || !x || !q || !s || !wg || !g) return -3;
   const hipStream_t st = (hipStream_t)stream;
-  if (vec_ok(x, q, K, ld) && (wg & 15) == 0)
+  if (vec_ok(x, q, K, ld) && (wg & 15) == 0 && launch_wave<true>(x, q, s, wg, g, M, K, ld, st)) {
+  } else if (vec_ok(x, q, K, ld) && (wg & 15) == 0)
     hipLaunchKernelGGL(quant_rows_vec_kernel<true>, dim3(M), dim3(QT), 0, st, (const uint16_t*)x, (uint8_t*)q,
                        (float*)s, K, (long)ld, (const uint16_t*)wg, (float*)g);
   else
@@ -213,7 +337,17 @@ extern "C" int r9k_silu_mul_quant_fp8(long gu, long q, long s, int M, int I, lon
   if (M <= 0) return 0;
   if (I <= 0 || !gu || !q || !s) return -3;
   const int vec = (gu & 15) == 0 && (q & 7) == 0 && I % 8 == 0 && I <= QT * 8 * QR;
-  hipLaunchKernelGGL(silu_mul_quant_kernel, dim3(M), dim3(QT), 0, (hipStream_t)stream, (const uint16_t*)gu,
+  const int R = vec ? wave_chunks(I) : 0;
+  const dim3 wgrid((M + WR - 1) / WR), wblk(WR * WAVE);
+  const hipStream_t st = (hipStream_t)stream;
+#define SW(RV) hipLaunchKernelGGL(silu_mul_quant_wave_kernel<RV>, wgrid, wblk, 0, st, (const uint16_t*)gu, (uint8_t*)q, \
+                                  (float*)s, M, I)
+  if (R == 1) SW(1);
+  else if (R == 2) SW(2);
+  else if (R == 4) SW(4);
+  else if (R == 8) SW(8);
+#undef SW
+  else hipLaunchKernelGGL(silu_mul_quant_kernel, dim3(M), dim3(QT), 0, (hipStream_t)stream, (const uint16_t*)gu,
                      (uint8_t*)q, (float*)s, I, vec);
   return hipGetLastError() == hipSuccess ? 0 : -6;
 }

@@ -473,7 +473,7 @@ def _align_scratch(device: torch.device, n: int) -> torch.Tensor:
     key = (device.type, device.index)
     t = _ALIGN_SCRATCH.get(key)
     if t is None or t.numel() < n:
-        t = torch.zeros(max(n, 1 << 16), dtype=torch.int32, device=device)   # zero once; the kernels leave it zero
+        t = torch.empty(max(n, 1 << 16), dtype=torch.int32, device=device)   # per-chunk histograms, rewritten per call
         _ALIGN_SCRATCH[key] = t
     return t
 

@@ -56,8 +56,9 @@ def capacity(numel: int, num_experts: int, blk: int) -> int:
 
 
 def scratch_ints(E: int) -> int:
-    """int32 count of the routing scratch of the reference contract (counts[E], cursor[E], arrive). The gfx950
-    kernel keeps that state in LDS and never touches it; the size is kept so callers allocate as before."""
+    """int32 count of the routing scratch of the reference contract (counts[E], cursor[E], arrive), zeroed once by
+    the caller. The gfx950 kernel keeps counts and cursors in LDS and uses only the first int, the workgroups'
+    arrival counter, which it leaves zero; the size is kept so callers allocate as before."""
     return 2 * E + 1
 
 
