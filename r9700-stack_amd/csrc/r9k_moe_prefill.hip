@@ -21,6 +21,8 @@
 // (the column blocks of one routing block share an L2) and dead blocks past ntpp never occupy an XCD.
 #include "r9k_common.h"
 
+#include <cstdlib>
+
 namespace {
 
 using namespace r9k;
@@ -28,6 +30,12 @@ using namespace r9k;
 typedef int v8i __attribute__((ext_vector_type(8)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// Two fp32 values to packed bf16, round to nearest even (v_cvt_pk_bf16_f32), a in the low half.
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  return __builtin_bit_cast(uint32_t, (bf16x2){(__bf16)a, (__bf16)b});
+}
 
 constexpr int BM = 256, BN = 256, KC = 128;   // rows, columns, K per chunk
 constexpr int NTH = 512;                       // 8 waves
@@ -51,6 +59,46 @@ __device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
 __device__ __forceinline__ void dma4(const void* g, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(lds) : "memory", "m0");
 }
+// The same from a wave-uniform base (SGPR pair) plus a 32-bit per-lane byte offset.
+__device__ __forceinline__ void dma16s(const void* base, uint32_t off, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(lds) : "memory", "m0");
+}
+__device__ __forceinline__ void dma4s(const void* base, uint32_t off, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1" ::"v"(off), "s"(base), "s"(lds) : "memory", "m0");
+}
+// A wave-uniform copy of a pointer computed from per-lane-equal values (kept in SGPRs).
+__device__ __forceinline__ const uint8_t* uniform_ptr(const void* p) {
+  const uint64_t v = (uint64_t)(uintptr_t)p;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v), hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return reinterpret_cast<const uint8_t*>(((uint64_t)hi << 32) | lo);
+}
+// n / d for 32-bit unsigned n by a divisor fixed per launch, as a multiply-high and shifts (Granlund & Montgomery,
+// "Division by invariant integers using multiplication", 1994, fig. 4.1): with l = ceil(log2 d) and
+// m = floor(2^32 (2^l - d) / d) + 1, n / d = (t + ((n - t) >> 1)) >> (l - 1), t = mulhi(n, m); l = 0 means d = 1.
+struct DivMagic {
+  uint32_t m;
+  int l;
+};
+
+DivMagic div_magic(uint32_t d) {
+  int l = 0;
+  while ((1ull << l) < d) l++;
+  const uint64_t m = ((1ull << 32) * ((1ull << l) - d)) / d + 1;
+  return {(uint32_t)m, l};
+}
+
+__device__ __forceinline__ uint32_t div_by(uint32_t n, DivMagic dm) {
+  if (dm.l == 0) return n;
+  const uint32_t t = __umulhi(n, dm.m);
+  return (t + ((n - t) >> 1)) >> (dm.l - 1);
+}
+
+// 1 when the environment variable is set to "0" (a switch turned off).
+int getenv_flag_off_pf(const char* name) {
+  const char* v = getenv(name);
+  return v && v[0] == '0' ? 1 : 0;
+}
+
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)p);
 }
@@ -222,9 +270,276 @@ __global__ void __launch_bounds__(NTH) moe_prefill_kernel(
   }
 }
 
+
+// ------------------------------------------------------------------------------------------ persistent variant
+// LDS beyond the chunk stages: per-tile metadata that arrives by DMA ahead of the tile's first chunk.
+struct __align__(16) Aux {
+  int rows[4][BM];     // tile sorted_ids, a ring of 4 tiles
+  int eid[4][WAVE];    // tile expert id (64 copies), same ring
+  float as[2][BM];     // As[row / a_row_div] of each tile row, two tiles
+  float tw[2][BM];     // topk_w[row] of each tile row, two tiles
+  int dummy[WAVE];     // target of the loads that keep every group at 9 loads a wave
+};
+constexpr size_t SMEM_P = sizeof(Stage) * NSTAGE + sizeof(Aux);
+static_assert(SMEM_P <= 160 * 1024, "LDS");
+
+// LDS fragment offsets of one wave within a stage. The B fragment of column tile j and K-half ks sits at
+// b + j * 2048 + ks * 512 (its exponent byte at s + j * 128 + ks * 32); the A fragment of M tile i at
+// a[half][ks] + i * 4096, the swizzle depending only on lane % 32.
+struct FragOff {
+  int b, s;
+  int a[2][2];
+};
+
+__device__ __forceinline__ FragOff frag_offsets(int wm, int wn, int lane) {
+  const int g = lane >> 5, c32 = lane & 31;
+  FragOff f;
+  const int t16 = wn * 8 + (c32 >> 4), l16 = g * 16 + (c32 & 15);
+  f.b = t16 * 1024 + l16 * 16;
+  f.s = t16 * 64 + l16;
+  const int row = wm * 64 + c32, sw = (row & 7) ^ ((row >> 3) & 1);
+#pragma unroll
+  for (int ks = 0; ks < 2; ks++) {
+    f.a[0][ks] = (row * 8 + ((4 * ks + g) ^ sw)) * 16;
+    f.a[1][ks] = (row * 8 + ((4 * ks + 2 + g) ^ sw)) * 16;
+  }
+  return f;
+}
+
+// One wave's fragments for one 64-K half of a chunk: 4 weight fragments (fp4) with their exponent bytes, 2
+// activation fragments (fp8, low and high K quarters).
+struct KFrag {
+  u32x4 w[4];
+  int sb[4];
+  u32x4 lo[2], hi[2];
+};
+
+__device__ __forceinline__ void load_kfrag(const Stage& S, const FragOff& f, int ks, KFrag& F) {
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    F.w[j] = *reinterpret_cast<const u32x4*>(&S.b[f.b + j * 2048 + ks * 512]);
+    F.sb[j] = S.s[f.s + j * 128 + ks * 32];
+  }
+#pragma unroll
+  for (int i = 0; i < 2; i++) {
+    F.lo[i] = *reinterpret_cast<const u32x4*>(&S.a[f.a[0][ks] + i * 4096]);
+    F.hi[i] = *reinterpret_cast<const u32x4*>(&S.a[f.a[1][ks] + i * 4096]);
+  }
+}
+
+__device__ __forceinline__ void mfma_kfrag(v16f (&acc)[2][4], const KFrag& F) {
+#pragma unroll
+  for (int i = 0; i < 2; i++) {
+    const v8i af = (v8i){(int)F.lo[i].x, (int)F.lo[i].y, (int)F.lo[i].z, (int)F.lo[i].w,
+                         (int)F.hi[i].x, (int)F.hi[i].y, (int)F.hi[i].z, (int)F.hi[i].w};
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const v8i wf = (v8i){(int)F.w[j].x, (int)F.w[j].y, (int)F.w[j].z, (int)F.w[j].w, 0, 0, 0, 0};
+      acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(wf, af, acc[i][j], 4, 0, 0, F.sb[j], 0, E8M0_ONE);
+    }
+  }
+}
+
+// The same tiles and numerics as moe_prefill_kernel, but each workgroup (one per CU) walks a list of tiles and the
+// K-chunk stream runs on across tile boundaries, with DMA three chunks ahead of the MFMAs. Within a chunk the two
+// 64-K halves are software-pipelined: the second half's fragments are read from LDS under the first half's MFMAs,
+// and the wait + barrier that publish the next chunk sit between the halves, so the next chunk's first fragments
+// load under the current chunk's second-half MFMAs. Group j (chunk j + 3 plus 2 metadata dwords) is issued after
+// barrier j, into the stage chunk j was read from. A tile's sorted_ids and expert id arrive 6 chunks before its
+// first chunk, its per-row scales (As, topk_w) with its first chunk's DMA; its output is stored after its last
+// chunk. Every wave issues exactly 9 loads a group (7 chunk pieces and 2 metadata or dummy dwords), so the waits
+// are fixed counts: at barrier i chunk i + 1's loads are complete once at most 2 + 9 younger loads are outstanding.
+// Needs K / 128 >= 3 (a metadata slot -- 4 tiles of sorted_ids, 2 of scales -- is refilled at least one barrier
+// after its tile's last reader).
+__global__ void __launch_bounds__(NTH) moe_prefill_persistent_kernel(
+    const uint8_t* __restrict__ A, const float* __restrict__ As, const uint8_t* __restrict__ Wq,
+    const uint8_t* __restrict__ Ws, uint16_t* __restrict__ C, const int* __restrict__ sorted_ids,
+    const int* __restrict__ expert_ids, const int* __restrict__ ntpp, const float* __restrict__ topk_w,
+    long wq_estride, long ws_estride, int numel, DivMagic rdiv, int K, int N, int nnb) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  Stage* st = reinterpret_cast<Stage*>(smem);
+  Aux& ax = *reinterpret_cast<Aux*>(smem + NSTAGE * sizeof(Stage));
+
+  // tiles: XCD x (dispatch goes round-robin over the XCDs) owns a contiguous range of the live tiles (the column
+  // blocks of a routing block, and the blocks of an expert, share its L2); its workgroups take every S-th tile
+  const int G = gridDim.x, w = blockIdx.x, x = w % NXCD, jj = w / NXCD;
+  const int S = (G - x + NXCD - 1) / NXCD;
+  const int total = (ntpp[0] / BM) * nnb;
+  const int q = total / NXCD, rem = total % NXCD;
+  const int start = x * q + min(x, rem), cnt = q + (x < rem ? 1 : 0);
+  if (jj >= cnt) return;
+  const int ntiles = (cnt - jj + S - 1) / S;
+  const int nchunk = K / KC, iters = ntiles * nchunk;
+  const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
+  const int NTt = N / 16, KB = K / 32;
+  auto tile_rb = [&](int m) { return (start + jj + m * S) / nnb; };
+  auto tile_nb = [&](int m) { return (start + jj + m * S) % nnb; };
+
+  // metadata of the tiles whose DMA slot would come before the first group: plain loads
+  for (int m = 0; m < ntiles && m * nchunk < 3; m++) {
+    const int rb = tile_rb(m);
+    if (tid < BM) ax.rows[m & 3][tid] = sorted_ids[(size_t)rb * BM + tid];
+    if (tid < WAVE) ax.eid[m & 3][tid] = expert_ids[rb];
+  }
+  __syncthreads();
+
+  auto tile_nlive = [&](int slot) {                            // live rows (a prefix of the block), per wave
+    int n = 0;
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      const int fr = ax.rows[slot][u * WAVE + lane];
+      n += __popcll(__ballot(fr >= 0 && fr < numel));
+    }
+    return n;
+  };
+
+  // DMA sources of the tile being issued: uniform bases, 32-bit per-lane offsets (the host keeps A and one expert's
+  // codes below 2 GiB)
+  uint32_t ga[4], gb[2], gs = 0;
+  const uint8_t* wbase = Wq;
+  const uint8_t* sbase = Ws;
+  int issue_nl = 0, issue_slot = 0;
+  auto setup_issue = [&](int m) {
+    const int slot = m & 3;
+    const int nl = tile_nlive(slot);
+    int e = __builtin_amdgcn_readfirstlane(ax.eid[slot][0]);
+    e = e < 0 ? 0 : e;
+    const int nb = tile_nb(m);
+    int first = ax.rows[slot][0];
+    first = (first >= 0 && first < numel) ? first : 0;
+    const int piece = (tid & 7) ^ ((tid >> 3) & 7) ^ ((tid >> 6) & 1);
+#pragma unroll
+    for (int p = 0; p < 4; p++) {
+      const int row = p * 64 + (tid >> 3);
+      const int fr = row < nl ? ax.rows[slot][row] : first;
+      ga[p] = div_by((uint32_t)fr, rdiv) * (uint32_t)K + piece * 16;
+    }
+    wbase = uniform_ptr(Wq + (size_t)e * wq_estride);
+    sbase = uniform_ptr(Ws + (size_t)e * ws_estride);
+#pragma unroll
+    for (int p = 0; p < 2; p++) {
+      int nt = nb * NT16 + p * 8 + wave;
+      nt = nt < NTt ? nt : NTt - 1;
+      gb[p] = (uint32_t)nt * (uint32_t)(8 * K) + lane * 16;
+    }
+    int nt = nb * NT16 + (wave & 3) * 4 + (lane >> 4);
+    nt = nt < NTt ? nt : NTt - 1;
+    gs = (uint32_t)nt * (uint32_t)(16 * KB) + (lane & 15) * 4;
+    issue_nl = nl;
+    issue_slot = slot;
+  };
+
+  const uint32_t la0 = lds_addr(&st[0].a[wave * 64 * 16]);
+  const uint32_t lb0 = lds_addr(&st[0].b[wave * 64 * 16]);
+  const uint32_t ls0 = lds_addr(&st[0].s[wave < 4 ? wave * 256 : 1024 + (wave - 4) * 256]);
+  const uint32_t ldum = lds_addr(&ax.dummy[0]);
+  const uint32_t doff = lane * 4;                              // dummy loads: sorted_ids[lane], always valid
+
+  // group j (issued after barrier j, j >= -3): chunk j + 3, then the metadata dwords
+  auto issue_group = [&](int j) {
+    const int ci = j + 3, m = ci / nchunk, c = ci - m * nchunk;
+    if (c == 0) setup_issue(m);
+    const uint32_t so = (uint32_t)((ci % NSTAGE) * (int)sizeof(Stage));
+#pragma unroll
+    for (int p = 0; p < 4; p++) dma16s(A, ga[p] + (uint32_t)(c * KC), la0 + so + p * 512 * 16);
+#pragma unroll
+    for (int p = 0; p < 2; p++) dma16s(wbase, gb[p] + (uint32_t)(c * 1024), lb0 + so + p * 512 * 16);
+    dma4s(sbase, gs + (uint32_t)(c * 64), ls0 + so);
+    // sorted_ids and expert id of tile (j + 6) / nchunk
+    const int j6 = j + 6, m0 = j6 / nchunk;
+    if (j6 - m0 * nchunk == 0 && m0 < ntiles) {
+      const int slot = m0 & 3, rb = tile_rb(m0);
+      if (wave < 4) dma4s(sorted_ids, (uint32_t)(rb * BM + wave * 64 + lane) * 4, lds_addr(&ax.rows[slot][wave * 64]));
+      else if (wave == 4) dma4s(expert_ids, (uint32_t)rb * 4, lds_addr(&ax.eid[slot][0]));
+      else dma4s(sorted_ids, doff, ldum);
+    } else {
+      dma4s(sorted_ids, doff, ldum);
+    }
+    // per-row scales of tile m, with its first chunk
+    if (c == 0) {
+      const int r = (wave & 3) * 64 + lane;
+      int fr = r < issue_nl ? ax.rows[issue_slot][r] : ax.rows[issue_slot][0];
+      fr = (fr >= 0 && fr < numel) ? fr : 0;
+      if (wave < 4) dma4s(As, div_by((uint32_t)fr, rdiv) * 4, lds_addr(&ax.as[m & 1][wave * 64]));
+      else if (topk_w) dma4s(topk_w, (uint32_t)fr * 4, lds_addr(&ax.tw[m & 1][(wave - 4) * 64]));
+      else dma4s(sorted_ids, doff, ldum);
+    } else {
+      dma4s(sorted_ids, doff, ldum);
+    }
+  };
+
+  const int wm = wave >> 1, wn = wave & 1;
+  const int g = lane >> 5, c32 = lane & 31;
+  const FragOff fo = frag_offsets(wm, wn, lane);
+
+  issue_group(-3);
+  issue_group(-2);
+  issue_group(-1);
+  asm volatile("s_waitcnt vmcnt(20)" ::: "memory");             // chunk 0 (younger: 2 + 9 + 9)
+  asm volatile("s_barrier" ::: "memory");
+  KFrag F0, F1;
+  load_kfrag(st[0], fo, 0, F0);
+  int sidx = 0, i = 0;
+  for (int m = 0; m < ntiles; m++) {
+    v16f acc[2][4];
+#pragma unroll
+    for (int a = 0; a < 2; a++)
+#pragma unroll
+      for (int b = 0; b < 4; b++) acc[a][b] = (v16f){};
+    for (int c = 0; c < nchunk; c++, i++) {
+      // MFMAs are queued, not executed, when issued, and an LDS read into a fragment register waits until every
+      // queued MFMA that reads it has started. So each fragment set is refilled only after the other set's MFMAs
+      // have been issued behind its own: F0 holds chunk i's first half (read at the end of iteration i - 1).
+      // (Scheduling barriers keep this order.)
+      mfma_kfrag(acc, F0);
+      __builtin_amdgcn_sched_barrier(0);
+      load_kfrag(st[sidx], fo, 1, F1);                         // second half of chunk i, under the first half
+      __builtin_amdgcn_sched_barrier(0);
+      const int nidx = sidx == NSTAGE - 1 ? 0 : sidx + 1;
+      if (i + 1 < iters) {
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");    // this wave's reads of chunk i are done
+        if (i + 2 < iters) asm volatile("s_waitcnt vmcnt(11)" ::: "memory");
+        else asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
+        asm volatile("s_barrier" ::: "memory");
+        if (i + 3 < iters) issue_group(i);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      mfma_kfrag(acc, F1);
+      __builtin_amdgcn_sched_barrier(0);
+      if (i + 1 < iters) load_kfrag(st[nidx], fo, 0, F0);     // first half of chunk i + 1, under the second half
+      __builtin_amdgcn_sched_barrier(0);
+      sidx = nidx;
+    }
+    // tile m's output (rows and scales from its metadata slots, valid until a barrier after this)
+    const int nl = tile_nlive(m & 3), nb = tile_nb(m);
+#pragma unroll
+    for (int ii = 0; ii < 2; ii++) {
+      const int row = wm * 64 + ii * 32 + c32;
+      if (row >= nl) continue;
+      const int fr = ax.rows[m & 3][row];
+      float sc = ax.as[m & 1][row];
+      if (topk_w) sc *= ax.tw[m & 1][row];
+      uint16_t* __restrict__ crow = C + (size_t)fr * N;
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+#pragma unroll
+        for (int qb = 0; qb < 4; qb++) {
+          const int n = nb * BN + wn * 128 + j * 32 + 8 * qb + 4 * g;
+          if (n < N)
+            *reinterpret_cast<uint2*>(crow + n) =
+                make_uint2(pack_bf16x2(acc[ii][j][4 * qb] * sc, acc[ii][j][4 * qb + 1] * sc),
+                           pack_bf16x2(acc[ii][j][4 * qb + 2] * sc, acc[ii][j][4 * qb + 3] * sc));
+        }
+      }
+    }
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
+
 }  // namespace
 
 // Internal entry used by the prefill dispatch in r9k_moe_gemm.hip: tables with blocks of 256 rows, K % 128 == 0.
+// K >= 384 runs the persistent kernel (one workgroup per CU), K = 128 and 256 the one-tile-per-workgroup kernel.
 int r9k_prefill_launch(long a, long as, long wq, long ws, long c, long sorted_ids, long expert_ids, long ntpp,
                        long topk_w, long ws_estride, int max_blocks, int numel, int a_row_div, int K, int N,
                        long stream) {
@@ -233,7 +548,26 @@ int r9k_prefill_launch(long a, long as, long wq, long ws, long c, long sorted_id
   if (max_blocks <= 0 || numel <= 0) return 0;
   if (max_blocks > 65535) return -3;
   if ((a & 15) || (wq & 15) || (ws & 3) || (c & 7)) return -3;              // 16-byte DMA sources, 8-byte stores
-  const dim3 grid((N / 16 + NT16 - 1) / NT16, max_blocks);
+  const int nnb = (N / 16 + NT16 - 1) / NT16;
+  const long a_rows = ((long)numel + a_row_div - 1) / a_row_div;
+  if (a_rows * K >= (1L << 31) || (long)N * K / 2 >= (1L << 31) || (long)numel * 4 >= (1L << 31)) return -3;
+  if (K / KC >= 3 && getenv_flag_off_pf("R9K_PREFILL_PERSIST") == 0) {
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(moe_prefill_persistent_kernel),
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)SMEM_P);
+    if (attr != hipSuccess) return -4;
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+      return -6;
+    const long tiles = (long)max_blocks * nnb;
+    const int grid = (int)(tiles < cus ? tiles : cus);
+    hipLaunchKernelGGL(moe_prefill_persistent_kernel, dim3(grid), dim3(NTH), SMEM_P, (hipStream_t)stream,
+                       (const uint8_t*)a, (const float*)as, (const uint8_t*)wq, (const uint8_t*)ws, (uint16_t*)c,
+                       (const int*)sorted_ids, (const int*)expert_ids, (const int*)ntpp, (const float*)topk_w,
+                       (long)N * K / 2, ws_estride, numel, div_magic((uint32_t)a_row_div), K, N, nnb);
+    return hipGetLastError() == hipSuccess ? 0 : -6;
+  }
+  const dim3 grid(nnb, max_blocks);
   static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(moe_prefill_kernel),
                                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)SMEM);
   if (attr != hipSuccess) return -4;
