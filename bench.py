@@ -3,9 +3,9 @@ MXFP4 TFLOPS at prefill).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
 
-A step is one MoE layer forward over one batch of synthetic tokens: fused routing (softmax top-8 + align tables) ->
-per-token fp8 quant -> grouped gate_up GEMM -> SiLU*up + fp8 quant -> grouped down GEMM (router weight folded) ->
-top-k sum, six launches on one stream. The headline `value` is BASELINE config 2 (E=288 experts, hidden 2048,
+A step is one MoE layer forward over one batch of synthetic tokens: routing (softmax top-8 + align tables, and at
+T <= 64 the per-token fp8 quant of x in the same launch) -> grouped gate_up GEMM -> SiLU*up + fp8 quant -> grouped
+down GEMM (router weight folded) -> top-k sum, five launches on one stream (six above T = 64). The headline `value` is BASELINE config 2 (E=288 experts, hidden 2048,
 expert intermediate 512, top-8) at T=64 tokens, the bandwidth-bound decode point; T = 1, 8, 16 and the config 3
 prefill (T=8192) are reported beside it.
 
@@ -105,9 +105,10 @@ class Step:
     def __call__(self, c: int):
         K, route, L = self.K, self.route, self.layer
         if self.fused:
-            w, ids = route.moe_route(self.logits, self.topk, True, self.blk, self.sid, self.eid, self.ntpp,
-                                     self.scratch)
-            self.routed._r9k_tables = route.Tables(ids, self.sid, self.eid, self.ntpp, self.blk, self.numel)
+            w, ids, xq, xs = route.moe_route_quant(self.logits, self.topk, True, self.blk, self.sid, self.eid,
+                                                   self.ntpp, self.scratch, self.x)
+            self.routed._r9k_tables = route.Tables(ids, self.sid, self.eid, self.ntpp, self.blk, self.numel,
+                                                   self.x, self.x._version, xq, xs)
         else:
             w, ids = K.moe_topk(self.logits, self.topk, True)
             self.routed._r9k_tables = None

@@ -89,6 +89,16 @@ int r9k_moe_sum(long down, long shared, long out, int M, int topk, int N, long l
  * its fused router is off: r9700_vllm/moe/route.py:159-163). Same numerics as r9k_moe_route. 0 / 1 / HIP error. */
 int r9k_moe_topk(long logits, int ldl, long weights, long ids, int M, int E, int topk, int renorm, long stream);
 
+/* r9k_moe_route plus the per-token fp8 quant of the layer's activations in the same launch (the work the reference
+ * does in r9k_moe_route and then r9k_quant_rows_fp8, r9700_vllm/moe/experts.py:185): x bf16 [M][H] (row stride
+ * ldx) -> xq e4m3fn [M][H], xs fp32 [M], the bytes of r9k_quant_rows_fp8. scratch as for r9k_moe_route (its first
+ * int is the arrival counter, used above 16 rows). Decode widths only: M <= 64, E <= 512, the tables within 16384
+ * entries, H % 8 == 0, H <= 4096, x 16-byte and xq 8-byte aligned; any other shape returns 2 with nothing launched
+ * (run r9k_moe_route + r9k_quant_rows_fp8 instead). 0 / 1 bad arguments / 2 / HIP error. */
+int r9k_moe_route_quant(long logits, int ldl, long weights, long ids, long sorted_ids, long expert_ids, long ntpp,
+                        long scratch, int M, int E, int topk, int renorm, int blk, long x, long ldx, int H, long xq,
+                        long xs, long stream);
+
 /* Align tables only, from ids int32 [numel] (the role of vLLM's moe_align_block_size, called at
  * r9700_vllm/moe/experts.py:172 of the reference). ids outside [0, E) are left out. scratch: at least
  * r9k_moe_align_scratch_ints(numel, E) int32 of per-chunk histograms, rewritten by every call (no initial

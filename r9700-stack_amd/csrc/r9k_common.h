@@ -26,19 +26,15 @@ __device__ __forceinline__ uint16_t f2bf(float f) {
 //   |f| >= 2^-6 : 3 mantissa bits kept with RNE on the dropped 20 bits; exponent bias 7
 //   rounding past 448 (the largest finite, 0x7e) or a NaN input -> 0x7f
 // The sign bit is kept for zeros, so -0.0 and negative values that round to zero give 0x80.
+// Both roundings are computed and the result selected (no divergent branches in a vector of conversions).
 __device__ __forceinline__ uint32_t f32_to_e4m3(float f) {
   const uint32_t u = __float_as_uint(f);
   const uint32_t sign = (u >> 24) & 0x80u;
   const uint32_t a = u & 0x7fffffffu;
-  uint32_t r;
-  if (a > 0x43e80000u) {                 // > 464 (or inf / NaN): rounds past 448
-    r = 0x7fu;
-  } else if (a < 0x3c800000u) {          // < 2^-6: subnormal grid, exact scale by 2^9 then RNE to an integer
-    r = (uint32_t)__builtin_rintf(__uint_as_float(a) * 512.0f);
-  } else {
-    const uint32_t lsb = (a >> 20) & 1u;
-    r = ((a + 0x7ffffu + lsb) >> 20) - ((127u - 7u) << 3);
-  }
+  const uint32_t rn = ((a + 0x7ffffu + ((a >> 20) & 1u)) >> 20) - ((127u - 7u) << 3);     // normal, |f| >= 2^-6
+  const uint32_t rs = (uint32_t)__builtin_rintf(fminf(__uint_as_float(a), 0x1p-6f) * 512.0f);  // subnormal grid
+  uint32_t r = a < 0x3c800000u ? rs : rn;
+  r = a > 0x43e80000u ? 0x7fu : r;       // > 464 (or inf / NaN): rounds past 448
   return sign | r;
 }
 
@@ -72,6 +68,51 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
     v = w > v ? w : v;
   }
   return v;
+}
+
+// bf16 halves of a packed 32-bit word as fp32.
+__device__ __forceinline__ float lo16(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float hi16(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+__device__ __forceinline__ uint32_t pack4_e4m3(float a, float b, float c, float d) {
+  return f32_to_e4m3(a) | (f32_to_e4m3(b) << 8) | (f32_to_e4m3(c) << 16) | (f32_to_e4m3(d) << 24);
+}
+
+// One wave quantises one row of K bf16 values (K % 8 == 0, K <= 512 * RMAX, the row 16-byte aligned, the code row
+// 8-byte aligned) to OCP e4m3 with a per-row scale:
+//   amax = max(max_k |x_k|, 1e-12);  inv = 448 / amax;  q_k = e4m3_rne(x_k * inv);  s = amax / 448.
+// Each lane keeps its 16-byte chunks (lane + 64 i) in registers, so the row is read once.
+template <int RMAX>
+__device__ __forceinline__ void quant_row_wave(const uint16_t* __restrict__ xrow, int K, uint8_t* __restrict__ qrow,
+                                               float* __restrict__ s_out, int lane) {
+  const uint4* xr = reinterpret_cast<const uint4*>(xrow);
+  const int nvec = K / 8;
+  uint4 v[RMAX];
+  float m = 0.f;
+#pragma unroll
+  for (int i = 0; i < RMAX; i++) {
+    const int c = lane + i * WAVE;
+    v[i] = c < nvec ? xr[c] : make_uint4(0u, 0u, 0u, 0u);
+  }
+#pragma unroll
+  for (int i = 0; i < RMAX; i++) {
+    const uint32_t w[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+#pragma unroll
+    for (int j = 0; j < 4; j++) m = fmaxf(m, fmaxf(fabsf(lo16(w[j])), fabsf(hi16(w[j]))));
+  }
+  const float amax = fmaxf(wave_max(m), 1e-12f);
+  const float inv = 448.f / amax;
+  if (lane == 0) *s_out = amax / 448.f;
+  uint2* qr = reinterpret_cast<uint2*>(qrow);
+#pragma unroll
+  for (int i = 0; i < RMAX; i++) {
+    const int c = lane + i * WAVE;
+    if (c < nvec) {
+      const uint32_t lo = pack4_e4m3(lo16(v[i].x) * inv, hi16(v[i].x) * inv, lo16(v[i].y) * inv, hi16(v[i].y) * inv);
+      const uint32_t hi = pack4_e4m3(lo16(v[i].z) * inv, hi16(v[i].z) * inv, lo16(v[i].w) * inv, hi16(v[i].w) * inv);
+      qr[c] = make_uint2(lo, hi);
+    }
+  }
 }
 
 // Block-wide max of a float; `sh` holds one float per wave. Every thread gets the result.

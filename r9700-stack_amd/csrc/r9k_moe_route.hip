@@ -324,6 +324,197 @@ __global__ void __launch_bounds__(FT) route_fused_kernel(const uint16_t* __restr
   if (!single && threadIdx.x == 0) *arrive = 0;
 }
 
+// ------------------------------------------------------------------ small batches: M <= 64 rows in one workgroup
+constexpr int ST = 1024;          // threads of the small-batch routing workgroup (16 waves)
+constexpr int SW = ST / WAVE;
+constexpr int SMALL_ROWS = 64;    // token rows it routes: one bit each in the per-expert token masks
+constexpr int SMALL_E = 512;      // experts (EPL <= 8)
+constexpr int SMALL_CAP = 16384;  // table capacity kept in LDS
+constexpr int QRMAX = 8;          // 16-byte chunks per lane of the fused activation quant: hidden <= 4096
+
+// Wave-inclusive prefix sum of an int: Hillis-Steele over 16-lane rows (DPP row_shr 1, 2, 4, 8; lanes shifted past
+// the row start read 0), then the totals of the lower rows through v_readlane.
+__device__ __forceinline__ int wave_incl_scan(int v, int lane) {
+  v += (int)R9K_DPP(v, 0x111);
+  v += (int)R9K_DPP(v, 0x112);
+  v += (int)R9K_DPP(v, 0x114);
+  v += (int)R9K_DPP(v, 0x118);
+  const int r0 = __builtin_amdgcn_readlane(v, 15), r1 = __builtin_amdgcn_readlane(v, 31);
+  const int r2 = __builtin_amdgcn_readlane(v, 47);
+  const int row = lane >> 4;
+  return v + (row > 0 ? r0 : 0) + (row > 1 ? r1 : 0) + (row > 2 ? r2 : 0);
+}
+
+// Top-k of NR rows per wave, interleaved so that their reduction chains overlap (same order and numerics as
+// topk_core). The selection loop only finds keys; lane k then rebuilds its entry's exp from the key (the key holds
+// the bf16 logit) and forms p_k = e_k / sum, and the selected sum is accumulated in k order as before. Returns,
+// on lane k < topk, the expert id and the (renormalised) weight of selection k of each row.
+template <int EPL, int NR>
+__device__ __forceinline__ void topk_rows(const uint16_t (&h)[NR][EPL], int E, int topk, bool renorm, int lane,
+                                          int (&id)[NR], float (&w)[NR]) {
+  float mx[NR], s[NR];
+  uint32_t key[NR][EPL];
+#pragma unroll
+  for (int r = 0; r < NR; r++) {
+    float m = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < EPL; i++) m = fmaxf(m, bf2f(h[r][i]));
+    mx[r] = wave_max_dpp(m);
+  }
+#pragma unroll
+  for (int r = 0; r < NR; r++) {
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < EPL; i++) {
+      const int e = lane + WAVE * i;
+      const float d = bf2f(h[r][i]) - mx[r];
+      const bool live = d >= -87.f;
+      acc += (e < E && live) ? expf(d) : 0.f;
+      key[r][i] = e < E ? route_key(h[r][i], live, e) : 0u;
+    }
+    s[r] = wave_sum_dpp(acc);
+  }
+  uint32_t sel[NR];
+#pragma unroll
+  for (int r = 0; r < NR; r++) sel[r] = 0u;
+  for (int k = 0; k < topk; k++) {
+#pragma unroll
+    for (int r = 0; r < NR; r++) {
+      uint32_t b = key[r][0];
+#pragma unroll
+      for (int i = 1; i < EPL; i++) b = max(b, key[r][i]);
+      b = wave_max_key(b);                          // nonzero: an unselected e < E is left while k < topk <= E
+#pragma unroll
+      for (int i = 0; i < EPL; i++) key[r][i] = key[r][i] == b ? 0u : key[r][i];   // keys are unique
+      sel[r] = lane == k ? b : sel[r];
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < NR; r++) {
+    const uint32_t b = sel[r];
+    const uint32_t ord = (b >> 10) & 0xffffu;
+    const uint32_t hb = (ord & 0x8000u) ? (ord & 0x7fffu) : (~ord & 0xffffu);
+    const float eb = ((b >> 26) & 1u) ? expf(bf2f((uint16_t)hb) - mx[r]) : 0.f;
+    float p = s[r] > 0.f ? eb / s[r] : 0.f;
+    float tot = 0.f;
+    for (int k = 0; k < topk; k++) tot += __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(p), k));
+    if (renorm) p = tot > 0.f ? p / tot : 0.f;
+    const int idx = 1023 - (int)(b & 1023u);
+    id[r] = (idx < 0 || idx >= E) ? 0 : idx;        // lanes >= topk only
+    w[r] = p;
+  }
+}
+
+// Routing + tables + (optionally) the per-token fp8 quant of the activations for M <= 64 rows, one launch.
+// Routing workgroups g < nrt = ceil(M / rpw) take rows g * rpw + wave (wave < rpw, one row a wave; waves without a
+// row skip the top-k, which is VALU-bound at 4 cycles an instruction). With one routing workgroup (rpw = 16,
+// M <= 16) the ids stay on chip; with several (rpw = 4: one row per SIMD) each stores its ids as agent-scope
+// atomics, waits for them to complete (vmcnt) and then counts itself in `arrive`; the last to arrive reads every id
+// back with agent-scope atomic loads and builds the tables, resetting `arrive` to zero. (Agent-scope atomic
+// accesses are coherent across the XCDs' L2s on their own, so no whole-L2 writeback / invalidate fence is needed.)
+// Table build, one thread per flat row t = row * topk + k with expert e: LDS mask[e] |= 1 << row (an expert's
+// routed rows are its set bits: count = popcount; t goes to offs[e] + popcount(mask[e] & bits below row), which is
+// the stable ascending order). The tables are assembled in LDS (padding = numel, expert_ids = -1 past the end) and
+// written out with 16-byte stores. Workgroups nrt.. quantise 16 activation rows each (quant_row_wave).
+// Dynamic LDS: mask u64 [Ep], offs [Ep], scan [64], tab [cap], eids [cap / blk], lids [numel] (Ep = E rounded up
+// to 16).
+template <int EPL>
+__global__ void __launch_bounds__(ST) route_small_kernel(
+    const uint16_t* __restrict__ logits, int ldl, float* __restrict__ weights, int* __restrict__ ids,
+    int* __restrict__ sorted_ids, int* __restrict__ expert_ids, int* __restrict__ ntpp, int* __restrict__ arrive,
+    int M, int E, int topk, int renorm, int blk, int cap, int rpw, const uint16_t* __restrict__ x, long ldx, int H,
+    uint8_t* __restrict__ xq, float* __restrict__ xs) {
+  const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
+  const int nrt = (M + rpw - 1) / rpw;
+  if ((int)blockIdx.x >= nrt) {
+    const int row = ((int)blockIdx.x - nrt) * SW + wave;
+    if (row < M) quant_row_wave<QRMAX>(x + (size_t)row * ldx, H, xq + (size_t)row * H, xs + row, lane);
+    return;
+  }
+  extern __shared__ __align__(16) uint8_t smem[];
+  const int Ep = (E + 15) & ~15;
+  unsigned long long* mask = reinterpret_cast<unsigned long long*>(smem);
+  int* offs = reinterpret_cast<int*>(mask + Ep);
+  int* scan = offs + Ep;                                       // [0, SW): per-wave totals; [SW]: last-arrival flag
+  int* tab = scan + 64;
+  int* eids = tab + cap;
+  int* lids = eids + cap / blk;
+  const int numel = M * topk, nblk = cap / blk;
+  const int row = (int)blockIdx.x * rpw + wave;
+  const bool has_row = wave < rpw && row < M;
+
+  uint16_t h[1][EPL];
+  if (has_row) load_row<EPL>(logits + (size_t)row * ldl, E, lane, h[0]);
+  // LDS set-up under the logit loads
+  for (int e = tid; e < E; e += ST) mask[e] = 0ull;
+  for (int i = tid; i < cap; i += ST) tab[i] = numel;
+  for (int b = tid; b < nblk; b += ST) eids[b] = -1;
+
+  if (has_row) {
+    int id[1];
+    float wt[1];
+    topk_rows<EPL, 1>(h, E, topk, renorm != 0, lane, id, wt);
+    if (lane < topk) {
+      weights[(size_t)row * topk + lane] = wt[0];
+      if (nrt == 1) {
+        ids[(size_t)row * topk + lane] = id[0];
+        lids[row * topk + lane] = id[0];
+      } else {
+        __hip_atomic_store(ids + (size_t)row * topk + lane, id[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+  }
+  int e = 0;
+  if (nrt > 1) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");           // this wave's id stores have completed
+    lds_barrier();
+    if (tid == 0) scan[SW] = __hip_atomic_fetch_add(arrive, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == nrt - 1;
+    lds_barrier();
+    if (!scan[SW]) return;
+    if (tid == 0) __hip_atomic_store(arrive, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid < numel) e = __hip_atomic_load(ids + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  } else {
+    lds_barrier();
+    if (tid < numel) e = lids[tid];
+  }
+  const int trow = tid < numel ? tid / topk : 0;
+  if (tid < numel) atomicOr(&mask[e], 1ull << trow);
+  lds_barrier();
+
+  // block-padded counts, scanned over the experts (one per thread)
+  const int c = tid < E ? __popcll(mask[tid]) : 0;
+  const int n = (c + blk - 1) & ~(blk - 1);
+  const int incl = wave_incl_scan(n, lane);
+  if (lane == WAVE - 1) scan[wave] = incl;
+  lds_barrier();
+  int wbase = 0, total = 0;
+#pragma unroll
+  for (int w = 0; w < SW; w++) {
+    const int t = scan[w];
+    wbase += w < wave ? t : 0;
+    total += t;
+  }
+  if (tid < E) {
+    const int o = wbase + incl - n;
+    offs[tid] = o;
+    for (int b = o / blk; b < (o + n) / blk; b++) eids[b] = tid;
+  }
+  if (tid == 0) ntpp[0] = total;
+  lds_barrier();
+  if (tid < numel) tab[offs[e] + __popcll(mask[e] & ((1ull << trow) - 1ull))] = tid;
+  lds_barrier();
+
+  // write-out: 16-byte stores where the destination allows, the rest one int at a time
+  int done = 0;
+  if ((reinterpret_cast<uintptr_t>(sorted_ids) & 15) == 0) {
+    const int n4 = cap / 4;
+    for (int i = tid; i < n4; i += ST) reinterpret_cast<int4*>(sorted_ids)[i] = reinterpret_cast<const int4*>(tab)[i];
+    done = n4 * 4;
+  }
+  for (int i = done + tid; i < cap; i += ST) sorted_ids[i] = tab[i];
+  for (int b = tid; b < nblk; b += ST) expert_ids[b] = eids[b];
+}
+
 template <int EPL>
 __global__ void __launch_bounds__(RW * WAVE) topk_kernel(const uint16_t* __restrict__ logits, int ldl,
                                                          float* __restrict__ weights, int* __restrict__ ids, int M,
@@ -485,6 +676,60 @@ bool route_args_ok(int M, int E, int topk, int blk) {
          (blk & (blk - 1)) == 0;
 }
 
+long table_capacity(long numel, int E, int blk) { return (numel + (long)E * (blk - 1) + blk - 1) / blk * blk; }
+
+template <int EPL>
+hipError_t launch_small_inst(dim3 grid, size_t lds, hipStream_t st, const uint16_t* logits, int ldl, float* w,
+                             int* ids, int* sorted_ids, int* expert_ids, int* ntpp, int* arrive, int M, int E,
+                             int topk, int renorm, int blk, int cap, int rpw, const uint16_t* x, long ldx, int H,
+                             uint8_t* xq, float* xs) {
+  static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(route_small_kernel<EPL>),
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+  if (attr != hipSuccess) return attr;
+  hipLaunchKernelGGL(route_small_kernel<EPL>, grid, dim3(ST), lds, st, logits, ldl, w, ids, sorted_ids, expert_ids,
+                     ntpp, arrive, M, E, topk, renorm, blk, cap, rpw, x, ldx, H, xq, xs);
+  return hipGetLastError();
+}
+
+// Routing rows per workgroup of route_small_kernel: all M in one workgroup up to this many rows (no cross-workgroup
+// hand-off), else SMALL_RPW rows each (one row per SIMD) and the last workgroup to arrive builds the tables.
+constexpr int SMALL_ONE_WG = 16;
+constexpr int SMALL_RPW = 4;
+int small_rpw(int M) { return M <= SMALL_ONE_WG ? SMALL_ONE_WG : SMALL_RPW; }
+
+// Whether route_small_kernel takes this call (and, with x, the activation quant): M <= 64 rows, E <= 512, a table
+// that fits LDS, an arrival counter when several workgroups route, and x rows the wave quant reads as 16-byte chunks.
+bool small_fits(int M, int E, int topk, int blk, const void* arrive, const void* x, long ldx, int H, const void* xq,
+                const void* xs) {
+  if (M > SMALL_ROWS || E > SMALL_E || table_capacity((long)M * topk, E, blk) > SMALL_CAP) return false;
+  if (M > SMALL_ONE_WG && !arrive) return false;
+  if (!x) return true;
+  return xq && xs && H >= 8 && H % 8 == 0 && H <= 512 * QRMAX && ldx >= H && ldx % 8 == 0 &&
+         (reinterpret_cast<uintptr_t>(x) & 15) == 0 && (reinterpret_cast<uintptr_t>(xq) & 7) == 0;
+}
+
+// One launch: the routing workgroups, then (with x) ceil(M / 16) quant workgroups.
+hipError_t launch_small(const uint16_t* logits, int ldl, float* w, int* ids, int* sorted_ids, int* expert_ids,
+                        int* ntpp, int* arrive, int M, int E, int topk, int renorm, int blk, const uint16_t* x,
+                        long ldx, int H, uint8_t* xq, float* xs, hipStream_t st) {
+  const int cap = (int)table_capacity((long)M * topk, E, blk);
+  const int Ep = (E + 15) & ~15;
+  const size_t lds = (size_t)Ep * 12 + 64 * 4 + (size_t)cap * 4 + (size_t)(cap / blk) * 4 + (size_t)M * topk * 4;
+  const int rpw = small_rpw(M);
+  const dim3 grid((M + rpw - 1) / rpw + (x ? (M + SW - 1) / SW : 0));
+#define RS(EPLV)                                                                                                   \
+  return launch_small_inst<EPLV>(grid, lds, st, logits, ldl, w, ids, sorted_ids, expert_ids, ntpp, arrive, M, E, \
+                                 topk, renorm, blk, cap, rpw, x, ldx, H, xq, xs)
+  switch (epl_for(E)) {
+    case 2: RS(2);
+    case 4: RS(4);
+    case 6: RS(6);
+    case 8: RS(8);
+    default: return hipErrorInvalidValue;
+  }
+#undef RS
+}
+
 }  // namespace
 
 // Reference: kernels/r9k_moe_route.hip:217-233. logits [M, E] bf16 (row stride ldl) -> weights fp32 [M, topk],
@@ -497,6 +742,10 @@ extern "C" int r9k_moe_route(long logits, int ldl, long weights, long ids, long 
   if (!route_args_ok(M, E, topk, blk) || ldl < E) return 1;
   const hipStream_t st = (hipStream_t)stream;
   const long numel = (long)M * topk;
+  if (small_fits(M, E, topk, blk, (const void*)scratch, nullptr, 0, 0, nullptr, nullptr))
+    return (int)launch_small((const uint16_t*)logits, ldl, (float*)weights, (int*)ids, (int*)sorted_ids,
+                             (int*)expert_ids, (int*)ntpp, (int*)scratch, M, E, topk, renorm, blk, nullptr, 0, 0,
+                             nullptr, nullptr, st);
   if (numel <= SMALL_MAX) {
     const int nblk = (M + FW - 1) / FW;
     if (nblk > 1 && !scratch) return 1;
@@ -521,6 +770,22 @@ extern "C" int r9k_moe_route(long logits, int ldl, long weights, long ids, long 
                        (int*)sorted_ids, (int*)expert_ids, (int*)ntpp);
   }
   return (int)hipGetLastError();
+}
+
+// r9k_moe_route plus the per-token fp8 quant of the layer's activations in the same launch (the quant of
+// r9k_quant_rows_fp8, same bytes): x bf16 [M, H] (row stride ldx) -> xq e4m3 [M, H], xs fp32 [M]. scratch as for
+// r9k_moe_route. Only at decode widths (M <= 64, E <= 512, the tables within 16384 entries) for rows that suit the
+// wave quant (H % 8 == 0, H <= 4096, x 16-byte and xq 8-byte aligned); returns 2 for any other shape, with
+// nothing launched, so the caller runs r9k_moe_route and r9k_quant_rows_fp8. 1 bad arguments, else the HIP error.
+extern "C" int r9k_moe_route_quant(long logits, int ldl, long weights, long ids, long sorted_ids, long expert_ids,
+                                   long ntpp, long scratch, int M, int E, int topk, int renorm, int blk, long x,
+                                   long ldx, int H, long xq, long xs, long stream) {
+  if (!route_args_ok(M, E, topk, blk) || ldl < E || !x) return 1;
+  if (!small_fits(M, E, topk, blk, (const void*)scratch, (const void*)x, ldx, H, (const void*)xq, (const void*)xs))
+    return 2;
+  return (int)launch_small((const uint16_t*)logits, ldl, (float*)weights, (int*)ids, (int*)sorted_ids,
+                           (int*)expert_ids, (int*)ntpp, (int*)scratch, M, E, topk, renorm, blk, (const uint16_t*)x,
+                           ldx, H, (uint8_t*)xq, (float*)xs, (hipStream_t)stream);
 }
 
 extern "C" int r9k_moe_route_max_experts(void) { return MAX_E; }

@@ -23,16 +23,10 @@ using namespace r9k;
 constexpr int QT = 256;     // threads per row
 constexpr int QR = 4;       // 16-byte chunks per thread kept in registers: K <= 8192 on the vectorised path
 
-__device__ __forceinline__ float lo16(uint32_t w) { return __uint_as_float(w << 16); }
-__device__ __forceinline__ float hi16(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
-
-__device__ __forceinline__ uint32_t pack4_e4m3(float a, float b, float c, float d) {
-  return f32_to_e4m3(a) | (f32_to_e4m3(b) << 8) | (f32_to_e4m3(c) << 16) | (f32_to_e4m3(d) << 24);
-}
-
 constexpr int WR = 4;       // rows (waves) per workgroup of the wave-per-row kernels
 
-// One wave per row, R 16-byte chunks per lane (K <= 512 * R).
+// One wave per row, R 16-byte chunks per lane (K <= 512 * R). The plain quant is quant_row_wave (shared with the
+// routing kernel's fused activation quant, so both give the same bytes).
 template <bool GATE, int R>
 __global__ void __launch_bounds__(WR * WAVE) quant_rows_wave_kernel(const uint16_t* __restrict__ x,
                                                                     uint8_t* __restrict__ q, float* __restrict__ s,
@@ -41,6 +35,10 @@ __global__ void __launch_bounds__(WR * WAVE) quant_rows_wave_kernel(const uint16
                                                                     float* __restrict__ g) {
   const int row = blockIdx.x * WR + threadIdx.x / WAVE, lane = threadIdx.x % WAVE, nvec = K / 8;
   if (row >= M) return;
+  if constexpr (!GATE) {
+    quant_row_wave<R>(x + (size_t)row * ld, K, q + (size_t)row * K, s + row, lane);
+    return;
+  }
   const uint4* xr = reinterpret_cast<const uint4*>(x + (size_t)row * ld);
   uint4 v[R];
   float m = 0.f, dot = 0.f;

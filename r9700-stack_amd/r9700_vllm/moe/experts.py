@@ -148,13 +148,15 @@ class R9700Mxfp4Experts(_experts_base()):
             pf_down = K.pick_moe_prefill(MT, K2)
             pf_gate = K.pick_moe_prefill(MT, K1, gate_up=True)
         tabs = route.take(getattr(self, "r9k_layer", None), topk_ids, blk, numel) if expert_map is None else None
+        tabs_routed = tabs is not None
         if tabs is None:
             tabs = K.moe_align(topk_ids, blk, E, expert_map)
         sid, eid, ntpp = tabs
         W1 = K.Mxfp4Experts(w1, self.w1_scale, N1, K1)
         W2 = K.Mxfp4Experts(w2, self.w2_scale, N2, K2)
 
-        xq, xs = K.quant_rows_fp8(hidden_states)
+        q = route.take_quant(getattr(self, "r9k_layer", None), topk_ids, hidden_states) if tabs_routed else None
+        xq, xs = q if q is not None else K.quant_rows_fp8(hidden_states)
         gate_up = torch.empty((numel, N1), dtype=torch.bfloat16, device=dev)
         K.moe_gemm(xq, xs, W1, gate_up, sid, eid, ntpp, numel, topk, None, num_experts=E, MT=MT, prefill=pf_gate)
         aq, as_ = K.silu_mul_quant_fp8(gate_up)

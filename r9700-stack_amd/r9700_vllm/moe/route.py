@@ -36,6 +36,9 @@ def lib():
         L.r9k_moe_route.restype = ctypes.c_int
         L.r9k_moe_route.argtypes = [ctypes.c_long, ctypes.c_int] + [ctypes.c_long] * 6 + [ctypes.c_int] * 5 \
             + [ctypes.c_long]
+        L.r9k_moe_route_quant.restype = ctypes.c_int
+        L.r9k_moe_route_quant.argtypes = [ctypes.c_long, ctypes.c_int] + [ctypes.c_long] * 6 + [ctypes.c_int] * 5 \
+            + [ctypes.c_long, ctypes.c_long, ctypes.c_int, ctypes.c_long, ctypes.c_long, ctypes.c_long]
         L.r9k_moe_route_max_experts.restype = ctypes.c_int
         L.r9k_moe_route_max_topk.restype = ctypes.c_int
         _L = L
@@ -83,12 +86,50 @@ def _moe_route_fake(logits: torch.Tensor, topk: int, renorm: bool, blk: int, sor
     return (logits.new_empty((M, topk), dtype=torch.float32), logits.new_empty((M, topk), dtype=torch.int32))
 
 
+def moe_route_quant(logits: torch.Tensor, topk: int, renorm: bool, blk: int, sorted_ids: torch.Tensor,
+                    expert_ids: torch.Tensor, ntpp: torch.Tensor, scratch: torch.Tensor,
+                    x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+    """moe_route plus the per-token fp8 quant of the layer input x bf16 [M, H] (the bytes of quant_rows_fp8):
+    (weights, ids, xq e4m3fn [M, H], xs fp32 [M]). One launch (r9k_moe_route_quant) at decode widths; other shapes
+    run moe_route and quant_rows_fp8."""
+    M, E = logits.shape
+    if not (x.dim() == 2 and x.dtype == torch.bfloat16 and x.stride(1) == 1 and x.shape[0] == M):
+        raise ValueError("moe_route_quant: x must be bf16 [M, H] with unit column stride")
+    H = x.shape[1]
+    w = torch.empty((M, topk), dtype=torch.float32, device=logits.device)
+    ids = torch.empty((M, topk), dtype=torch.int32, device=logits.device)
+    xq = torch.empty((M, H), dtype=torch.float8_e4m3fn, device=x.device)
+    xs = torch.empty((M,), dtype=torch.float32, device=x.device)
+    rc = lib().r9k_moe_route_quant(logits.data_ptr(), logits.stride(0), w.data_ptr(), ids.data_ptr(),
+                                   sorted_ids.data_ptr(), expert_ids.data_ptr(), ntpp.data_ptr(),
+                                   scratch.data_ptr(), M, E, topk,
+                                   1 if renorm else 0, blk, x.data_ptr(), x.stride(0), H, xq.data_ptr(),
+                                   xs.data_ptr(), torch.cuda.current_stream().cuda_stream)
+    if rc == 2:
+        w, ids = moe_route(logits, topk, renorm, blk, sorted_ids, expert_ids, ntpp, scratch)
+        xq, xs = KM.quant_rows_fp8(x)
+        return w, ids, xq, xs
+    if rc:
+        raise RuntimeError(f"r9k_moe_route_quant failed ({rc}) M={M} E={E} topk={topk} blk={blk} H={H}")
+    return w, ids, xq, xs
+
+
+def _moe_route_quant_fake(logits: torch.Tensor, topk: int, renorm: bool, blk: int, sorted_ids: torch.Tensor,
+                          expert_ids: torch.Tensor, ntpp: torch.Tensor, scratch: torch.Tensor,
+                          x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+    M = logits.shape[0]
+    return (logits.new_empty((M, topk), dtype=torch.float32), logits.new_empty((M, topk), dtype=torch.int32),
+            x.new_empty(x.shape, dtype=torch.float8_e4m3fn), x.new_empty((M,), dtype=torch.float32))
+
+
 def register() -> None:
     global _DONE
     if _DONE:
         return
     register_custom_op(_LIB, "moe_route", moe_route, ["sorted_ids", "expert_ids", "ntpp", "scratch"],
                        _moe_route_fake)
+    register_custom_op(_LIB, "moe_route_quant", moe_route_quant, ["sorted_ids", "expert_ids", "ntpp", "scratch"],
+                       _moe_route_quant_fake)
     _DONE = True
 
 
@@ -101,10 +142,20 @@ class Tables:
     ntpp: torch.Tensor
     blk: int
     numel: int
+    x: torch.Tensor | None = None          # the layer input the router quantised, with its version at that time
+    x_version: int = -1
+    xq: torch.Tensor | None = None
+    xs: torch.Tensor | None = None
 
     def matches(self, topk_ids: torch.Tensor, blk: int, numel: int) -> bool:
         return (self.ids.data_ptr() == topk_ids.data_ptr() and self.ids.shape == topk_ids.shape
                 and self.blk == blk and self.numel == numel)
+
+    def quant_for(self, x: torch.Tensor):
+        """(xq, xs) when the router quantised this very tensor, unmodified since; else None."""
+        if self.xq is None or self.x is not x or x._version != self.x_version:
+            return None
+        return self.xq, self.xs
 
 
 def _fits(logits: torch.Tensor, topk: int, E: int) -> bool:
@@ -152,6 +203,14 @@ def make_router(stock, routed_experts):
             numel = M * self.top_k
             blk = KM.MOE_BLOCK * KM.pick_mt(numel, E)
             sorted_ids, expert_ids, ntpp, scratch = self._buffers(router_logits.device, E)
+            if _quantisable(hidden_states, M):
+                # the experts' fp8 input quant rides along in the routing launch (Tables.quant_for hands it over)
+                w, ids, xq, xs = torch.ops.r9700.moe_route_quant(router_logits, self.top_k, self.renormalize, blk,
+                                                                 sorted_ids, expert_ids, ntpp, scratch,
+                                                                 hidden_states)
+                self.routed_experts._r9k_tables = Tables(ids, sorted_ids, expert_ids, ntpp, blk, numel,
+                                                         hidden_states, hidden_states._version, xq, xs)
+                return w, ids
             w, ids = torch.ops.r9700.moe_route(router_logits, self.top_k, self.renormalize, blk, sorted_ids,
                                                expert_ids, ntpp, scratch)
             self.routed_experts._r9k_tables = Tables(ids, sorted_ids, expert_ids, ntpp, blk, numel)
@@ -166,6 +225,20 @@ def take(layer, topk_ids: torch.Tensor, blk: int, numel: int):
     if t is None or not t.matches(topk_ids, blk, numel):
         return None
     return t.sorted_ids, t.expert_ids, t.ntpp
+
+
+def take_quant(layer, topk_ids: torch.Tensor, x: torch.Tensor):
+    """The (xq, xs) fp8 quant of `x` the router produced with this call's tables, or None."""
+    t = getattr(layer, "_r9k_tables", None)
+    if t is None or t.ids.data_ptr() != topk_ids.data_ptr():
+        return None
+    return t.quant_for(x)
+
+
+def _quantisable(x, M: int) -> bool:
+    """A layer input the routing launch can quantise (decode widths; the kernel checks the rest)."""
+    return (isinstance(x, torch.Tensor) and x.dim() == 2 and x.dtype == torch.bfloat16 and x.shape[0] == M
+            and x.is_contiguous() and M <= 64)
 
 
 def install(model: torch.nn.Module) -> int:

@@ -97,6 +97,46 @@ def test_moe_route_fused(dev, M, E, topk, blk, renorm):
     check_tables(so, eo, no, ido, blk, numel, E)
 
 
+@pytest.mark.parametrize("M,E,topk,blk,H,ldx", [(1, 288, 8, 16, 2048, 2048), (64, 288, 8, 16, 2048, 2048),
+                                                 (37, 384, 8, 16, 4096, 4096), (13, 100, 6, 32, 520, 528),
+                                                 (16, 512, 10, 16, 2048, 2560),
+                                                 (100, 288, 8, 16, 2048, 2048),     # M > 64: two launches
+                                                 (8, 288, 8, 16, 8192, 8192)])      # H > 4096: two launches
+def test_moe_route_quant(dev, M, E, topk, blk, H, ldx):
+    """Routing + tables + the activation quant in one launch: every output bit-exact against the oracle, and the
+    quant bytes equal to r9k_quant_rows_fp8's."""
+    print(f"route_quant M={M} E={E} topk={topk} blk={blk} H={H} ldx={ldx}", flush=True)
+    g = torch.Generator().manual_seed(M * 11 + H)
+    logits = torch.randn(M, E, generator=g).to(torch.bfloat16)
+    xb = (torch.randn(M, ldx, generator=g) * 3.0).to(torch.bfloat16)
+    xb[0, :H] = 0.0                                                    # all-zero row: amax clamps to 1e-12
+    x = xb.to(dev)[:, :H]
+    numel = M * topk
+    cap = route.capacity(numel, E, blk)
+    s_ = torch.full((cap + 64,), -9, dtype=torch.int32, device=dev)
+    e_ = torch.full((cap // blk + 64,), -9, dtype=torch.int32, device=dev)
+    n_ = torch.zeros(1, dtype=torch.int32, device=dev)
+    scratch = torch.zeros(route.scratch_ints(E), dtype=torch.int32, device=dev)
+    for rep in range(2):                                               # a second call on the same buffers
+        w, ids, xq, xs = route.moe_route_quant(logits.to(dev), topk, True, blk, s_[:cap], e_[:cap // blk], n_,
+                                               scratch, x)
+    torch.cuda.synchronize()
+    wo, ido = O.route(logits, topk, True)
+    assert np.array_equal(ids.cpu().numpy(), ido)
+    assert np.abs(w.cpu().numpy() - wo).max() < 2e-6
+    so, eo, no = O.align(ido, E, blk)
+    assert np.array_equal(s_[:cap].cpu().numpy(), so) and np.array_equal(e_[:cap // blk].cpu().numpy(), eo)
+    assert n_.item() == no[0]
+    assert bool((s_[cap:] == -9).all()) and bool((e_[cap // blk:] == -9).all()), "wrote past the tables"
+    qo, so_ = O.quant_rows_fp8(xb[:, :H])
+    assert np.array_equal(u8(xq), qo) and np.array_equal(xs.cpu().numpy().view(np.uint32), so_.view(np.uint32))
+    q2, s2 = K.quant_rows_fp8(x)
+    assert torch.equal(xq.view(torch.uint8), q2.view(torch.uint8)) and torch.equal(xs, s2)
+    w2, ids2 = route.moe_route(logits.to(dev), topk, True, blk, s_[:cap], e_[:cap // blk], n_, scratch)
+    assert torch.equal(w, w2) and torch.equal(ids, ids2)
+    assert not scratch.any()
+
+
 def test_moe_route_degenerate_rows(dev):
     """NaN, +-inf, all-equal and -3e38 rows, E not a multiple of 64 (tests/test_moe_route_r9k.py:84-104)."""
     for Ed in (512, 100, 48):
