@@ -5,9 +5,9 @@ MXFP4 TFLOPS at prefill).
 
 A step is one MoE layer forward over one batch of synthetic tokens: routing (softmax top-8 + align tables, and at
 T <= 64 the per-token fp8 quant of x in the same launch) -> grouped gate_up GEMM -> SiLU*up + fp8 quant -> grouped
-down GEMM (router weight folded) -> top-k sum, five launches on one stream (six above T = 64). The headline `value` is BASELINE config 2 (E=288 experts, hidden 2048,
-expert intermediate 512, top-8) at T=64 tokens, the bandwidth-bound decode point; T = 1, 8, 16 and the config 3
-prefill (T=8192) are reported beside it.
+down GEMM (router weight folded) -> top-k sum, five launches on one stream (six above T = 64). The headline `value`
+is BASELINE config 2 (E=288 experts, hidden 2048, expert intermediate 512, top-8) at T=64 tokens, the
+bandwidth-bound decode point; T = 1, 8, 16 and the config 3 prefill (T=8192) are reported beside it.
 
 Method: weights and inputs are resident in HBM before timing. Steps run as HIP-graph replays that cycle through
 COPIES independent weight copies (> 2x the 256 MB Infinity Cache per cycle), so weight bytes come from HBM, not from
@@ -170,18 +170,52 @@ def gate_up_kernel_time(step: Step, reps: int = 40):
     for i in range(8):
         launch(i % copies)
     torch.cuda.synchronize()
-    s = torch.cuda.current_stream()
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
-    for i, (a, b) in enumerate(evs):
-        a.record(s)
-        launch(i % copies)
-        b.record(s)
+    # `reps` back-to-back launches in one HIP graph, HIP events around its replay on this stream: the average is the
+    # kernel's own duration (separate event pairs per launch would add the launch gap to every sample)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(reps):
+            launch(i % copies)
+    g.replay()
     torch.cuda.synchronize()
-    ms = float(np.mean([a.elapsed_time(b) for a, b in evs]))
+    s = torch.cuda.current_stream()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(s)
+    g.replay()
+    b.record(s)
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / reps
     touched = int(torch.unique(ids).numel())
     nbytes = touched * (N1 * K1 // 2 + N1 * K1 // 32) + step.T * K1 + step.T * 4 + step.numel * N1 * 2
     flops = 2 * step.numel * N1 * K1
     return ms, nbytes, flops, touched
+
+
+CALIB_BYTES = 256 << 20
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "moe_gate_up_t64_pmc_traffic.md")
+
+
+def calib_copy(dev) -> None:
+    """One plain elementwise copy of known size (CALIB_BYTES read, CALIB_BYTES written; torch's neg kernel on fp32),
+    outside every timed region: the reference the PMC byte counters (FETCH_SIZE, WRITE_SIZE) are scaled by when the
+    traffic profile is made from this script."""
+    src = torch.ones(CALIB_BYTES // 4, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+
+
+def measured_traffic():
+    """HBM bytes per gate_up launch at T=64 from the committed PMC summary (its line 'traffic_bytes_per_launch: N'),
+    or None when there is none."""
+    try:
+        with open(TRAFFIC_PROFILE) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1].strip())
+    except OSError:
+        return None
+    return None
 
 
 def layer_bytes(step: Step) -> tuple[int, int]:
@@ -249,6 +283,7 @@ def main():
         if T == 64:
             main_step, main_ms, main_n = st, ms, n
 
+    calib_copy(dev)
     k_ms, k_bytes, k_flops, k_touched = gate_up_kernel_time(main_step)
     k_gbs = k_bytes / (k_ms * 1e-3) / 1e9
     print(f"# gate_up GEMM alone: {k_ms * 1e3:.1f} us, {k_gbs:.0f} GB/s", file=sys.stderr, flush=True)
@@ -283,7 +318,8 @@ def main():
                    "weight_copies_rotated": COPIES},
         "roofline": {"bound": "hbm", "kernel": "r9k_moe_mxfp4a8 gate_up (T=64)", "achieved": round(k_gbs, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(k_gbs / HBM_PEAK_GBS, 4),
-                     "traffic": None, "kernel_us": round(k_ms * 1e3, 2), "bytes_per_launch": k_bytes},
+                     "traffic": measured_traffic(), "kernel_us": round(k_ms * 1e3, 2),
+                     "bytes_per_launch": k_bytes},
         "cpu_baseline": cpu,
         "decode_sweep": sweep,
         "prefill": prefill,

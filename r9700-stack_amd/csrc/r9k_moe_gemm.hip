@@ -74,15 +74,19 @@ __global__ void __launch_bounds__(WAVE * SK) moe_mxfp4_kernel(
   extern __shared__ float red[];
 
   const int rb = blockIdx.y / subs, sub = blockIdx.y - rb * subs;
-  if (rb * blk >= ntpp[0]) return;
-  const int e = expert_ids[rb];
-  if (e < 0) return;
   const int row0 = rb * blk + sub * BLK;
-  const int first = sorted_ids[rb * blk];
-  if (first < 0 || first >= numel || sorted_ids[row0] >= numel) return;   // padding sits at the end of a block
-
   const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
   const int g = lane >> 4, r = lane & 15;
+  // the table reads are independent (every block index below the launch's max_blocks is inside the tables), so
+  // they go out together and the block is checked once they are back: one memory round trip, not three
+  const int np = ntpp[0];
+  const int e = expert_ids[rb];
+  const int first = sorted_ids[rb * blk];
+  int fr_in[MT];
+#pragma unroll
+  for (int i = 0; i < MT; i++) fr_in[i] = sorted_ids[row0 + i * 16 + r];
+  if (rb * blk >= np || e < 0) return;
+  if (first < 0 || first >= numel || __shfl(fr_in[0], 0, WAVE) >= numel) return;   // padding: end of a block
   const int NT = N / 16;
   const int nkt = (K + KT - 1) / KT, nkt_full = K / KT, tg = (K % KT) / GROUP;
   const int KB = K / GROUP;
@@ -94,11 +98,15 @@ __global__ void __launch_bounds__(WAVE * SK) moe_mxfp4_kernel(
   const bool b_live_tail = g < tg, lo_live_tail = g < 2 * tg, hi_live_tail = g < 2 * tg - 4;
 
   size_t arow[MT];
+  float rsc[MT];                                           // output scale of row r of M-tile i (lane r's row)
 #pragma unroll
   for (int i = 0; i < MT; i++) {
-    int fr = sorted_ids[row0 + i * 16 + r];
+    int fr = fr_in[i];
     if (fr >= numel || fr < 0) fr = first;
     arow[i] = (size_t)(fr / a_row_div) * K;
+    float sc = As[fr / a_row_div];                         // loaded with the operands, used in the epilogue
+    if (topk_w) sc *= topk_w[fr];
+    rsc[i] = sc;
   }
   const uint8_t* __restrict__ We = Wq + (size_t)e * wq_estride;
   const uint8_t* __restrict__ Se = Ws + (size_t)e * ws_estride;
@@ -166,15 +174,15 @@ __global__ void __launch_bounds__(WAVE * SK) moe_mxfp4_kernel(
   }
 
   if constexpr (SK == 1) {
-    // C layout of a 16x16 tile: lane holds column lane % 16, rows 4g .. 4g + 3: store straight from registers
+    // C layout of a 16x16 tile: lane holds column lane % 16, rows 4g .. 4g + 3: store straight from registers; the
+    // row ids and scales come from the lanes that loaded them (lane 4g + q holds row 4g + q)
 #pragma unroll
     for (int i = 0; i < MT; i++)
 #pragma unroll
       for (int q = 0; q < 4; q++) {
-        const int fr = sorted_ids[row0 + i * 16 + 4 * g + q];
+        const int fr = __shfl(fr_in[i], 4 * g + q, WAVE);
+        const float sc = __shfl(rsc[i], 4 * g + q, WAVE);
         if (fr < 0 || fr >= numel) continue;
-        float sc = As[fr / a_row_div];
-        if (topk_w) sc *= topk_w[fr];
 #pragma unroll
         for (int j = 0; j < NPW; j++) {
           const int n = (blockIdx.x * NPW + j) * 16 + r;
@@ -182,6 +190,15 @@ __global__ void __launch_bounds__(WAVE * SK) moe_mxfp4_kernel(
         }
       }
   } else {
+    __shared__ int s_fr[MT * 16];
+    __shared__ float s_sc[MT * 16];
+    if (wave == 0 && g == 0) {
+#pragma unroll
+      for (int i = 0; i < MT; i++) {
+        s_fr[i * 16 + r] = fr_in[i];
+        s_sc[i * 16 + r] = rsc[i];
+      }
+    }
     // partial tiles to LDS as [row][col], then each thread sums SK partials of some outputs
 #pragma unroll
     for (int j = 0; j < NPW; j++)
@@ -198,14 +215,12 @@ __global__ void __launch_bounds__(WAVE * SK) moe_mxfp4_kernel(
       const int j = ti / MT, i = ti - j * MT;
       const int n = (blockIdx.x * NPW + j) * 16 + col;
       if (n >= N) continue;
-      const int fr = sorted_ids[row0 + i * 16 + row];
+      const int fr = s_fr[i * 16 + row];
       if (fr < 0 || fr >= numel) continue;
       float v = 0.f;
 #pragma unroll
       for (int s = 0; s < SK; s++) v += red[(size_t)s * TOT + idx];
-      float sc = As[fr / a_row_div];
-      if (topk_w) sc *= topk_w[fr];
-      C[(size_t)fr * N + n] = f2bf(v * sc);
+      C[(size_t)fr * N + n] = f2bf(v * s_sc[i * 16 + row]);
     }
   }
 }
@@ -225,7 +240,8 @@ int env_int(const char* name, int dflt) {
 
 // Launch shape for the decode-family kernel, from the host-known shape only (graph-capturable). Two column tiles a
 // wave. Long K (>= 8 K-tiles) splits over SK waves so that fewer dependent load batches sit on one wave: 4 while the
-// grid is small, 2 once it holds >= 12K waves' worth of tiles; short K stays in one wave (no LDS reduction), with
+// grid is small, 2 once it holds >= 12K waves' worth of tiles, in 2-tile load batches; short K stays in one wave (no
+// LDS reduction), with
 // 4-tile load batches while the grid is small. Measured on MI355X over config-2 decode widths (T = 1..64).
 // R9K_GEMM_SK / R9K_GEMM_NPW / R9K_GEMM_U override (tuning sweeps).
 Pick pick(int MT, int N, int K, int max_blocks) {
@@ -236,7 +252,7 @@ Pick pick(int MT, int N, int K, int max_blocks) {
   int SK, U;
   if (nkt >= 8) {
     SK = tiles >= 12288 ? 2 : 4;
-    U = SK == 2 ? 2 : 1;
+    U = 2;
   } else {
     SK = 1;
     U = tiles >= 8192 ? 1 : 4;
