@@ -17,19 +17,22 @@
 // experts ascending, padding value numel; expert_ids[b] = expert of block b or -1 past the end; ntpp[0] = padded
 // total. Unlike the reference kernel (atomics: row order within an expert unspecified) the scatter here is STABLE:
 // rows ascend within each expert, which is exactly align_block_size_ref's canonical order, so the tables are
-// bit-exact against it. The ids sit in LDS; after an LDS histogram and a scan of the block-padded counts, rows are
+// bit-exact against it. At decode widths (route_small_kernel) the stable order comes from a 64-bit token mask per
+// expert; elsewhere the ids sit in LDS and, after an LDS histogram and a scan of the block-padded counts, rows are
 // placed in rounds of one row per thread: a row's rank among equal ids of its wave comes from a branch-free compare
-// against all 64 lanes (v_readlane), earlier waves' rows from per-wave counts in LDS. The whole capacity (sorted_ids [cap], expert_ids [cap / blk], cap =
-// ceil((numel + E * (blk - 1)) / blk) * blk) is written, the tail with numel / -1. Barriers between phases wait for
-// LDS traffic only; global stores are never waited for inside a kernel (nothing reads them back).
+// against all 64 lanes (v_readlane), earlier waves' rows from per-wave counts in LDS. The whole capacity
+// (sorted_ids [cap], expert_ids [cap / blk], cap = ceil((numel + E * (blk - 1)) / blk) * blk) is written, the tail
+// with numel / -1. Barriers between phases wait for LDS traffic only; global stores are never waited for inside a
+// kernel unless another workgroup reads them back.
 //
 // Entry points:
-//   r9k_moe_route   the reference's one-launch routing + tables (any M; numel <= 4096: one wave per row over
-//                   ceil(M / 8) workgroups, the last to arrive builds the tables; larger numel as a top-k launch plus
-//                   a single-workgroup table launch)
-//   r9k_moe_topk    routing only (the stock top-k router's role)
-//   r9k_moe_align   tables only from given ids (vLLM's moe_align_block_size role); large numel runs as a
-//                   per-chunk histogram launch plus a scatter launch (bases from the histograms), caller scratch.
+//   r9k_moe_route        the reference's one-launch routing + tables (M <= 64: route_small_kernel; numel <= 4096:
+//                        one wave per row over ceil(M / 8) workgroups, the last to arrive builds the tables; larger
+//                        numel as a top-k launch plus a single-workgroup table launch)
+//   r9k_moe_route_quant  the same at decode widths with the experts' per-token fp8 input quant in the launch
+//   r9k_moe_topk         routing only (the stock top-k router's role)
+//   r9k_moe_align        tables only from given ids (vLLM's moe_align_block_size role); large numel runs as a
+//                        per-chunk histogram launch plus a scatter launch (bases from the histograms), caller scratch.
 #include "r9k_common.h"
 
 namespace {
@@ -331,6 +334,7 @@ constexpr int SMALL_ROWS = 64;    // token rows it routes: one bit each in the p
 constexpr int SMALL_E = 512;      // experts (EPL <= 8)
 constexpr int SMALL_CAP = 16384;  // table capacity kept in LDS
 constexpr int QRMAX = 8;          // 16-byte chunks per lane of the fused activation quant: hidden <= 4096
+constexpr int QPW = 4;            // activation rows per quant workgroup: one wave per SIMD (the quant is VALU-bound)
 
 // Wave-inclusive prefix sum of an int: Hillis-Steele over 16-lane rows (DPP row_shr 1, 2, 4, 8; lanes shifted past
 // the row start read 0), then the totals of the lower rows through v_readlane.
@@ -415,9 +419,9 @@ __device__ __forceinline__ void topk_rows(const uint16_t (&h)[NR][EPL], int E, i
 // Table build, one thread per flat row t = row * topk + k with expert e: LDS mask[e] |= 1 << row (an expert's
 // routed rows are its set bits: count = popcount; t goes to offs[e] + popcount(mask[e] & bits below row), which is
 // the stable ascending order). The tables are assembled in LDS (padding = numel, expert_ids = -1 past the end) and
-// written out with 16-byte stores. Workgroups nrt.. quantise 16 activation rows each (quant_row_wave).
-// Dynamic LDS: mask u64 [Ep], offs [Ep], scan [64], tab [cap], eids [cap / blk], lids [numel] (Ep = E rounded up
-// to 16).
+// written out with 16-byte stores. Workgroups nrt.. quantise 4 activation rows each (quant_row_wave, one wave per
+// SIMD). Dynamic LDS: mask u64 [Ep], offs [Ep], scan [64], tab [cap], eids [cap / blk], lids [numel] (Ep = E
+// rounded up to 16).
 template <int EPL>
 __global__ void __launch_bounds__(ST) route_small_kernel(
     const uint16_t* __restrict__ logits, int ldl, float* __restrict__ weights, int* __restrict__ ids,
@@ -427,8 +431,8 @@ __global__ void __launch_bounds__(ST) route_small_kernel(
   const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
   const int nrt = (M + rpw - 1) / rpw;
   if ((int)blockIdx.x >= nrt) {
-    const int row = ((int)blockIdx.x - nrt) * SW + wave;
-    if (row < M) quant_row_wave<QRMAX>(x + (size_t)row * ldx, H, xq + (size_t)row * H, xs + row, lane);
+    const int row = ((int)blockIdx.x - nrt) * QPW + wave;
+    if (wave < QPW && row < M) quant_row_wave<QRMAX>(x + (size_t)row * ldx, H, xq + (size_t)row * H, xs + row, lane);
     return;
   }
   extern __shared__ __align__(16) uint8_t smem[];
@@ -708,7 +712,7 @@ bool small_fits(int M, int E, int topk, int blk, const void* arrive, const void*
          (reinterpret_cast<uintptr_t>(x) & 15) == 0 && (reinterpret_cast<uintptr_t>(xq) & 7) == 0;
 }
 
-// One launch: the routing workgroups, then (with x) ceil(M / 16) quant workgroups.
+// One launch: the routing workgroups, then (with x) ceil(M / 4) quant workgroups.
 hipError_t launch_small(const uint16_t* logits, int ldl, float* w, int* ids, int* sorted_ids, int* expert_ids,
                         int* ntpp, int* arrive, int M, int E, int topk, int renorm, int blk, const uint16_t* x,
                         long ldx, int H, uint8_t* xq, float* xs, hipStream_t st) {
@@ -716,7 +720,7 @@ hipError_t launch_small(const uint16_t* logits, int ldl, float* w, int* ids, int
   const int Ep = (E + 15) & ~15;
   const size_t lds = (size_t)Ep * 12 + 64 * 4 + (size_t)cap * 4 + (size_t)(cap / blk) * 4 + (size_t)M * topk * 4;
   const int rpw = small_rpw(M);
-  const dim3 grid((M + rpw - 1) / rpw + (x ? (M + SW - 1) / SW : 0));
+  const dim3 grid((M + rpw - 1) / rpw + (x ? (M + QPW - 1) / QPW : 0));
 #define RS(EPLV)                                                                                                   \
   return launch_small_inst<EPLV>(grid, lds, st, logits, ldl, w, ids, sorted_ids, expert_ids, ntpp, arrive, M, E, \
                                  topk, renorm, blk, cap, rpw, x, ldx, H, xq, xs)
