@@ -510,25 +510,42 @@ __global__ void __launch_bounds__(NTH) moe_prefill_persistent_kernel(
       __builtin_amdgcn_sched_barrier(0);
       sidx = nidx;
     }
-    // tile m's output (rows and scales from its metadata slots, valid until a barrier after this)
+    // tile m's output (rows and scales from its metadata slots, valid until a barrier after this). Lane l (g = 0)
+    // and lane l + 32 (g = 1) hold the same row: runs of 4 columns at 8 qb + 4 g. One v_permlane32_swap per packed
+    // dword trades runs so that g = 0 holds columns 0-7 and 16-23 of each 32-column tile and g = 1 holds 8-15 and
+    // 24-31: two 16-byte stores per tile and lane, each instruction writing 32 contiguous bytes of 32 rows (half the
+    // store instructions of 8-byte runs, and the epilogue is bound by the rows each store touches). Every lane takes
+    // part in the swaps; padding rows only skip the stores.
     const int nl = tile_nlive(m & 3), nb = tile_nb(m);
 #pragma unroll
     for (int ii = 0; ii < 2; ii++) {
       const int row = wm * 64 + ii * 32 + c32;
-      if (row >= nl) continue;
+      const bool live = row < nl;
       const int fr = ax.rows[m & 3][row];
       float sc = ax.as[m & 1][row];
       if (topk_w) sc *= ax.tw[m & 1][row];
-      uint16_t* __restrict__ crow = C + (size_t)fr * N;
+      uint16_t* __restrict__ crow = C + (size_t)(live ? fr : 0) * N;
 #pragma unroll
       for (int j = 0; j < 4; j++) {
+        uint32_t p[4][2];
 #pragma unroll
         for (int qb = 0; qb < 4; qb++) {
-          const int n = nb * BN + wn * 128 + j * 32 + 8 * qb + 4 * g;
-          if (n < N)
-            *reinterpret_cast<uint2*>(crow + n) =
-                make_uint2(pack_bf16x2(acc[ii][j][4 * qb] * sc, acc[ii][j][4 * qb + 1] * sc),
-                           pack_bf16x2(acc[ii][j][4 * qb + 2] * sc, acc[ii][j][4 * qb + 3] * sc));
+          p[qb][0] = pack_bf16x2(acc[ii][j][4 * qb] * sc, acc[ii][j][4 * qb + 1] * sc);
+          p[qb][1] = pack_bf16x2(acc[ii][j][4 * qb + 2] * sc, acc[ii][j][4 * qb + 3] * sc);
+        }
+#pragma unroll
+        for (int h = 0; h < 2; h++) {                  // column runs 16 h .. 16 h + 15 of the 32-column tile
+          uint32_t got[2];
+#pragma unroll
+          for (int k = 0; k < 2; k++) {
+            // swap(old = A, src = B): a low lane receives its partner's A, a high lane its partner's B
+            const auto r = __builtin_amdgcn_permlane32_swap(p[2 * h][k], p[2 * h + 1][k], false, false);
+            got[k] = g == 0 ? r[1] : r[0];
+          }
+          const uint4 v = g == 0 ? make_uint4(p[2 * h][0], p[2 * h][1], got[0], got[1])
+                                 : make_uint4(got[0], got[1], p[2 * h + 1][0], p[2 * h + 1][1]);
+          const int n = nb * BN + wn * 128 + j * 32 + 16 * h + 8 * g;
+          if (live && n < N) *reinterpret_cast<uint4*>(crow + n) = v;
         }
       }
     }
@@ -547,7 +564,7 @@ int r9k_prefill_launch(long a, long as, long wq, long ws, long c, long sorted_id
   if (K % KC) return -2;
   if (max_blocks <= 0 || numel <= 0) return 0;
   if (max_blocks > 65535) return -3;
-  if ((a & 15) || (wq & 15) || (ws & 3) || (c & 7)) return -3;              // 16-byte DMA sources, 8-byte stores
+  if ((a & 15) || (wq & 15) || (ws & 3) || (c & 15)) return -3;             // 16-byte DMA sources and stores
   const int nnb = (N / 16 + NT16 - 1) / NT16;
   const long a_rows = ((long)numel + a_row_div - 1) / a_row_div;
   if (a_rows * K >= (1L << 31) || (long)N * K / 2 >= (1L << 31) || (long)numel * 4 >= (1L << 31)) return -3;
