@@ -28,6 +28,7 @@ namespace {
 using namespace r9k;
 
 typedef int v8i __attribute__((ext_vector_type(8)));
+typedef int v4i __attribute__((ext_vector_type(4)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
@@ -471,6 +472,12 @@ __global__ void __launch_bounds__(NTH) moe_prefill_persistent_kernel(
   const int wm = wave >> 1, wn = wave & 1;
   const int g = lane >> 5, c32 = lane & 31;
   const FragOff fo = frag_offsets(wm, wn, lane);
+  // the output as a raw buffer (numel * N * 2 bytes, checked < 2^31 by the host): the epilogue's 16-byte stores go
+  // out unconditionally and a padding row or a column past N stores at offset `cbytes`, which the buffer's range
+  // check drops. Every wave so issues exactly 16 stores per tile, a fixed count the vmcnt waits below account for.
+  const uint32_t cbytes = (uint32_t)numel * (uint32_t)N * 2u;
+  const auto crs = __builtin_amdgcn_make_buffer_rsrc(C, (short)0, (int)cbytes, 0x00020000);
+  constexpr int EPI_STORES = 16;
 
   issue_group(-3);
   issue_group(-2);
@@ -498,13 +505,24 @@ __global__ void __launch_bounds__(NTH) moe_prefill_persistent_kernel(
       const int nidx = sidx == NSTAGE - 1 ? 0 : sidx + 1;
       if (i + 1 < iters) {
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");    // this wave's reads of chunk i are done
-        if (i + 2 < iters) asm volatile("s_waitcnt vmcnt(11)" ::: "memory");
-        else asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
+        // chunk i + 1 (group i - 2) is complete once no more than its 2 metadata dwords, group i - 1 (when issued)
+        // and the previous tile's 16 output stores (when they came after group i - 2: c = 0 or 1) are outstanding
+        const bool epi = m > 0 && c < 2;
+        if (i + 2 < iters) {
+          if (epi) asm volatile("s_waitcnt vmcnt(27)" ::: "memory");
+          else asm volatile("s_waitcnt vmcnt(11)" ::: "memory");
+        } else {
+          if (epi) asm volatile("s_waitcnt vmcnt(18)" ::: "memory");
+          else asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
+        }
         asm volatile("s_barrier" ::: "memory");
-        if (i + 3 < iters) issue_group(i);
       }
       __builtin_amdgcn_sched_barrier(0);
       mfma_kfrag(acc, F1);
+      __builtin_amdgcn_sched_barrier(0);
+      // the next DMA group goes out behind the second-half MFMAs, so its issue overlaps their execution instead of
+      // holding them back (the stage it fills, chunk i's, was released by the barrier)
+      if (i + 3 < iters) issue_group(i);
       __builtin_amdgcn_sched_barrier(0);
       if (i + 1 < iters) load_kfrag(st[nidx], fo, 0, F0);     // first half of chunk i + 1, under the second half
       __builtin_amdgcn_sched_barrier(0);
@@ -524,7 +542,7 @@ __global__ void __launch_bounds__(NTH) moe_prefill_persistent_kernel(
       const int fr = ax.rows[m & 3][row];
       float sc = ax.as[m & 1][row];
       if (topk_w) sc *= ax.tw[m & 1][row];
-      uint16_t* __restrict__ crow = C + (size_t)(live ? fr : 0) * N;
+      const uint32_t rowoff = (uint32_t)(live ? fr : 0) * (uint32_t)N;
 #pragma unroll
       for (int j = 0; j < 4; j++) {
         uint32_t p[4][2];
@@ -542,10 +560,11 @@ __global__ void __launch_bounds__(NTH) moe_prefill_persistent_kernel(
             const auto r = __builtin_amdgcn_permlane32_swap(p[2 * h][k], p[2 * h + 1][k], false, false);
             got[k] = g == 0 ? r[1] : r[0];
           }
-          const uint4 v = g == 0 ? make_uint4(p[2 * h][0], p[2 * h][1], got[0], got[1])
-                                 : make_uint4(got[0], got[1], p[2 * h + 1][0], p[2 * h + 1][1]);
+          const v4i v = g == 0 ? (v4i){(int)p[2 * h][0], (int)p[2 * h][1], (int)got[0], (int)got[1]}
+                               : (v4i){(int)got[0], (int)got[1], (int)p[2 * h + 1][0], (int)p[2 * h + 1][1]};
           const int n = nb * BN + wn * 128 + j * 32 + 16 * h + 8 * g;
-          if (live && n < N) *reinterpret_cast<uint4*>(crow + n) = v;
+          const uint32_t off = (live && n < N) ? (rowoff + (uint32_t)n) * 2u : cbytes;
+          __builtin_amdgcn_raw_buffer_store_b128(v, crs, (int)off, 0, 0);
         }
       }
     }
@@ -567,7 +586,9 @@ int r9k_prefill_launch(long a, long as, long wq, long ws, long c, long sorted_id
   if ((a & 15) || (wq & 15) || (ws & 3) || (c & 15)) return -3;             // 16-byte DMA sources and stores
   const int nnb = (N / 16 + NT16 - 1) / NT16;
   const long a_rows = ((long)numel + a_row_div - 1) / a_row_div;
-  if (a_rows * K >= (1L << 31) || (long)N * K / 2 >= (1L << 31) || (long)numel * 4 >= (1L << 31)) return -3;
+  if (a_rows * K >= (1L << 31) || (long)N * K / 2 >= (1L << 31) || (long)numel * 4 >= (1L << 31) ||
+      (long)numel * N * 2 >= (1L << 31))
+    return -3;
   if (K / KC >= 3 && getenv_flag_off_pf("R9K_PREFILL_PERSIST") == 0) {
     static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(moe_prefill_persistent_kernel),
                                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)SMEM_P);
