@@ -74,7 +74,15 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
 __device__ __forceinline__ float lo16(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float hi16(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
+// Four fp32 values to e4m3 bytes, a in the low byte. V_CVT_PK_FP8_F32 (OCP e4m3 on gfx950, round to nearest even)
+// gives f32_to_e4m3's bytes for every |v| <= 464, signed zeros and the subnormal grid included; a lane holding a NaN
+// or a larger magnitude (codes 0x7f with the sign, which the hardware need not produce) takes the bit routine.
 __device__ __forceinline__ uint32_t pack4_e4m3(float a, float b, float c, float d) {
+  if (fabsf(a) <= 464.f && fabsf(b) <= 464.f && fabsf(c) <= 464.f && fabsf(d) <= 464.f) {
+    int r = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+    r = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, r, true);
+    return (uint32_t)r;
+  }
   return f32_to_e4m3(a) | (f32_to_e4m3(b) << 8) | (f32_to_e4m3(c) << 16) | (f32_to_e4m3(d) << 24);
 }
 
