@@ -26,6 +26,10 @@ CFLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",  # no packed fp32 VALU ops
     "-Wno-unused-command-line-argument",
 ]
+# Per-source additions. The prefill GEMM interleaves its MFMAs with LDS reads and DMA issue under scheduling
+# barriers; machine sinking would move the MFMAs (pure operations) past the loop's wait/barrier branches into one
+# block at the end of the loop body and undo that order.
+FILE_FLAGS = {"r9k_moe_prefill.hip": ["-mllvm", "-disable-machine-sink"]}
 
 
 def hipcc() -> str:
@@ -37,7 +41,7 @@ def hipcc() -> str:
 
 def _compile(src: str) -> str:
     obj = os.path.join(BUILD, os.path.basename(src).replace(".hip", ".o"))
-    cmd = [hipcc(), *CFLAGS, "-I", CSRC, "-c", src, "-o", obj]
+    cmd = [hipcc(), *CFLAGS, *FILE_FLAGS.get(os.path.basename(src), []), "-I", CSRC, "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode:
         raise RuntimeError(f"hipcc failed for {src}:\n{r.stdout}\n{r.stderr}")

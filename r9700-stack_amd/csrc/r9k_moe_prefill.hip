@@ -341,6 +341,36 @@ __device__ __forceinline__ void mfma_kfrag(v16f (&acc)[2][4], const KFrag& F) {
   }
 }
 
+// The 8 MFMAs of one K half from F (those of M tile i only when bit i of the wave-uniform `live` is set: a tile of
+// 32 padding rows is skipped), MFMA k followed by extra(k) and the k-th of 8 groups of LDS reads that fill G from
+// half `ks` of stage S. An MFMA holds its wave at issue until the matrix pipe takes it, so reads (or DMA
+// issue) placed only after the last MFMA of a half run while the pipe idles; spread one group per MFMA, they run
+// under the MFMAs instead. Scheduling barriers keep the order (G is a register set no queued MFMA still reads).
+template <typename Extra>
+__device__ __forceinline__ void mfma_load_kfrag(v16f (&acc)[2][4], const KFrag& F, const Stage& S,
+                                                const FragOff& f, int ks, KFrag& G, int live, Extra extra) {
+#pragma unroll
+  for (int k = 0; k < 8; k++) {
+    const int i = k >> 2, j = k & 3;
+    const v8i af = (v8i){(int)F.lo[i].x, (int)F.lo[i].y, (int)F.lo[i].z, (int)F.lo[i].w,
+                         (int)F.hi[i].x, (int)F.hi[i].y, (int)F.hi[i].z, (int)F.hi[i].w};
+    const v8i wf = (v8i){(int)F.w[j].x, (int)F.w[j].y, (int)F.w[j].z, (int)F.w[j].w, 0, 0, 0, 0};
+    if (live & (1 << i))
+      acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(wf, af, acc[i][j], 4, 0, 0, F.sb[j], 0, E8M0_ONE);
+    __builtin_amdgcn_sched_barrier(0);
+    extra(k);
+    if (k < 4) {
+      G.w[k] = *reinterpret_cast<const u32x4*>(&S.b[f.b + k * 2048 + ks * 512]);
+      G.sb[k] = S.s[f.s + k * 128 + ks * 32];
+    } else {
+      const int ii = (k - 4) >> 1;
+      if ((k & 1) == 0) G.lo[ii] = *reinterpret_cast<const u32x4*>(&S.a[f.a[0][ks] + ii * 4096]);
+      else G.hi[ii] = *reinterpret_cast<const u32x4*>(&S.a[f.a[1][ks] + ii * 4096]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
 // The same tiles and numerics as moe_prefill_kernel, but each workgroup (one per CU) walks a list of tiles and the
 // K-chunk stream runs on across tile boundaries, with DMA three chunks ahead of the MFMAs. Within a chunk the two
 // 64-K halves are software-pipelined: the second half's fragments are read from LDS under the first half's MFMAs,
@@ -436,37 +466,49 @@ __global__ void __launch_bounds__(NTH) moe_prefill_persistent_kernel(
   const uint32_t ldum = lds_addr(&ax.dummy[0]);
   const uint32_t doff = lane * 4;                              // dummy loads: sorted_ids[lane], always valid
 
-  // group j (issued after barrier j, j >= -3): chunk j + 3, then the metadata dwords
-  auto issue_group = [&](int j) {
-    const int ci = j + 3, m = ci / nchunk, c = ci - m * nchunk;
-    if (c == 0) setup_issue(m);
-    const uint32_t so = (uint32_t)((ci % NSTAGE) * (int)sizeof(Stage));
-#pragma unroll
-    for (int p = 0; p < 4; p++) dma16s(A, ga[p] + (uint32_t)(c * KC), la0 + so + p * 512 * 16);
-#pragma unroll
-    for (int p = 0; p < 2; p++) dma16s(wbase, gb[p] + (uint32_t)(c * 1024), lb0 + so + p * 512 * 16);
-    dma4s(sbase, gs + (uint32_t)(c * 64), ls0 + so);
-    // sorted_ids and expert id of tile (j + 6) / nchunk
-    const int j6 = j + 6, m0 = j6 / nchunk;
-    if (j6 - m0 * nchunk == 0 && m0 < ntiles) {
-      const int slot = m0 & 3, rb = tile_rb(m0);
-      if (wave < 4) dma4s(sorted_ids, (uint32_t)(rb * BM + wave * 64 + lane) * 4, lds_addr(&ax.rows[slot][wave * 64]));
-      else if (wave == 4) dma4s(expert_ids, (uint32_t)rb * 4, lds_addr(&ax.eid[slot][0]));
-      else dma4s(sorted_ids, doff, ldum);
-    } else {
-      dma4s(sorted_ids, doff, ldum);
+  // group j (issued after barrier j, j >= -3): chunk j + 3, then the metadata dwords, in 8 parts that the main
+  // loop places one behind each MFMA of a K half (part 0: the tile set-up on a tile's first chunk and A piece 0;
+  // 1-3: A pieces; 4-5: the weight pieces, 5 also the exponents; 6: sorted_ids / expert id of the tile that starts
+  // at chunk j + 6; 7: the per-row scales of a tile, with its first chunk). The positions of chunks j + 3 and j + 6
+  // advance per group (no division by the chunk count).
+  int g_m = 0, g_c = 0, g_s = 0;                               // tile, chunk within it, stage of chunk j + 3
+  int h_m = 3 / nchunk, h_c = 3 % nchunk;                      // tile and chunk within it of chunk j + 6
+  auto issue_part = [&](int part) {
+    const uint32_t so = (uint32_t)(g_s * (int)sizeof(Stage));
+    if (part == 0 && g_c == 0) setup_issue(g_m);
+    if (part < 4) dma16s(A, ga[part] + (uint32_t)(g_c * KC), la0 + so + part * 512 * 16);
+    if (part == 4 || part == 5)
+      dma16s(wbase, gb[part - 4] + (uint32_t)(g_c * 1024), lb0 + so + (part - 4) * 512 * 16);
+    if (part == 5) dma4s(sbase, gs + (uint32_t)(g_c * 64), ls0 + so);
+    if (part == 6) {
+      if (h_c == 0 && h_m < ntiles) {
+        const int slot = h_m & 3, rb = tile_rb(h_m);
+        if (wave < 4) dma4s(sorted_ids, (uint32_t)(rb * BM + wave * 64 + lane) * 4, lds_addr(&ax.rows[slot][wave * 64]));
+        else if (wave == 4) dma4s(expert_ids, (uint32_t)rb * 4, lds_addr(&ax.eid[slot][0]));
+        else dma4s(sorted_ids, doff, ldum);
+      } else {
+        dma4s(sorted_ids, doff, ldum);
+      }
     }
-    // per-row scales of tile m, with its first chunk
-    if (c == 0) {
-      const int r = (wave & 3) * 64 + lane;
-      int fr = r < issue_nl ? ax.rows[issue_slot][r] : ax.rows[issue_slot][0];
-      fr = (fr >= 0 && fr < numel) ? fr : 0;
-      if (wave < 4) dma4s(As, div_by((uint32_t)fr, rdiv) * 4, lds_addr(&ax.as[m & 1][wave * 64]));
-      else if (topk_w) dma4s(topk_w, (uint32_t)fr * 4, lds_addr(&ax.tw[m & 1][(wave - 4) * 64]));
-      else dma4s(sorted_ids, doff, ldum);
-    } else {
-      dma4s(sorted_ids, doff, ldum);
+    if (part == 7) {
+      if (g_c == 0) {
+        const int r = (wave & 3) * 64 + lane;
+        int fr = r < issue_nl ? ax.rows[issue_slot][r] : ax.rows[issue_slot][0];
+        fr = (fr >= 0 && fr < numel) ? fr : 0;
+        if (wave < 4) dma4s(As, div_by((uint32_t)fr, rdiv) * 4, lds_addr(&ax.as[g_m & 1][wave * 64]));
+        else if (topk_w) dma4s(topk_w, (uint32_t)fr * 4, lds_addr(&ax.tw[g_m & 1][(wave - 4) * 64]));
+        else dma4s(sorted_ids, doff, ldum);
+      } else {
+        dma4s(sorted_ids, doff, ldum);
+      }
+      if (++g_c == nchunk) g_c = 0, g_m++;
+      g_s = g_s == NSTAGE - 1 ? 0 : g_s + 1;
+      if (++h_c == nchunk) h_c = 0, h_m++;
     }
+  };
+  auto issue_group = [&]() {
+#pragma unroll
+    for (int part = 0; part < 8; part++) issue_part(part);
   };
 
   const int wm = wave >> 1, wn = wave & 1;
@@ -479,9 +521,9 @@ __global__ void __launch_bounds__(NTH) moe_prefill_persistent_kernel(
   const auto crs = __builtin_amdgcn_make_buffer_rsrc(C, (short)0, (int)cbytes, 0x00020000);
   constexpr int EPI_STORES = 16;
 
-  issue_group(-3);
-  issue_group(-2);
-  issue_group(-1);
+  issue_group();                                               // groups -3, -2, -1: chunks 0, 1, 2
+  issue_group();
+  issue_group();
   asm volatile("s_waitcnt vmcnt(20)" ::: "memory");             // chunk 0 (younger: 2 + 9 + 9)
   asm volatile("s_barrier" ::: "memory");
   KFrag F0, F1;
@@ -493,14 +535,13 @@ __global__ void __launch_bounds__(NTH) moe_prefill_persistent_kernel(
     for (int a = 0; a < 2; a++)
 #pragma unroll
       for (int b = 0; b < 4; b++) acc[a][b] = (v16f){};
+    // this wave's M tiles (rows wm * 64 + 32 i ..) that hold a live row (the live rows are a prefix of the block)
+    const int nlm = __builtin_amdgcn_readfirstlane(tile_nlive(m & 3));
+    const int live = __builtin_amdgcn_readfirstlane((wm * 64 < nlm ? 1 : 0) | (wm * 64 + 32 < nlm ? 2 : 0));
     for (int c = 0; c < nchunk; c++, i++) {
-      // MFMAs are queued, not executed, when issued, and an LDS read into a fragment register waits until every
-      // queued MFMA that reads it has started. So each fragment set is refilled only after the other set's MFMAs
-      // have been issued behind its own: F0 holds chunk i's first half (read at the end of iteration i - 1).
-      // (Scheduling barriers keep this order.)
-      mfma_kfrag(acc, F0);
-      __builtin_amdgcn_sched_barrier(0);
-      load_kfrag(st[sidx], fo, 1, F1);                         // second half of chunk i, under the first half
+      // F0 holds chunk i's first K half (read under the MFMAs of iteration i - 1); the second half's reads go out
+      // between its MFMAs
+      mfma_load_kfrag(acc, F0, st[sidx], fo, 1, F1, live, [](int) {});
       __builtin_amdgcn_sched_barrier(0);
       const int nidx = sidx == NSTAGE - 1 ? 0 : sidx + 1;
       if (i + 1 < iters) {
@@ -518,13 +559,11 @@ __global__ void __launch_bounds__(NTH) moe_prefill_persistent_kernel(
         asm volatile("s_barrier" ::: "memory");
       }
       __builtin_amdgcn_sched_barrier(0);
-      mfma_kfrag(acc, F1);
-      __builtin_amdgcn_sched_barrier(0);
-      // the next DMA group goes out behind the second-half MFMAs, so its issue overlaps their execution instead of
-      // holding them back (the stage it fills, chunk i's, was released by the barrier)
-      if (i + 3 < iters) issue_group(i);
-      __builtin_amdgcn_sched_barrier(0);
-      if (i + 1 < iters) load_kfrag(st[nidx], fo, 0, F0);     // first half of chunk i + 1, under the second half
+      // second-half MFMAs, each followed by a part of the next DMA group (into chunk i's stage, released by the
+      // barrier) and reads of chunk i + 1's first half (after the last chunk they read a stale stage, unused)
+      mfma_load_kfrag(acc, F1, st[nidx], fo, 0, F0, live, [&](int k) {
+        if (i + 3 < iters) issue_part(k);
+      });
       __builtin_amdgcn_sched_barrier(0);
       sidx = nidx;
     }
@@ -534,7 +573,7 @@ __global__ void __launch_bounds__(NTH) moe_prefill_persistent_kernel(
     // 24-31: two 16-byte stores per tile and lane, each instruction writing 32 contiguous bytes of 32 rows (half the
     // store instructions of 8-byte runs, and the epilogue is bound by the rows each store touches). Every lane takes
     // part in the swaps; padding rows only skip the stores.
-    const int nl = tile_nlive(m & 3), nb = tile_nb(m);
+    const int nl = nlm, nb = tile_nb(m);
 #pragma unroll
     for (int ii = 0; ii < 2; ii++) {
       const int row = wm * 64 + ii * 32 + c32;
