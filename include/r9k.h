@@ -31,6 +31,16 @@ int r9k_moe_mxfp4a8(long a, long as, long wq, long ws, long wref, long c, long s
                     long ntpp, long topk_w, long ws_estride, long wref_estride, int max_blocks, int numel,
                     int a_row_div, int K, int N, int WV, int SK, int NPW, int MT, long stream);
 
+/* Fused decode variants of the same GEMM. Replaces kernels/r9k_moe_mxfp4a8.hip:618-626 (r9k_moe_mxfp4a8_f).
+ * fuse 1: gate_up with the activation in the epilogue: c fp32 [numel][N / 2] = silu(g) * u of the bf16-rounded gate
+ * (columns n) and up (columns n + N / 2) outputs; N % 32 == 0. fuse 2: down with a = fp32 [numel][K] (fuse 1's
+ * output) quantised per row on load (e4m3, scale absmax / 448, the r9k_silu_mul_quant_fp8 rule), as ignored (may be
+ * 0), a_row_div 1. Routing blocks of 16 rows: MT & 7 must be 1 (-7). Results equal the unfused chain's bit for bit.
+ * -8 fuse not 1 or 2; other errors as r9k_moe_mxfp4a8. */
+int r9k_moe_mxfp4a8_f(int fuse, long a, long as, long wq, long ws, long wref, long c, long sorted_ids,
+                      long expert_ids, long ntpp, long topk_w, long ws_estride, long wref_estride, int max_blocks,
+                      int numel, int a_row_div, int K, int N, int WV, int SK, int NPW, int MT, long stream);
+
 /* Prefill entry of the same GEMM. Replaces kernels/r9k_moe_mxfp4a8.hip:1227-1230 (r9k_moe_4bit_prefill).
  * nv: 0 MXFP4 (2, the reference's folded MXFP4, is the same data here); 1 NVFP4 and 3 fp8 weights return -8.
  * Tables built with blk = r9k_moe_prefill_bm(cfg). -7 unknown cfg, -2 K % r9k_moe_prefill_bk(cfg). */

@@ -86,6 +86,15 @@ __device__ __forceinline__ uint32_t pack4_e4m3(float a, float b, float c, float 
   return f32_to_e4m3(a) | (f32_to_e4m3(b) << 8) | (f32_to_e4m3(c) << 16) | (f32_to_e4m3(d) << 24);
 }
 
+// silu(g) * u with g, u the stored bf16 values, evaluated as (g / (1 + exp(-g))) * u in fp32 with the hardware
+// exponential (__expf, as the reference: kernels/r9k_moe_mxfp4a8.hip:526) and a reciprocal-multiply division
+// (V_RCP_F32, 1 ulp; within 2 ulp of the reference's IEEE division, whose sequence is 10 instructions an element in a
+// VALU-bound kernel). A code can move one step where the product sits within a few ulp of an e4m3 rounding point.
+// The standalone SiLU kernel and the gate_up GEMM's fused epilogue both use this one definition.
+__device__ __forceinline__ float silu_mul(float gv, float uv) {
+  return gv * __builtin_amdgcn_rcpf(1.f + __expf(-gv)) * uv;
+}
+
 // One wave quantises one row of K bf16 values (K % 8 == 0, K <= 512 * RMAX, the row 16-byte aligned, the code row
 // 8-byte aligned) to OCP e4m3 with a per-row scale:
 //   amax = max(max_k |x_k|, 1e-12);  inv = 448 / amax;  q_k = e4m3_rne(x_k * inv);  s = amax / 448.

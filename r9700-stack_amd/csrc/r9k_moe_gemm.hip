@@ -63,7 +63,15 @@ __device__ __forceinline__ uint32_t ld1(const uint8_t* p) {
 // U*NPW*MT MFMAs run. Addresses are clamped instead of branched around (a lane past a partial K-tile, or a batch
 // slot past the wave's range, re-reads a valid location and its operand is zeroed by select), so the compiler
 // never has to drain the memory queue inside a batch.
-template <int MT, int NPW, int SK, int U>
+//
+// FUSE (the reference's r9k_moe_mxfp4a8_f, kernels/r9k_moe_mxfp4a8.hip:236-250, 358-368, 452-467; MT = 1):
+//   1: gate_up with the activation in the epilogue. The workgroup's two column tiles are gate tile x and the up
+//      tile N/32 further (NPW = 2), and it writes h = silu(bf16(g)) * bf16(u) as fp32 [numel, N/2] -- g and u
+//      rounded exactly as the unfused kernel stores them, the activation the standalone SiLU kernel's.
+//   2: down with fp32 A rows [numel, K] (h) quantised on load: each lane group of a row first takes the row's
+//      absmax over all K, then every A chunk is encoded as e4m3(h * (448 / amax)) and the row scale amax / 448
+//      replaces As -- the per-row quant of the standalone SiLU kernel, so fused and unfused results are identical.
+template <int MT, int NPW, int SK, int U, int FUSE>
 __global__ void __launch_bounds__(WAVE * SK) moe_mxfp4_kernel(
     const uint8_t* __restrict__ A, const float* __restrict__ As, const uint8_t* __restrict__ Wq,
     const uint8_t* __restrict__ Ws, uint16_t* __restrict__ C, const int* __restrict__ sorted_ids,
@@ -71,6 +79,7 @@ __global__ void __launch_bounds__(WAVE * SK) moe_mxfp4_kernel(
     long wq_estride, long ws_estride, int numel, int a_row_div, int K, int N, int blk, int subs) {
   constexpr int BLK = 16 * MT;
   constexpr bool NTL = MT == 1;                            // decode: every weight byte is read once
+  static_assert(FUSE == 0 || (MT == 1 && (FUSE == 2 || NPW == 2)), "fused variants: MT = 1; gate_up NPW = 2");
   extern __shared__ float red[];
 
   const int rb = blockIdx.y / subs, sub = blockIdx.y - rb * subs;
@@ -99,14 +108,38 @@ __global__ void __launch_bounds__(WAVE * SK) moe_mxfp4_kernel(
 
   size_t arow[MT];
   float rsc[MT];                                           // output scale of row r of M-tile i (lane r's row)
+  float a_inv[MT];                                         // FUSE 2: 448 / row absmax
 #pragma unroll
   for (int i = 0; i < MT; i++) {
     int fr = fr_in[i];
     if (fr >= numel || fr < 0) fr = first;
     arow[i] = (size_t)(fr / a_row_div) * K;
-    float sc = As[fr / a_row_div];                         // loaded with the operands, used in the epilogue
-    if (topk_w) sc *= topk_w[fr];
-    rsc[i] = sc;
+    if constexpr (FUSE == 2) {
+      // lanes r, r + 16, r + 32, r + 48 each take a quarter of row r (K % 32 == 0), 8 loads in flight at a time
+      const float4* q4 = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(A) + arow[i] + g * (K / 4));
+      const int n4 = K / 16;
+      float m = 0.f;
+      for (int k0 = 0; k0 < n4; k0 += 8) {
+        float4 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) v[u] = q4[min(k0 + u, n4 - 1)];
+#pragma unroll
+        for (int u = 0; u < 8; u++)
+          m = fmaxf(m, fmaxf(fmaxf(fabsf(v[u].x), fabsf(v[u].y)), fmaxf(fabsf(v[u].z), fabsf(v[u].w))));
+      }
+      m = fmaxf(m, __shfl_xor(m, 16, WAVE));
+      m = fmaxf(m, __shfl_xor(m, 32, WAVE));
+      const float amax = fmaxf(m, 1e-12f);
+      a_inv[i] = 448.f / amax;
+      float sc = amax / 448.f;
+      if (topk_w) sc *= topk_w[fr];
+      rsc[i] = sc;
+    } else {
+      a_inv[i] = 0.f;
+      float sc = As[fr / a_row_div];                       // loaded with the operands, used in the epilogue
+      if (topk_w) sc *= topk_w[fr];
+      rsc[i] = sc;
+    }
   }
   const uint8_t* __restrict__ We = Wq + (size_t)e * wq_estride;
   const uint8_t* __restrict__ Se = Ws + (size_t)e * ws_estride;
@@ -114,7 +147,7 @@ __global__ void __launch_bounds__(WAVE * SK) moe_mxfp4_kernel(
   const uint8_t* stile[NPW];
 #pragma unroll
   for (int j = 0; j < NPW; j++) {
-    int nt = blockIdx.x * NPW + j;
+    int nt = FUSE == 1 ? (int)blockIdx.x + j * (NT / 2) : (int)blockIdx.x * NPW + j;
     nt = nt < NT ? nt : NT - 1;                            // out-of-range tiles compute a copy, never stored
     wtile[j] = We + (size_t)nt * (size_t)(8 * K);
     stile[j] = Se + (size_t)nt * (size_t)(16 * KB);
@@ -131,6 +164,7 @@ __global__ void __launch_bounds__(WAVE * SK) moe_mxfp4_kernel(
     u32x4 bf[U][NPW];
     uint32_t sb[U][NPW];
     uint4 alo[U][MT], ahi[U][MT];
+    float4 flo[FUSE == 2 ? U : 1][MT][4], fhi[FUSE == 2 ? U : 1][MT][4];   // FUSE 2: the fp32 A chunks
 #pragma unroll
     for (int u = 0; u < U; u++) {
       const int k = min(kt + u, kt1 - 1);
@@ -145,14 +179,39 @@ __global__ void __launch_bounds__(WAVE * SK) moe_mxfp4_kernel(
       const int olo = full ? 16 * g : a_lo_tail, ohi = full ? 64 + 16 * g : a_hi_tail;
 #pragma unroll
       for (int i = 0; i < MT; i++) {
-        const uint8_t* ap = A + arow[i] + (size_t)k * KT;
-        alo[u][i] = *reinterpret_cast<const uint4*>(ap + olo);
-        ahi[u][i] = *reinterpret_cast<const uint4*>(ap + ohi);
+        if constexpr (FUSE == 2) {
+          const float* ap = reinterpret_cast<const float*>(A) + arow[i] + (size_t)k * KT;
+#pragma unroll
+          for (int v = 0; v < 4; v++) {
+            flo[u][i][v] = reinterpret_cast<const float4*>(ap + olo)[v];
+            fhi[u][i][v] = reinterpret_cast<const float4*>(ap + ohi)[v];
+          }
+        } else {
+          const uint8_t* ap = A + arow[i] + (size_t)k * KT;
+          alo[u][i] = *reinterpret_cast<const uint4*>(ap + olo);
+          ahi[u][i] = *reinterpret_cast<const uint4*>(ap + ohi);
+        }
       }
     }
 #pragma unroll
     for (int u = 0; u < U; u++) {
       const int k = kt + u;
+      if constexpr (FUSE == 2) {
+        // the fp32 chunks to e4m3 codes (16 bytes each half), as the standalone per-row quant encodes them
+#pragma unroll
+        for (int i = 0; i < MT; i++) {
+          const float s = a_inv[i];
+          uint32_t wl[4], wh[4];
+#pragma unroll
+          for (int v = 0; v < 4; v++) {
+            const float4 a = flo[u][i][v], b = fhi[u][i][v];
+            wl[v] = pack4_e4m3(a.x * s, a.y * s, a.z * s, a.w * s);
+            wh[v] = pack4_e4m3(b.x * s, b.y * s, b.z * s, b.w * s);
+          }
+          alo[u][i] = make_uint4(wl[0], wl[1], wl[2], wl[3]);
+          ahi[u][i] = make_uint4(wh[0], wh[1], wh[2], wh[3]);
+        }
+      }
       if (k < kt1) {
         const bool full = k < nkt_full;
         const bool bl = full || b_live_tail, lo = full || lo_live_tail, hi = full || hi_live_tail;
@@ -183,10 +242,17 @@ __global__ void __launch_bounds__(WAVE * SK) moe_mxfp4_kernel(
         const int fr = __shfl(fr_in[i], 4 * g + q, WAVE);
         const float sc = __shfl(rsc[i], 4 * g + q, WAVE);
         if (fr < 0 || fr >= numel) continue;
+        if constexpr (FUSE == 1) {
+          const int n = blockIdx.x * 16 + r, Nh = N / 2;
+          if (n < Nh)
+            reinterpret_cast<float*>(C)[(size_t)fr * Nh + n] =
+                silu_mul(bf2f(f2bf(acc[0][i][q] * sc)), bf2f(f2bf(acc[1][i][q] * sc)));
+        } else {
 #pragma unroll
-        for (int j = 0; j < NPW; j++) {
-          const int n = (blockIdx.x * NPW + j) * 16 + r;
-          if (n < N) C[(size_t)fr * N + n] = f2bf(acc[j][i][q] * sc);
+          for (int j = 0; j < NPW; j++) {
+            const int n = (blockIdx.x * NPW + j) * 16 + r;
+            if (n < N) C[(size_t)fr * N + n] = f2bf(acc[j][i][q] * sc);
+          }
         }
       }
   } else {
@@ -210,6 +276,26 @@ __global__ void __launch_bounds__(WAVE * SK) moe_mxfp4_kernel(
       }
     __syncthreads();
     constexpr int TOT = NPW * MT * 256;
+    if constexpr (FUSE == 1) {
+      // gate (tile 0) and up (tile 1) partials of the same row and column, summed in the unfused kernel's order
+      const int Nh = N / 2;
+      for (int idx = tid; idx < MT * 256; idx += WAVE * SK) {
+        const int col = idx & 15, row = (idx >> 4) & 15, i = idx >> 8;
+        const int n = blockIdx.x * 16 + col;
+        if (n >= Nh) continue;
+        const int fr = s_fr[i * 16 + row];
+        if (fr < 0 || fr >= numel) continue;
+        float vg = 0.f, vu = 0.f;
+#pragma unroll
+        for (int s = 0; s < SK; s++) {
+          vg += red[(size_t)s * TOT + idx];
+          vu += red[(size_t)s * TOT + MT * 256 + idx];
+        }
+        const float sc = s_sc[i * 16 + row];
+        reinterpret_cast<float*>(C)[(size_t)fr * Nh + n] = silu_mul(bf2f(f2bf(vg * sc)), bf2f(f2bf(vu * sc)));
+      }
+      return;
+    }
     for (int idx = tid; idx < TOT; idx += WAVE * SK) {
       const int col = idx & 15, row = (idx >> 4) & 15, ti = idx >> 8;   // ti = j * MT + i
       const int j = ti / MT, i = ti - j * MT;
@@ -264,37 +350,55 @@ Pick pick(int MT, int N, int K, int max_blocks) {
   return {MT, NPW, SK, U};
 }
 
-template <int MT, int NPW, int SK, int U>
+template <int MT, int NPW, int SK, int U, int FUSE = 0>
 int launch_one(dim3 grid, hipStream_t st, long a, long as, long wq, long ws, long c, long sorted_ids,
                long expert_ids, long ntpp, long topk_w, long wq_estride, long ws_estride, int numel, int a_row_div,
                int K, int N, int blk, int subs) {
   const size_t smem = SK > 1 ? (size_t)SK * NPW * MT * 256 * sizeof(float) : 0;
-  hipLaunchKernelGGL((moe_mxfp4_kernel<MT, NPW, SK, U>), grid, dim3(WAVE * SK), smem, st, (const uint8_t*)a,
+  hipLaunchKernelGGL((moe_mxfp4_kernel<MT, NPW, SK, U, FUSE>), grid, dim3(WAVE * SK), smem, st, (const uint8_t*)a,
                      (const float*)as, (const uint8_t*)wq, (const uint8_t*)ws, (uint16_t*)c, (const int*)sorted_ids,
                      (const int*)expert_ids, (const int*)ntpp, (const float*)topk_w, wq_estride, ws_estride, numel,
                      a_row_div, K, N, blk, subs);
   return 0;
 }
 
-// Host dispatch shared by the decode (blk = 16 * MT) and prefill (blk = cfg BM) entries.
+// Host dispatch shared by the decode (blk = 16 * MT) and prefill (blk = cfg BM) entries, and the fused decode
+// variants (fuse 1 / 2, MT = 1; see moe_mxfp4_kernel).
 // ws_estride: bytes per expert of the packed scale tensor; the code stride is N * K / 2 bytes.
 int moe_dispatch(long a, long as, long wq, long ws, long c, long sorted_ids, long expert_ids, long ntpp, long topk_w,
                  long ws_estride, int max_blocks, int numel, int a_row_div, int K, int N, int MT, int blk,
-                 long stream) {
+                 long stream, int fuse = 0) {
   if (N % 16 || N <= 0) return -1;
   if (K % GROUP || K <= 0) return -2;
   if (MT != 1 && MT != 2 && MT != 4) return -7;
   if (blk % (16 * MT)) return -7;
   if (a_row_div < 1) return -3;
+  if (fuse < 0 || fuse > 2) return -8;
+  if (fuse && MT != 1) return -7;
+  if (fuse == 1 && N % 32) return -1;                       // gate and up halves of whole 16-column tiles
   if (max_blocks <= 0 || numel <= 0) return 0;
-  if (!a || !as || !wq || !ws || !c || !sorted_ids || !expert_ids || !ntpp) return -3;
-  const Pick p = pick(MT, N, K, max_blocks);
+  if (!a || (!as && fuse != 2) || !wq || !ws || !c || !sorted_ids || !expert_ids || !ntpp) return -3;
+  Pick p = pick(MT, N, K, max_blocks);
+  if (fuse == 1) p.NPW = 2;
   const int subs = blk / (16 * MT);
   const long ny = (long)max_blocks * subs;
   if (ny > 0x7fffffffL || p.NPW < 1) return -3;
-  const dim3 grid((N / 16 + p.NPW - 1) / p.NPW, (unsigned)ny);
+  const dim3 grid(fuse == 1 ? N / 32 : (N / 16 + p.NPW - 1) / p.NPW, (unsigned)ny);
   const long wq_estride = (long)N * K / 2;
   const hipStream_t st = (hipStream_t)stream;
+  if (fuse) {
+#define F(FV, NPWv, SKv, Uv)                                                                                      \
+  if (fuse == FV && p.NPW == NPWv && p.SK == SKv && p.U == Uv)                                                    \
+    return launch_one<1, NPWv, SKv, Uv, FV>(grid, st, a, as, wq, ws, c, sorted_ids, expert_ids, ntpp, topk_w,     \
+                                            wq_estride, ws_estride, numel, a_row_div, K, N, blk, subs);
+#define FU(FV, NPWv, SKv) F(FV, NPWv, SKv, 1) F(FV, NPWv, SKv, 2) F(FV, NPWv, SKv, 4)
+#define FS(FV, NPWv) FU(FV, NPWv, 1) FU(FV, NPWv, 2) FU(FV, NPWv, 4)
+    FS(1, 2) FS(2, 1) FS(2, 2) FS(2, 4)
+#undef FS
+#undef FU
+#undef F
+    return -5;
+  }
 #define L(MTv, NPWv, SKv, Uv)                                                                               \
   if (p.MT == MTv && p.NPW == NPWv && p.SK == SKv && p.U == Uv)                                             \
     return launch_one<MTv, NPWv, SKv, Uv>(grid, st, a, as, wq, ws, c, sorted_ids, expert_ids, ntpp, topk_w, \
@@ -336,6 +440,23 @@ extern "C" int r9k_moe_mxfp4a8(long a, long as, long wq, long ws, long wref, lon
   const int mt = MT & 7;
   const int rc = moe_dispatch(a, as, wq, ws, c, sorted_ids, expert_ids, ntpp, topk_w, ws_estride, max_blocks, numel,
                               a_row_div, K, N, mt, 16 * mt, stream);
+  if (rc) return rc;
+  return hipGetLastError() == hipSuccess ? 0 : -6;
+}
+
+// Reference: kernels/r9k_moe_mxfp4a8.hip:618-626 (r9k_moe_mxfp4a8_f). fuse 1: gate_up with silu(g) * u in the
+// epilogue, c = fp32 [numel, N / 2]; fuse 2: down with fp32 A rows [numel, K] quantised per row on load (as
+// ignored). Decode routing blocks only (MT & 7 == 1); the tile knobs are ignored as in r9k_moe_mxfp4a8. -8 for
+// another fuse value.
+extern "C" int r9k_moe_mxfp4a8_f(int fuse, long a, long as, long wq, long ws, long wref, long c, long sorted_ids,
+                                 long expert_ids, long ntpp, long topk_w, long ws_estride, long wref_estride,
+                                 int max_blocks, int numel, int a_row_div, int K, int N, int WV, int SK, int NPW,
+                                 int MT, long stream) {
+  (void)wref; (void)wref_estride; (void)WV; (void)SK; (void)NPW;
+  if (fuse < 1 || fuse > 2) return -8;
+  if ((MT & 7) != 1) return -7;
+  const int rc = moe_dispatch(a, as, wq, ws, c, sorted_ids, expert_ids, ntpp, topk_w, ws_estride, max_blocks, numel,
+                              a_row_div, K, N, 1, 16, stream, fuse);
   if (rc) return rc;
   return hipGetLastError() == hipSuccess ? 0 : -6;
 }

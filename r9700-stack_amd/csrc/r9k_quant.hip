@@ -172,13 +172,6 @@ __global__ void __launch_bounds__(QT) quant_rows_scalar_kernel(const uint16_t* _
   for (int k = tid; k < K; k += QT) qr[k] = (uint8_t)f32_to_e4m3(bf2f(xr[k]) * inv);
 }
 
-// silu(g) * u with g, u the stored bf16 values, evaluated as (g / (1 + exp(-g))) * u in fp32 with the hardware
-// exponential (__expf, as the reference: kernels/r9k_moe_mxfp4a8.hip:526) and a reciprocal-multiply division
-// (V_RCP_F32, 1 ulp; within 2 ulp of the reference's IEEE division, whose sequence is 10 instructions an element in a
-// VALU-bound kernel). A code can move one step where the product sits within a few ulp of an e4m3 rounding point.
-__device__ __forceinline__ float silu_mul(float gv, float uv) {
-  return gv * __builtin_amdgcn_rcpf(1.f + __expf(-gv)) * uv;
-}
 
 // One wave per row, R 16-byte chunks of gate and of up per lane (I <= 512 * R), activations kept in registers.
 template <int R>

@@ -34,6 +34,8 @@ def lib() -> ctypes.CDLL:
         i, l = ctypes.c_int, ctypes.c_long
         L.r9k_moe_mxfp4a8.restype = i
         L.r9k_moe_mxfp4a8.argtypes = [l] * 12 + [i] * 9 + [l]
+        L.r9k_moe_mxfp4a8_f.restype = i
+        L.r9k_moe_mxfp4a8_f.argtypes = [i] + [l] * 12 + [i] * 9 + [l]
         L.r9k_moe_4bit_prefill.restype = i
         L.r9k_moe_4bit_prefill.argtypes = [i] + [l] * 12 + [i] * 6 + [l]
         L.r9k_moe_prefill_bm.restype = i
@@ -354,13 +356,36 @@ def moe_gemm(a_q: torch.Tensor, a_s: torch.Tensor, w: Mxfp4Experts, out: torch.T
     are the reference's gfx1201 launch knobs and are accepted but not used: the gfx950 kernel picks its own split.
     The grid covers at most ceil(numel/BLK) + min(numel, E) blocks -- the most an align can fill with numel routed
     rows over E experts -- so the launch stays graph-capturable."""
+    E = num_experts if num_experts is not None else w.wq.shape[0]
     if fuse:
-        raise RuntimeError("moe_gemm(fuse=...) is not available in this build")
+        # fuse 1: gate_up with silu(g)*u in the epilogue -> out fp32 [numel, N/2]; fuse 2: down with the fp32 A rows
+        # quantised per row on load (a_s unused). Decode routing blocks (MT == 1), MXFP4 experts
+        # (reference contract: kernels/moe.py:416-434).
+        if fuse not in (1, 2):
+            raise RuntimeError(f"moe_gemm: fuse={fuse} is not a fused variant (1 gate_up+act, 2 down+quant)")
+        assert isinstance(w, Mxfp4Experts) and MT == 1 and prefill is None and not a_tiled
+        assert a_q.shape[1] == w.K and a_q.is_contiguous() and out.is_contiguous()
+        assert (out.dtype == torch.float32 and out.shape[1] == w.N // 2 if fuse == 1
+                else out.dtype == torch.bfloat16 and out.shape[1] == w.N)
+        if fuse == 2:
+            assert a_q.dtype == torch.float32 and a_row_div == 1
+        else:
+            assert a_s is not None and a_s.dtype == torch.float32
+        if topk_w is not None:
+            assert topk_w.dtype == torch.float32 and topk_w.is_contiguous()
+        max_blocks = min(expert_ids.numel(), (numel + MOE_BLOCK - 1) // MOE_BLOCK + min(numel, E))
+        rc = lib().r9k_moe_mxfp4a8_f(
+            fuse, a_q.data_ptr(), a_s.data_ptr() if a_s is not None else 0, w.wq.data_ptr(), w.wsr.data_ptr(),
+            w.wsr.data_ptr() + (w.K // GROUP) * w.N, out.data_ptr(), sorted_ids.data_ptr(), expert_ids.data_ptr(),
+            ntpp.data_ptr(), topk_w.data_ptr() if topk_w is not None else 0, w.estride, w.estride, max_blocks,
+            numel, a_row_div, w.K, w.N, WV, SK, NPW, 1 | (16 if w.fold else 0), _stream())
+        if rc:
+            raise RuntimeError(f"r9k_moe_mxfp4a8_f failed ({rc}) fuse={fuse} N={w.N} K={w.K}")
+        return out
     if a_tiled:
         raise RuntimeError("moe_gemm(a_tiled=True) is a gfx1201 kernel format")
     if isinstance(w, Nvfp4Experts):
         raise RuntimeError("native NVFP4 experts are not served on gfx950: convert with quant.nvfp4.nvfp4_to_mxfp4")
-    E = num_experts if num_experts is not None else w.wq.shape[0]
     assert out.dtype == torch.bfloat16 and out.shape[1] == w.N and a_q.shape[1] == w.K and out.is_contiguous()
     assert a_q.is_contiguous() and a_s.dtype == torch.float32
     if topk_w is not None:

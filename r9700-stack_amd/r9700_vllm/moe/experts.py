@@ -25,6 +25,10 @@ from ..kernels import moe as K
 from . import route
 
 ZERO_DOWN = os.environ.get("R9K_MOE_ZERO_DOWN", "0") == "1"
+# R9K_MOE_FUSE=1: at decode (MT == 1) the activation runs in the gate_up GEMM's epilogue and the per-row fp8 quant in
+# the down GEMM's A-load (r9k_moe_mxfp4a8_f), so there is no SiLU launch; results equal the unfused chain's
+# (reference switch: moe/experts.py:55-58).
+MOE_FUSE = os.environ.get("R9K_MOE_FUSE", "0") == "1"
 
 
 def r9k_available() -> bool:
@@ -157,15 +161,22 @@ class R9700Mxfp4Experts(_experts_base()):
 
         q = route.take_quant(getattr(self, "r9k_layer", None), topk_ids, hidden_states) if tabs_routed else None
         xq, xs = q if q is not None else K.quant_rows_fp8(hidden_states)
-        gate_up = torch.empty((numel, N1), dtype=torch.bfloat16, device=dev)
-        K.moe_gemm(xq, xs, W1, gate_up, sid, eid, ntpp, numel, topk, None, num_experts=E, MT=MT, prefill=pf_gate)
-        aq, as_ = K.silu_mul_quant_fp8(gate_up)
+        fused = MOE_FUSE and MT == 1 and pf_gate is None and pf_down is None
+        if fused:
+            aq = torch.empty((numel, N1 // 2), dtype=torch.float32, device=dev)
+            K.moe_gemm(xq, xs, W1, aq, sid, eid, ntpp, numel, topk, None, num_experts=E, MT=1, fuse=1)
+            as_ = None
+        else:
+            gate_up = torch.empty((numel, N1), dtype=torch.bfloat16, device=dev)
+            K.moe_gemm(xq, xs, W1, gate_up, sid, eid, ntpp, numel, topk, None, num_experts=E, MT=MT, prefill=pf_gate)
+            aq, as_ = K.silu_mul_quant_fp8(gate_up)
         # Rows no table places (experts on other ranks under an expert map) must not feed moe_sum garbage.
         if expert_map is not None or ZERO_DOWN:
             down = torch.zeros((numel, N2), dtype=torch.bfloat16, device=dev)
         else:
             down = torch.empty((numel, N2), dtype=torch.bfloat16, device=dev)
         tw = topk_weights.reshape(-1).to(torch.float32).contiguous()
-        K.moe_gemm(aq, as_, W2, down, sid, eid, ntpp, numel, 1, tw, num_experts=E, MT=MT, prefill=pf_down)
+        K.moe_gemm(aq, as_, W2, down, sid, eid, ntpp, numel, 1, tw, num_experts=E, MT=MT, prefill=pf_down,
+                   fuse=2 if fused else 0)
         K.moe_sum(down.view(M, topk, N2), None, output)
         return output

@@ -216,3 +216,53 @@ def test_layer_config5_skewed(dev, T):
 def test_layer_config5_skewed_4096_sampled(dev):
     tokens = np.sort(np.random.default_rng(5).choice(4096, 32, replace=False))
     run_layer(dev, 384, 4096, 2048, 4096, 8, seed=20261201 + 5000 + 4096, tokens=tokens, zipf=True, lo=116, hi=126)
+
+
+@pytest.mark.parametrize("E,T,H,I,topk", [(288, 1, 2048, 512, 8), (288, 8, 2048, 512, 8), (288, 64, 2048, 512, 8),
+                                          (16, 5, 512, 256, 4), (8, 3, 320, 160, 2), (4, 2, 64, 32, 2)])
+def test_fused_decode_gemms_equal_unfused(dev, E, T, H, I, topk):
+    """r9k_moe_mxfp4a8_f: gate_up + activation (fuse 1), then down with the per-row quant on load (fuse 2), gives
+    the unfused chain's (gate_up -> r9k_silu_mul_quant_fp8 -> down) output bit for bit; the fused activation is
+    silu(g) * u of the unfused gate_up output (torch's exp and division: within a few fp32 ulp)."""
+    seed = 20261201 + 7000 + E + T + H
+    (_, _), (_, _), W13, W2 = make_layer(dev, E, H, I, seed)
+    g = torch.Generator().manual_seed(seed + 1)
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16).to(dev)
+    logits = torch.randn(T, E, generator=g).to(torch.bfloat16).to(dev)
+    w, ids = K.moe_topk(logits, topk, True)
+    numel = T * topk
+    sid, eid, ntpp = K.moe_align(ids, 16, E)
+    xq, xs = K.quant_rows_fp8(x)
+    tw = w.reshape(-1).float().contiguous()
+    gu = torch.empty(numel, 2 * I, dtype=torch.bfloat16, device=dev)
+    K.moe_gemm(xq, xs, W13, gu, sid, eid, ntpp, numel, topk, None, num_experts=E, MT=1)
+    aq, as_ = K.silu_mul_quant_fp8(gu)
+    d0 = torch.empty(numel, H, dtype=torch.bfloat16, device=dev)
+    K.moe_gemm(aq, as_, W2, d0, sid, eid, ntpp, numel, 1, tw, num_experts=E, MT=1)
+    h = torch.full((numel, I), float("nan"), dtype=torch.float32, device=dev)
+    K.moe_gemm(xq, xs, W13, h, sid, eid, ntpp, numel, topk, None, num_experts=E, MT=1, fuse=1)
+    d1 = torch.full((numel, H), float("nan"), dtype=torch.bfloat16, device=dev)
+    K.moe_gemm(h, None, W2, d1, sid, eid, ntpp, numel, 1, tw, num_experts=E, MT=1, fuse=2)
+    torch.cuda.synchronize()
+    gf, uf = gu[:, :I].float(), gu[:, I:].float()
+    href = gf / (1 + torch.exp(-gf)) * uf
+    assert not torch.isnan(h).any(), "a routed row of the fused activation was not written"
+    assert torch.allclose(h, href, rtol=4e-6, atol=1e-30), float(((h - href).abs() / href.abs()).max())
+    same = torch.equal(d0.view(torch.int16), d1.view(torch.int16))
+    print(f"fused E={E} T={T} H={H} I={I} k={topk}: down bit-equal {same}", flush=True)
+    assert same
+
+
+def test_layer_config2_decode_fused(dev, monkeypatch):
+    """The layer with R9K_MOE_FUSE on (no SiLU launch at decode) against the oracle."""
+    import r9700_vllm.moe.experts as X
+    monkeypatch.setattr(X, "MOE_FUSE", True)
+    for T in (1, 64):
+        run_layer(dev, 288, 2048, 512, T, 8, seed=20261201 + 2000 + T)
+
+
+def test_fused_entry_rejects_bad_args(dev):
+    L = K.lib()
+    # fuse values other than 1 / 2 -> -8; multi-tile routing blocks -> -7 (checked before any launch)
+    assert L.r9k_moe_mxfp4a8_f(3, *([1] * 12), 1, 16, 1, 64, 64, 2, 4, 2, 1, 0) == -8
+    assert L.r9k_moe_mxfp4a8_f(1, *([1] * 12), 1, 16, 1, 64, 64, 2, 4, 2, 2, 0) == -7
