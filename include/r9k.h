@@ -111,8 +111,8 @@ int r9k_moe_route_quant(long logits, int ldl, long weights, long ids, long sorte
 
 /* Align tables only, from ids int32 [numel] (the role of vLLM's moe_align_block_size, called at
  * r9700_vllm/moe/experts.py:172 of the reference). ids outside [0, E) are left out. scratch: at least
- * r9k_moe_align_scratch_ints(numel, E) int32 of per-chunk histograms, rewritten by every call (no initial
- * contents needed; calls sharing one scratch must not overlap). */
+ * r9k_moe_align_scratch_ints(numel, E) int32, zeroed once by the caller: an arrival counter (left zero by every
+ * call) and the per-chunk histograms (rewritten by every call); calls sharing one scratch must not overlap. */
 int r9k_moe_align(long ids, int numel, int E, int blk, long sorted_ids, long expert_ids, long ntpp, long scratch,
                   long scratch_ints, long stream);
 long r9k_moe_align_scratch_ints(int numel, int E);

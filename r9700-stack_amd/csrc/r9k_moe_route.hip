@@ -213,14 +213,16 @@ template <int NT>
 __device__ __forceinline__ void write_layout(TabLds<NT>& sh, int E, int blk, int numel, int total, int pre,
                                              int share, int nshare, int* __restrict__ sorted_ids,
                                              int* __restrict__ expert_ids) {
-  const int tid = threadIdx.x;
-  if (tid < E) {
-    const int c = sh.cnt[tid], o = sh.offs[tid];
-    sh.cursor[tid] = o + pre;
-    if (c > 0 && tid % nshare == share) {
+  constexpr int NW = NT / WAVE;
+  const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
+  if (tid < E) sh.cursor[tid] = sh.offs[tid] + pre;
+  // a wave per expert of the share: its block ids and its padding entries (up to blk - 1) written by the wave's lanes
+  for (int e = share + wave * nshare; e < E; e += NW * nshare) {
+    const int c = sh.cnt[e], o = sh.offs[e];
+    if (c > 0) {
       const int n = ((c + blk - 1) / blk) * blk;
-      for (int b = o / blk; b < (o + n) / blk; b++) expert_ids[b] = tid;
-      for (int i = o + c; i < o + n; i++) sorted_ids[i] = numel;
+      for (int b = o / blk + lane; b < (o + n) / blk; b += WAVE) expert_ids[b] = e;
+      for (int i = o + c + lane; i < o + n; i += WAVE) sorted_ids[i] = numel;
     }
   }
   const long cap = ((long)numel + (long)E * (blk - 1) + blk - 1) / blk * blk;
@@ -233,9 +235,23 @@ __device__ __forceinline__ void write_layout(TabLds<NT>& sh, int E, int blk, int
   lds_barrier();
 }
 
+// The lanes of this wave whose id equals this lane's (ids in [0, 2^nbits), -1 = none): the valid lanes ANDed with,
+// per id bit, the ballot of that bit or its complement -- nbits + 1 ballots instead of a compare against every lane.
+__device__ __forceinline__ uint64_t same_id_lanes(int e, int nbits) {
+  uint64_t m = __ballot(e >= 0);
+  for (int b = 0; b < nbits; b++) {
+    const int bit = (e >> b) & 1;
+    const uint64_t B = __ballot(bit);
+    m &= bit ? B : ~B;
+  }
+  return m;
+}
+
+__device__ __forceinline__ int id_bits(int E) { return E <= 1 ? 0 : 32 - __builtin_clz((unsigned)(E - 1)); }
+
 // Stable placement of ids[base, base + NT) (LDS; -1 = not placed) at their experts' cursors: a lane's rank among
-// the equal ids of lower lanes in its wave comes from a 64-step compare against every lane's id (v_readlane, no
-// branch), the rows of earlier waves from the per-wave counts. Advances the cursors; leaves wcnt zero.
+// the equal ids of lower lanes in its wave is the count of same-id lanes below it (same_id_lanes), the rows of
+// earlier waves come from the per-wave counts. Advances the cursors; leaves wcnt zero.
 template <int NT>
 __device__ __forceinline__ void stable_round(TabLds<NT>& sh, const short* ids, int base, int n, int row0, int E,
                                              int* __restrict__ sorted_ids) {
@@ -244,13 +260,10 @@ __device__ __forceinline__ void stable_round(TabLds<NT>& sh, const short* ids, i
   const int t = base + tid;
   const int e = t < n ? ids[t] : -1;
   int rank = 0, cw = 0;
-  if (base + wave * WAVE < n) {                                     // waves past the rows skip the compare loop
-#pragma unroll
-    for (int j = 0; j < WAVE; j++) {
-      const int m = __builtin_amdgcn_readlane(e, j) == e;
-      cw += m;
-      rank += j < lane ? m : 0;
-    }
+  if (base + wave * WAVE < n) {                                     // waves past the rows skip the ballots
+    const uint64_t m = same_id_lanes(e, id_bits(E));
+    rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+    cw = __popcll(m);
   }
   if (e >= 0 && rank == cw - 1) sh.wcnt[wave][e] = (uint16_t)cw;     // the last of its expert in this wave
   lds_barrier();
@@ -579,12 +592,23 @@ __global__ void __launch_bounds__(AT) align_big_single_kernel(const int* __restr
   }
 }
 
-// Multi-block align, pass 1: per-chunk histogram of CH routed rows into hist[c * E + e] (every entry written).
-__global__ void __launch_bounds__(AT) align_count_kernel(const int* __restrict__ ids, int numel, int E,
-                                                         int* __restrict__ hist) {
-  __shared__ int cnt[MAX_E];
-  const int tid = threadIdx.x, c = blockIdx.x;
-  for (int e = tid; e < E; e += AT) cnt[e] = 0;
+// Scratch of the multi-block align (int32): [0] the arrival counter (zero at entry, left zero), from ALIGN_HIST on
+// (nch + 2) rows of E: rows c < nch the chunks' histograms, then their bases; row nch each expert's first slot, row
+// nch + 1 its row count; then the padded total.
+constexpr int ALIGN_HIST = 16;
+
+// Multi-block align, pass 1 (one workgroup per chunk of CH routed rows): the chunk's per-expert histogram, stored
+// with agent-scope stores (coherent across the XCDs' L2s); after they complete each workgroup counts itself in the
+// arrival counter, and the last to arrive reads every histogram back with agent-scope loads and turns them into the
+// placement bases in place: row c = an expert's rows in chunks before c, row nch = its first slot (the padded
+// exclusive scan), row nch + 1 = its count, then the padded total, also written to ntpp.
+__global__ void __launch_bounds__(AT) align_count_kernel(const int* __restrict__ ids, int numel, int E, int blk,
+                                                         int* __restrict__ scratch, int* __restrict__ ntpp) {
+  __shared__ TabLds<AT> sh;
+  __shared__ int s_last;
+  int* __restrict__ hist = scratch + ALIGN_HIST;
+  const int tid = threadIdx.x, c = blockIdx.x, nch = gridDim.x;
+  for (int e = tid; e < E; e += AT) sh.cnt[e] = 0;
   const int t0 = c * CH, t1 = min(numel, t0 + CH);
   int v[CH / AT];
 #pragma unroll
@@ -592,19 +616,56 @@ __global__ void __launch_bounds__(AT) align_count_kernel(const int* __restrict__
   lds_barrier();
 #pragma unroll
   for (int u = 0; u < CH / AT; u++)
-    if (v[u] >= 0 && v[u] < E) atomicAdd(&cnt[v[u]], 1);
+    if (v[u] >= 0 && v[u] < E) atomicAdd(&sh.cnt[v[u]], 1);
   lds_barrier();
-  for (int e = tid; e < E; e += AT) hist[(size_t)c * E + e] = cnt[e];
+  for (int e = tid; e < E; e += AT)
+    __hip_atomic_store(hist + (size_t)c * E + e, sh.cnt[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");             // this thread's histogram stores have completed
+  lds_barrier();
+  if (tid == 0) s_last = __hip_atomic_fetch_add(scratch, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == nch - 1;
+  lds_barrier();
+  if (!s_last) return;
+  if (tid == 0) __hip_atomic_store(scratch, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  int tot = 0;
+  if (tid < E) {                                               // E <= AT: one expert a thread, 16 loads in flight
+    for (int c0 = 0; c0 < nch; c0 += 16) {
+      int h[16];
+#pragma unroll
+      for (int u = 0; u < 16; u++)
+        h[u] = c0 + u < nch
+                   ? __hip_atomic_load(hist + (size_t)(c0 + u) * E + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                   : 0;
+#pragma unroll
+      for (int u = 0; u < 16; u++)
+        if (c0 + u < nch) {
+          hist[(size_t)(c0 + u) * E + tid] = tot;
+          tot += h[u];
+        }
+    }
+    sh.cnt[tid] = tot;
+  }
+  lds_barrier();
+  const int total = padded_scan(sh, E, blk);
+  if (tid < E) {
+    hist[(size_t)nch * E + tid] = sh.offs[tid];
+    hist[(size_t)(nch + 1) * E + tid] = tot;
+  }
+  if (tid == 0) {
+    hist[(size_t)(nch + 2) * E] = total;
+    ntpp[0] = total;
+  }
 }
 
-// Multi-block align, pass 2 (one workgroup per chunk): totals and this chunk's per-expert base from the histograms
-// (the previous launch's writes are visible), the padded scan, this chunk's share of the layout writes (expert
-// blocks of experts e = c, c + nch, ...; the capacity tail split by chunk), then the stable placement of its rows.
+// Multi-block align, pass 2 (one workgroup per chunk): this chunk's bases, each expert's first slot and count and
+// the padded total from pass 1 (the previous launch's writes are visible), this chunk's share of the layout writes
+// (expert blocks of experts e = c, c + nch, ...; the capacity tail split by chunk), then the stable placement of its
+// rows.
 __global__ void __launch_bounds__(AT) align_scatter_kernel(const int* __restrict__ ids, int numel, int E, int blk,
                                                            int* __restrict__ sorted_ids, int* __restrict__ expert_ids,
-                                                           int* __restrict__ ntpp, const int* __restrict__ hist) {
+                                                           const int* __restrict__ scratch) {
   __shared__ TabLds<AT> sh;
   __shared__ short lids[CH];
+  const int* __restrict__ hist = scratch + ALIGN_HIST;
   const int tid = threadIdx.x, c = blockIdx.x, nch = gridDim.x;
   const int t0 = c * CH, t1 = min(numel, t0 + CH), n = t1 - t0;
   zero_counts(sh, E);
@@ -614,22 +675,12 @@ __global__ void __launch_bounds__(AT) align_scatter_kernel(const int* __restrict
   }
   int pre = 0;
   if (tid < E) {
-    int tot = 0;
-    for (int c0 = 0; c0 < nch; c0 += 8) {                      // 8 independent loads in flight per thread
-      int v[8];
-#pragma unroll
-      for (int u = 0; u < 8; u++) v[u] = c0 + u < nch ? hist[(size_t)(c0 + u) * E + tid] : 0;
-#pragma unroll
-      for (int u = 0; u < 8; u++) {
-        tot += v[u];
-        pre += c0 + u < c ? v[u] : 0;
-      }
-    }
-    sh.cnt[tid] = tot;
+    pre = hist[(size_t)c * E + tid];
+    sh.offs[tid] = hist[(size_t)nch * E + tid];
+    sh.cnt[tid] = hist[(size_t)(nch + 1) * E + tid];
   }
+  const int total = hist[(size_t)(nch + 2) * E];
   lds_barrier();
-  const int total = padded_scan(sh, E, blk);
-  if (c == 0 && tid == 0) ntpp[0] = total;
   write_layout(sh, E, blk, numel, total, pre, c, nch, sorted_ids, expert_ids);
   for (int base = 0; base < n; base += AT) stable_round(sh, lids, base, n, t0, E, sorted_ids);
 }
@@ -659,19 +710,24 @@ int launch_topk(const uint16_t* logits, int ldl, float* w, int* ids, int M, int 
 }
 
 // Tables for numel routed rows from ids in global memory (any numel): one workgroup up to SMALL_MAX, else the
-// histogram + placement launches over CH-row chunks (hist: (numel / CH rounded up) * E int32).
-int launch_align(const int* ids, int numel, int E, int blk, int* sorted_ids, int* expert_ids, int* ntpp, int* hist,
-                 hipStream_t st) {
+// histogram + placement launches over CH-row chunks (scratch: align_scratch_ints(numel, E) int32, zeroed once by
+// the caller; the launches leave its arrival counter zero).
+long align_scratch_ints(int numel, int E) {
+  return numel <= SMALL_MAX ? 1 : ALIGN_HIST + (long)((numel + CH - 1) / CH + 2) * E + 1;
+}
+
+int launch_align(const int* ids, int numel, int E, int blk, int* sorted_ids, int* expert_ids, int* ntpp,
+                 int* scratch, hipStream_t st) {
   if (numel <= SMALL_MAX) {
     hipLaunchKernelGGL(align_single_kernel, dim3(1), dim3(AT), 0, st, ids, numel, E, blk, sorted_ids, expert_ids,
                        ntpp);
     return 0;
   }
-  if (!hist) return 1;
+  if (!scratch) return 1;
   const int nch = (numel + CH - 1) / CH;
-  hipLaunchKernelGGL(align_count_kernel, dim3(nch), dim3(AT), 0, st, ids, numel, E, hist);
+  hipLaunchKernelGGL(align_count_kernel, dim3(nch), dim3(AT), 0, st, ids, numel, E, blk, scratch, ntpp);
   hipLaunchKernelGGL(align_scatter_kernel, dim3(nch), dim3(AT), 0, st, ids, numel, E, blk, sorted_ids, expert_ids,
-                     ntpp, (const int*)hist);
+                     (const int*)scratch);
   return 0;
 }
 
@@ -805,15 +861,14 @@ extern "C" int r9k_moe_topk(long logits, int ldl, long weights, long ids, int M,
   return (int)hipGetLastError();
 }
 
-// int32 count of the scratch r9k_moe_align needs for `numel` routed rows over E experts (per-chunk histograms,
-// rewritten by every call; no initial contents needed).
-extern "C" long r9k_moe_align_scratch_ints(int numel, int E) {
-  if (numel <= SMALL_MAX) return 1;
-  return (long)((numel + CH - 1) / CH) * E;
-}
+// int32 count of the scratch r9k_moe_align needs for `numel` routed rows over E experts (an arrival counter and the
+// per-chunk histograms / bases; zeroed once by the caller, the counter left zero by every call).
+extern "C" long r9k_moe_align_scratch_ints(int numel, int E) { return align_scratch_ints(numel, E); }
 
 // Tables only, from ids int32 [numel] (the stock moe_align_block_size role; ids outside [0, E) are skipped).
-// scratch: r9k_moe_align_scratch_ints(numel, E) int32 (histograms, any contents). 0 / 1 bad args / HIP error.
+// scratch: r9k_moe_align_scratch_ints(numel, E) int32, zeroed once by the caller (its first int is the arrival
+// counter of the histogram launch, left zero; calls sharing one scratch must not overlap). 0 / 1 bad args / HIP
+// error.
 extern "C" int r9k_moe_align(long ids, int numel, int E, int blk, long sorted_ids, long expert_ids, long ntpp,
                              long scratch, long scratch_ints, long stream) {
   if (numel < 1 || E < 1 || E > MAX_E || blk < 1 || (blk & (blk - 1))) return 1;

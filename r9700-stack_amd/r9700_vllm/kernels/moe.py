@@ -498,7 +498,8 @@ def _align_scratch(device: torch.device, n: int) -> torch.Tensor:
     key = (device.type, device.index)
     t = _ALIGN_SCRATCH.get(key)
     if t is None or t.numel() < n:
-        t = torch.empty(max(n, 1 << 16), dtype=torch.int32, device=device)   # per-chunk histograms, rewritten per call
+        # arrival counter + per-chunk histograms: zeroed once here, the counter left zero by every call
+        t = torch.zeros(max(n, 1 << 16), dtype=torch.int32, device=device)
         _ALIGN_SCRATCH[key] = t
     return t
 
