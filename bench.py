@@ -71,7 +71,8 @@ class Layer:
 
 class Step:
     """The layer forward for T tokens, graph-capturable: fused routing when the decode router path applies
-    (T * topk <= 4096 rows, as R9kTopKRouter), otherwise top-k + the in-apply align."""
+    (T * topk <= 4096 rows, as R9kTopKRouter), otherwise top-k + activation quant in one launch (as R9kTopKRouter
+    above its row limit) and the in-apply align."""
 
     def __init__(self, layer: Layer, T: int, topk: int, dev, seed: int):
         from r9700_vllm.kernels import moe as K
@@ -110,8 +111,15 @@ class Step:
             self.routed._r9k_tables = route.Tables(ids, self.sid, self.eid, self.ntpp, self.blk, self.numel,
                                                    self.x, self.x._version, xq, xs)
         else:
-            w, ids = K.moe_topk(self.logits, self.topk, True)
-            self.routed._r9k_tables = None
+            # prefill widths, as R9kTopKRouter: top-k and the activation quant in one launch, tables in apply
+            r = K.moe_topk_quant(self.logits, self.topk, True, self.x)
+            if r is None:
+                w, ids = K.moe_topk(self.logits, self.topk, True)
+                self.routed._r9k_tables = None
+            else:
+                w, ids, xq, xs = r
+                self.routed._r9k_tables = route.Tables(ids, None, None, None, -1, self.numel, self.x,
+                                                       self.x._version, xq, xs)
         self.experts[c].apply(self.out, self.x, L.W13[c].wq, L.W2[c].wq, w, ids, "silu", L.E, None, None, None,
                               None, None, None, False)
         self.w, self.ids = w, ids

@@ -99,6 +99,15 @@ int r9k_moe_sum(long down, long shared, long out, int M, int topk, int N, long l
  * its fused router is off: r9700_vllm/moe/route.py:159-163). Same numerics as r9k_moe_route. 0 / 1 / HIP error. */
 int r9k_moe_topk(long logits, int ldl, long weights, long ids, int M, int E, int topk, int renorm, long stream);
 
+/* r9k_moe_topk plus r9k_quant_rows_fp8 of the layer's activations in ONE launch, any M (the work the reference does
+ * in vLLM's topk_softmax and then r9k_quant_rows_fp8, r9700_vllm/moe/experts.py:185, at prefill widths): x bf16
+ * [M][H] (row stride ldx) -> xq e4m3fn [M][H], xs fp32 [M], the bytes of r9k_quant_rows_fp8; weights / ids as
+ * r9k_moe_topk. Top-k and quant workgroups alternate so each CU runs both. Returns 2 with nothing launched for H % 8,
+ * H > 4096, ldx % 8 or misaligned x (16 bytes) / xq (8 bytes): then call the two entries. 1 bad arguments, else the
+ * HIP error. */
+int r9k_moe_topk_quant(long logits, int ldl, long weights, long ids, int M, int E, int topk, int renorm, long x,
+                       long ldx, int H, long xq, long xs, long stream);
+
 /* r9k_moe_route plus the per-token fp8 quant of the layer's activations in the same launch (the work the reference
  * does in r9k_moe_route and then r9k_quant_rows_fp8, r9700_vllm/moe/experts.py:185): x bf16 [M][H] (row stride
  * ldx) -> xq e4m3fn [M][H], xs fp32 [M], the bytes of r9k_quant_rows_fp8. scratch as for r9k_moe_route (its first

@@ -544,6 +544,28 @@ __global__ void __launch_bounds__(RW * WAVE) topk_kernel(const uint16_t* __restr
                  threadIdx.x % WAVE);
 }
 
+// Top-k routing plus the per-token fp8 quant of the layer's activations in one launch (any M): even blocks route RW
+// rows each (one row a wave, VALU-bound), odd blocks quantise RW rows of x each (quant_row_wave, HBM-bound), so every
+// CU runs both kinds at once instead of one launch after the other. Outputs are topk_kernel's and
+// r9k_quant_rows_fp8's.
+template <int EPL, int R>
+__global__ void __launch_bounds__(RW * WAVE) topk_quant_kernel(const uint16_t* __restrict__ logits, int ldl,
+                                                               float* __restrict__ weights, int* __restrict__ ids,
+                                                               int M, int E, int topk, int renorm,
+                                                               const uint16_t* __restrict__ x, long ldx, int H,
+                                                               uint8_t* __restrict__ xq, float* __restrict__ xs) {
+  const int lane = threadIdx.x % WAVE;
+  const int r = (int)(blockIdx.x >> 1) * RW + (int)threadIdx.x / WAVE;
+  if (r >= M) return;
+  if ((blockIdx.x & 1) == 0) {
+    uint16_t h[EPL];
+    load_row<EPL>(logits + (size_t)r * ldl, E, lane, h);
+    topk_core<EPL>(h, E, topk, renorm != 0, weights + (size_t)r * topk, ids + (size_t)r * topk, nullptr, lane);
+  } else {
+    quant_row_wave<R>(x + (size_t)r * ldx, H, xq + (size_t)r * H, xs + r, lane);
+  }
+}
+
 // Tables from ids in global memory, one workgroup, numel <= SMALL_MAX.
 __global__ void __launch_bounds__(AT) align_single_kernel(const int* __restrict__ ids, int numel, int E, int blk,
                                                           int* __restrict__ sorted_ids, int* __restrict__ expert_ids,
@@ -850,6 +872,43 @@ extern "C" int r9k_moe_route_quant(long logits, int ldl, long weights, long ids,
 
 extern "C" int r9k_moe_route_max_experts(void) { return MAX_E; }
 extern "C" int r9k_moe_route_max_topk(void) { return MAX_K; }
+
+// r9k_moe_topk plus r9k_quant_rows_fp8 of the layer's activations in one launch, any M: x bf16 [M, H] (row stride
+// ldx) -> xq e4m3 [M, H], xs fp32 [M], the bytes of r9k_quant_rows_fp8. Rows the wave quant does not take (H % 8,
+// H > 4096, x not 16-byte or xq not 8-byte aligned, ldx % 8) return 2 with nothing launched, so the caller runs the
+// two calls. 1 bad arguments, else the HIP error.
+extern "C" int r9k_moe_topk_quant(long logits, int ldl, long weights, long ids, int M, int E, int topk, int renorm,
+                                  long x, long ldx, int H, long xq, long xs, long stream) {
+  if (!route_args_ok(M, E, topk, 1) || ldl < E || !x || !xq || !xs) return 1;
+  if (H < 8 || H % 8 || H > 512 * QRMAX || ldx < H || ldx % 8 || (x & 15) || (xq & 7)) return 2;
+  const int nv = (H / 8 + WAVE - 1) / WAVE;
+  const int R = nv <= 1 ? 1 : nv <= 2 ? 2 : nv <= 4 ? 4 : 8;
+  const dim3 grid(2 * ((M + RW - 1) / RW)), block(RW * WAVE);
+  const hipStream_t st = (hipStream_t)stream;
+#define TQ(EPLV, RV)                                                                                              \
+  hipLaunchKernelGGL((topk_quant_kernel<EPLV, RV>), grid, block, 0, st, (const uint16_t*)logits, ldl,            \
+                     (float*)weights, (int*)ids, M, E, topk, renorm, (const uint16_t*)x, ldx, H, (uint8_t*)xq,      \
+                     (float*)xs)
+#define TQR(EPLV)                 \
+  switch (R) {                    \
+    case 1: TQ(EPLV, 1); break;   \
+    case 2: TQ(EPLV, 2); break;   \
+    case 4: TQ(EPLV, 4); break;   \
+    default: TQ(EPLV, 8); break;  \
+  }
+  switch (epl_for(E)) {
+    case 2: TQR(2); break;
+    case 4: TQR(4); break;
+    case 6: TQR(6); break;
+    case 8: TQR(8); break;
+    case 12: TQR(12); break;
+    case 16: TQR(16); break;
+    default: return 1;
+  }
+#undef TQR
+#undef TQ
+  return (int)hipGetLastError();
+}
 
 // Routing only: the stock top-k softmax router's outputs (no tables). 0 / 1 unsupported / HIP error.
 extern "C" int r9k_moe_topk(long logits, int ldl, long weights, long ids, int M, int E, int topk, int renorm,

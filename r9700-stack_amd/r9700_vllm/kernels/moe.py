@@ -52,6 +52,8 @@ def lib() -> ctypes.CDLL:
         L.r9k_moe_sum.argtypes = [l] * 3 + [i] * 3 + [l] * 3
         L.r9k_moe_topk.restype = i
         L.r9k_moe_topk.argtypes = [l, i, l, l, i, i, i, i, l]
+        L.r9k_moe_topk_quant.restype = i
+        L.r9k_moe_topk_quant.argtypes = [l, i, l, l, i, i, i, i, l, l, i, l, l, l]
         L.r9k_moe_align.restype = i
         L.r9k_moe_align.argtypes = [l, i, i, i, l, l, l, l, l, l]
         L.r9k_moe_align_scratch_ints.restype = l
@@ -542,6 +544,30 @@ def moe_topk(logits: torch.Tensor, topk: int, renorm: bool):
     if rc:
         raise RuntimeError(f"r9k_moe_topk failed ({rc}) M={M} E={E} topk={topk}")
     return w, ids
+
+
+def moe_topk_quant(logits: torch.Tensor, topk: int, renorm: bool, x: torch.Tensor):
+    """moe_topk and quant_rows_fp8(x) in one launch (r9k_moe_topk_quant; the two kernels' work interleaved over the
+    CUs): (w, ids, xq e4m3fn [M, H], xs fp32 [M]), the same values as the two calls. None when x's shape or
+    alignment does not suit the fused launch (then nothing ran: call the two functions)."""
+    assert logits.dtype == torch.bfloat16 and logits.dim() == 2 and logits.stride(1) == 1
+    M, E = logits.shape
+    if not (x.dim() == 2 and x.dtype == torch.bfloat16 and x.shape[0] == M and x.stride(1) == 1) or M == 0:
+        return None
+    dev = logits.device
+    H = x.shape[1]
+    w = torch.empty((M, topk), dtype=torch.float32, device=dev)
+    ids = torch.empty((M, topk), dtype=torch.int32, device=dev)
+    xq = torch.empty((M, H), dtype=torch.float8_e4m3fn, device=dev)
+    xs = torch.empty((M,), dtype=torch.float32, device=dev)
+    rc = lib().r9k_moe_topk_quant(logits.data_ptr(), logits.stride(0), w.data_ptr(), ids.data_ptr(), M, E, topk,
+                                  1 if renorm else 0, x.data_ptr(), x.stride(0), H, xq.data_ptr(), xs.data_ptr(),
+                                  _stream())
+    if rc == 2:
+        return None
+    if rc:
+        raise RuntimeError(f"r9k_moe_topk_quant failed ({rc}) M={M} E={E} topk={topk} H={H}")
+    return w, ids, xq, xs
 
 
 def align_block_size_ref(topk_ids: torch.Tensor, num_experts: int, block: int = MOE_BLOCK):

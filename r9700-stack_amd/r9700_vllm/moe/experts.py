@@ -152,14 +152,14 @@ class R9700Mxfp4Experts(_experts_base()):
             pf_down = K.pick_moe_prefill(MT, K2)
             pf_gate = K.pick_moe_prefill(MT, K1, gate_up=True)
         tabs = route.take(getattr(self, "r9k_layer", None), topk_ids, blk, numel) if expert_map is None else None
-        tabs_routed = tabs is not None
         if tabs is None:
             tabs = K.moe_align(topk_ids, blk, E, expert_map)
         sid, eid, ntpp = tabs
         W1 = K.Mxfp4Experts(w1, self.w1_scale, N1, K1)
         W2 = K.Mxfp4Experts(w2, self.w2_scale, N2, K2)
 
-        q = route.take_quant(getattr(self, "r9k_layer", None), topk_ids, hidden_states) if tabs_routed else None
+        # the router's fp8 quant of this input, when it made one (with its tables at decode, alone at prefill)
+        q = route.take_quant(getattr(self, "r9k_layer", None), topk_ids, hidden_states) if expert_map is None else None
         xq, xs = q if q is not None else K.quant_rows_fp8(hidden_states)
         fused = MOE_FUSE and MT == 1 and pf_gate is None and pf_down is None
         if fused:

@@ -135,11 +135,12 @@ def register() -> None:
 
 @dataclass
 class Tables:
-    """Routing tables for one call, keyed by the topk_ids tensor the router returned with them."""
+    """Routing tables for one call, keyed by the topk_ids tensor the router returned with them (at prefill widths
+    only the activation quant: sorted_ids / expert_ids / ntpp None, and the experts build the tables)."""
     ids: torch.Tensor
-    sorted_ids: torch.Tensor
-    expert_ids: torch.Tensor
-    ntpp: torch.Tensor
+    sorted_ids: torch.Tensor | None
+    expert_ids: torch.Tensor | None
+    ntpp: torch.Tensor | None
     blk: int
     numel: int
     x: torch.Tensor | None = None          # the layer input the router quantised, with its version at that time
@@ -148,8 +149,8 @@ class Tables:
     xs: torch.Tensor | None = None
 
     def matches(self, topk_ids: torch.Tensor, blk: int, numel: int) -> bool:
-        return (self.ids.data_ptr() == topk_ids.data_ptr() and self.ids.shape == topk_ids.shape
-                and self.blk == blk and self.numel == numel)
+        return (self.sorted_ids is not None and self.ids.data_ptr() == topk_ids.data_ptr()
+                and self.ids.shape == topk_ids.shape and self.blk == blk and self.numel == numel)
 
     def quant_for(self, x: torch.Tensor):
         """(xq, xs) when the router quantised this very tensor, unmodified since; else None."""
@@ -163,6 +164,15 @@ def _fits(logits: torch.Tensor, topk: int, E: int) -> bool:
     return (logits.dim() == 2 and logits.dtype == torch.bfloat16 and logits.stride(1) == 1
             and 1 <= logits.shape[0] <= MAX_ROWS and logits.shape[1] == E and E <= L.r9k_moe_route_max_experts()
             and 1 <= topk <= min(E, L.r9k_moe_route_max_topk()))
+
+
+def _fits_wide(logits: torch.Tensor, topk: int, E: int, x) -> bool:
+    """Rows above MAX_ROWS whose top-k and activation quant can share one launch (r9k_moe_topk_quant)."""
+    L = lib()
+    return (logits.dim() == 2 and logits.dtype == torch.bfloat16 and logits.stride(1) == 1
+            and logits.shape[0] > MAX_ROWS and logits.shape[1] == E and E <= L.r9k_moe_route_max_experts()
+            and 1 <= topk <= min(E, L.r9k_moe_route_max_topk()) and isinstance(x, torch.Tensor)
+            and x.dim() == 2 and x.shape[0] == logits.shape[0])
 
 
 def make_router(stock, routed_experts):
@@ -196,6 +206,15 @@ def make_router(stock, routed_experts):
 
         def _compute_routing(self, hidden_states, router_logits, indices_type, *, input_ids=None):
             E = self.global_num_experts
+            if indices_type in (None, torch.int32) and _fits_wide(router_logits, self.top_k, E, hidden_states):
+                # prefill widths: top-k and the experts' fp8 input quant in one launch; the experts build the
+                # tables (multi-workgroup align) and take the quant from here (Tables.quant_for)
+                r = KM.moe_topk_quant(router_logits, self.top_k, self.renormalize, hidden_states)
+                if r is not None:
+                    w, ids, xq, xs = r
+                    self.routed_experts._r9k_tables = Tables(ids, None, None, None, -1, ids.numel(), hidden_states,
+                                                             hidden_states._version, xq, xs)
+                    return w, ids
             if indices_type not in (None, torch.int32) or not _fits(router_logits, self.top_k, E):
                 self.routed_experts._r9k_tables = None
                 return super()._compute_routing(hidden_states, router_logits, indices_type, input_ids=input_ids)

@@ -219,3 +219,23 @@ def test_moe_sum_bit_exact(dev, M, topk, N):
     out2 = torch.empty(M, N + 16, dtype=torch.bfloat16, device=dev)[:, :N]          # strided output rows
     K.moe_sum(down.to(dev), shared.to(dev), out2)
     assert np.array_equal(O.bf16_bits(out2), O.moe_sum(down, shared))
+
+
+@pytest.mark.parametrize("M,E,topk,H", [(8192, 288, 8, 2048), (300, 288, 8, 2048), (4096, 384, 8, 4096),
+                                        (257, 64, 4, 512), (33, 1024, 16, 136), (5, 16, 2, 100)])
+def test_moe_topk_quant(dev, M, E, topk, H):
+    """r9k_moe_topk_quant: the top-k and the activation quant of one launch equal moe_topk's and quant_rows_fp8's
+    outputs bit for bit (H % 8 != 0 returns None: nothing launched, the caller runs the two calls)."""
+    g = torch.Generator().manual_seed(20261201 + 9000 + M + E + H)
+    logits = torch.randn(M, E, generator=g).to(torch.bfloat16).to(dev)
+    x = (torch.randn(M, H, generator=g) * 3).to(torch.bfloat16).to(dev)
+    r = K.moe_topk_quant(logits, topk, True, x)
+    if H % 8:
+        assert r is None
+        return
+    w, ids, xq, xs = r
+    w0, ids0 = K.moe_topk(logits, topk, True)
+    xq0, xs0 = K.quant_rows_fp8(x)
+    torch.cuda.synchronize()
+    assert torch.equal(ids, ids0) and torch.equal(w, w0)
+    assert torch.equal(xq.view(torch.uint8), xq0.view(torch.uint8)) and torch.equal(xs, xs0)
