@@ -326,8 +326,8 @@ int env_int(const char* name, int dflt) {
 
 // Launch shape for the decode-family kernel, from the host-known shape only (graph-capturable). Two column tiles a
 // wave. Long K (>= 8 K-tiles) splits over SK waves so that fewer dependent load batches sit on one wave: 4 while the
-// grid is small, 2 once it holds >= 12K waves' worth of tiles, in 2-tile load batches; short K stays in one wave (no
-// LDS reduction), with
+// grid is small, 2 once it holds >= 12K waves' worth of tiles, in 4-tile load batches below 4K tiles (config 2 at
+// T <= 8: one memory round trip a wave) and 2-tile batches above; short K stays in one wave (no LDS reduction), with
 // 4-tile load batches while the grid is small. Measured on MI355X over config-2 decode widths (T = 1..64).
 // R9K_GEMM_SK / R9K_GEMM_NPW / R9K_GEMM_U override (tuning sweeps).
 Pick pick(int MT, int N, int K, int max_blocks) {
@@ -338,7 +338,7 @@ Pick pick(int MT, int N, int K, int max_blocks) {
   int SK, U;
   if (nkt >= 8) {
     SK = tiles >= 12288 ? 2 : 4;
-    U = 2;
+    U = tiles < 4096 ? 4 : 2;                              // small grids: a wave's K range in one load batch
   } else {
     SK = 1;
     U = tiles >= 8192 ? 1 : 4;
