@@ -178,7 +178,9 @@ def test_moe_route_large_m_path(dev):
 
 
 @pytest.mark.parametrize("T,E,topk,blk,zipf", [(8192, 288, 8, 64, False), (4096, 384, 8, 64, True),
-                                               (256, 384, 8, 16, True), (3000, 64, 4, 128, False)])
+                                               (256, 384, 8, 16, True), (3000, 64, 4, 128, False),
+                                               (8192, 288, 8, 256, False), (600, 1024, 16, 256, True),
+                                               (2049, 7, 2, 1, False)])
 def test_topk_and_align_multiblock(dev, T, E, topk, blk, zipf):
     print(f"topk+align T={T} E={E} blk={blk} zipf={zipf}", flush=True)
     g = torch.Generator().manual_seed(T + E)
@@ -195,6 +197,20 @@ def test_topk_and_align_multiblock(dev, T, E, topk, blk, zipf):
         so, eo, no = O.align(ido, E, blk)
         assert np.array_equal(s_.cpu().numpy(), so) and np.array_equal(e_.cpu().numpy(), eo)
         assert n_.item() == no[0]
+    # the multi-workgroup path's arrival counter (first int of the zero-once scratch) is left zero
+    assert int(K._align_scratch(torch.device(dev), 1)[0]) == 0
+
+
+@pytest.mark.parametrize("T", [40, 3000])
+def test_align_skips_foreign_experts_wide(dev, T):
+    """Expert-map holes at both table builders (one workgroup, and chunked over workgroups above 4096 rows)."""
+    g = torch.Generator().manual_seed(T)
+    ids = torch.stack([torch.randperm(64, generator=g)[:4] for _ in range(T)]).to(torch.int32)
+    emap = torch.tensor([i // 2 if i % 2 == 0 else -1 for i in range(64)], dtype=torch.int32)
+    s_, e_, n_ = K.moe_align(ids.to(dev), 64, 32, emap.to(dev))
+    mapped = emap[ids.long()].numpy()
+    so, eo, no = O.align(mapped, 32, 64)
+    assert np.array_equal(s_.cpu().numpy(), so) and np.array_equal(e_.cpu().numpy(), eo) and n_.item() == no[0]
 
 
 def test_align_skips_foreign_experts(dev):
