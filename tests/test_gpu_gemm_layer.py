@@ -266,3 +266,31 @@ def test_fused_entry_rejects_bad_args(dev):
     # fuse values other than 1 / 2 -> -8; multi-tile routing blocks -> -7 (checked before any launch)
     assert L.r9k_moe_mxfp4a8_f(3, *([1] * 12), 1, 16, 1, 64, 64, 2, 4, 2, 1, 0) == -8
     assert L.r9k_moe_mxfp4a8_f(1, *([1] * 12), 1, 16, 1, 64, 64, 2, 4, 2, 2, 0) == -7
+
+
+@pytest.mark.parametrize("M", [1, 16, 300, 2048])
+def test_shared_expert(dev, M):
+    """moe/shared.shared_expert (gated shared expert: quant + gate, gate_up, SiLU quant, down with the gate folded into
+    the row scale) against the oracle chain on the same gate values: norm ratio <= 1e-2, cosine >= 0.9999."""
+    from r9700_vllm.moe import shared
+    H, I = 2048, 512
+    g = torch.Generator().manual_seed(20261201 + 6000 + M)
+    p1, e1 = make_experts(1, 2 * I, H, g)
+    p2, e2 = make_experts(1, H, I, g)
+    W1 = K.prepare_mxfp4_weights(p1.to(dev), e1.to(dev))
+    W2 = K.prepare_mxfp4_weights(p2.to(dev), e2.to(dev))
+    x = torch.randn(M, H, generator=g).to(torch.bfloat16)
+    wg = (torch.randn(H, generator=g) * 0.02).to(torch.bfloat16)
+    out = shared.shared_expert(x.to(dev), W1.wq, W1.wsr, W2.wq, W2.wsr, wg.to(dev), 2 * I, H, H, I, False, False)
+    _, _, gate = K.quant_rows_fp8_gate(x.to(dev), wg.to(dev))          # the gate values (own test: bit-level)
+    torch.cuda.synchronize()
+    qo, so = O.quant_rows_fp8(x)
+    zeros = np.zeros(M, dtype=np.int64)
+    gu = O.grouped_gemm(qo, so, {0: O.mxfp4_dequant(p1[0], e1[0])}, zeros, 1, acc_dtype=torch.float32)
+    aq, as_, _ = O.silu_mul_quant_fp8(O.bits_to_bf16(gu))
+    ref = O.grouped_gemm(aq, as_, {0: O.mxfp4_dequant(p2[0], e2[0])}, zeros, 1, gate.cpu().numpy(),
+                         acc_dtype=torch.float32)
+    a, b = bf16_bits_to_f64(O.bf16_bits(out)), bf16_bits_to_f64(ref)
+    r, c = rel_err(a, b), cosine(a, b)
+    print(f"shared expert M={M}: rel {r:.2e} cos {c:.7f}", flush=True)
+    assert r <= 1e-2 and c >= 0.9999
