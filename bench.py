@@ -7,7 +7,8 @@ A step is one MoE layer forward over one batch of synthetic tokens: routing (sof
 T <= 64 the per-token fp8 quant of x in the same launch) -> grouped gate_up GEMM -> SiLU*up + fp8 quant -> grouped
 down GEMM (router weight folded) -> top-k sum, five launches on one stream (six above T = 64). The headline `value`
 is BASELINE config 2 (E=288 experts, hidden 2048, expert intermediate 512, top-8) at T=64 tokens, the
-bandwidth-bound decode point; T = 1, 8, 16 and the config 3 prefill (T=8192) are reported beside it.
+bandwidth-bound decode point; T = 1, 8, 16, the config 3 prefill (T=8192) and the router gate GEMM that produces
+the layer's logits (r9k_router_gemm against stock's F.linear) are reported beside it.
 
 Method: weights and inputs are resident in HBM before timing. Steps run as HIP-graph replays that cycle through
 COPIES independent weight copies (> 2x the 256 MB Infinity Cache per cycle), so weight bytes come from HBM, not from
@@ -45,6 +46,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-prefill", action="store_true", help="skip the T=8192 prefill line")
+    ap.add_argument("--no-router", action="store_true", help="skip the router gate GEMM timings")
     return ap.parse_args()
 
 
@@ -199,6 +201,50 @@ def gate_up_kernel_time(step: Step, reps: int = 40):
     return ms, nbytes, flops, touched
 
 
+def router_times(dev, reps_bytes: int = 512 << 20):
+    """The router gate GEMM (r9k_router_gemm via router.router_gemm, bf16 out) beside stock's F.linear, kernel time
+    alone: back-to-back launches in one HIP graph cycling through enough weight copies (>= 512 MB, twice the Infinity
+    Cache) that every launch reads its weight from HBM, HIP events on the stream around the replay. Shapes: config 2's
+    gate (E=288, hidden 2048) and the reference's Flash-Next gate (E=512, hidden 2560) at decode widths."""
+    from r9700_vllm import router as R
+    g = torch.Generator(device=dev).manual_seed(SEED + 77)
+    out = []
+    for E, H in ((288, 2048), (512, 2560)):
+        wbytes = E * H * 2
+        copies = -(-reps_bytes // wbytes)
+        ws = [(torch.randn(E, H, generator=g, device=dev) * 0.05).to(torch.bfloat16) for _ in range(copies)]
+        for M in (1, 8, 32):
+            x = torch.randn(M, H, generator=g, device=dev).to(torch.bfloat16)
+            row = {"E": E, "hidden": H, "M": M}
+            for name, fn in (("r9k", lambda w: R.router_gemm(x, w, True)),
+                             ("stock", lambda w: torch.nn.functional.linear(x, w))):
+                for w in ws[:4]:
+                    fn(w)
+                torch.cuda.synchronize()
+                gr = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(gr):
+                    for w in ws:
+                        fn(w)
+                gr.replay()
+                torch.cuda.synchronize()
+                s = torch.cuda.current_stream()
+                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                a.record(s)
+                gr.replay()
+                b.record(s)
+                torch.cuda.synchronize()
+                row[f"{name}_us"] = round(a.elapsed_time(b) * 1e3 / copies, 3)
+                del gr
+            nbytes = wbytes + M * H * 2 + M * E * 2
+            row["r9k_GBps"] = round(nbytes / (row["r9k_us"] * 1e-6) / 1e9, 1)
+            row["speedup_vs_stock"] = round(row["stock_us"] / row["r9k_us"], 3)
+            out.append(row)
+            print(f"# router E={E} H={H} M={M}: {row['r9k_us']} us (stock F.linear {row['stock_us']} us)",
+                  file=sys.stderr, flush=True)
+        del ws
+    return {"kernel": "r9k_router_gemm (bf16 out)", "shapes": out}
+
+
 CALIB_BYTES = 256 << 20
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "moe_gate_up_t64_pmc_traffic.md")
 
@@ -307,6 +353,7 @@ def main():
                    "frac_fp8_peak": round(tf / FP8_PEAK_TFLOPS, 4), "steps": n}
         print(f"# prefill T=8192: {ms:.3f} ms/layer, {tf:.1f} TFLOPS", file=sys.stderr, flush=True)
 
+    router = None if args.no_router else router_times(dev)
     cpu = None if args.no_cpu else cpu_baseline(main_step)
     line = {
         "metric": "MoE-layer tokens/s + HBM GB/s (decode) / MXFP4 TFLOPS (prefill), 1 GPU",
@@ -331,6 +378,7 @@ def main():
         "cpu_baseline": cpu,
         "decode_sweep": sweep,
         "prefill": prefill,
+        "router": router,
     }
     print(json.dumps(line), flush=True)
 

@@ -93,6 +93,16 @@ int r9k_moe_route_max_topk(void);      /* 16;   replaces r9k_moe_route.hip:236 *
  * Replaces kernels/r9k_moe_sum.hip:62-69. */
 int r9k_moe_sum(long down, long shared, long out, int M, int topk, int N, long ld_shared, long ld_out, long stream);
 
+/* Router (gate) GEMM at decode widths: out[M][E] = x[M][K] bf16 . w[E][K]^T bf16 with fp32 accumulation, rounded
+ * once to bf16 (out_bf16 = 1) or stored fp32; row strides sx / sw / so in elements. act_cols > 0 applies the
+ * hyper-connection epilogue s = bf16(v) / hc, s / (1 + exp(-s)) to the first act_cols columns. Rules: 1 <= M <= 32,
+ * E >= 1, K >= 8, split in {1, 2, 4, 8}, K % (8 split) == 0, sx and sw multiples of 8, x and w 16-byte aligned.
+ * 0, or -1 M / E / K, -2 split, -3 K % (8 split), -4 strides or alignment, -7 act_cols with hc <= 0, -6 launch error.
+ * Replaces kernels/r9k_router.hip:120-155 (r9k_router_gemm). */
+int r9k_router_gemm(long x, long sx, long w, long sw, long out, long so, int M, int E, int K, int split, int out_bf16,
+                    int act_cols, float hc, long stream);
+int r9k_router_max_m(void);            /* 32; replaces r9k_router.hip:155 */
+
 /* --- entry points with no reference C symbol ------------------------------------------------------------------ */
 
 /* Routing only (the role of vLLM's topk_softmax behind the stock FusedTopKRouter, which the reference calls when

@@ -19,6 +19,7 @@ Parity status per function (what pins it; tests/test_oracle_*.py):
   nvfp4 dequant / search           E2M1 closed form, brute-force nearest value and exponent, the reference
                                    test's error-floor criterion, fp32-log2 agreement on all NVFP4-derivable maxima
   gemm / layer                     pure-Python dot products on tiny inputs
+  router_gemm / hc_silu            pure-Python dot products; torch silu (library routine) and its closed-form limits
 """
 from __future__ import annotations
 
@@ -261,6 +262,23 @@ def grouped_gemm(aq: np.ndarray, a_s: np.ndarray, w_deq, expert_of_row: np.ndarr
         if topk_w is not None:
             sc = sc * torch.from_numpy(topk_w[r].astype(np.float32))
         out[sel] = bf16_bits((acc * sc[:, None]).to(torch.bfloat16))
+    return out
+
+
+def router_gemm(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """Router logits [M, E] = x [M, K] . w [E, K]^T from the bf16 values, accumulated in fp64 (the gate GEMM the
+    reference's router kernel computes, kernels/r9k_router.hip:120-155; its test measures against this fp64 product,
+    tests/test_router_r9k.py:50-56)."""
+    return x.detach().cpu().double() @ w.detach().cpu().double().t()
+
+
+def hc_silu(v: torch.Tensor, act_cols: int, hc: float) -> torch.Tensor:
+    """The router kernel's hyper-connection epilogue (kernels/r9k_router.hip:34-40): columns < act_cols become
+    s * sigmoid(s) with s = bf16(v) / hc; the others keep v. fp64 from the fp32 GEMM values v."""
+    v = v.detach().cpu().float()
+    s = v.to(torch.bfloat16).double() / hc
+    out = v.double().clone()
+    out[:, :act_cols] = (s / (1.0 + torch.exp(-s)))[:, :act_cols]
     return out
 
 

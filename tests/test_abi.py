@@ -56,6 +56,17 @@ def test_shape_errors_before_launch():
     # quant: nothing to do for M == 0; tiled gate refused
     assert L.r9k_quant_rows_fp8(1, 1, 1, 0, 64, 64, z) == 0
     assert L.r9k_quant_rows_fp8_gate(16, 16, 16, 16, 16, 1, 64, 64, 1, z) == -3
+    # router GEMM: M, split, K % (8 split), strides / alignment, act_cols with hc <= 0
+    from r9700_vllm import router as R
+    Lr = R.lib()
+    assert Lr.r9k_router_max_m() == 32
+    assert Lr.r9k_router_gemm(16, 64, 16, 64, 16, 64, 33, 64, 64, 1, 1, 0, 1.0, z) == -1
+    assert Lr.r9k_router_gemm(16, 64, 16, 64, 16, 64, 1, 64, 4, 1, 1, 0, 1.0, z) == -1
+    assert Lr.r9k_router_gemm(16, 64, 16, 64, 16, 64, 1, 64, 64, 3, 1, 0, 1.0, z) == -2
+    assert Lr.r9k_router_gemm(16, 64, 16, 64, 16, 64, 1, 64, 72, 2, 1, 0, 1.0, z) == -3
+    assert Lr.r9k_router_gemm(16, 60, 16, 64, 16, 64, 1, 64, 64, 1, 1, 0, 1.0, z) == -4
+    assert Lr.r9k_router_gemm(24, 64, 16, 64, 16, 64, 1, 64, 64, 1, 1, 0, 1.0, z) == -4
+    assert Lr.r9k_router_gemm(16, 64, 16, 64, 16, 64, 1, 64, 64, 1, 1, 8, 0.0, z) == -7
     # converter: K % 32
     assert L.r9k_nvfp4_to_mxfp4(16, 16, 16, 16, 16, 4, 48, z) == -2
     assert L.r9k_quantize_mxfp4_search(16, 16, 16, 4, 40, z) == -2

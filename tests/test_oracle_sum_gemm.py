@@ -63,3 +63,26 @@ def test_grouped_gemm_python_loop():
             v = np.float32(np.float32(acc) * sc)
             ref = torch.tensor([v]).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)[0]
             assert out[r, n] == ref
+
+
+def test_router_gemm_python_loop():
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(3, 24, generator=g).to(torch.bfloat16)
+    w = torch.randn(5, 24, generator=g).to(torch.bfloat16)
+    ref = O.router_gemm(x, w)
+    xf, wf = x.double().tolist(), w.double().tolist()
+    for m in range(3):
+        for e in range(5):
+            assert ref[m, e].item() == sum(a * b for a, b in zip(xf[m], wf[e]))
+
+
+def test_hc_silu_epilogue():
+    v = torch.tensor([[0.0, 3.0, -40.0, 40.0, 1.0078125, 2.5]], dtype=torch.float32)
+    hc = 2.0
+    out = O.hc_silu(v, 5, hc)
+    s = v.to(torch.bfloat16).double() / hc
+    assert torch.allclose(out[:, :5], torch.nn.functional.silu(s)[:, :5], rtol=1e-15, atol=0)
+    assert out[0, 0] == 0.0 and abs(out[0, 2]) < 1e-7 and abs(out[0, 3] - 20.0) < 1e-7    # silu(0), the limits
+    assert out[0, 5] == 2.5                                                                # past act_cols: v
+    # s is taken from the bf16-rounded v: 1.0078125 is bf16-exact, 1.00390625 rounds to 1.0 (tie to even)
+    assert O.hc_silu(torch.tensor([[1.00390625]]), 1, 1.0)[0, 0] == O.hc_silu(torch.tensor([[1.0]]), 1, 1.0)[0, 0]
