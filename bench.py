@@ -8,7 +8,9 @@ T <= 64 the per-token fp8 quant of x in the same launch) -> grouped gate_up GEMM
 down GEMM (router weight folded) -> top-k sum, five launches on one stream (six above T = 64). The headline `value`
 is BASELINE config 2 (E=288 experts, hidden 2048, expert intermediate 512, top-8) at T=64 tokens, the
 bandwidth-bound decode point; T = 1, 8, 16, the config 3 prefill (T=8192) and the router gate GEMM that produces
-the layer's logits (r9k_router_gemm against stock's F.linear) are reported beside it.
+the layer's logits (r9k_router_gemm against stock's F.linear) are reported beside it, with config 4 (NVFP4 -> MXFP4
+conversion of a [17408, 5120] weight, then the dense GEMM at M = 1, 4, 16, 4096) and config 5 (E=384, hidden 4096,
+Zipf-skewed routing, T = 1, 32, 256, 4096).
 
 Method: weights and inputs are resident in HBM before timing. Steps run as HIP-graph replays that cycle through
 COPIES independent weight copies (> 2x the 256 MB Infinity Cache per cycle), so weight bytes come from HBM, not from
@@ -47,6 +49,8 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-prefill", action="store_true", help="skip the T=8192 prefill line")
     ap.add_argument("--no-router", action="store_true", help="skip the router gate GEMM timings")
+    ap.add_argument("--no-cfg4", action="store_true", help="skip the config 4 converter + dense GEMM lines")
+    ap.add_argument("--no-cfg5", action="store_true", help="skip the config 5 (E=384, Zipf) layer lines")
     return ap.parse_args()
 
 
@@ -76,7 +80,7 @@ class Step:
     (T * topk <= 4096 rows, as R9kTopKRouter), otherwise top-k + activation quant in one launch (as R9kTopKRouter
     above its row limit) and the in-apply align."""
 
-    def __init__(self, layer: Layer, T: int, topk: int, dev, seed: int):
+    def __init__(self, layer: Layer, T: int, topk: int, dev, seed: int, zipf: bool = False):
         from r9700_vllm.kernels import moe as K
         from r9700_vllm.moe import route
         from r9700_vllm.moe.experts import R9700Mxfp4Experts
@@ -84,7 +88,12 @@ class Step:
         self.layer, self.T, self.topk, self.dev = layer, T, topk, dev
         g = torch.Generator().manual_seed(seed)
         self.x_cpu = torch.randn(T, layer.H, generator=g).to(torch.bfloat16)
-        self.logits_cpu = torch.randn(T, layer.E, generator=g).to(torch.bfloat16)
+        logits = torch.randn(T, layer.E, generator=g)
+        if zipf:
+            # config 5's skew: expert popularity ~ Zipf(1.1) over a seeded ranking of the experts
+            rank = torch.randperm(layer.E, generator=g).float() + 1
+            logits = logits - 1.1 * torch.log(rank)[None, :]
+        self.logits_cpu = logits.to(torch.bfloat16)
         self.x = self.x_cpu.to(dev)
         self.logits = self.logits_cpu.to(dev)
         self.out = torch.empty(T, layer.H, dtype=torch.bfloat16, device=dev)
@@ -199,6 +208,98 @@ def gate_up_kernel_time(step: Step, reps: int = 40):
     nbytes = touched * (N1 * K1 // 2 + N1 * K1 // 32) + step.T * K1 + step.T * 4 + step.numel * N1 * 2
     flops = 2 * step.numel * N1 * K1
     return ms, nbytes, flops, touched
+
+
+def events_ms(fn, reps: int) -> float:
+    """Average ms of fn() over `reps` calls, HIP events on the current stream around them (after one warm call)."""
+    fn()
+    torch.cuda.synchronize()
+    s = torch.cuda.current_stream()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(s)
+    for _ in range(reps):
+        fn()
+    b.record(s)
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / reps
+
+
+def cfg4_lines(dev) -> dict:
+    """the load-time NVFP4 -> MXFP4 conversion of a [17408, 5120] dense weight (uniform codes,
+    s16 = e4m3(|N(0,1)| * 0.05), global 1), one launch over all rows, then the fp8-act x MXFP4 GEMM on the converted
+    weight at M = 1, 4, 16, 4096 (ops.mxfp4_linear: per-row quant + GEMM). GEMM timing: one HIP graph cycling through
+    12 weight copies (570 MB, > 2x the Infinity Cache), HIP events around its replays."""
+    from r9700_vllm import ops
+    from r9700_vllm.kernels import moe as K
+    from r9700_vllm.quant import nvfp4 as NV
+    N, Kd = 17408, 5120
+    g = torch.Generator(device=dev).manual_seed(SEED + 4000)
+    packed = torch.randint(0, 256, (N, Kd // 2), generator=g, device=dev, dtype=torch.int32).to(torch.uint8)
+    s16 = (torch.randn(N, Kd // 16, generator=g, device=dev).abs() * 0.05).to(torch.float8_e4m3fn)
+    row_div = torch.ones(N, device=dev)
+    res = {}
+    conv = lambda: NV.nvfp4_to_mxfp4(packed, s16, row_div, rows_per_chunk=N)
+    ms = events_ms(conv, 5)
+    cin, cout = N * Kd // 2 + N * Kd // 16, N * Kd // 2 + N * Kd // 32
+    res["convert"] = {"ms": round(ms, 4), "GBps": round((cin + cout) / (ms * 1e-3) / 1e9, 1),
+                      "bytes_in": cin, "bytes_out": cout}
+    print(f"# cfg4 convert [17408, 5120]: {ms * 1e3:.1f} us, {res['convert']['GBps']} GB/s", file=sys.stderr,
+          flush=True)
+    mp, me = conv()
+    W0 = K.prepare_mxfp4_weights(mp.unsqueeze(0), me.unsqueeze(0))
+    del packed, s16, mp, me
+    Ws = [W0] + [K.Mxfp4Experts(W0.wq.clone(), W0.wsr.clone(), N, Kd) for _ in range(11)]
+    wbytes = N * Kd // 2 + N * Kd // 32
+    gemm = {}
+    for M in (1, 4, 16, 4096):
+        x = torch.randn(M, Kd, generator=g, device=dev).to(torch.bfloat16)
+        calls = Ws if M <= 16 else Ws[:2]
+        for W in calls[:2]:
+            ops.mxfp4_linear(x, W.wq, W.wsr, N, Kd)
+        torch.cuda.synchronize()
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr):
+            for W in calls:
+                ops.mxfp4_linear(x, W.wq, W.wsr, N, Kd)
+        reps = 20 if M <= 16 else 5
+        ms = events_ms(gr.replay, reps) / len(calls)
+        del gr
+        nbytes = wbytes + M * Kd * 2 + M * N * 2
+        flops = 2 * M * N * Kd
+        gemm[str(M)] = {"us": round(ms * 1e3, 2), "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                        "hbm_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                        "TFLOPS": round(flops / (ms * 1e-3) / 1e12, 1)}
+        print(f"# cfg4 GEMM M={M}: {ms * 1e3:.1f} us, {gemm[str(M)]['GBps']} GB/s, {gemm[str(M)]['TFLOPS']} TFLOPS",
+              file=sys.stderr, flush=True)
+    res["gemm"] = gemm
+    del Ws, W0
+    torch.cuda.empty_cache()
+    return {"workload": "cfg4 dense [17408, 5120]: NVFP4 -> MXFP4 conversion, then fp8-act x MXFP4 GEMM", **res}
+
+
+def cfg5_lines(dev, steps: int, warmup: int) -> dict:
+    """hidden 4096, intermediate 2048, 384 experts (e8m0 in [116, 126]), top-8 over Zipf(1.1)-biased
+    logits, T = 1, 32, 256, 4096; the same Step and graph timing as config 2 (4 weight copies, 19 GB)."""
+    layer = Layer(384, 4096, 2048, dev, lo=116, hi=126, seed=SEED + 5000)
+    out = {}
+    for T in (1, 32, 256, 4096):
+        st = Step(layer, T, 8, dev, SEED + 5000 + T, zipf=True)
+        ms, n = graph_time(st, steps if T < 4096 else max(8, steps // 10), warmup)
+        nbytes, touched = layer_bytes(st)
+        counts = torch.bincount(st.ids.reshape(-1).long(), minlength=layer.E).float()
+        flops = 6 * T * 8 * layer.H * layer.I
+        out[str(T)] = {"ms_per_step": round(ms, 5), "tokens_per_s": round(T / (ms * 1e-3), 1),
+                       "experts_touched": touched, "layer_GBps": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                       "hbm_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                       "TFLOPS": round(flops / (ms * 1e-3) / 1e12, 1),
+                       "top_expert_share": round(float(counts.max() / counts.sum()), 4)}
+        print(f"# cfg5 T={T}: {ms * 1e3:.1f} us/layer, {out[str(T)]['layer_GBps']} GB/s, "
+              f"{out[str(T)]['TFLOPS']} TFLOPS over {touched} experts", file=sys.stderr, flush=True)
+        del st
+    del layer
+    torch.cuda.empty_cache()
+    return {"workload": "cfg5 layer: E=384, hidden 4096, intermediate 2048, top-8, Zipf(1.1) routing",
+            "sweep": out}
 
 
 def router_times(dev, reps_bytes: int = 512 << 20):
@@ -354,6 +455,8 @@ def main():
         print(f"# prefill T=8192: {ms:.3f} ms/layer, {tf:.1f} TFLOPS", file=sys.stderr, flush=True)
 
     router = None if args.no_router else router_times(dev)
+    cfg4 = None if args.no_cfg4 else cfg4_lines(dev)
+    cfg5 = None if args.no_cfg5 else cfg5_lines(dev, args.steps, args.warmup)
     cpu = None if args.no_cpu else cpu_baseline(main_step)
     line = {
         "metric": "MoE-layer tokens/s + HBM GB/s (decode) / MXFP4 TFLOPS (prefill), 1 GPU",
@@ -379,6 +482,8 @@ def main():
         "decode_sweep": sweep,
         "prefill": prefill,
         "router": router,
+        "cfg4": cfg4,
+        "cfg5": cfg5,
     }
     print(json.dumps(line), flush=True)
 
