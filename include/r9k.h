@@ -48,8 +48,11 @@ int r9k_moe_4bit_prefill(int nv, long a, long as, long wq, long ws, long wref, l
                          long expert_ids, long ntpp, long topk_w, long ws_estride, long wref_estride, int max_blocks,
                          int numel, int a_row_div, int K, int N, int cfg, long stream);
 
-/* Native NVFP4 experts (kernels/r9k_moe_mxfp4a8.hip:641-647): not served on gfx950, returns -8 (NVFP4 checkpoints
- * are converted to MXFP4 at load with r9k_nvfp4_to_mxfp4). Exported so the reference's bindings load. */
+/* Native NVFP4 experts: the same grouped GEMM over the checkpoint's e2m1 codes, e4m3 per-16 scales and a per-row fp32
+ * multiplier wg (wg_estride floats per expert), exact; ws / wq in prepare_nvfp4_weights' layout (ws_estride bytes per
+ * expert, code stride N * ceil(K/128) * 64 bytes). Decode-family tables (16 * MT-row blocks, MT 1 / 2 / 4). WV and
+ * NPW are accepted and not used; K % (16 SK) as the reference's rule. 0, -1 N % 16, -2 K, -3 argument, -7 MT,
+ * -6 launch error. Replaces kernels/r9k_moe_mxfp4a8.hip:641-647 (r9k_moe_nvfp4a8). */
 int r9k_moe_nvfp4a8(long a, long as, long wq, long ws, long wg, long c, long sorted_ids, long expert_ids, long ntpp,
                     long topk_w, long ws_estride, long wg_estride, int max_blocks, int numel, int a_row_div, int K,
                     int N, int WV, int SK, int NPW, int MT, long stream);

@@ -20,6 +20,7 @@ Parity status per function (what pins it; tests/test_oracle_*.py):
                                    test's error-floor criterion, fp32-log2 agreement on all NVFP4-derivable maxima
   gemm / layer                     pure-Python dot products on tiny inputs
   router_gemm / hc_silu            pure-Python dot products; torch silu (library routine) and its closed-form limits
+  nvfp4_gemm                       pure-Python dot products over the closed-form e2m1 / e4m3 values on tiny inputs
 """
 from __future__ import annotations
 
@@ -262,6 +263,32 @@ def grouped_gemm(aq: np.ndarray, a_s: np.ndarray, w_deq, expert_of_row: np.ndarr
         if topk_w is not None:
             sc = sc * torch.from_numpy(topk_w[r].astype(np.float32))
         out[sel] = bf16_bits((acc * sc[:, None]).to(torch.bfloat16))
+    return out
+
+
+def nvfp4_gemm(aq: np.ndarray, a_s: np.ndarray, packed: np.ndarray, s16: np.ndarray, wg: np.ndarray,
+               expert_of_row: np.ndarray, a_row_div: int, topk_w: np.ndarray | None = None,
+               rows: np.ndarray | None = None) -> np.ndarray:
+    """bf16 bits [R, N] of the native NVFP4 grouped GEMM for the routed rows `rows` (default all):
+    out[r, n] = bf16(acc * ((wg[e, n] * a_s[r // d]) * topk_w[r])), acc = deq(aq[r // d]) . (e2m1 * s16)[e, n, :] in
+    fp64 -- the reference's native path: exact e2m1 x e4m3 weights (kernels/r9k_moe_mxfp4a8.hip:89-96, 300-340), the
+    per-row fp32 multiplier and the row scale in the epilogue in that order (:469-482). packed [E, N, K/2] u8,
+    s16 [E, N, K/16] e4m3 bits, wg [E, N] fp32."""
+    rows = np.arange(expert_of_row.size) if rows is None else np.asarray(rows)
+    eor = expert_of_row[rows]
+    E, N, Kh = packed.shape
+    out = np.zeros((rows.size, N), dtype=np.uint16)
+    for e in np.unique(eor):
+        sel = np.nonzero(eor == e)[0]
+        r = rows[sel]
+        W = torch.from_numpy(dequant_nvfp4(packed[e], s16[e], np.ones(N, dtype=np.float32))).double()
+        a = e4m3_dequant(aq[r // a_row_div], torch.float64)
+        acc = (a @ W.T).to(torch.float32)
+        sc = torch.from_numpy(wg[e].astype(np.float32))[None, :] * torch.from_numpy(
+            a_s[r // a_row_div].astype(np.float32))[:, None]
+        if topk_w is not None:
+            sc = sc * torch.from_numpy(topk_w[r].astype(np.float32))[:, None]
+        out[sel] = bf16_bits((acc * sc).to(torch.bfloat16))
     return out
 
 

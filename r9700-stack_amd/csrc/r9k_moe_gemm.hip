@@ -481,17 +481,6 @@ extern "C" int r9k_moe_4bit_prefill(int nv, long a, long as, long wq, long ws, l
   return hipGetLastError() == hipSuccess ? 0 : -6;
 }
 
-// Reference: kernels/r9k_moe_mxfp4a8.hip:641-647 (native NVFP4 experts). Not served on gfx950: NVFP4 checkpoints are
-// converted to MXFP4 at load (r9k_nvfp4_to_mxfp4). Exported so the reference's bindings load; returns -8.
-extern "C" int r9k_moe_nvfp4a8(long a, long as, long wq, long ws, long wg, long c, long sorted_ids, long expert_ids,
-                               long ntpp, long topk_w, long ws_estride, long wg_estride, int max_blocks, int numel,
-                               int a_row_div, int K, int N, int WV, int SK, int NPW, int MT, long stream) {
-  (void)a; (void)as; (void)wq; (void)ws; (void)wg; (void)c; (void)sorted_ids; (void)expert_ids; (void)ntpp;
-  (void)topk_w; (void)ws_estride; (void)wg_estride; (void)max_blocks; (void)numel; (void)a_row_div; (void)K;
-  (void)N; (void)WV; (void)SK; (void)NPW; (void)MT; (void)stream;
-  return -8;
-}
-
 extern "C" int r9k_moe_prefill_bm(int cfg) { return (cfg < 0 || cfg >= NPF) ? -1 : kPf[cfg].BM; }
 extern "C" int r9k_moe_prefill_bk(int cfg) { return (cfg < 0 || cfg >= NPF) ? -1 : kPf[cfg].BK; }
 extern "C" int r9k_moe_block(void) { return 16; }

@@ -36,6 +36,8 @@ def lib() -> ctypes.CDLL:
         L.r9k_moe_mxfp4a8.argtypes = [l] * 12 + [i] * 9 + [l]
         L.r9k_moe_mxfp4a8_f.restype = i
         L.r9k_moe_mxfp4a8_f.argtypes = [i] + [l] * 12 + [i] * 9 + [l]
+        L.r9k_moe_nvfp4a8.restype = i
+        L.r9k_moe_nvfp4a8.argtypes = [l] * 12 + [i] * 9 + [l]
         L.r9k_moe_4bit_prefill.restype = i
         L.r9k_moe_4bit_prefill.argtypes = [i] + [l] * 12 + [i] * 6 + [l]
         L.r9k_moe_prefill_bm.restype = i
@@ -100,26 +102,47 @@ class Mxfp4Experts:
         return (self.K // GROUP + 1) * self.N
 
 
+NV_KT = 128            # K per NVFP4 weight tile (8 groups of 16)
+
+
 @dataclass
 class Nvfp4Experts:
-    """Native NVFP4 (e2m1 + e4m3 scale per 16 + fp32 global per row); not served by the gfx950 library."""
+    """Native NVFP4 experts (e2m1 codes, e4m3 scale per 16, fp32 multiplier per row) in the gfx950 kernel layout
+    (prepare_nvfp4_weights): wq int32 [E, N * ceil(K/128) * 16], ws uint8 [E, ceil(K/128) * 8, N] (the reference's
+    [E, K/16, N] size when K % 128 == 0; the bytes are in the kernel's order), wg fp32 [E, N]."""
     wq: torch.Tensor
     ws: torch.Tensor
     wg: torch.Tensor
     N: int
     K: int
 
+    @property
+    def ws_estride(self) -> int:
+        return self.N * ((self.K + NV_KT - 1) // NV_KT) * 8
+
 
 def prepare_nvfp4_weights(packed: torch.Tensor, scale16: torch.Tensor, row_mult: torch.Tensor) -> Nvfp4Experts:
-    """packed [E, N, K/2] u8, scale16 [E, N, K/16] e4m3, row_mult [E, N] fp32 -> Nvfp4Experts (fragment-order codes,
-    scales transposed to [E, K/16, N]). The layout is kept for API parity; moe_gemm refuses it on gfx950."""
+    """packed [E, N, K/2] u8, scale16 [E, N, K/16] e4m3, row_mult [E, N] fp32 -> Nvfp4Experts, the checkpoint bits
+    kept (reference: kernels/moe.py:86-104; the layout is this kernel's, csrc/r9k_moe_nvfp4.hip).
+
+    Codes: the MXFP4 fragment order over K-tiles of 128 -- column tile nt (16 rows) holds ceil(K/128) K-tiles of 1 KB,
+    lane l = g*16 + c holding the 16 checkpoint bytes W[nt*16 + c, kt*64 + 16g .. +16] at l*16. Scales: per column
+    tile and K-tile 128 bytes, lane l's 2 bytes at l*2 the scales of groups kt*8 + 2g, kt*8 + 2g + 1 of row nt*16 + c.
+    A partial last K-tile is zero-padded (codes and scales)."""
     E, N, Kh = packed.shape
     K = Kh * 2
-    assert N % 16 == 0 and K % 32 == 0, (N, K)
+    assert N % 16 == 0 and K % 16 == 0, (N, K)
     assert scale16.shape == (E, N, K // 16), (scale16.shape, (E, N, K // 16))
-    ws = scale16.view(torch.uint8).transpose(1, 2).contiguous()
-    return Nvfp4Experts(permute_fragments(packed.view(torch.uint8)), ws,
-                        row_mult.float().reshape(E, N).contiguous(), N, K)
+    nkt = (K + NV_KT - 1) // NV_KT
+    p = packed.view(torch.uint8)
+    sc = scale16.view(torch.uint8)
+    if nkt * 64 != Kh:
+        p = torch.nn.functional.pad(p, (0, nkt * 64 - Kh))
+        sc = torch.nn.functional.pad(sc, (0, nkt * 8 - K // 16))
+    NT = N // 16
+    wq = p.reshape(E, NT, 16, nkt, 4, 16).permute(0, 1, 3, 4, 2, 5).contiguous().reshape(E, -1)
+    ws = sc.reshape(E, NT, 16, nkt, 4, 2).permute(0, 1, 3, 4, 2, 5).contiguous().reshape(E, nkt * 8, N)
+    return Nvfp4Experts(wq.view(torch.int32), ws, row_mult.float().reshape(E, N).contiguous(), N, K)
 
 
 def permute_fragments(packed: torch.Tensor) -> torch.Tensor:
@@ -387,7 +410,23 @@ def moe_gemm(a_q: torch.Tensor, a_s: torch.Tensor, w: Mxfp4Experts, out: torch.T
     if a_tiled:
         raise RuntimeError("moe_gemm(a_tiled=True) is a gfx1201 kernel format")
     if isinstance(w, Nvfp4Experts):
-        raise RuntimeError("native NVFP4 experts are not served on gfx950: convert with quant.nvfp4.nvfp4_to_mxfp4")
+        # decode-family kernel only (16*MT-row blocks; reference entry kernels/r9k_moe_mxfp4a8.hip:641-647)
+        if prefill is not None:
+            raise RuntimeError("moe_gemm: native NVFP4 experts run the decode-family kernel (prefill=None, MT <= 4)")
+        assert out.dtype == torch.bfloat16 and out.shape[1] == w.N and a_q.shape[1] == w.K and out.is_contiguous()
+        assert a_q.is_contiguous() and a_s.dtype == torch.float32
+        if topk_w is not None:
+            assert topk_w.dtype == torch.float32 and topk_w.is_contiguous()
+        blk = MOE_BLOCK * MT
+        max_blocks = min(expert_ids.numel(), (numel + blk - 1) // blk + min(numel, E))
+        rc = lib().r9k_moe_nvfp4a8(
+            a_q.data_ptr(), a_s.data_ptr(), w.wq.data_ptr(), w.ws.data_ptr(), w.wg.data_ptr(), out.data_ptr(),
+            sorted_ids.data_ptr(), expert_ids.data_ptr(), ntpp.data_ptr(),
+            topk_w.data_ptr() if topk_w is not None else 0, w.ws_estride, w.N, max_blocks, numel, a_row_div, w.K,
+            w.N, WV, 1, NPW, MT, _stream())
+        if rc:
+            raise RuntimeError(f"r9k_moe_nvfp4a8 failed ({rc}) N={w.N} K={w.K} MT={MT}")
+        return out
     assert out.dtype == torch.bfloat16 and out.shape[1] == w.N and a_q.shape[1] == w.K and out.is_contiguous()
     assert a_q.is_contiguous() and a_s.dtype == torch.float32
     if topk_w is not None:

@@ -68,11 +68,13 @@ def _experts_base():
 class R9700Mxfp4Experts(_experts_base()):
 
     @classmethod
-    def standalone(cls, w1_scale: torch.Tensor, w2_scale: torch.Tensor) -> "R9700Mxfp4Experts":
-        """An experts object outside vLLM over pack_scales-layout scale tensors."""
+    def standalone(cls, w1_scale: torch.Tensor, w2_scale: torch.Tensor, nv=None) -> "R9700Mxfp4Experts":
+        """An experts object outside vLLM over pack_scales-layout scale tensors, or, with nv = (w13 row multipliers,
+        w2 row multipliers), over native NVFP4 scale tensors (prepare_nvfp4_weights)."""
         obj = cls.__new__(cls)
         obj.w1_scale = w1_scale
         obj.w2_scale = w2_scale
+        obj.nv = nv
         return obj
 
     @staticmethod
@@ -106,19 +108,32 @@ class R9700Mxfp4Experts(_experts_base()):
                     or getattr(moe_parallel_config, "use_fi_nvl_one_sided_kernels", False))
 
     fold = (False, False)
+    # native NVFP4 experts (quant/nvfp4.py prep_native_moe): (w13, w2) per-row fp32 multipliers [E, N]; the scale
+    # tensors then hold prepare_nvfp4_weights' layout and both GEMMs run r9k_moe_nvfp4a8 on decode-family blocks
+    # (reference: moe/experts.py:118-145)
+    nv: tuple[torch.Tensor, torch.Tensor] | None = None
 
     def _dims(self, ws: torch.Tensor) -> tuple[int, int]:
         """(N, K) of one GEMM from its pack_scales tensor [E, K/32 + 1, N]."""
         return ws.shape[2], (ws.shape[1] - 1) * K.GROUP
+
+    def _gemm_dims(self, hidden: int) -> tuple[int, int, int, int]:
+        """(N1, K1, N2, K2): from the scale tensors for MXFP4, from the row multipliers and the input for NVFP4."""
+        if self.nv is not None:
+            N1, N2 = self.nv[0].shape[1], self.nv[1].shape[1]
+            return N1, hidden, N2, N1 // 2
+        return (*self._dims(self.w1_scale), *self._dims(self.w2_scale))
 
     def process_weights_after_loading(self, layer) -> None:
         sup = getattr(super(), "process_weights_after_loading", None)
         if sup is not None:
             sup(layer)
         self.fold = (False, False)
+        self.nv = ((layer.w13_weight_row_mult, layer.w2_weight_row_mult)
+                   if getattr(layer, "_r9k_nvfp4", False) else None)
 
     def moe_problem_size(self, a1, w1, w2, topk_ids):
-        N1, _ = self._dims(self.w1_scale)
+        N1 = self._gemm_dims(a1.size(-1))[0]
         return w1.size(0), a1.size(0), N1 // 2, a1.size(-1), topk_ids.size(1)
 
     def workspace_shapes(self, M, N, K_, topk, global_num_experts, local_num_experts, expert_tokens_meta,
@@ -131,8 +146,7 @@ class R9700Mxfp4Experts(_experts_base()):
               apply_router_weight_on_input):
         assert not apply_router_weight_on_input, "R9700Mxfp4Experts: router weight on input not supported"
         assert hidden_states.dtype == torch.bfloat16 and hidden_states.is_contiguous()
-        N1, K1 = self._dims(self.w1_scale)
-        N2, K2 = self._dims(self.w2_scale)
+        N1, K1, N2, K2 = self._gemm_dims(hidden_states.shape[1])
         M, topk = hidden_states.shape[0], topk_ids.shape[1]
         E = w1.shape[0]
         if global_num_experts == -1:
@@ -142,26 +156,31 @@ class R9700Mxfp4Experts(_experts_base()):
         if M == 0:
             return
 
+        nv = self.nv
         MT = K.pick_mt(numel, global_num_experts)
-        big = K.pick_moe_prefill_block(numel, global_num_experts, K1, K2)
+        big = None if nv is not None else K.pick_moe_prefill_block(numel, global_num_experts, K1, K2)
         if big is not None:                                  # prefill widths: one 256-row block ~ one expert
             pf_gate = pf_down = big[0]
             blk = big[1]
-        else:
+        else:                                                # (native NVFP4: the decode-family kernel at every width)
             blk = K.MOE_BLOCK * MT
-            pf_down = K.pick_moe_prefill(MT, K2)
-            pf_gate = K.pick_moe_prefill(MT, K1, gate_up=True)
+            pf_down = None if nv is not None else K.pick_moe_prefill(MT, K2)
+            pf_gate = None if nv is not None else K.pick_moe_prefill(MT, K1, gate_up=True)
         tabs = route.take(getattr(self, "r9k_layer", None), topk_ids, blk, numel) if expert_map is None else None
         if tabs is None:
             tabs = K.moe_align(topk_ids, blk, E, expert_map)
         sid, eid, ntpp = tabs
-        W1 = K.Mxfp4Experts(w1, self.w1_scale, N1, K1)
-        W2 = K.Mxfp4Experts(w2, self.w2_scale, N2, K2)
+        if nv is not None:
+            W1 = K.Nvfp4Experts(w1, self.w1_scale, nv[0], N1, K1)
+            W2 = K.Nvfp4Experts(w2, self.w2_scale, nv[1], N2, K2)
+        else:
+            W1 = K.Mxfp4Experts(w1, self.w1_scale, N1, K1)
+            W2 = K.Mxfp4Experts(w2, self.w2_scale, N2, K2)
 
         # the router's fp8 quant of this input, when it made one (with its tables at decode, alone at prefill)
         q = route.take_quant(getattr(self, "r9k_layer", None), topk_ids, hidden_states) if expert_map is None else None
         xq, xs = q if q is not None else K.quant_rows_fp8(hidden_states)
-        fused = MOE_FUSE and MT == 1 and pf_gate is None and pf_down is None
+        fused = MOE_FUSE and nv is None and MT == 1 and pf_gate is None and pf_down is None
         if fused:
             aq = torch.empty((numel, N1 // 2), dtype=torch.float32, device=dev)
             K.moe_gemm(xq, xs, W1, aq, sid, eid, ntpp, numel, topk, None, num_experts=E, MT=1, fuse=1)

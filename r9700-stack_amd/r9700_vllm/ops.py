@@ -2,9 +2,9 @@
 captured into HIP graphs (reference: r9700_vllm/ops.py:1-170, MXFP4 path).
 
   torch.ops.r9700.mxfp4_linear(x[M,K] bf16, wq, wsr, N, K, fold) -> [M,N] bf16   MXFP4 weight x per-token fp8 act
+  torch.ops.r9700.nvfp4_linear(x[M,K] bf16, wq, ws, wg, N, K) -> [M,N] bf16      native NVFP4 weight (exact bits)
 
-The reference's fp8_linear / fp8_block_linear (dense fp8 GEMMs) and nvfp4_linear (native NVFP4) are not part of
-the gfx950 MoE build.
+The reference's fp8_linear / fp8_block_linear (dense fp8 GEMMs) are not part of the gfx950 MoE build.
 """
 from __future__ import annotations
 
@@ -66,11 +66,34 @@ def _mxfp4_linear_fake(x: torch.Tensor, wq: torch.Tensor, wsr: torch.Tensor, N: 
     return x.new_empty((x.shape[0], N))
 
 
+def _nvfp4_linear(x: torch.Tensor, wq: torch.Tensor, ws: torch.Tensor, wg: torch.Tensor, N: int, K: int
+                  ) -> torch.Tensor:
+    """x [M, K] bf16 -> [M, N] bf16 over native NVFP4 weights (prepare_nvfp4_weights of one expert) with per-row fp8
+    activations (reference: r9700_vllm/ops.py nvfp4_linear). The decode-family kernel serves every M (64-row tiles
+    from M = 64; there is no NVFP4 prefill kernel on gfx950)."""
+    from .kernels import moe as KM
+    M = x.shape[0]
+    out = torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
+    if M == 0:
+        return out
+    W = KM.Nvfp4Experts(wq, ws, wg, N, K)
+    q, s = KM.quant_rows_fp8(x)
+    t, MT = _identity_tables(q, M)
+    KM.moe_gemm(q, s, W, out, *t, M, 1, None, num_experts=1, MT=MT)
+    return out
+
+
+def _nvfp4_linear_fake(x: torch.Tensor, wq: torch.Tensor, ws: torch.Tensor, wg: torch.Tensor, N: int, K: int
+                       ) -> torch.Tensor:
+    return x.new_empty((x.shape[0], N))
+
+
 def register() -> None:
     global _DONE
     if _DONE:
         return
     register_custom_op(_LIB, "mxfp4_linear", _mxfp4_linear, [], _mxfp4_linear_fake)
+    register_custom_op(_LIB, "nvfp4_linear", _nvfp4_linear, [], _nvfp4_linear_fake)
     _DONE = True
 
 
@@ -81,3 +104,12 @@ def mxfp4_linear(x: torch.Tensor, wq: torch.Tensor, wsr: torch.Tensor, N: int, K
     x2 = x.reshape(-1, K)
     x2 = (x2 if x2.dtype == torch.bfloat16 else x2.to(torch.bfloat16)).contiguous()
     return torch.ops.r9700.mxfp4_linear(x2, wq, wsr, N, K, fold).reshape(*lead, N)
+
+
+def nvfp4_linear(x: torch.Tensor, wq: torch.Tensor, ws: torch.Tensor, wg: torch.Tensor, N: int, K: int
+                 ) -> torch.Tensor:
+    register()
+    lead = x.shape[:-1]
+    x2 = x.reshape(-1, K)
+    x2 = (x2 if x2.dtype == torch.bfloat16 else x2.to(torch.bfloat16)).contiguous()
+    return torch.ops.r9700.nvfp4_linear(x2, wq, ws, wg, N, K).reshape(*lead, N)

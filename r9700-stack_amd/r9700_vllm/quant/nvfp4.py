@@ -1,8 +1,13 @@
-"""NVFP4 checkpoints on gfx950: convert to MXFP4 while loading, then serve with the libr9k MXFP4 kernels.
+"""NVFP4 checkpoints on gfx950: served natively (exact checkpoint bits) or converted to MXFP4 while loading.
 
-Mirrors the reference's r9700_vllm/quant/nvfp4.py (names, argument meaning). NVFP4 = E2M1 values with an FP8-E4M3
-scale per 16 values and an FP32 global scale (stored by compressed-tensors as a divisor). Conversion per 32-group
-(reference nvfp4.py:39-90), done by one libr9k kernel (r9k_nvfp4_to_mxfp4) per chunk:
+Mirrors the reference's r9700_vllm/quant/nvfp4.py (names, argument meaning, modes). NVFP4 = E2M1 values with an
+FP8-E4M3 scale per 16 values and an FP32 global scale (stored by compressed-tensors as a divisor).
+
+Modes, as the reference's: dense linears default to NATIVE (R9K_NVFP4=native: libr9k's r9k_moe_nvfp4a8 over the
+checkpoint's codes and scales, the global scale as a per-row fp32 multiplier; R9K_NVFP4=mxfp4 converts); MoE layers
+CONVERT by default (R9K_NVFP4_MOE=native serves them natively, on the decode-family kernel at every width).
+
+Conversion per 32-group (reference nvfp4.py:39-90), done by one libr9k kernel (r9k_nvfp4_to_mxfp4) per chunk:
 
   exact dequant   w = e2m1 * s16_e4m3 / global      (fp32)
   requant         E8M0 exponent e = ceil(log2(amax/6)) (no clipping) vs e-1 (clips the top value(s), finer grid for
@@ -115,8 +120,63 @@ def make_dense_scheme_cls(base):
     return R9kNvfp4AsMxfp4
 
 
+def make_native_dense_scheme_cls(base):
+    """Subclass of vLLM's CompressedTensorsW4A4Fp4 served by libr9k's native NVFP4 kernel (R9K_NVFP4=native, the
+    default for dense linears; reference nvfp4.py:145-180): the checkpoint's e2m1 codes and e4m3 per-16 scales are
+    kept bit-exact (re-laid out only), the per-partition global scale becomes a per-row fp32 multiplier, and the
+    activations run as per-row fp8 (the checkpoint's NVFP4 activation quantisation is dropped)."""
+
+    class R9kNvfp4Native(base):
+
+        def process_weights_after_loading(self, layer) -> None:
+            from torch.nn.parameter import Parameter
+            w, s16 = layer.weight_packed.data, layer.weight_scale.data
+            N, Kh = w.shape
+            if N % 16 or (2 * Kh) % 16:
+                raise ValueError(f"r9700 native NVFP4: unsupported shape N={N} K={2 * Kh}")
+            mult = 1.0 / _row_div(layer.weight_global_scale.data, list(layer.logical_widths))
+            W = KM.prepare_nvfp4_weights(w[None], s16[None], mult[None].to(w.device))
+            for n in ("weight_packed", "weight_global_scale", "input_global_scale", "weight_scale"):
+                if hasattr(layer, n):
+                    delattr(layer, n)
+            layer.weight = Parameter(W.wq, requires_grad=False)
+            layer.weight_scale = Parameter(W.ws, requires_grad=False)
+            layer.weight_row_mult = Parameter(W.wg, requires_grad=False)
+            layer._r9k_nk = (N, 2 * Kh)
+            logger.info("r9700: NVFP4 linears on libr9k's native NVFP4 kernel (exact weights, fp8 activations)")
+
+        def apply_weights(self, layer, x, bias=None):
+            from .. import ops
+            N, Kd = layer._r9k_nk
+            out = ops.nvfp4_linear(x, layer.weight, layer.weight_scale, layer.weight_row_mult, N, Kd).to(x.dtype)
+            return out + bias if bias is not None else out
+
+    return R9kNvfp4Native
+
+
 # -------------------------------------------------------------------------------------------------- MoE
 MOE_MODE = (os.environ.get("R9K_NVFP4_MOE", "") or "mxfp4").lower()
+
+
+def prep_native_moe(layer, div13: torch.Tensor, div2: torch.Tensor) -> None:
+    """Serve the layer's NVFP4 experts exactly (reference nvfp4.py:185-206): codes and e4m3 scales re-laid out for
+    r9k_moe_nvfp4a8 (prepare_nvfp4_weights), the per-shard global divisors (div13 [E, 2I], div2 [E, N]) as per-row
+    fp32 multipliers. Leaves w13_weight / w2_weight (int32), *_weight_scale (uint8), *_weight_row_mult (fp32) on the
+    layer and drops *_weight_packed."""
+    from torch.nn.parameter import Parameter
+    for pre, div in (("w13", div13), ("w2", div2)):
+        packed = getattr(layer, f"{pre}_weight_packed")
+        scale = getattr(layer, f"{pre}_weight_scale")
+        E, N, Kh = packed.shape
+        assert scale.shape == (E, N, Kh * 2 // 16), (pre, scale.shape, packed.shape)
+        assert div.shape == (E, N), (pre, div.shape, (E, N))
+        W = KM.prepare_nvfp4_weights(packed.data, scale.data, (1.0 / div.float()).to(packed.device))
+        delattr(layer, f"{pre}_weight_packed")
+        setattr(layer, f"{pre}_weight", Parameter(W.wq, requires_grad=False))
+        setattr(layer, f"{pre}_weight_scale", Parameter(W.ws, requires_grad=False))
+        setattr(layer, f"{pre}_weight_row_mult", Parameter(W.wg, requires_grad=False))
+    layer._r9k_fold = (False, False)
+    layer._r9k_nvfp4 = True
 
 
 def make_moe_method_cls(mxfp4_method_cls):
@@ -154,13 +214,20 @@ def make_moe_method_cls(mxfp4_method_cls):
 
         def process_weights_after_loading(self, layer) -> None:
             from torch.nn.parameter import Parameter
-            if MOE_MODE == "native":
-                logger.warning("r9700: R9K_NVFP4_MOE=native is not served on gfx950; converting to MXFP4")
             I2 = layer.w13_weight_packed.shape[1]
             g13 = layer.w13_weight_global_scale.data.float()                  # [E, shards]
             div13 = g13.repeat_interleave(I2 // g13.shape[1], dim=1)          # [E, 2I]
             g2 = layer.w2_weight_global_scale.data.float()                    # [E]
             div2 = g2[:, None].expand(-1, layer.w2_weight_packed.shape[1])
+            if MOE_MODE == "native":
+                prep_native_moe(layer, div13, div2)
+                for n in ("w13_weight_global_scale", "w2_weight_global_scale", "w13_input_global_scale",
+                          "w2_input_global_scale"):
+                    if hasattr(layer, n):
+                        delattr(layer, n)
+                logger.info("r9700: NVFP4 MoE experts served natively by libr9k (exact checkpoint bits)")
+                self._install_kernel(layer)
+                return
             s13 = self._convert(layer.w13_weight_packed, layer.w13_weight_scale, div13)
             s2 = self._convert(layer.w2_weight_packed, layer.w2_weight_scale, div2)
             layer.w13_weight_scale = Parameter(s13, requires_grad=False)

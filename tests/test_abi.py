@@ -41,8 +41,13 @@ def test_shape_errors_before_launch():
     assert L.r9k_moe_4bit_prefill(0, 1, 1, 1, 1, 1, 1, 1, 1, 1, z, 0, 0, 4, 16, 1, 64, 16, 99, z) == -7
     assert L.r9k_moe_4bit_prefill(3, 1, 1, 1, 1, 1, 1, 1, 1, 1, z, 0, 0, 4, 16, 1, 64, 16, 17, z) == -8
     assert L.r9k_moe_4bit_prefill(1, 1, 1, 1, 1, 1, 1, 1, 1, 1, z, 0, 0, 4, 16, 1, 64, 16, 17, z) == -8
-    L.r9k_moe_nvfp4a8.argtypes = [ctypes.c_long] * 12 + [ctypes.c_int] * 9 + [ctypes.c_long]
-    assert L.r9k_moe_nvfp4a8(1, 1, 1, 1, 1, 1, 1, 1, 1, z, 0, 0, 4, 16, 1, 64, 16, 2, 4, 2, 1, z) == -8
+    # native NVFP4: N % 16, K % 16, K % (16 SK), bad MT; nothing to do for numel == 0 (every case returns before a
+    # launch)
+    assert L.r9k_moe_nvfp4a8(1, 1, 1, 1, 1, 1, 1, 1, 1, z, 0, 0, 4, 16, 1, 64, 17, 2, 1, 2, 1, z) == -1
+    assert L.r9k_moe_nvfp4a8(1, 1, 1, 1, 1, 1, 1, 1, 1, z, 0, 0, 4, 16, 1, 72, 16, 2, 1, 2, 1, z) == -2
+    assert L.r9k_moe_nvfp4a8(1, 1, 1, 1, 1, 1, 1, 1, 1, z, 0, 0, 4, 16, 1, 96, 16, 2, 4, 2, 1, z) == -2
+    assert L.r9k_moe_nvfp4a8(1, 1, 1, 1, 1, 1, 1, 1, 1, z, 0, 0, 4, 16, 1, 64, 16, 2, 1, 2, 3, z) == -7
+    assert L.r9k_moe_nvfp4a8(1, 1, 1, 1, 1, 1, 1, 1, 1, z, 0, 0, 4, 0, 1, 64, 16, 2, 1, 2, 1, z) == 0
     # route: topk > 16, E > 1024, blk not a power of two (the reference returns 1)
     assert L.r9k_moe_route(1, 64, 1, 1, 1, 1, 1, 1, 1, 64, 17, 1, 16, z) == 1
     assert L.r9k_moe_route(1, 2048, 1, 1, 1, 1, 1, 1, 1, 2048, 8, 1, 16, z) == 1

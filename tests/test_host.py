@@ -78,3 +78,32 @@ def test_align_block_size_ref_canonical():
     s, e, n = K.align_block_size_ref(ids, 4, 4)
     assert n.item() == 16 and s[:16].tolist() == [3, 6, 6, 6, 1, 2, 6, 6, 5, 6, 6, 6, 0, 4, 6, 6]
     assert e[:4].tolist() == [0, 1, 2, 3] and (e[4:] == -1).all()
+
+
+def test_nvfp4_layout_places_checkpoint_bytes():
+    """prepare_nvfp4_weights: lane l = g*16 + c of K-tile kt holds checkpoint bytes kt*64 + 16g .. +16 of row
+    nt*16 + c, its 2 scale bytes are groups kt*8 + 2g, +1 of that row, and a partial last K-tile is zero-padded."""
+    import torch
+    from r9700_vllm.kernels import moe as K
+    E, N, Kd = 2, 32, 272                      # K % 128 = 16: one live group in the last K-tile
+    g = torch.Generator().manual_seed(0)
+    p = torch.randint(0, 256, (E, N, Kd // 2), generator=g, dtype=torch.int32).to(torch.uint8)
+    s8 = torch.randint(0, 0x7f, (E, N, Kd // 16), generator=g, dtype=torch.int32).to(torch.uint8)
+    W = K.prepare_nvfp4_weights(p, s8.view(torch.float8_e4m3fn), torch.ones(E, N))
+    nkt = 3
+    assert W.wq.dtype == torch.int32 and W.ws.shape == (E, nkt * 8, N) and W.ws_estride == N * nkt * 8
+    wq = W.wq.view(torch.uint8).reshape(E, N // 16, nkt, 64, 16)               # [e, nt, kt, lane, byte]
+    ws = W.ws.reshape(E, N // 16, nkt, 64, 2)                                  # [e, nt, kt, lane, group of 2]
+    for e in range(E):
+        for n in range(N):
+            for kt in range(nkt):
+                for gg in range(4):
+                    lane = gg * 16 + n % 16
+                    for b in range(16):
+                        kb = kt * 64 + 16 * gg + b
+                        want = int(p[e, n, kb]) if kb < Kd // 2 else 0
+                        assert int(wq[e, n // 16, kt, lane, b]) == want, (e, n, kt, gg, b)
+                    for h in range(2):
+                        gi = kt * 8 + 2 * gg + h
+                        want = int(s8[e, n, gi]) if gi < Kd // 16 else 0
+                        assert int(ws[e, n // 16, kt, lane, h]) == want, (e, n, kt, gg, h)

@@ -86,3 +86,40 @@ def test_hc_silu_epilogue():
     assert out[0, 5] == 2.5                                                                # past act_cols: v
     # s is taken from the bf16-rounded v: 1.0078125 is bf16-exact, 1.00390625 rounds to 1.0 (tie to even)
     assert O.hc_silu(torch.tensor([[1.00390625]]), 1, 1.0)[0, 0] == O.hc_silu(torch.tensor([[1.0]]), 1, 1.0)[0, 0]
+
+
+def test_nvfp4_gemm_python_loop():
+    """The native NVFP4 GEMM against dot products over the closed-form code values (e2m1 table, e4m3 exponent /
+    mantissa), the multiplier and the row scale applied in the kernel's order, on a tiny routed case."""
+    rng = np.random.default_rng(5)
+    E, N, Kd, R = 2, 3, 32, 3
+    packed = rng.integers(0, 256, (E, N, Kd // 2), dtype=np.uint8)
+    s16 = rng.integers(0, 0x7f, (E, N, Kd // 16), dtype=np.uint8)       # finite e4m3 codes, subnormals included
+    wg = rng.uniform(0.5, 2.0, (E, N)).astype(np.float32)
+    aq = rng.integers(0, 256, (R, Kd), dtype=np.uint8)
+    aq[(aq & 0x7f) == 0x7f] = 0                                          # no NaN codes
+    a_s = rng.uniform(0.01, 0.1, R).astype(np.float32)
+    tw = rng.uniform(0.1, 1.0, R).astype(np.float32)
+    eor = np.array([1, 0, 1], dtype=np.int32)
+    got = O.nvfp4_gemm(aq, a_s, packed, s16, wg, eor, 1, tw)
+
+    def e2m1(c):
+        m = [0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0][c & 7]
+        return -m if c & 8 else m
+
+    def e4m3(b):
+        e, m = (b >> 3) & 15, b & 7
+        v = (1 + m / 8) * 2.0 ** (e - 7) if e else m / 8 * 2.0 ** -6
+        return -v if b & 0x80 else v
+
+    for r in range(R):
+        e = eor[r]
+        for n in range(N):
+            acc = 0.0
+            for k in range(Kd):
+                byte = int(packed[e, n, k // 2])
+                code = byte & 15 if k % 2 == 0 else byte >> 4
+                acc += e4m3(int(aq[r, k])) * e2m1(code) * e4m3(int(s16[e, n, k // 16]))
+            sc = np.float32(np.float32(wg[e, n]) * np.float32(a_s[r])) * np.float32(tw[r])
+            want = torch.tensor([np.float32(acc) * sc], dtype=torch.float32).to(torch.bfloat16)
+            assert got[r, n] == O.bf16_bits(want)[0], (r, n)
