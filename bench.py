@@ -227,8 +227,9 @@ def events_ms(fn, reps: int) -> float:
 def cfg4_lines(dev) -> dict:
     """the load-time NVFP4 -> MXFP4 conversion of a [17408, 5120] dense weight (uniform codes,
     s16 = e4m3(|N(0,1)| * 0.05), global 1), one launch over all rows, then the fp8-act x MXFP4 GEMM on the converted
-    weight at M = 1, 4, 16, 4096 (ops.mxfp4_linear: per-row quant + GEMM). GEMM timing: one HIP graph cycling through
-    12 weight copies (570 MB, > 2x the Infinity Cache), HIP events around its replays."""
+    weight at M = 1, 4, 16, 4096 (ops.mxfp4_linear: per-row quant + GEMM), and the native NVFP4 GEMM
+    (ops.nvfp4_linear, exact checkpoint bits) at M = 1, 4, 16. GEMM timing: one HIP graph cycling through 12 weight
+    copies (570-600 MB, > 2x the Infinity Cache), HIP events around its replays."""
     from r9700_vllm import ops
     from r9700_vllm.kernels import moe as K
     from r9700_vllm.quant import nvfp4 as NV
@@ -273,6 +274,33 @@ def cfg4_lines(dev) -> dict:
               file=sys.stderr, flush=True)
     res["gemm"] = gemm
     del Ws, W0
+    # native NVFP4 (the checkpoint's codes and e4m3 scales kept; the reference's default for dense NVFP4 linears) on
+    # the same codes, decode widths, the same copy rotation
+    pk = torch.randint(0, 256, (1, N, Kd // 2), generator=g, device=dev, dtype=torch.int32).to(torch.uint8)
+    s16b = (torch.randn(1, N, Kd // 16, generator=g, device=dev).abs() * 0.05).to(torch.float8_e4m3fn)
+    WN0 = K.prepare_nvfp4_weights(pk, s16b, torch.ones(1, N, device=dev))
+    del pk, s16b
+    WNs = [WN0] + [K.Nvfp4Experts(WN0.wq.clone(), WN0.ws.clone(), WN0.wg.clone(), N, Kd) for _ in range(11)]
+    nbytes_w = N * Kd // 2 + N * Kd // 16 + N * 4
+    native = {}
+    for M in (1, 4, 16):
+        x = torch.randn(M, Kd, generator=g, device=dev).to(torch.bfloat16)
+        for W in WNs[:2]:
+            ops.nvfp4_linear(x, W.wq, W.ws, W.wg, N, Kd)
+        torch.cuda.synchronize()
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr):
+            for W in WNs:
+                ops.nvfp4_linear(x, W.wq, W.ws, W.wg, N, Kd)
+        ms = events_ms(gr.replay, 20) / len(WNs)
+        del gr
+        nbytes = nbytes_w + M * Kd * 2 + M * N * 2
+        native[str(M)] = {"us": round(ms * 1e3, 2), "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                          "hbm_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+        print(f"# cfg4 native NVFP4 GEMM M={M}: {ms * 1e3:.1f} us, {native[str(M)]['GBps']} GB/s", file=sys.stderr,
+              flush=True)
+    res["gemm_nvfp4_native"] = native
+    del WNs, WN0
     torch.cuda.empty_cache()
     return {"workload": "cfg4 dense [17408, 5120]: NVFP4 -> MXFP4 conversion, then fp8-act x MXFP4 GEMM", **res}
 

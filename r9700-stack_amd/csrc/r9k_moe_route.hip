@@ -114,7 +114,7 @@ __device__ __forceinline__ void load_row(const uint16_t* __restrict__ row, int E
 // (global) and, when given, the ids to LDS.
 template <int EPL>
 __device__ __forceinline__ void topk_core(const uint16_t* h, int E, int topk, bool renorm, float* __restrict__ w_out,
-                                          int* __restrict__ id_out, short* lds_ids, int lane) {
+                                          int* __restrict__ id_out, short* lds_ids, int lane, bool agent = false) {
   float mx = -INFINITY;
 #pragma unroll
   for (int i = 0; i < EPL; i++) mx = fmaxf(mx, bf2f(h[i]));
@@ -158,7 +158,8 @@ __device__ __forceinline__ void topk_core(const uint16_t* h, int E, int topk, bo
   if (isel < 0 || isel >= E) isel = 0;               // unreachable (topk <= E); keeps every table write in range
   if (lane < topk) {
     w_out[lane] = p;
-    id_out[lane] = isel;
+    if (agent) __hip_atomic_store(id_out + lane, isel, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);   // read by
+    else id_out[lane] = isel;                                                                        // another CU
     if (lds_ids) lds_ids[lane] = (short)isel;
   }
 }
@@ -303,9 +304,10 @@ __device__ __forceinline__ void build_tables(TabLds<NT>& sh, const short* ids, i
 }
 
 // Fused routing + tables (reference: r9k_moe_route_kernel, kernels/r9k_moe_route.hip:67-210), numel <= SMALL_MAX:
-// one wave per token row over ceil(M / 8) workgroups of 8 waves (the rows' latency chains spread over CUs); the
-// last workgroup to arrive (counter `arrive`, zero at entry and left zero) reads all ids into LDS and builds the
-// tables. With one workgroup the ids go straight to LDS.
+// one wave per token row over ceil(M / 8) workgroups of 8 waves (the rows' latency chains spread over CUs). Each
+// workgroup stores its ids as agent-scope atomics, waits for them (vmcnt) and counts itself in `arrive` (zero at
+// entry, left zero); the last to arrive reads every id back with agent-scope loads, 8 in flight a thread, into LDS
+// and builds the tables. With one workgroup the ids go straight to LDS.
 template <int EPL>
 __global__ void __launch_bounds__(FT) route_fused_kernel(const uint16_t* __restrict__ logits, int ldl,
                                                          float* __restrict__ weights, int* __restrict__ ids,
@@ -323,21 +325,31 @@ __global__ void __launch_bounds__(FT) route_fused_kernel(const uint16_t* __restr
     uint16_t h[EPL];
     load_row<EPL>(logits + (size_t)r * ldl, E, lane, h);
     topk_core<EPL>(h, E, topk, renorm != 0, weights + (size_t)r * topk, ids + (size_t)r * topk,
-                   single ? lids + r * topk : nullptr, lane);
+                   single ? lids + r * topk : nullptr, lane, !single);
   }
   if (!single) {
-    __threadfence();
-    __syncthreads();
-    if (threadIdx.x == 0) s_last = atomicAdd(arrive, 1) == (int)gridDim.x - 1;
-    __syncthreads();
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");           // this wave's id stores have completed
+    lds_barrier();
+    if (threadIdx.x == 0)
+      s_last = __hip_atomic_fetch_add(arrive, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (int)gridDim.x - 1;
+    lds_barrier();
     if (!s_last) return;
-    __threadfence();
-    for (int t = threadIdx.x; t < numel; t += FT)                // ids of other workgroups: read past this CU's L1
-      lids[t] = (short)__hip_atomic_load(ids + t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (threadIdx.x == 0) __hip_atomic_store(arrive, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int t0 = 0; t0 < numel; t0 += 8 * FT) {                // other workgroups' ids, past this CU's caches
+      int v[8];
+#pragma unroll
+      for (int u = 0; u < 8; u++)
+        v[u] = __hip_atomic_load(ids + min(t0 + u * FT + (int)threadIdx.x, numel - 1), __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+      for (int u = 0; u < 8; u++) {
+        const int t = t0 + u * FT + threadIdx.x;
+        if (t < numel) lids[t] = (short)v[u];
+      }
+    }
   }
   lds_barrier();
   build_tables(sh, lids, numel, E, blk, sorted_ids, expert_ids, ntpp);
-  if (!single && threadIdx.x == 0) *arrive = 0;
 }
 
 // ------------------------------------------------------------------ small batches: M <= 64 rows in one workgroup

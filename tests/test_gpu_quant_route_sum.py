@@ -72,7 +72,8 @@ def test_silu_mul_quant_fp8(dev, M, I, scale):
 
 
 @pytest.mark.parametrize("M,E,topk,blk", [(1, 288, 8, 16), (8, 288, 8, 16), (16, 288, 8, 16), (64, 288, 8, 16),
-                                          (37, 512, 10, 32), (256, 384, 8, 64), (5, 48, 6, 16), (300, 100, 10, 16)])
+                                          (37, 512, 10, 32), (256, 384, 8, 64), (5, 48, 6, 16), (300, 100, 10, 16),
+                                          (512, 288, 8, 16)])
 @pytest.mark.parametrize("renorm", [True, False])
 def test_moe_route_fused(dev, M, E, topk, blk, renorm):
     print(f"route M={M} E={E} topk={topk} blk={blk} renorm={renorm}", flush=True)
