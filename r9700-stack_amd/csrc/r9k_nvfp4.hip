@@ -22,16 +22,54 @@ namespace {
 
 using namespace r9k;
 
-__device__ __forceinline__ float e2m1_val(uint32_t c) {
-  const float mag[8] = {0.f, 0.5f, 1.f, 1.5f, 2.f, 3.f, 4.f, 6.f};
-  const float m = mag[c & 7u];
-  return (c & 8u) ? -m : m;
+// (E2M1[c] * s) / rd for the 16 codes of one group, with IEEE division semantics, from two divisions: every E2M1
+// magnitude is 2^j or 1.5 * 2^j, and scaling a correctly rounded quotient by 2^j is exact while it stays normal, so
+// RN(1.5^b * 2^j * s / rd) = 2^j * RN(1.5^b * s / rd). Groups whose quotients could leave the normal range (or a
+// non-finite / non-positive divisor) divide per element.
+__device__ __forceinline__ void e2m1_decode8(uint32_t w, float (&v)[8]);
+
+__device__ __forceinline__ void dequant_group(const uint32_t w0, const uint32_t w1, float s, float rd, float* x) {
+  const float q1 = s / rd, q3 = (1.5f * s) / rd;
+  const float aq1 = fabsf(q1), aq3 = fabsf(q3);
+  const bool fast = (aq1 >= 0x1p-125f || aq1 == 0.f) && aq3 <= 0x1p125f && rd > 0.f && rd <= 3.0e38f;
+  float v[16];
+  e2m1_decode8(w0, *reinterpret_cast<float(*)[8]>(v));
+  e2m1_decode8(w1, *reinterpret_cast<float(*)[8]>(v + 8));
+  if (fast) {
+    // V = E2M1[c] = +-2^j (mantissa bit clear) or +-1.5 * 2^j (set): x = (V with its mantissa cleared) * (q1 or q3)
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+      const uint32_t vb = __float_as_uint(v[i]);
+      x[i] = __uint_as_float(vb & 0xff800000u) * ((vb & 0x00400000u) ? q3 : q1);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 16; i++) x[i] = (v[i] * s) / rd;
+  }
 }
 
+// Nearest E2M1 code of v with ties to the smaller magnitude (the reference's bucketize on 0.25 .. 5.0, > 5
+// saturating to 6), sign bit for v < 0. V_CVT_SCALEF32_PK_FP4_F32 (scale 1) rounds to nearest even and saturates
+// (measured on gfx950 against this rule over 1M values): it differs exactly at the ties whose lower neighbour is odd
+// (|v| = 0.75, 1.75, 3.5, where it takes the even code above) and at -0.0 / NaN (sign or code kept; the rule gives 0).
 __device__ __forceinline__ uint32_t e2m1_encode(float v) {
-  const float a = fabsf(v);
-  uint32_t c = (a > 0.25f) + (a > 0.75f) + (a > 1.25f) + (a > 1.75f) + (a > 2.5f) + (a > 3.5f) + (a > 5.0f);
-  return c | (v < 0.f ? 8u : 0u);
+  const uint32_t hw = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(0u, v, 0.f, 1.0f, 0) & 0xfu;
+  const uint32_t b = __float_as_uint(v), t = b & 0x7fffffffu;
+  // |v| in {0.75, 1.75, 3.5}: low 21 bits zero and t >> 21 = 0x1fa + {0, 5, 9} (bits 0, 5, 9 of 0x221), branch-free
+  const uint32_t k = (t >> 21) - 0x1fau;
+  const uint32_t tie = (uint32_t)((t & 0x1fffffu) == 0u) & (uint32_t)(k < 10u) & ((0x221u >> (k & 15u)) & 1u);
+  const uint32_t zero = (uint32_t)(b == 0x80000000u) | (uint32_t)(t > 0x7f800000u);
+  return zero ? 0u : hw - tie;
+}
+
+// The 8 E2M1 codes of one dword (low nibble first) as fp32 values, exact.
+__device__ __forceinline__ void e2m1_decode8(uint32_t w, float (&v)[8]) {
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  const f2 a = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 0);
+  const f2 b = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 1);
+  const f2 c = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 2);
+  const f2 d = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 3);
+  v[0] = a[0]; v[1] = a[1]; v[2] = b[0]; v[3] = b[1]; v[4] = c[0]; v[5] = c[1]; v[6] = d[0]; v[7] = d[1];
 }
 
 // smallest integer e with a <= 6 * 2^e, for a normal positive fp32 a
@@ -51,18 +89,26 @@ __device__ __forceinline__ uint32_t search_block(const float (&x)[32], uint32_t 
   e0 = e0 < -126 ? -126 : (e0 > 127 ? 127 : e0);
   int best_e = 0;
   double best_err = 0.0;
+  double xd[32];
+#pragma unroll
+  for (int i = 0; i < 32; i++) xd[i] = (double)x[i];
 #pragma unroll
   for (int d = 0; d >= -1; d--) {
     int e = e0 + d;
     e = e < -127 ? -127 : (e > 127 ? 127 : e);
     uint32_t cw[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int i = 0; i < 32; i++) cw[i >> 3] |= e2m1_encode(ldexpf(x[i], -e)) << (4 * (i & 7));
     double err = 0.0;
 #pragma unroll
-    for (int i = 0; i < 32; i++) {
-      const uint32_t c = e2m1_encode(ldexpf(x[i], -e));
-      cw[i >> 3] |= c << (4 * (i & 7));
-      const double dv = (double)ldexpf(e2m1_val(c), e) - (double)x[i];
-      err += dv * dv;
+    for (int q = 0; q < 4; q++) {
+      float v[8];
+      e2m1_decode8(cw[q], v);                              // the codes' values (exact), back at the block scale
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        const double dv = (double)ldexpf(v[j], e) - xd[8 * q + j];
+        err += dv * dv;
+      }
     }
     if (d == 0 || err < best_err) {
       best_err = err;
@@ -86,13 +132,9 @@ __global__ void __launch_bounds__(256) nvfp4_to_mxfp4_kernel(const uint8_t* __re
   const uint32_t sc = *reinterpret_cast<const uint16_t*>(s16 + b * 2);
   const float rd = row_div[row];
   const float s0 = e4m3_to_f32(sc & 0xffu), s1 = e4m3_to_f32(sc >> 8);
-  const uint32_t w[4] = {pk.x, pk.y, pk.z, pk.w};
   float x[32];
-#pragma unroll
-  for (int i = 0; i < 32; i++) {
-    const uint32_t c = (w[i >> 3] >> (4 * (i & 7))) & 0xfu;
-    x[i] = (e2m1_val(c) * (i < 16 ? s0 : s1)) / rd;
-  }
+  dequant_group(pk.x, pk.y, s0, rd, x);
+  dequant_group(pk.z, pk.w, s1, rd, x + 16);
   uint32_t bw[4];
   const uint32_t eb = search_block(x, bw);
   *reinterpret_cast<uint4*>(out_p + b * 16) = make_uint4(bw[0], bw[1], bw[2], bw[3]);
