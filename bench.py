@@ -228,7 +228,7 @@ def cfg4_lines(dev) -> dict:
     """the load-time NVFP4 -> MXFP4 conversion of a [17408, 5120] dense weight (uniform codes,
     s16 = e4m3(|N(0,1)| * 0.05), global 1), one launch over all rows, then the fp8-act x MXFP4 GEMM on the converted
     weight at M = 1, 4, 16, 4096 (ops.mxfp4_linear: per-row quant + GEMM), and the native NVFP4 GEMM
-    (ops.nvfp4_linear, exact checkpoint bits) at M = 1, 4, 16. GEMM timing: one HIP graph cycling through 12 weight
+    (ops.nvfp4_linear, exact checkpoint bits) at M = 1, 4, 16, 4096. GEMM timing: one HIP graph cycling through 12 weight
     copies (570-600 MB, > 2x the Infinity Cache), HIP events around its replays."""
     from r9700_vllm import ops
     from r9700_vllm.kernels import moe as K
@@ -283,22 +283,24 @@ def cfg4_lines(dev) -> dict:
     WNs = [WN0] + [K.Nvfp4Experts(WN0.wq.clone(), WN0.ws.clone(), WN0.wg.clone(), N, Kd) for _ in range(11)]
     nbytes_w = N * Kd // 2 + N * Kd // 16 + N * 4
     native = {}
-    for M in (1, 4, 16):
+    for M in (1, 4, 16, 4096):
         x = torch.randn(M, Kd, generator=g, device=dev).to(torch.bfloat16)
-        for W in WNs[:2]:
+        calls = WNs if M <= 16 else WNs[:2]
+        for W in calls[:2]:
             ops.nvfp4_linear(x, W.wq, W.ws, W.wg, N, Kd)
         torch.cuda.synchronize()
         gr = torch.cuda.CUDAGraph()
         with torch.cuda.graph(gr):
-            for W in WNs:
+            for W in calls:
                 ops.nvfp4_linear(x, W.wq, W.ws, W.wg, N, Kd)
-        ms = events_ms(gr.replay, 20) / len(WNs)
+        ms = events_ms(gr.replay, 20 if M <= 16 else 5) / len(calls)
         del gr
         nbytes = nbytes_w + M * Kd * 2 + M * N * 2
         native[str(M)] = {"us": round(ms * 1e3, 2), "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1),
-                          "hbm_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
-        print(f"# cfg4 native NVFP4 GEMM M={M}: {ms * 1e3:.1f} us, {native[str(M)]['GBps']} GB/s", file=sys.stderr,
-              flush=True)
+                          "hbm_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                          "TFLOPS": round(2 * M * N * Kd / (ms * 1e-3) / 1e12, 1)}
+        print(f"# cfg4 native NVFP4 GEMM M={M}: {ms * 1e3:.1f} us, {native[str(M)]['GBps']} GB/s, "
+              f"{native[str(M)]['TFLOPS']} TFLOPS", file=sys.stderr, flush=True)
     res["gemm_nvfp4_native"] = native
     del WNs, WN0
     torch.cuda.empty_cache()

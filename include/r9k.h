@@ -42,7 +42,9 @@ int r9k_moe_mxfp4a8_f(int fuse, long a, long as, long wq, long ws, long wref, lo
                       int numel, int a_row_div, int K, int N, int WV, int SK, int NPW, int MT, long stream);
 
 /* Prefill entry of the same GEMM. Replaces kernels/r9k_moe_mxfp4a8.hip:1227-1230 (r9k_moe_4bit_prefill).
- * nv: 0 MXFP4 (2, the reference's folded MXFP4, is the same data here); 1 NVFP4 and 3 fp8 weights return -8.
+ * nv: 0 MXFP4 (2, the reference's folded MXFP4, is the same data here); 1 native NVFP4 (ws / wref = the scales and
+ * per-row fp32 multipliers of r9k_moe_nvfp4a8, wref_estride floats; cfgs with 128- or 256-row blocks, else -7);
+ * 3 fp8 weights returns -8.
  * Tables built with blk = r9k_moe_prefill_bm(cfg). -7 unknown cfg, -2 K % r9k_moe_prefill_bk(cfg). */
 int r9k_moe_4bit_prefill(int nv, long a, long as, long wq, long ws, long wref, long c, long sorted_ids,
                          long expert_ids, long ntpp, long topk_w, long ws_estride, long wref_estride, int max_blocks,

@@ -429,6 +429,9 @@ int r9k_prefill_launch(long a, long as, long wq, long ws, long c, long sorted_id
                        long topk_w, long ws_estride, int max_blocks, int numel, int a_row_div, int K, int N,
                        long stream);
 int r9k_prefill_block_rows();
+int r9k_nvfp4_prefill_launch(long a, long as, long wq, long ws, long wg, long c, long sorted_ids, long expert_ids,
+                             long ntpp, long topk_w, long ws_estride, long wg_estride, int max_blocks, int numel,
+                             int a_row_div, int K, int N, int blk, long stream);
 
 // Reference: kernels/r9k_moe_mxfp4a8.hip:625-638 (r9k_moe_mxfp4a8). `wref`, WV, SK, NPW and the MT bits 3 (LDS-A)
 // and 4 (fold) are gfx1201 tuning / layout knobs with no meaning here and are ignored; MT & 7 in {1, 2, 4} sets the
@@ -466,10 +469,14 @@ extern "C" int r9k_moe_mxfp4a8_f(int fuse, long a, long as, long wq, long ws, lo
 extern "C" int r9k_moe_4bit_prefill(int nv, long a, long as, long wq, long ws, long wref, long c, long sorted_ids,
                                     long expert_ids, long ntpp, long topk_w, long ws_estride, long wref_estride,
                                     int max_blocks, int numel, int a_row_div, int K, int N, int cfg, long stream) {
-  (void)wref; (void)wref_estride;
   if (N % 16) return -1;
   if (cfg < 0 || cfg >= NPF) return -7;
   if (K % kPf[cfg].BK) return -2;
+  // native NVFP4 (ws = its scales, wref = the per-row fp32 multipliers): the fp16-MFMA tile kernel, 128- or 256-row
+  // routing blocks (r9k_moe_nvfp4.hip)
+  if (nv == 1)
+    return r9k_nvfp4_prefill_launch(a, as, wq, ws, wref, c, sorted_ids, expert_ids, ntpp, topk_w, ws_estride,
+                                    wref_estride, max_blocks, numel, a_row_div, K, N, kPf[cfg].BM, stream);
   if (nv != 0 && nv != 2) return -8;
   // 256-row blocks with K a multiple of 128: the LDS-tiled 32x32x64 kernel (r9k_moe_prefill.hip)
   if (kPf[cfg].BM == r9k_prefill_block_rows() && K % 128 == 0 && getenv_flag_off("R9K_PREFILL_LDS") == 0)

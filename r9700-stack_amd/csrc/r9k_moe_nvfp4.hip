@@ -274,7 +274,181 @@ void nv_launch(dim3 grid, hipStream_t st, long a, long as, long wq, long ws, lon
                      wq_estride, ws_estride, wg_estride, numel, a_row_div, K, N, blk, subs);
 }
 
+// ------------------------------------------------------------------------------------------ prefill (tiles of 128)
+// Routed rows in blocks of 128 (a routing block of 128 or 256 rows covered by 1 or 2 workgroups along grid.y) x 128
+// output columns per workgroup; 4 waves in 2 x 2, each 64 rows x 64 columns = 4 x 4 tiles of the fp16 MFMA above.
+// K runs in 128-wide tiles through two LDS stages (activations 16 KB, codes 8 KB, scales 1 KB), the next tile's
+// global loads in flight while the current one is computed. Each wave widens its 4 column tiles' weights once per
+// K-tile (codes and scales straight from LDS, as in the decode kernel) and reuses them over its 4 row tiles; the
+// activation rows are widened per row tile. Activation row pieces are stored XOR-swizzled (16-byte piece p of row r
+// at p ^ (r & 7)) so the 16 rows a fragment read touches land in different banks.
+constexpr int PV_BM = 128, PV_BN = 128, PV_THREADS = 256;
+
+struct PvStage {
+  uint8_t a[PV_BM * NV_KT];        // fp8 activations, row-major, swizzled 16-byte pieces
+  uint8_t b[8 * 1024];             // codes of the 8 column tiles, the global layout's K-tile
+  uint8_t s[8 * 128];              // their scales
+};
+
+__global__ void __launch_bounds__(PV_THREADS, 2) nvfp4_prefill_kernel(
+    const uint8_t* __restrict__ A, const float* __restrict__ As, const uint8_t* __restrict__ Wq,
+    const uint8_t* __restrict__ Ws, const float* __restrict__ Wg, uint16_t* __restrict__ C,
+    const int* __restrict__ sorted_ids, const int* __restrict__ expert_ids, const int* __restrict__ ntpp,
+    const float* __restrict__ topk_w, long wq_estride, long ws_estride, long wg_estride, int numel, int a_row_div,
+    int K, int N, int blk, int subs) {
+  __shared__ PvStage st[2];
+  __shared__ int s_fr[PV_BM];
+  const int rb = blockIdx.y / subs, sub = blockIdx.y - rb * subs;
+  const int row0 = rb * blk + sub * PV_BM;
+  const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
+  const int g = lane >> 4, c = lane & 15, wm = wave >> 1, wn = wave & 1;
+  const int np = ntpp[0];
+  const int e = expert_ids[rb];
+  const int first = sorted_ids[row0];
+  if (rb * blk >= np || e < 0 || first < 0 || first >= numel) return;     // uniform: a dead block or padding
+  if (tid < PV_BM) {
+    const int fr = sorted_ids[row0 + tid];
+    s_fr[tid] = fr;
+  }
+  __syncthreads();
+  const int NT = N / 16, nkt = (K + NV_KT - 1) / NV_KT;
+  const int nt0 = blockIdx.x * (PV_BN / 16);
+  const uint8_t* __restrict__ We = Wq + (size_t)e * wq_estride;
+  const uint8_t* __restrict__ Se = Ws + (size_t)e * ws_estride;
+  const float* __restrict__ Ge = Wg + (size_t)e * wg_estride;
+
+  // this thread's load slots: activation pieces q = tid + 256 i (row q >> 3, piece q & 7), code chunks
+  // q = tid + 256 i (column tile q >> 6, lane q & 63), scale chunks tid < 64 (column tile tid >> 3, part tid & 7).
+  // Rows are q >> 3 = (tid >> 3) + 32 i and pieces tid & 7 for every i.
+  const int prow = tid >> 3, ppiece = tid & 7;
+  const uint8_t* asrc0;
+  const uint8_t* asrc1;
+  const uint8_t* asrc2;
+  const uint8_t* asrc3;
+  {
+    int f0 = s_fr[prow], f1 = s_fr[prow + 32], f2 = s_fr[prow + 64], f3 = s_fr[prow + 96];
+    f0 = (f0 < 0 || f0 >= numel) ? first : f0;              // padding rows load a valid row, never stored
+    f1 = (f1 < 0 || f1 >= numel) ? first : f1;
+    f2 = (f2 < 0 || f2 >= numel) ? first : f2;
+    f3 = (f3 < 0 || f3 >= numel) ? first : f3;
+    asrc0 = A + (size_t)(f0 / a_row_div) * K + ppiece * 16;
+    asrc1 = A + (size_t)(f1 / a_row_div) * K + ppiece * 16;
+    asrc2 = A + (size_t)(f2 / a_row_div) * K + ppiece * 16;
+    asrc3 = A + (size_t)(f3 / a_row_div) * K + ppiece * 16;
+  }
+  const int aoff_l = ((ppiece ^ (prow & 7)) * 16);              // rows prow + 32 i share prow & 7
+  const uint8_t* bsrc0 = We + (size_t)min(nt0 + (tid >> 6), NT - 1) * nkt * 1024 + (size_t)(tid & 63) * 16;
+  const uint8_t* bsrc1 = We + (size_t)min(nt0 + 4 + (tid >> 6), NT - 1) * nkt * 1024 + (size_t)(tid & 63) * 16;
+  const uint8_t* ssrc = Se + (size_t)min(nt0 + (tid >> 3), NT - 1) * nkt * 128 + (size_t)(tid & 7) * 16;
+
+  uint4 ra0, ra1, ra2, ra3, rb0, rb1, rs = make_uint4(0u, 0u, 0u, 0u);
+#define PV_LOAD(kt)                                                                                               \
+  {                                                                                                               \
+    const int koff = (kt) * NV_KT + ppiece * 16;                                                                  \
+    const int kc = min(koff, K - 16) - ppiece * 16;              /* K tail: a clamped valid piece, zeroed below */ \
+    ra0 = *reinterpret_cast<const uint4*>(asrc0 + kc);                                                            \
+    ra1 = *reinterpret_cast<const uint4*>(asrc1 + kc);                                                            \
+    ra2 = *reinterpret_cast<const uint4*>(asrc2 + kc);                                                            \
+    ra3 = *reinterpret_cast<const uint4*>(asrc3 + kc);                                                            \
+    if (koff >= K) ra0 = ra1 = ra2 = ra3 = make_uint4(0u, 0u, 0u, 0u);                                            \
+    rb0 = *reinterpret_cast<const uint4*>(bsrc0 + (size_t)(kt) * 1024);                                          \
+    rb1 = *reinterpret_cast<const uint4*>(bsrc1 + (size_t)(kt) * 1024);                                          \
+    if (tid < 64) rs = *reinterpret_cast<const uint4*>(ssrc + (size_t)(kt) * 128);                                \
+  }
+#define PV_STORE(S)                                                                                               \
+  {                                                                                                               \
+    *reinterpret_cast<uint4*>((S).a + prow * NV_KT + aoff_l) = ra0;                                               \
+    *reinterpret_cast<uint4*>((S).a + (prow + 32) * NV_KT + aoff_l) = ra1;                                        \
+    *reinterpret_cast<uint4*>((S).a + (prow + 64) * NV_KT + aoff_l) = ra2;                                        \
+    *reinterpret_cast<uint4*>((S).a + (prow + 96) * NV_KT + aoff_l) = ra3;                                        \
+    *reinterpret_cast<uint4*>((S).b + tid * 16) = rb0;                                                            \
+    *reinterpret_cast<uint4*>((S).b + (tid + PV_THREADS) * 16) = rb1;                                             \
+    if (tid < 64) *reinterpret_cast<uint4*>((S).s + tid * 16) = rs;                                               \
+  }
+
+  v4f acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int j = 0; j < 4; j++) acc[i][j] = (v4f){0.f, 0.f, 0.f, 0.f};
+
+  PV_LOAD(0)
+  PV_STORE(st[0])
+  __syncthreads();
+  for (int kt = 0; kt < nkt; kt++) {
+    if (kt + 1 < nkt) PV_LOAD(kt + 1)
+    const PvStage& S = st[kt & 1];
+    h8 b[4][4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int ntl = wn * 4 + j;
+      const u32x4 bw = *reinterpret_cast<const u32x4*>(S.b + ntl * 1024 + lane * 16);
+      const uint32_t sw = *reinterpret_cast<const uint16_t*>(S.s + ntl * 128 + lane * 2);
+      const GroupScale s0 = group_scale(sw & 0xffu), s1 = group_scale((sw >> 8) & 0xffu);
+#pragma unroll
+      for (int t = 0; t < 4; t++) b[j][t] = e2m1x8_f16(bw[t], t < 2 ? s0 : s1);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int r = (wm * 4 + i) * 16 + c;
+      const uint4 l = *reinterpret_cast<const uint4*>(S.a + r * NV_KT + (((2 * g) ^ (r & 7)) * 16));
+      const uint4 h = *reinterpret_cast<const uint4*>(S.a + r * NV_KT + (((2 * g + 1) ^ (r & 7)) * 16));
+      const h8 a0 = e4m3x8_f16(l.x, l.y), a1 = e4m3x8_f16(l.z, l.w), a2 = e4m3x8_f16(h.x, h.y),
+               a3 = e4m3x8_f16(h.z, h.w);
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, b[j][0], acc[i][j], 0, 0, 0);
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, b[j][1], acc[i][j], 0, 0, 0);
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a2, b[j][2], acc[i][j], 0, 0, 0);
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a3, b[j][3], acc[i][j], 0, 0, 0);
+      }
+    }
+    if (kt + 1 < nkt) PV_STORE(st[(kt + 1) & 1])
+    __syncthreads();
+  }
+#undef PV_LOAD
+#undef PV_STORE
+
+  // epilogue: lane holds column c of each column tile, rows 4g .. 4g + 3 of each row tile
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const int n = (nt0 + wn * 4 + j) * 16 + c;
+    if (n >= N) continue;
+    const float wg = Ge[n];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const int fr = s_fr[(wm * 4 + i) * 16 + 4 * g + q];
+        if (fr < 0 || fr >= numel) continue;
+        float sc = wg * As[fr / a_row_div];
+        if (topk_w) sc *= topk_w[fr];
+        C[(size_t)fr * N + n] = f2bf(acc[i][j][q] * sc);
+      }
+  }
+}
+
 }  // namespace
+
+// The prefill entry's native-NVFP4 case (r9k_moe_4bit_prefill with nv = 1; reference kernels/r9k_moe_mxfp4a8.hip:
+// 1205-1230): routing blocks of blk = 128 or 256 rows, weights as r9k_moe_nvfp4a8 takes them. 0 / -7 blk / -3 / -6.
+int r9k_nvfp4_prefill_launch(long a, long as, long wq, long ws, long wg, long c, long sorted_ids, long expert_ids,
+                             long ntpp, long topk_w, long ws_estride, long wg_estride, int max_blocks, int numel,
+                             int a_row_div, int K, int N, int blk, long stream) {
+  if (blk != PV_BM && blk != 2 * PV_BM) return -7;
+  if (max_blocks <= 0 || numel <= 0) return 0;
+  if (!a || !as || !wq || !ws || !wg || !c || !sorted_ids || !expert_ids || !ntpp || a_row_div < 1) return -3;
+  const int subs = blk / PV_BM;
+  const long ny = (long)max_blocks * subs;
+  if (ny > 0x7fffffffL) return -3;
+  const dim3 grid((N + PV_BN - 1) / PV_BN, (unsigned)ny);
+  const long wq_estride = (long)N * ((K + NV_KT - 1) / NV_KT) * 64;
+  hipLaunchKernelGGL(nvfp4_prefill_kernel, grid, dim3(PV_THREADS), 0, (hipStream_t)stream, (const uint8_t*)a,
+                     (const float*)as, (const uint8_t*)wq, (const uint8_t*)ws, (const float*)wg, (uint16_t*)c,
+                     (const int*)sorted_ids, (const int*)expert_ids, (const int*)ntpp, (const float*)topk_w,
+                     wq_estride, ws_estride, wg_estride, numel, a_row_div, K, N, blk, subs);
+  return hipGetLastError() == hipSuccess ? 0 : -6;
+}
 
 // Reference: kernels/r9k_moe_mxfp4a8.hip:641-647 (r9k_moe_nvfp4a8): same arguments and routing contract. ws / wg as
 // the layout above (ws_estride bytes, wg_estride floats per expert); the code stride is N * ceil(K / 128) * 64 bytes

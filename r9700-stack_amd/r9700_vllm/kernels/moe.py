@@ -410,13 +410,23 @@ def moe_gemm(a_q: torch.Tensor, a_s: torch.Tensor, w: Mxfp4Experts, out: torch.T
     if a_tiled:
         raise RuntimeError("moe_gemm(a_tiled=True) is a gfx1201 kernel format")
     if isinstance(w, Nvfp4Experts):
-        # decode-family kernel only (16*MT-row blocks; reference entry kernels/r9k_moe_mxfp4a8.hip:641-647)
-        if prefill is not None:
-            raise RuntimeError("moe_gemm: native NVFP4 experts run the decode-family kernel (prefill=None, MT <= 4)")
+        # decode family (16*MT-row blocks; reference entry kernels/r9k_moe_mxfp4a8.hip:641-647) or the prefill entry's
+        # nv = 1 tile kernel (prefill_block(prefill) = 128 or 256 rows; :1205-1230)
         assert out.dtype == torch.bfloat16 and out.shape[1] == w.N and a_q.shape[1] == w.K and out.is_contiguous()
         assert a_q.is_contiguous() and a_s.dtype == torch.float32
         if topk_w is not None:
             assert topk_w.dtype == torch.float32 and topk_w.is_contiguous()
+        if prefill is not None:
+            blk = prefill_block(prefill)
+            max_blocks = min(expert_ids.numel(), (numel + blk - 1) // blk + min(numel, E))
+            rc = lib().r9k_moe_4bit_prefill(
+                1, a_q.data_ptr(), a_s.data_ptr(), w.wq.data_ptr(), w.ws.data_ptr(), w.wg.data_ptr(), out.data_ptr(),
+                sorted_ids.data_ptr(), expert_ids.data_ptr(), ntpp.data_ptr(),
+                topk_w.data_ptr() if topk_w is not None else 0, w.ws_estride, w.N, max_blocks, numel, a_row_div,
+                w.K, w.N, prefill, _stream())
+            if rc:
+                raise RuntimeError(f"r9k_moe_4bit_prefill(nv=1) failed ({rc}) N={w.N} K={w.K} cfg={prefill}")
+            return out
         blk = MOE_BLOCK * MT
         max_blocks = min(expert_ids.numel(), (numel + blk - 1) // blk + min(numel, E))
         rc = lib().r9k_moe_nvfp4a8(
@@ -500,6 +510,9 @@ MOE_PREFILL_CFG_GATE_UP = int(os.environ.get("R9K_MOE_PREFILL_CFG1", "17"))
 # 256-row blocks win from ~24 average rows per expert on MI355X (measured at E = 288 / 384, hidden 2048 / 4096,
 # uniform and Zipf(1.1) routing: 2.1x at 114 rows, even at 28-43; 6% behind at 21 uniform, ahead from 8 under Zipf)
 PREFILL_MOE_ROWS = int(os.environ.get("R9K_PREFILL_MOE_ROWS", "24"))
+# native NVFP4 dense linears: 128-row tiles of the nv = 1 prefill kernel from this many rows (cfg 2: 128-row blocks)
+NV_PREFILL_MIN_M = int(os.environ.get("R9K_NVFP4_PREFILL_MIN_M", "128"))
+NV_PREFILL_CFG = 2
 MOE_PREFILL_CFG_BIG = int(os.environ.get("R9K_MOE_PREFILL_CFG_BIG", "12"))
 
 

@@ -158,11 +158,11 @@ class R9700Mxfp4Experts(_experts_base()):
 
         nv = self.nv
         MT = K.pick_mt(numel, global_num_experts)
-        big = None if nv is not None else K.pick_moe_prefill_block(numel, global_num_experts, K1, K2)
+        big = K.pick_moe_prefill_block(numel, global_num_experts, K1, K2)
         if big is not None:                                  # prefill widths: one 256-row block ~ one expert
             pf_gate = pf_down = big[0]
             blk = big[1]
-        else:                                                # (native NVFP4: the decode-family kernel at every width)
+        else:
             blk = K.MOE_BLOCK * MT
             pf_down = None if nv is not None else K.pick_moe_prefill(MT, K2)
             pf_gate = None if nv is not None else K.pick_moe_prefill(MT, K1, gate_up=True)

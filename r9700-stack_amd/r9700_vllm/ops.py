@@ -69,8 +69,8 @@ def _mxfp4_linear_fake(x: torch.Tensor, wq: torch.Tensor, wsr: torch.Tensor, N: 
 def _nvfp4_linear(x: torch.Tensor, wq: torch.Tensor, ws: torch.Tensor, wg: torch.Tensor, N: int, K: int
                   ) -> torch.Tensor:
     """x [M, K] bf16 -> [M, N] bf16 over native NVFP4 weights (prepare_nvfp4_weights of one expert) with per-row fp8
-    activations (reference: r9700_vllm/ops.py nvfp4_linear). The decode-family kernel serves every M (64-row tiles
-    from M = 64; there is no NVFP4 prefill kernel on gfx950)."""
+    activations (reference: r9700_vllm/ops.py nvfp4_linear): the decode-family kernel below NV_PREFILL_MIN_M rows,
+    the 128 x 128-tile prefill kernel (r9k_moe_4bit_prefill nv = 1) from there."""
     from .kernels import moe as KM
     M = x.shape[0]
     out = torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
@@ -78,8 +78,12 @@ def _nvfp4_linear(x: torch.Tensor, wq: torch.Tensor, ws: torch.Tensor, wg: torch
         return out
     W = KM.Nvfp4Experts(wq, ws, wg, N, K)
     q, s = KM.quant_rows_fp8(x)
-    t, MT = _identity_tables(q, M)
-    KM.moe_gemm(q, s, W, out, *t, M, 1, None, num_experts=1, MT=MT)
+    if M >= KM.NV_PREFILL_MIN_M and K % 32 == 0:
+        t, _ = _identity_tables(q, M, KM.prefill_block(KM.NV_PREFILL_CFG) // KM.MOE_BLOCK)
+        KM.moe_gemm(q, s, W, out, *t, M, 1, None, num_experts=1, prefill=KM.NV_PREFILL_CFG)
+    else:
+        t, MT = _identity_tables(q, M)
+        KM.moe_gemm(q, s, W, out, *t, M, 1, None, num_experts=1, MT=MT)
     return out
 
 

@@ -40,7 +40,9 @@ def test_shape_errors_before_launch():
     assert L.r9k_moe_mxfp4a8(1, 1, 1, 1, 1, 1, 1, 1, 1, z, 0, 0, 4, 16, 1, 64, 16, 2, 4, 2, 3, z) == -7
     assert L.r9k_moe_4bit_prefill(0, 1, 1, 1, 1, 1, 1, 1, 1, 1, z, 0, 0, 4, 16, 1, 64, 16, 99, z) == -7
     assert L.r9k_moe_4bit_prefill(3, 1, 1, 1, 1, 1, 1, 1, 1, 1, z, 0, 0, 4, 16, 1, 64, 16, 17, z) == -8
-    assert L.r9k_moe_4bit_prefill(1, 1, 1, 1, 1, 1, 1, 1, 1, 1, z, 0, 0, 4, 16, 1, 64, 16, 17, z) == -8
+    # native NVFP4 prefill: 64-row cfg 17 is refused (-7); nothing to do for numel == 0 (no launch)
+    assert L.r9k_moe_4bit_prefill(1, 1, 1, 1, 1, 1, 1, 1, 1, 1, z, 0, 0, 4, 16, 1, 64, 16, 17, z) == -7
+    assert L.r9k_moe_4bit_prefill(1, 1, 1, 1, 1, 1, 1, 1, 1, 1, z, 0, 0, 4, 0, 1, 64, 16, 2, z) == 0
     # native NVFP4: N % 16, K % 16, K % (16 SK), bad MT; nothing to do for numel == 0 (every case returns before a
     # launch)
     assert L.r9k_moe_nvfp4a8(1, 1, 1, 1, 1, 1, 1, 1, 1, z, 0, 0, 4, 16, 1, 64, 17, 2, 1, 2, 1, z) == -1

@@ -66,7 +66,36 @@ def test_nvfp4_grouped_gemm(dev, E, M, topk, N, Kd, MT, down):
     print(f"  rel {r:.2e} cos {c:.7f}", flush=True)
 
 
-@pytest.mark.parametrize("M,N,Kd", [(1, 1024, 2048), (16, 512, 5120), (300, 256, 1024), (1, 17408, 5120)])
+@pytest.mark.parametrize("E,M,topk,N,Kd,cfg,down", [
+    (8, 200, 2, 256, 512, 2, False), (16, 300, 4, 384, 2080, 12, False), (32, 512, 8, 2048, 512, 12, True),
+    (4, 64, 1, 48, 256, 2, False), (8, 700, 8, 1024, 2048, 12, False),
+])
+def test_nvfp4_grouped_gemm_prefill(dev, E, M, topk, N, Kd, cfg, down):
+    """The prefill entry's native-NVFP4 tile kernel (r9k_moe_4bit_prefill nv = 1) on 128- (cfg 2) and 256-row (cfg 12)
+    routing blocks: a K tail (K % 128 = 32), N not a multiple of the 128-column tile, the router-weighted down."""
+    print(f"nvfp4 prefill gemm E={E} M={M} topk={topk} N={N} K={Kd} cfg={cfg} down={down}", flush=True)
+    g = torch.Generator().manual_seed(E * 11 + M + N + Kd)
+    packed, s16, wg = make_nv(E, N, Kd, g)
+    W = K.prepare_nvfp4_weights(packed.to(dev), s16.to(dev), wg.to(dev))
+    numel = M * topk
+    rows_a = numel if down else M
+    x = (torch.randn(rows_a, Kd, generator=g) * 0.5).to(torch.bfloat16)
+    ids = torch.stack([torch.randperm(E, generator=g)[:topk] for _ in range(M)]).to(torch.int32)
+    tw = torch.rand(numel, generator=g).float() if down else None
+    sid, eid, ntpp = (t.to(dev) for t in K.align_block_size_ref(ids, E, K.prefill_block(cfg)))
+    xq, xs = K.quant_rows_fp8(x.to(dev))
+    out = torch.full((numel, N), float("nan"), dtype=torch.bfloat16, device=dev)
+    K.moe_gemm(xq, xs, W, out, sid, eid, ntpp, numel, 1 if down else topk, tw.to(dev) if down else None,
+               num_experts=E, prefill=cfg)
+    qo, so = O.quant_rows_fp8(x)
+    ref = O.nvfp4_gemm(qo, so, packed.numpy(), s16.view(torch.uint8).numpy(), wg.numpy(),
+                       ids.reshape(-1).numpy(), 1 if down else topk, tw.numpy() if down else None)
+    r, c = check(O.bf16_bits(out), ref)
+    print(f"  rel {r:.2e} cos {c:.7f}", flush=True)
+
+
+@pytest.mark.parametrize("M,N,Kd", [(1, 1024, 2048), (16, 512, 5120), (300, 256, 1024), (1, 17408, 5120),
+                                    (1000, 512, 1024)])
 def test_nvfp4_linear(dev, M, N, Kd):
     print(f"nvfp4 linear M={M} N={N} K={Kd}", flush=True)
     g = torch.Generator().manual_seed(M + N + Kd)
@@ -80,7 +109,24 @@ def test_nvfp4_linear(dev, M, N, Kd):
     check(O.bf16_bits(out), ref)
 
 
-@pytest.mark.parametrize("T", [1, 16, 64, 300])
+def test_nvfp4_linear_config4_prefill_sampled(dev):
+    """BASELINE config 4's shape at M = 4096 on native NVFP4 weights (the 128 x 128 tile kernel), checked on 48
+    sampled rows (rows are independent)."""
+    M, N, Kd = 4096, 17408, 5120
+    print("nvfp4 linear config 4 M=4096", flush=True)
+    g = torch.Generator().manual_seed(4097)
+    packed, s16, wg = make_nv(1, N, Kd, g)
+    W = K.prepare_nvfp4_weights(packed.to(dev), s16.to(dev), wg.to(dev))
+    x = torch.randn(M, Kd, generator=g).to(torch.bfloat16)
+    out = ops.nvfp4_linear(x.to(dev), W.wq, W.ws, W.wg, N, Kd)
+    rows = np.sort(np.random.default_rng(1).choice(M, 48, replace=False))
+    qo, so = O.quant_rows_fp8(x)
+    ref = O.nvfp4_gemm(qo, so, packed.numpy(), s16.view(torch.uint8).numpy(), wg.numpy(),
+                       np.zeros(M, dtype=np.int32), 1, rows=rows)
+    check(O.bf16_bits(out)[rows], ref)
+
+
+@pytest.mark.parametrize("T", [1, 16, 64, 300, 1024])
 def test_nvfp4_native_layer(dev, T):
     """Config 2's layer shape (E=288, hidden 2048, I 512, top-8) on native NVFP4 experts through
     R9700Mxfp4Experts.apply, against the oracle chain: route -> fp8 quant -> NVFP4 gate_up -> SiLU quant -> NVFP4
