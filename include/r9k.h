@@ -149,6 +149,40 @@ int r9k_nvfp4_to_mxfp4(long packed, long s16, long row_div, long out_packed, lon
 /* The same MSE search on fp32 weights [N][K] (r9700_vllm/quant/nvfp4.py:54-75, quantize_mxfp4_search). */
 int r9k_quantize_mxfp4_search(long w, long out_packed, long out_e8m0, int N, int K, long stream);
 
+/* ---- Host-offloaded experts: device LRU cache (reference r9700_vllm/moe/cache.py:1-20, 182-395) ---- */
+
+/* One manage step (replaces kernels/third_party/davetha/r4d_lru.hip:187-274, bound at moe/cache.py:39-41):
+ * ids int32 [mk] (<0 or >= E ignored); table int32 [E] expert -> slot or -1; map_cold int32 [E] expert -> itself
+ * when not resident else -1; slot_expert int32 [S]; slot_stamp int64 [S]; routed u8 [E] (out: this step's flags);
+ * step int64 [1]; miss int32 [max_inserts][2] (out: (expert, slot) of each insert); n_miss int32 [1]. When more
+ * than max_distinct experts are routed only step and routed change; otherwise resident routed experts are
+ * restamped and the non-resident ones, in expert-id order and at most max_inserts, take the slots of the smallest
+ * (stamp << 20 | slot) among slots whose expert is not routed. One workgroup, no atomics (deterministic).
+ * -1 E <= 0 / E > 8192 / S <= 0 / S > 1024 / S > E / mk < 0, -2 max_inserts outside [0, S], -3 null pointer,
+ * -4 int64 arrays not 8-byte aligned, -6 launch error. */
+int r4d_lru_manage(long ids, int mk, int E, int S, int max_distinct, int max_inserts, long table, long map_cold,
+                   long slot_expert, long slot_stamp, long routed, long step, long miss, long n_miss, long stream);
+
+/* Copy each listed expert's six per-expert slabs host -> slot (replaces r4d_lru.hip:276-303, bound at
+ * moe/cache.py:42-44): slab i of expert e at s_i + e * b_i goes to d_i + slot * b_i for the first n_miss[0]
+ * (expert, slot) pairs of miss. Bytes b_i multiples of 16 (0 = unused slab), pointers 16-byte aligned. Grid
+ * (chunks, lanes) of 256-thread workgroups. -2 chunks / lanes outside [1, 65535], -3 null pointer, -4 size or
+ * alignment, -6 launch error. */
+int r4d_lru_gather(long d0, long s0, long b0, long d1, long s1, long b1, long d2, long s2, long b2, long d3, long s3,
+                   long b3, long d4, long s4, long b4, long d5, long s5, long b5, long miss, long n_miss, int chunks,
+                   int lanes, long stream);
+
+/* hot[i] = table[ids[i]], cold[i] = map_cold[ids[i]] (-1 for ids outside [0, E)): the routing ids of the resident
+ * and the host pass, for r9k_moe_align. The reference computes them inside its fused manage kernel
+ * (r4d_lru.hip:305-631, moe/cache.py:336-354). -1 mk < 0 / E <= 0, -3 null pointer, -6 launch error. */
+int r9k_lru_map_ids(long ids, int mk, int E, long table, long map_cold, long hot, long cold, long stream);
+
+/* Mapped pinned host memory for the expert store (the role of the reference's UVA tensors, utils/hostmem.py):
+ * hipHostMalloc(Mapped | Portable), returned only when its device address equals its host address; 0 on failure or
+ * bytes <= 0. r9k_host_free: 0 / -6. */
+long r9k_host_alloc(long bytes);
+int r9k_host_free(long ptr);
+
 #ifdef __cplusplus
 }
 #endif

@@ -21,6 +21,9 @@ Parity status per function (what pins it; tests/test_oracle_*.py):
   gemm / layer                     pure-Python dot products on tiny inputs
   router_gemm / hc_silu            pure-Python dot products; torch silu (library routine) and its closed-form limits
   nvfp4_gemm                       pure-Python dot products over the closed-form e2m1 / e4m3 values on tiny inputs
+  lru_manage / lru_gather          a serial one-argmin-per-insert simulation written independently in the test,
+                                   hand-worked step sequences, and the cache invariants (table / map_cold
+                                   complementary, slot_expert inverse of table, no routed resident evicted)
 """
 from __future__ import annotations
 
@@ -334,3 +337,68 @@ def moe_layer(x: torch.Tensor, logits: torch.Tensor, w13: tuple, w2: tuple, topk
     out = moe_sum(bits_to_bf16(down.reshape(tok.size, topk, -1)))
     return dict(w=w, ids=ids, xq=xq, xs=xs, rows=rows, gate_up=gate_up, aq=aq, a_s=a_s, down=down, out=out,
                 tokens=tok)
+
+
+class LruState:
+    """The device LRU expert cache's state (reference moe/cache.py:193-206): table [E] expert -> slot or -1,
+    map_cold [E] expert -> itself when not resident else -1, slot_expert [S], slot_stamp [S] int64, step."""
+
+    def __init__(self, E: int, S: int):
+        self.E, self.S = E, S
+        self.table = np.full(E, -1, dtype=np.int32)
+        self.map_cold = np.arange(E, dtype=np.int32)
+        self.slot_expert = np.full(S, -1, dtype=np.int32)
+        self.slot_stamp = np.zeros(S, dtype=np.int64)
+        self.step = 0
+
+    def copy(self) -> "LruState":
+        c = LruState(self.E, self.S)
+        c.table, c.map_cold = self.table.copy(), self.map_cold.copy()
+        c.slot_expert, c.slot_stamp, c.step = self.slot_expert.copy(), self.slot_stamp.copy(), self.step
+        return c
+
+
+def lru_manage(st: LruState, ids, max_distinct: int, max_inserts: int):
+    """One manage call (reference kernels/third_party/davetha/r4d_lru.hip:187-274), in place on `st`. Returns
+    (routed flags uint8 [E], miss list [(expert, slot)] in insert order).
+
+    step += 1; routed = the valid ids' experts. More than max_distinct distinct experts: nothing else changes (the
+    step reads through; :222). Otherwise resident routed experts get stamp = step (:229-233); the non-resident routed
+    ones, in expert-id order, are the misses, at most max_inserts (:236-245); victims are the slots whose expert is
+    not routed, taken in ascending (stamp << 20 | slot) order (:108-183), the r-th miss into the r-th victim, as many
+    as there are victims; an evicted expert goes cold (table -1, map_cold itself) and the inserted one resident
+    (:91-105)."""
+    E, S = st.E, st.S
+    st.step += 1
+    ids = np.asarray(ids, dtype=np.int64).reshape(-1)
+    routed = np.zeros(E, dtype=np.uint8)
+    v = ids[(ids >= 0) & (ids < E)]
+    routed[v] = 1
+    if int(routed.sum()) > max_distinct:
+        return routed, []
+    for e in np.flatnonzero(routed):
+        if st.table[e] >= 0:
+            st.slot_stamp[st.table[e]] = st.step
+    misses = [int(e) for e in np.flatnonzero(routed) if st.table[e] < 0][:max_inserts]
+    if not misses:
+        return routed, []
+    evictable = [i for i in range(S) if not (st.slot_expert[i] >= 0 and routed[st.slot_expert[i]])]
+    victims = sorted(evictable, key=lambda i: (int(st.slot_stamp[i]) << 20) | i)[:len(misses)]
+    out = []
+    for e, sl in zip(misses, victims):
+        old = int(st.slot_expert[sl])
+        if old >= 0:
+            st.table[old] = -1
+            st.map_cold[old] = old
+        st.slot_expert[sl] = e
+        st.slot_stamp[sl] = st.step
+        st.table[e] = sl
+        st.map_cold[e] = -1
+        out.append((e, sl))
+    return routed, out
+
+
+def lru_gather(arena: np.ndarray, store: np.ndarray, misses) -> None:
+    """Copy each missed expert's slab from the host store into its slot (reference r4d_lru.hip:276-303)."""
+    for e, sl in misses:
+        arena[sl] = store[e]

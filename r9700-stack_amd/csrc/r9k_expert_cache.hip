@@ -1,0 +1,278 @@
+// Device-side LRU expert cache for host-offloaded experts (MI355X, gfx950).
+//
+// Reference behaviour (moe/cache.py:1-20, 182-395; kernels/third_party/davetha/r4d_lru.hip:187-274 manage,
+// :276-303 gather): every expert of a layer lives in mapped pinned host memory (the backing store); a VRAM arena of
+// S slots holds a subset. Per forward, before the GEMMs:
+//   manage  marks the experts routed this step; when more than max_distinct are routed it changes nothing else (the
+//           step reads every non-resident expert through from host); otherwise it refreshes the stamps of the
+//           resident routed experts, lists the non-resident routed experts in expert-id order (at most max_inserts),
+//           and gives the r-th of them the slot with the r-th smallest key (stamp << 20 | slot) among the slots
+//           whose expert is NOT routed this step, so nothing this step needs is evicted. table (expert -> slot or -1),
+//           map_cold (expert -> itself when not resident, else -1), slot_expert and slot_stamp are rewritten in
+//           place, and the (expert, slot) miss list is what gather copies host -> slot.
+//   gather  copies up to six per-expert slabs of each listed expert from the host store into its slot.
+// Both are device work with fixed pointers (no host sync), so a captured graph replays them.
+//
+// gfx950 design: manage is ONE workgroup of 16 waves. Routed flags, the slot mirror (expert, stamp, key) and the
+// victim ranks sit in LDS (E <= 8192, S <= 1024: 8 KB + 20 KB). Victims are chosen by ranking each evictable slot's
+// key against all S keys (each lane reads the keys as LDS broadcasts, 8 in flight), which equals taking the argmin
+// nins times in a row: installing an expert makes its slot non-evictable and changes no other key. Nothing uses
+// atomics, so the evolution is deterministic (identical on every rank that sees the same routing). gather reads the
+// host store over PCIe with 16-byte loads; it is link-bound.
+#include "r9k_common.h"
+
+#include <climits>
+
+namespace {
+
+using namespace r9k;
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int MT_THREADS = 1024;            // manage: one workgroup, 16 waves
+constexpr int MAX_E = 8192;                 // routed flags in LDS
+constexpr int MAX_S = 1024;                 // slot mirror in LDS (and the slot index fits the key's low 20 bits)
+constexpr int SLOT_BITS = 20;
+constexpr int NWAVE = MT_THREADS / WAVE;
+
+// exclusive prefix sum of one int per thread over the workgroup; *total = the sum of all
+__device__ __forceinline__ int block_exscan(int v, int* sh, int* total) {
+  const int t = threadIdx.x, lane = t % WAVE, w = t / WAVE;
+  int x = v;
+#pragma unroll
+  for (int o = 1; o < WAVE; o <<= 1) {
+    const int y = __shfl_up(x, o, WAVE);
+    if (lane >= o) x += y;
+  }
+  if (lane == WAVE - 1) sh[w] = x;
+  __syncthreads();
+  if (w == 0) {
+    int s = lane < NWAVE ? sh[lane] : 0;
+#pragma unroll
+    for (int o = 1; o < NWAVE; o <<= 1) {
+      const int y = __shfl_up(s, o, WAVE);
+      if (lane >= o) s += y;
+    }
+    if (lane < NWAVE) sh[NWAVE + lane] = s;        // inclusive wave-total prefix
+  }
+  __syncthreads();
+  const int before = w ? sh[NWAVE + w - 1] : 0;
+  *total = sh[2 * NWAVE - 1];
+  __syncthreads();                                  // sh is reused by the next call
+  return before + x - v;
+}
+
+__global__ void __launch_bounds__(MT_THREADS) lru_manage_kernel(
+    const int* __restrict__ ids, int mk, int E, int S, int max_distinct, int max_inserts, int* __restrict__ table,
+    int* __restrict__ map_cold, int* __restrict__ slot_expert, long long* __restrict__ slot_stamp,
+    uint8_t* __restrict__ routed_out, long long* __restrict__ step, int* __restrict__ miss, int* __restrict__ n_miss) {
+  __shared__ uint8_t s_routed[MAX_E];
+  __shared__ int s_se[MAX_S];
+  __shared__ long long s_st[MAX_S];
+  __shared__ long long s_key[MAX_S];
+  __shared__ int s_vic[MAX_S];
+  __shared__ int s_miss[MAX_S];
+  __shared__ int sh[2 * NWAVE];
+  const int t = threadIdx.x;
+
+  const long long st = step[0] + 1;                 // every lane reads before lane 0 writes (barrier below)
+  for (int e = t; e < E; e += MT_THREADS) s_routed[e] = 0;
+  __syncthreads();
+  if (t == 0) step[0] = st;
+  for (int i = t; i < mk; i += MT_THREADS) {
+    const int e = ids[i];
+    if (e >= 0 && e < E) s_routed[e] = 1;           // same value from every writer
+  }
+  __syncthreads();
+
+  // distinct routed experts; experts are taken in contiguous runs so the miss order below is expert-id order
+  const int C = (E + MT_THREADS - 1) / MT_THREADS;
+  const int lo = min(t * C, E), hi = min(lo + C, E);
+  int cnt = 0;
+  for (int e = lo; e < hi; e++) cnt += s_routed[e];
+  int distinct = 0;
+  block_exscan(cnt, sh, &distinct);
+
+  int nact = 0;
+  if (distinct <= max_distinct) {                   // else: a wide step reads through; nothing else changes
+    for (int i = t; i < S; i += MT_THREADS) {
+      s_se[i] = slot_expert[i];
+      s_st[i] = slot_stamp[i];
+    }
+    __syncthreads();
+    int local = 0;
+    for (int e = lo; e < hi; e++) {
+      if (!s_routed[e]) continue;
+      const int s = table[e];
+      if (s >= 0) s_st[s] = st;                      // a hit: distinct experts hold distinct slots
+      else local++;
+    }
+    int total = 0;
+    const int base = block_exscan(local, sh, &total);   // (its barriers also order the stamp refresh)
+    const int nins = min(total, max_inserts);
+    if (nins > 0) {
+      int j = base;
+      for (int e = lo; e < hi && j < nins; e++) {
+        if (!s_routed[e] || table[e] >= 0) continue;
+        s_miss[j++] = e;
+      }
+      int evictable = 0;
+      for (int i = t; i < S; i += MT_THREADS) {
+        const int se = s_se[i];
+        const bool keep = se >= 0 && se < E && s_routed[se];
+        s_key[i] = keep ? LLONG_MAX : (long long)(((unsigned long long)s_st[i] << SLOT_BITS) | (unsigned)i);
+        evictable += !keep;
+      }
+      for (int r = t; r < nins; r += MT_THREADS) s_vic[r] = -1;
+      int nev = 0;
+      block_exscan(evictable, sh, &nev);            // barrier: keys and misses are in LDS
+      nact = min(nins, nev);
+      // rank of each evictable key among all keys (keys are unique: the slot index is in the low bits)
+      for (int i = t; i < S; i += MT_THREADS) {
+        const long long ki = s_key[i];
+        if (ki == LLONG_MAX) continue;
+        int rank = 0, jj = 0;
+        for (; jj + 8 <= S; jj += 8) {
+          long long k8[8];
+#pragma unroll
+          for (int u = 0; u < 8; u++) k8[u] = s_key[jj + u];
+#pragma unroll
+          for (int u = 0; u < 8; u++) rank += k8[u] < ki;
+        }
+        for (; jj < S; jj++) rank += s_key[jj] < ki;
+        if (rank < nact) s_vic[rank] = i;
+      }
+      __syncthreads();
+      // installs are independent: distinct victim slots, distinct (routed) new experts, evicted experts unrouted
+      for (int r = t; r < nact; r += MT_THREADS) {
+        const int e = s_miss[r], sl = s_vic[r];
+        const int old = s_se[sl];
+        if (old >= 0 && old < E) {
+          table[old] = -1;
+          map_cold[old] = old;
+        }
+        s_se[sl] = e;
+        s_st[sl] = st;
+        table[e] = sl;
+        map_cold[e] = -1;
+        miss[2 * r] = e;
+        miss[2 * r + 1] = sl;
+      }
+      __syncthreads();
+    }
+    for (int i = t; i < S; i += MT_THREADS) {
+      slot_expert[i] = s_se[i];
+      slot_stamp[i] = s_st[i];
+    }
+  }
+  for (int e = t; e < E; e += MT_THREADS) routed_out[e] = s_routed[e];
+  if (t == 0) n_miss[0] = nact;
+}
+
+struct Slabs {
+  u32x4* d[6];
+  const u32x4* s[6];
+  long v[6];                                         // 16-byte units per expert
+};
+
+// grid (chunks, lanes): block (c, j) copies misses j, j + lanes, ...; each slab is split over the chunks' threads
+__global__ void __launch_bounds__(256) lru_gather_kernel(Slabs sl, const int* __restrict__ miss,
+                                                         const int* __restrict__ n_miss) {
+  const int nm = n_miss[0];
+  const long stride = (long)gridDim.x * blockDim.x, start = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  for (int j = blockIdx.y; j < nm; j += gridDim.y) {
+    const long e = miss[2 * j], slot = miss[2 * j + 1];
+#pragma unroll
+    for (int b = 0; b < 6; b++) {
+      const long v = sl.v[b];
+      const u32x4* __restrict__ p = sl.s[b] + e * v;
+      u32x4* __restrict__ q = sl.d[b] + slot * v;
+      long i = start;
+      for (; i + 3 * stride < v; i += 4 * stride) {  // four 16-byte host reads in flight per lane
+        const u32x4 a0 = p[i], a1 = p[i + stride], a2 = p[i + 2 * stride], a3 = p[i + 3 * stride];
+        q[i] = a0;
+        q[i + stride] = a1;
+        q[i + 2 * stride] = a2;
+        q[i + 3 * stride] = a3;
+      }
+      for (; i < v; i += stride) q[i] = p[i];
+    }
+  }
+}
+
+// hot[i] = table[ids[i]], cold[i] = map_cold[ids[i]] (-1 for ids outside [0, E)): the two passes' routing ids
+__global__ void __launch_bounds__(256) lru_map_ids_kernel(const int* __restrict__ ids, int mk, int E,
+                                                          const int* __restrict__ table,
+                                                          const int* __restrict__ map_cold, int* __restrict__ hot,
+                                                          int* __restrict__ cold) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= mk) return;
+  const int e = ids[i];
+  const bool ok = e >= 0 && e < E;
+  hot[i] = ok ? table[e] : -1;
+  cold[i] = ok ? map_cold[e] : -1;
+}
+
+}  // namespace
+
+extern "C" int r4d_lru_manage(long ids, int mk, int E, int S, int max_distinct, int max_inserts, long table,
+                              long map_cold, long slot_expert, long slot_stamp, long routed, long step, long miss,
+                              long n_miss, long stream) {
+  if (E <= 0 || E > MAX_E || S <= 0 || S > MAX_S || S > E || mk < 0) return -1;
+  if (max_inserts < 0 || max_inserts > S) return -2;
+  if ((mk && !ids) || !table || !map_cold || !slot_expert || !slot_stamp || !routed || !step || !miss || !n_miss)
+    return -3;
+  if ((slot_stamp | step) & 7) return -4;
+  hipLaunchKernelGGL(lru_manage_kernel, dim3(1), dim3(MT_THREADS), 0, (hipStream_t)stream, (const int*)ids, mk, E,
+                     S, max_distinct, max_inserts, (int*)table, (int*)map_cold, (int*)slot_expert,
+                     (long long*)slot_stamp, (uint8_t*)routed, (long long*)step, (int*)miss, (int*)n_miss);
+  return hipGetLastError() == hipSuccess ? 0 : -6;
+}
+
+extern "C" int r4d_lru_gather(long d0, long s0, long b0, long d1, long s1, long b1, long d2, long s2, long b2,
+                              long d3, long s3, long b3, long d4, long s4, long b4, long d5, long s5, long b5,
+                              long miss, long n_miss, int chunks, int lanes, long stream) {
+  if (chunks <= 0 || lanes <= 0 || chunks > 65535 || lanes > 65535) return -2;
+  if (!miss || !n_miss) return -3;
+  const long d[6] = {d0, d1, d2, d3, d4, d5}, s[6] = {s0, s1, s2, s3, s4, s5}, b[6] = {b0, b1, b2, b3, b4, b5};
+  Slabs sl;
+  for (int i = 0; i < 6; i++) {
+    if (b[i] < 0 || (b[i] % 16) || ((d[i] | s[i]) & 15)) return -4;
+    if (b[i] && (!d[i] || !s[i])) return -3;
+    sl.d[i] = (u32x4*)d[i];
+    sl.s[i] = (const u32x4*)s[i];
+    sl.v[i] = b[i] / 16;
+  }
+  hipLaunchKernelGGL(lru_gather_kernel, dim3(chunks, lanes), dim3(256), 0, (hipStream_t)stream, sl,
+                     (const int*)miss, (const int*)n_miss);
+  return hipGetLastError() == hipSuccess ? 0 : -6;
+}
+
+extern "C" int r9k_lru_map_ids(long ids, int mk, int E, long table, long map_cold, long hot, long cold,
+                               long stream) {
+  if (mk < 0 || E <= 0) return -1;
+  if (mk == 0) return 0;
+  if (!ids || !table || !map_cold || !hot || !cold) return -3;
+  hipLaunchKernelGGL(lru_map_ids_kernel, dim3((mk + 255) / 256), dim3(256), 0, (hipStream_t)stream,
+                     (const int*)ids, mk, E, (const int*)table, (const int*)map_cold, (int*)hot, (int*)cold);
+  return hipGetLastError() == hipSuccess ? 0 : -6;
+}
+
+// Mapped pinned host memory for the backing store: hipHostMalloc(Mapped | Portable); the device address is the host
+// address (checked), so one pointer serves the host-side copies and the kernels. Held until r9k_host_free.
+extern "C" long r9k_host_alloc(long bytes) {
+  if (bytes <= 0) return 0;
+  void* h = nullptr;
+  if (hipHostMalloc(&h, (size_t)bytes, hipHostMallocMapped | hipHostMallocPortable) != hipSuccess || !h) return 0;
+  void* d = nullptr;
+  if (hipHostGetDevicePointer(&d, h, 0) != hipSuccess || d != h) {
+    (void)hipHostFree(h);
+    return 0;
+  }
+  return (long)h;
+}
+
+extern "C" int r9k_host_free(long p) {
+  if (!p) return 0;
+  return hipHostFree((void*)p) == hipSuccess ? 0 : -6;
+}

@@ -1,0 +1,378 @@
+"""Per-layer device-side LRU expert cache over mapped pinned host memory (reference r9700_vllm/moe/cache.py:1-414).
+
+Every routed expert of a cached layer lives in mapped pinned host memory (`uva_empty`: hipHostMalloc, the device
+address equals the host address): the fragment-order weights w13 / w2 and the packed scales s13 / s2 are the
+backing store. A VRAM arena of S slots per layer holds a changing subset. Each forward, before the GEMMs,
+`r4d_lru_manage` (csrc/r9k_expert_cache.hip) refreshes the resident experts routed this step, picks victims among
+the slots not routed this step (least recently routed first, ties to the lower slot: deterministic, so ranks that
+see the same routing agree), rewrites `table` / `map_cold` and emits a miss list, and `r4d_lru_gather` copies the
+missed experts host -> slot. The GEMMs then run twice: over the arena with the routing ids mapped through `table`
+(expert -> slot) and over the host store with them mapped through `map_cold` (expert -> itself when not resident);
+the second pass is empty unless the step read through (more distinct experts than the threshold, or the insert cap
+was hit). Everything is device work on fixed addresses, so a captured HIP graph replays it.
+
+Config (per process, the reference's names): R9K_EXPERT_CACHE_GB (0 = off), R9K_EXPERT_CACHE_SLOTS,
+R9K_EXPERT_CACHE_LAYERS, R9K_LRU_THRESH (0.99: a step routing to more distinct experts than this share of the slots
+inserts nothing and reads every non-resident expert through from host), R9K_LRU_MAX_INSERTS (64),
+R9K_LRU_GATHER="chunks,lanes" (64,16), R9K_LRU_FUSED (1), R9K_EXPERT_CACHE_HOST_ONLY (1), R9K_EXPERT_CACHE_STATS.
+Warm start: the checkpoint's model-expertprofile.safetensors (expert_routing_counts [layers, experts]) when vLLM
+names a model directory holding one, else experts 0..S-1.
+
+On gfx950 the cold pass reads weights over PCIe inside the GEMM (the decode kernels read every weight byte once per
+routing block). R9K_STAGE_COLD (the reference's opt-in bulk staging of cold experts, recorded there as without a
+measured gain) is not built: `staging_enabled()` is always False.
+"""
+from __future__ import annotations
+
+import ctypes
+import logging
+import os
+
+import numpy as np
+import torch
+
+from ..kernels import moe as K
+
+logger = logging.getLogger("vllm." + __name__)
+
+_BOUND = False
+_PROFILE: torch.Tensor | None = None
+_PROFILE_LOADED = False
+_HOST_BUFFERS: list = []          # (pointer, bytes) of every mapped host buffer: held until the process ends
+
+
+def _L():
+    global _BOUND
+    L = K.lib()
+    if not _BOUND:
+        i, l = ctypes.c_int, ctypes.c_long
+        L.r4d_lru_manage.restype = i
+        L.r4d_lru_manage.argtypes = [l, i, i, i, i, i] + [l] * 8 + [l]
+        L.r4d_lru_gather.restype = i
+        L.r4d_lru_gather.argtypes = [l, l, l] * 6 + [l, l, i, i, l]
+        L.r9k_lru_map_ids.restype = i
+        L.r9k_lru_map_ids.argtypes = [l, i, i, l, l, l, l, l]
+        L.r9k_host_alloc.restype = l
+        L.r9k_host_alloc.argtypes = [l]
+        L.r9k_host_free.restype = i
+        L.r9k_host_free.argtypes = [l]
+        _BOUND = True
+    return L
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def uva_empty(shape, dtype) -> torch.Tensor:
+    """A CPU tensor over fresh mapped pinned host memory whose address kernels can read (r9k_host_alloc checks that
+    the device address is the host address). Marked `_r9k_host`; held until the process ends."""
+    shape = tuple(int(x) for x in shape)
+    itemsize = torch.empty((), dtype=dtype).element_size()
+    nbytes = max(16, int(np.prod(shape, dtype=np.int64)) * itemsize)
+    nbytes = (nbytes + 255) // 256 * 256
+    ptr = _L().r9k_host_alloc(nbytes)
+    if not ptr:
+        raise RuntimeError(f"r9k_host_alloc({nbytes}) failed: no mapped pinned host memory")
+    _HOST_BUFFERS.append((ptr, nbytes))
+    buf = (ctypes.c_uint8 * nbytes).from_address(ptr)
+    n = int(np.prod(shape, dtype=np.int64)) * itemsize
+    t = torch.from_numpy(np.frombuffer(buf, dtype=np.uint8, count=n)).view(dtype).view(shape)
+    t._r9k_host = ptr
+    return t
+
+
+def is_host(t: torch.Tensor) -> bool:
+    """True for a tensor in mapped host memory made by uva_empty (or marked by vLLM's UVA offloader)."""
+    return bool(getattr(t, "_vllm_is_uva_offloaded", False) or getattr(t, "_r9k_host", None) is not None)
+
+
+def to_host(t: torch.Tensor) -> torch.Tensor:
+    """Copy a (device) tensor into a fresh mapped host tensor, chunked along dim 0."""
+    h = uva_empty(t.shape, t.dtype)
+    step = max(1, (256 << 20) // max(1, t[0].numel() * t.element_size()))
+    for i in range(0, t.shape[0], step):
+        h[i:i + step].copy_(t[i:i + step])
+    return h
+
+
+def budget_gb() -> float:
+    return float(os.environ.get("R9K_EXPERT_CACHE_GB", "0") or 0)
+
+
+def _profile() -> torch.Tensor | None:
+    global _PROFILE, _PROFILE_LOADED
+    if _PROFILE_LOADED:
+        return _PROFILE
+    _PROFILE_LOADED = True
+    try:
+        from vllm.config import get_current_vllm_config
+        from safetensors.torch import load_file
+        p = os.path.join(get_current_vllm_config().model_config.model, "model-expertprofile.safetensors")
+        if os.path.isfile(p):
+            _PROFILE = load_file(p)["expert_routing_counts"].float()
+            logger.info("r9700: expert routing profile %s %s", p, tuple(_PROFILE.shape))
+    except Exception as e:                       # no vLLM config or no profile: cold start from experts 0..S-1
+        logger.debug("r9700: no expert routing profile (%s)", e)
+    return _PROFILE
+
+
+def _num_moe_layers() -> int:
+    try:
+        from vllm.config import get_current_vllm_config
+        hf = get_current_vllm_config().model_config.hf_text_config
+        return int(getattr(hf, "num_hidden_layers"))
+    except Exception:
+        return 48
+
+
+def staging_enabled() -> bool:
+    return False
+
+
+def stats_enabled() -> bool:
+    return os.environ.get("R9K_EXPERT_CACHE_STATS", "0") == "1"
+
+
+STAT_FIELDS = ("steps", "distinct", "inserts", "read_through", "wide")
+_STATS: list = []
+_STATS_THREAD = None
+
+
+def stats_snapshot() -> torch.Tensor:
+    """[layers, 5] int64 on the host: per cached layer, totals since load of STAT_FIELDS."""
+    if not _STATS:
+        return torch.zeros((0, len(STAT_FIELDS)), dtype=torch.int64)
+    return torch.stack([c.stats for c in _STATS]).cpu()
+
+
+def stats_line(delta: torch.Tensor, mib_per_expert: float) -> str:
+    """One line for a [layers, 5] difference of two snapshots; per layer-step means over the layers that stepped."""
+    t = delta.sum(0).tolist()
+    n = max(t[0], 1)
+    return (f"{t[0]} layer-steps: routed {t[1] / n:.1f} distinct experts, {t[2] / n:.1f} inserted, "
+            f"{t[3] / n:.1f} read through from host ({t[3] / n * mib_per_expert:.0f} MiB), "
+            f"{100.0 * t[4] / n:.0f}% of steps over the insert threshold")
+
+
+def _stats_loop(period: float):
+    import time
+    last = None
+    while True:
+        time.sleep(period)
+        try:
+            cur = stats_snapshot()
+            if last is not None and cur.shape == last.shape and int((cur - last)[:, 0].sum()) > 0:
+                c = _STATS[0]
+                logger.info("r9700: expert cache, last %.0f s (S=%d, threshold %d, insert cap %d): %s", period, c.S,
+                            c.max_distinct, c.max_inserts, stats_line(cur - last, sum(c.bytes) / 2**20))
+            last = cur
+        except Exception as e:                   # a diagnostic must never take the worker down
+            logger.warning("r9700: expert cache stats reader stopped: %s", e)
+            return
+
+
+def _stats_register(cache) -> None:
+    global _STATS_THREAD
+    _STATS.append(cache)
+    period = float(os.environ.get("R9K_EXPERT_CACHE_STATS_SEC", "10") or 0)
+    if _STATS_THREAD is None and period > 0:
+        import threading
+        _STATS_THREAD = threading.Thread(target=_stats_loop, args=(period,), name="r9k-cache-stats", daemon=True)
+        _STATS_THREAD.start()
+
+
+class LayerCache:
+    """One MoE layer's cache (reference moe/cache.py:182-395): host store of all E experts, S-slot VRAM arena,
+    LRU state, and one persistent set of align buffers (pointer-stable, so captured graphs replay through it)."""
+
+    def __init__(self, layer_idx: int, w13: torch.Tensor, w2: torch.Tensor, s13: torch.Tensor, s2: torch.Tensor,
+                 N1: int, K1: int, N2: int, K2: int, slots: int):
+        dev = torch.device("cuda", torch.cuda.current_device())
+        E = w13.shape[0]
+        self.E, self.S, self.layer_idx = E, min(slots, E, 1024), layer_idx
+        if self.S < 1:
+            raise ValueError("LayerCache: at least one slot")
+        if E > 8192:
+            raise ValueError(f"LayerCache: {E} experts (the device manager holds at most 8192)")
+        self.N1, self.K1, self.N2, self.K2 = N1, K1, N2, K2
+        self.fold = (False, False)
+        if not (is_host(w13) and is_host(w2)):
+            raise ValueError("LayerCache: w13 / w2 must be mapped host tensors (to_host / uva_empty)")
+        self.h_w13, self.h_w2 = w13, w2
+        self.h_s13 = s13 if is_host(s13) else to_host(s13.contiguous())
+        self.h_s2 = s2 if is_host(s2) else to_host(s2.contiguous())
+        S = self.S
+        self.a_w13 = torch.empty((S, *w13.shape[1:]), dtype=w13.dtype, device=dev)
+        self.a_w2 = torch.empty((S, *w2.shape[1:]), dtype=w2.dtype, device=dev)
+        self.a_s13 = torch.empty((S, *self.h_s13.shape[1:]), dtype=torch.uint8, device=dev)
+        self.a_s2 = torch.empty((S, *self.h_s2.shape[1:]), dtype=torch.uint8, device=dev)
+        self.bytes = [w13[0].numel() * w13.element_size(), w2[0].numel() * w2.element_size(),
+                      self.h_s13[0].numel(), self.h_s2[0].numel()]
+        for b in self.bytes:
+            if b % 16:
+                raise ValueError(f"LayerCache: per-expert slab sizes must be multiples of 16 bytes: {self.bytes}")
+        i32 = dict(dtype=torch.int32, device=dev)
+        self.table = torch.full((E,), -1, **i32)
+        self.map_cold = torch.arange(E, **i32)
+        self.slot_expert = torch.full((S,), -1, **i32)
+        self.slot_stamp = torch.zeros((S,), dtype=torch.int64, device=dev)
+        self.routed = torch.zeros((E,), dtype=torch.uint8, device=dev)
+        self.step = torch.zeros((1,), dtype=torch.int64, device=dev)
+        self.max_inserts = min(int(os.environ.get("R9K_LRU_MAX_INSERTS", "64")), S)
+        self.max_distinct = int(S * float(os.environ.get("R9K_LRU_THRESH", "0.99")))
+        self.miss = torch.full((max(1, self.max_inserts), 2), -1, **i32)
+        # rows per step up to which the cold pass cannot have work: distinct <= rows <= both limits
+        self.no_cold_limit = min(self.max_distinct, self.max_inserts) if S > self.max_distinct else 0
+        self.n_miss = torch.zeros((1,), **i32)
+        self.fused = os.environ.get("R9K_LRU_FUSED", "1") == "1"
+        self._one = None
+        self._one_old: list = []
+        g = os.environ.get("R9K_LRU_GATHER", "64,16").split(",")
+        self.chunks, self.lanes = int(g[0]), int(g[1])
+        self.stage = None
+        self._warm_start()
+        self.stats = None
+        if stats_enabled():
+            self.stats = torch.zeros((len(STAT_FIELDS),), dtype=torch.int64, device=dev)
+            _stats_register(self)
+
+    def _warm_start(self):
+        prof = _profile()
+        if prof is not None and self.layer_idx < prof.shape[0] and prof.shape[1] == self.E:
+            order = torch.argsort(prof[self.layer_idx], descending=True, stable=True)
+        else:
+            order = torch.arange(self.E)
+        init = order[: self.S].to(torch.int32)
+        n = init.numel()
+        dev = self.table.device
+        pairs = torch.stack([init, torch.arange(n, dtype=torch.int32)], dim=1).to(dev)
+        for i in range(0, n, max(1, self.max_inserts)):      # the gather kernel, in miss-list-sized batches
+            chunk = pairs[i: i + max(1, self.max_inserts)]
+            self.miss[: chunk.shape[0]].copy_(chunk)
+            self.n_miss.fill_(chunk.shape[0])
+            self._gather()
+        self.n_miss.zero_()
+        self.miss.fill_(-1)
+        il = init.long().to(dev)
+        self.table[il] = torch.arange(n, dtype=torch.int32, device=dev)
+        self.map_cold[il] = -1
+        self.slot_expert[:n] = init.to(dev)
+        # older stamps for colder warm experts, so the hottest are evicted last
+        self.slot_stamp[:n] = torch.arange(n, 0, -1, dtype=torch.int64, device=dev) - n
+        torch.cuda.synchronize()
+
+    def _gather(self):
+        b = self.bytes
+        rc = _L().r4d_lru_gather(
+            self.a_w13.data_ptr(), self.h_w13.data_ptr(), b[0], self.a_w2.data_ptr(), self.h_w2.data_ptr(), b[1],
+            self.a_s13.data_ptr(), self.h_s13.data_ptr(), b[2], self.a_s2.data_ptr(), self.h_s2.data_ptr(), b[3],
+            0, 0, 0, 0, 0, 0, self.miss.data_ptr(), self.n_miss.data_ptr(), self.chunks, self.lanes, _stream())
+        if rc:
+            raise RuntimeError(f"r4d_lru_gather failed ({rc})")
+
+    def _manage(self, ids: torch.Tensor) -> None:
+        rc = _L().r4d_lru_manage(ids.data_ptr(), ids.numel(), self.E, self.S, self.max_distinct, self.max_inserts,
+                                 self.table.data_ptr(), self.map_cold.data_ptr(), self.slot_expert.data_ptr(),
+                                 self.slot_stamp.data_ptr(), self.routed.data_ptr(), self.step.data_ptr(),
+                                 self.miss.data_ptr(), self.n_miss.data_ptr(), _stream())
+        if rc:
+            raise RuntimeError(f"r4d_lru_manage failed ({rc}) E={self.E} S={self.S}")
+
+    @staticmethod
+    def _ids(topk_ids: torch.Tensor) -> torch.Tensor:
+        ids = topk_ids.reshape(-1)
+        if ids.dtype != torch.int32:
+            ids = ids.to(torch.int32)
+        return ids.contiguous()
+
+    def update(self, topk_ids: torch.Tensor) -> None:
+        """LRU manage + gather of this step's inserts (host -> slots)."""
+        self._manage(self._ids(topk_ids))
+        self._gather()
+        if self.stats is not None:
+            self._record()
+
+    def _record(self):
+        """After manage + gather: routed marks this step's experts and table already holds the inserted ones, so
+        routed-and-not-resident is what the cold pass reads through from host memory."""
+        r = self.routed.to(torch.int64)
+        d = r.sum()
+        cold = (r * (self.table < 0)).sum()
+        self.stats.add_(torch.stack([torch.ones_like(d), d, self.n_miss[0].to(torch.int64), cold,
+                                     (d > self.max_distinct).to(torch.int64)]))
+
+    def _align_bufs(self, mk: int, bs: int):
+        """Align outputs for (mk, bs), sized as moe_align sizes them (capacity()), as views of ONE buffer set per
+        layer sized by the largest step seen. A larger step keeps the old set alive (a captured graph may replay
+        through it) and takes one at least twice the size, so the total stays under twice the largest."""
+        L = K.capacity(mk, self.E, bs)
+        NB = L // bs
+        o = self._one
+        if o is None or o[0] < L or o[1] < mk:
+            if o is not None:
+                self._one_old.append(o)
+            cl = max(L, 2 * o[0]) if o is not None else L
+            cm = max(mk, 2 * o[1]) if o is not None else mk
+            cn = cl // K.MOE_BLOCK + 1
+            i32 = dict(dtype=torch.int32, device=self.table.device)
+            o = (cl, cm, torch.empty((cl,), **i32), torch.empty((cn,), **i32), torch.empty((1,), **i32),
+                 torch.empty((cl,), **i32), torch.empty((cn,), **i32), torch.empty((1,), **i32),
+                 torch.empty((max(1, cm),), **i32), torch.empty((max(1, cm),), **i32))
+            self._one = o
+        return (L, NB, o[2][:L], o[3][:NB], o[4], o[5][:L], o[6][:NB], o[7], o[8][:mk], o[9][:mk])
+
+    def update_fused(self, topk_ids: torch.Tensor, bs: int):
+        """LRU manage + gather, then both align outputs: the resident one over slot ids (ids through table) and the
+        host one over expert ids (through map_cold). Returns ((sorted, eids, ntpp) hot, (sorted, eids, ntpp) cold),
+        views of the layer's persistent buffers."""
+        ids = self._ids(topk_ids)
+        mk = ids.numel()
+        L_, NB, sh, eh, nh, sc, ec, nc, hid, cid = self._align_bufs(mk, bs)
+        self._manage(ids)
+        self._gather()
+        if self.stats is not None:
+            self._record()
+        lib, st = _L(), _stream()
+        rc = lib.r9k_lru_map_ids(ids.data_ptr(), mk, self.E, self.table.data_ptr(), self.map_cold.data_ptr(),
+                                 hid.data_ptr(), cid.data_ptr(), st)
+        if rc:
+            raise RuntimeError(f"r9k_lru_map_ids failed ({rc})")
+        n = lib.r9k_moe_align_scratch_ints(mk, self.E)
+        scratch = K._align_scratch(ids.device, n)
+        for a, s_, e_, t_ in ((hid, sh, eh, nh), (cid, sc, ec, nc)):
+            rc = lib.r9k_moe_align(a.data_ptr(), mk, self.E, bs, s_.data_ptr(), e_.data_ptr(), t_.data_ptr(),
+                                   scratch.data_ptr(), scratch.numel(), st)
+            if rc:
+                raise RuntimeError(f"r9k_moe_align failed ({rc}) numel={mk} E={self.E} block={bs}")
+        return (sh, eh, nh), (sc, ec, nc)
+
+    def stage_cold(self, topk_ids: torch.Tensor):
+        raise RuntimeError("LayerCache.stage_cold: bulk staging of cold experts is not built for gfx950")
+
+    def hot(self):
+        return (K.Mxfp4Experts(self.a_w13, self.a_s13, self.N1, self.K1, self.fold[0]),
+                K.Mxfp4Experts(self.a_w2, self.a_s2, self.N2, self.K2, self.fold[1]))
+
+    def cold(self):
+        return (K.Mxfp4Experts(self.h_w13, self.h_s13, self.N1, self.K1, self.fold[0]),
+                K.Mxfp4Experts(self.h_w2, self.h_s2, self.N2, self.K2, self.fold[1]))
+
+
+def slots_per_layer(bytes_per_expert: int) -> int:
+    """Slots per cached layer: R9K_EXPERT_CACHE_SLOTS if set, else the R9K_EXPERT_CACHE_GB budget spread over the
+    layers that will be cached (R9K_EXPERT_CACHE_LAYERS, default all MoE layers)."""
+    slots = int(os.environ.get("R9K_EXPERT_CACHE_SLOTS", "0") or 0)
+    if slots > 0:
+        return slots
+    gb = budget_gb()
+    if gb <= 0:
+        return 0
+    nl = int(os.environ.get("R9K_EXPERT_CACHE_LAYERS", "0") or 0) or _num_moe_layers()
+    return int(gb * 2**30 // (nl * bytes_per_expert))
+
+
+def host_only() -> bool:
+    """Cache only layers whose experts are already host-offloaded (R9K_EXPERT_CACHE_HOST_ONLY=1, the default);
+    0 moves device-resident layers to host as well."""
+    return os.environ.get("R9K_EXPERT_CACHE_HOST_ONLY", "1") == "1"

@@ -166,16 +166,34 @@ class R9700Mxfp4Experts(_experts_base()):
             blk = K.MOE_BLOCK * MT
             pf_down = None if nv is not None else K.pick_moe_prefill(MT, K2)
             pf_gate = None if nv is not None else K.pick_moe_prefill(MT, K1, gate_up=True)
-        tabs = route.take(getattr(self, "r9k_layer", None), topk_ids, blk, numel) if expert_map is None else None
-        if tabs is None:
-            tabs = K.moe_align(topk_ids, blk, E, expert_map)
-        sid, eid, ntpp = tabs
-        if nv is not None:
-            W1 = K.Nvfp4Experts(w1, self.w1_scale, nv[0], N1, K1)
-            W2 = K.Nvfp4Experts(w2, self.w2_scale, nv[1], N2, K2)
+        cache = getattr(self, "r9k_cache", None)
+        if cache is not None:
+            # host-offloaded experts (moe/cache.py): LRU manage + gather, then a pass over the VRAM slots (ids
+            # through table) and, unless provably empty, one over the host store (ids through map_cold); every
+            # routed row belongs to exactly one pass (reference moe/experts.py:167-199)
+            if expert_map is not None or nv is not None:
+                raise RuntimeError("r9k expert cache: MXFP4 experts without an expert map only")
+            (h1, h2), (c1, c2) = cache.hot(), cache.cold()
+            if cache.fused:
+                hot_al, cold_al = cache.update_fused(topk_ids, blk)
+            else:
+                cache.update(topk_ids)
+                hot_al = K.moe_align(topk_ids, blk, E, cache.table)
+                cold_al = K.moe_align(topk_ids, blk, E, cache.map_cold)
+            passes = [(h1, h2, hot_al)]
+            if numel > cache.no_cold_limit:
+                passes.append((c1, c2, cold_al))
         else:
-            W1 = K.Mxfp4Experts(w1, self.w1_scale, N1, K1)
-            W2 = K.Mxfp4Experts(w2, self.w2_scale, N2, K2)
+            tabs = route.take(getattr(self, "r9k_layer", None), topk_ids, blk, numel) if expert_map is None else None
+            if tabs is None:
+                tabs = K.moe_align(topk_ids, blk, E, expert_map)
+            if nv is not None:
+                W1 = K.Nvfp4Experts(w1, self.w1_scale, nv[0], N1, K1)
+                W2 = K.Nvfp4Experts(w2, self.w2_scale, nv[1], N2, K2)
+            else:
+                W1 = K.Mxfp4Experts(w1, self.w1_scale, N1, K1)
+                W2 = K.Mxfp4Experts(w2, self.w2_scale, N2, K2)
+            passes = [(W1, W2, tabs)]
 
         # the router's fp8 quant of this input, when it made one (with its tables at decode, alone at prefill)
         q = route.take_quant(getattr(self, "r9k_layer", None), topk_ids, hidden_states) if expert_map is None else None
@@ -183,11 +201,14 @@ class R9700Mxfp4Experts(_experts_base()):
         fused = MOE_FUSE and nv is None and MT == 1 and pf_gate is None and pf_down is None
         if fused:
             aq = torch.empty((numel, N1 // 2), dtype=torch.float32, device=dev)
-            K.moe_gemm(xq, xs, W1, aq, sid, eid, ntpp, numel, topk, None, num_experts=E, MT=1, fuse=1)
+            for W1, _, (sid, eid, ntpp) in passes:
+                K.moe_gemm(xq, xs, W1, aq, sid, eid, ntpp, numel, topk, None, num_experts=E, MT=1, fuse=1)
             as_ = None
         else:
             gate_up = torch.empty((numel, N1), dtype=torch.bfloat16, device=dev)
-            K.moe_gemm(xq, xs, W1, gate_up, sid, eid, ntpp, numel, topk, None, num_experts=E, MT=MT, prefill=pf_gate)
+            for W1, _, (sid, eid, ntpp) in passes:
+                K.moe_gemm(xq, xs, W1, gate_up, sid, eid, ntpp, numel, topk, None, num_experts=E, MT=MT,
+                           prefill=pf_gate)
             aq, as_ = K.silu_mul_quant_fp8(gate_up)
         # Rows no table places (experts on other ranks under an expert map) must not feed moe_sum garbage.
         if expert_map is not None or ZERO_DOWN:
@@ -195,7 +216,8 @@ class R9700Mxfp4Experts(_experts_base()):
         else:
             down = torch.empty((numel, N2), dtype=torch.bfloat16, device=dev)
         tw = topk_weights.reshape(-1).to(torch.float32).contiguous()
-        K.moe_gemm(aq, as_, W2, down, sid, eid, ntpp, numel, 1, tw, num_experts=E, MT=MT, prefill=pf_down,
-                   fuse=2 if fused else 0)
+        for _, W2, (sid, eid, ntpp) in passes:
+            K.moe_gemm(aq, as_, W2, down, sid, eid, ntpp, numel, 1, tw, num_experts=E, MT=MT, prefill=pf_down,
+                       fuse=2 if fused else 0)
         K.moe_sum(down.view(M, topk, N2), None, output)
         return output

@@ -73,6 +73,29 @@ def test_shape_errors_before_launch():
     assert Lr.r9k_router_gemm(16, 64, 16, 64, 16, 64, 1, 64, 72, 2, 1, 0, 1.0, z) == -3
     assert Lr.r9k_router_gemm(16, 60, 16, 64, 16, 64, 1, 64, 64, 1, 1, 0, 1.0, z) == -4
     assert Lr.r9k_router_gemm(24, 64, 16, 64, 16, 64, 1, 64, 64, 1, 1, 0, 1.0, z) == -4
+    # expert cache: E / S / mk, the insert cap, pointers, int64 alignment; gather grid, slab sizes and alignment;
+    # map ids with nothing to do; host allocation of nothing (all return before a HIP call)
+    from r9700_vllm.moe import cache as C
+    Lc = C._L()
+    p8 = [8] * 8
+    assert Lc.r4d_lru_manage(8, 4, 0, 1, 1, 1, *p8, z) == -1
+    assert Lc.r4d_lru_manage(8, 4, 8192 + 1, 1, 1, 1, *p8, z) == -1
+    assert Lc.r4d_lru_manage(8, 4, 64, 1025, 1, 1, *p8, z) == -1
+    assert Lc.r4d_lru_manage(8, 4, 8, 16, 1, 1, *p8, z) == -1                   # more slots than experts
+    assert Lc.r4d_lru_manage(8, 4, 64, 16, 1, 17, *p8, z) == -2
+    assert Lc.r4d_lru_manage(8, 4, 64, 16, 1, 4, 8, 8, 8, 8, 8, 8, 0, 8, z) == -3
+    assert Lc.r4d_lru_manage(8, 4, 64, 16, 1, 4, 8, 8, 8, 12, 8, 8, 8, 8, z) == -4
+    slabs = [16, 16, 16] * 6
+    assert Lc.r4d_lru_gather(*slabs, 16, 16, 0, 16, z) == -2
+    assert Lc.r4d_lru_gather(*slabs, 16, 16, 64, 65536, z) == -2
+    assert Lc.r4d_lru_gather(*slabs, 0, 16, 64, 16, z) == -3
+    assert Lc.r4d_lru_gather(*([16, 16, 24] + [16, 16, 16] * 5), 16, 16, 64, 16, z) == -4
+    assert Lc.r4d_lru_gather(*([16, 24, 16] + [16, 16, 16] * 5), 16, 16, 64, 16, z) == -4
+    assert Lc.r4d_lru_gather(*([0, 16, 16] + [16, 16, 16] * 5), 16, 16, 64, 16, z) == -3
+    assert Lc.r9k_lru_map_ids(16, 0, 64, 16, 16, 16, 16, z) == 0
+    assert Lc.r9k_lru_map_ids(16, -1, 64, 16, 16, 16, 16, z) == -1
+    assert Lc.r9k_lru_map_ids(0, 4, 64, 16, 16, 16, 16, z) == -3
+    assert Lc.r9k_host_alloc(0) == 0 and Lc.r9k_host_free(0) == 0
     assert Lr.r9k_router_gemm(16, 64, 16, 64, 16, 64, 1, 64, 64, 1, 1, 8, 0.0, z) == -7
     # converter: K % 32
     assert L.r9k_nvfp4_to_mxfp4(16, 16, 16, 16, 16, 4, 48, z) == -2
