@@ -51,6 +51,7 @@ def parse():
     ap.add_argument("--no-router", action="store_true", help="skip the router gate GEMM timings")
     ap.add_argument("--no-cfg4", action="store_true", help="skip the config 4 converter + dense GEMM lines")
     ap.add_argument("--no-cfg5", action="store_true", help="skip the config 5 (E=384, Zipf) layer lines")
+    ap.add_argument("--no-cache", action="store_true", help="skip the host-offloaded expert cache lines")
     return ap.parse_args()
 
 
@@ -332,6 +333,77 @@ def cfg5_lines(dev, steps: int, warmup: int) -> dict:
             "sweep": out}
 
 
+def cache_lines(dev, steps: int) -> dict:
+    """Host-offloaded experts (moe/cache.py) on config 2's layer (E=288, hidden 2048, intermediate 512, top-8) with a
+    64-slot VRAM cache over the mapped host store, each from a HIP graph of the whole apply (LRU manage, gather,
+    align tables, GEMMs over the slots and, when needed, over host memory):
+      hit:   T = 1 routed to 8 resident experts every step (the cold pass is provably empty, no inserts);
+      wide:  T = 64 (~240 distinct experts > the 63-expert threshold): every non-resident expert is read through
+             from host memory inside the GEMMs (PCIe);
+      gather: r4d_lru_gather of 64 experts host -> slots alone (1.67 MB each)."""
+    from r9700_vllm.kernels import moe as K
+    from r9700_vllm.moe import cache as C
+    from r9700_vllm.moe.experts import R9700Mxfp4Experts
+    E, H, I, topk, S = 288, 2048, 512, 8, 64
+    layer = Layer(E, H, I, dev, copies=1, seed=SEED + 9000)
+    W13, W2 = layer.W13[0], layer.W2[0]
+    cache = C.LayerCache(0, C.to_host(W13.wq), C.to_host(W2.wq), W13.wsr, W2.wsr, 2 * I, H, H, I, S)
+    ex = R9700Mxfp4Experts.standalone(cache.h_s13, cache.h_s2)
+    ex.r9k_cache = cache
+    g = torch.Generator(device=dev).manual_seed(SEED + 9001)
+    out = {"slots": S, "bytes_per_expert": layer.bytes_per_expert()}
+
+    def timed(fn, n):
+        for _ in range(2):
+            fn()
+        torch.cuda.synchronize()
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr):
+            fn()
+        gr.replay()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(n):
+            gr.replay()
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / n
+
+    for name, T, ids_fn in (("hit_T1", 1, lambda: torch.arange(8, dtype=torch.int32, device=dev).view(1, 8)),
+                            ("wide_T64", 64, None)):
+        x = torch.randn(T, H, generator=g, device=dev).to(torch.bfloat16)
+        logits = torch.randn(T, E, generator=g, device=dev).to(torch.bfloat16)
+        w, ids = K.moe_topk(logits, topk, True)
+        if ids_fn is not None:
+            ids = ids_fn()
+        o = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
+        fn = lambda: ex.apply(o, x, cache.h_w13, cache.h_w2, w, ids, "silu", E, None, None, None, None, None, None,
+                              False)
+        ms = timed(fn, steps if T == 1 else max(4, steps // 10))
+        distinct = int(torch.unique(ids).numel())
+        resident = int((cache.table[ids.reshape(-1).long()] >= 0).sum())
+        cold = distinct - int((cache.table[torch.unique(ids).long()] >= 0).sum())
+        row = {"T": T, "ms_per_step": round(ms, 5), "distinct": distinct, "read_through": cold}
+        if cold:
+            row["host_GBps"] = round(cold * layer.bytes_per_expert() / (ms * 1e-3) / 1e9, 1)
+        out[name] = row
+        print(f"# cache {name}: {ms * 1e3:.1f} us/layer, {distinct} experts, {cold} read through from host, "
+              f"{resident} of {ids.numel()} rows resident", file=sys.stderr, flush=True)
+    miss = torch.stack([torch.arange(100, 164, dtype=torch.int32), torch.arange(0, 64, dtype=torch.int32)], 1)
+    cache.miss[:64].copy_(miss.to(dev))
+    cache.n_miss.fill_(64)
+    ms = timed(cache._gather, 10)
+    cache.n_miss.zero_()
+    nbytes = 64 * sum(cache.bytes)
+    out["gather_64"] = {"ms": round(ms, 4), "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1), "bytes": nbytes}
+    print(f"# cache gather of 64 experts: {ms * 1e3:.0f} us, {out['gather_64']['GBps']} GB/s host -> HBM",
+          file=sys.stderr, flush=True)
+    del ex, cache, layer
+    torch.cuda.empty_cache()
+    return out
+
+
 def router_times(dev, reps_bytes: int = 512 << 20):
     """The router gate GEMM (r9k_router_gemm via router.router_gemm, bf16 out) beside stock's F.linear, kernel time
     alone: back-to-back launches in one HIP graph cycling through enough weight copies (>= 512 MB, twice the Infinity
@@ -487,6 +559,7 @@ def main():
     router = None if args.no_router else router_times(dev)
     cfg4 = None if args.no_cfg4 else cfg4_lines(dev)
     cfg5 = None if args.no_cfg5 else cfg5_lines(dev, args.steps, args.warmup)
+    cache = None if args.no_cache else cache_lines(dev, args.steps)
     cpu = None if args.no_cpu else cpu_baseline(main_step)
     line = {
         "metric": "MoE-layer tokens/s + HBM GB/s (decode) / MXFP4 TFLOPS (prefill), 1 GPU",
@@ -514,6 +587,7 @@ def main():
         "router": router,
         "cfg4": cfg4,
         "cfg5": cfg5,
+        "expert_cache": cache,
     }
     print(json.dumps(line), flush=True)
 

@@ -163,6 +163,14 @@ int r9k_quantize_mxfp4_search(long w, long out_packed, long out_e8m0, int N, int
 int r4d_lru_manage(long ids, int mk, int E, int S, int max_distinct, int max_inserts, long table, long map_cold,
                    long slot_expert, long slot_stamp, long routed, long step, long miss, long n_miss, long stream);
 
+/* r4d_lru_manage, then in the same launch hot[i] = table[ids[i]], cold[i] = map_cold[ids[i]] (-1 for ids outside
+ * [0, E)) from the updated maps: the routing ids of the resident and the host pass (the reference derives its two
+ * align tables inside its fused manage kernel, r4d_lru.hip:305-631, bound at moe/cache.py:45-48). hot and cold
+ * int32 [mk], both given or both 0. Codes as r4d_lru_manage. */
+int r9k_lru_manage_map(long ids, int mk, int E, int S, int max_distinct, int max_inserts, long table, long map_cold,
+                       long slot_expert, long slot_stamp, long routed, long step, long miss, long n_miss, long hot,
+                       long cold, long stream);
+
 /* Copy each listed expert's six per-expert slabs host -> slot (replaces r4d_lru.hip:276-303, bound at
  * moe/cache.py:42-44): slab i of expert e at s_i + e * b_i goes to d_i + slot * b_i for the first n_miss[0]
  * (expert, slot) pairs of miss. Bytes b_i multiples of 16 (0 = unused slab), pointers 16-byte aligned. Grid

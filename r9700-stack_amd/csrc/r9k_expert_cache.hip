@@ -65,7 +65,8 @@ __device__ __forceinline__ int block_exscan(int v, int* sh, int* total) {
 __global__ void __launch_bounds__(MT_THREADS) lru_manage_kernel(
     const int* __restrict__ ids, int mk, int E, int S, int max_distinct, int max_inserts, int* __restrict__ table,
     int* __restrict__ map_cold, int* __restrict__ slot_expert, long long* __restrict__ slot_stamp,
-    uint8_t* __restrict__ routed_out, long long* __restrict__ step, int* __restrict__ miss, int* __restrict__ n_miss) {
+    uint8_t* __restrict__ routed_out, long long* __restrict__ step, int* __restrict__ miss, int* __restrict__ n_miss,
+    int* __restrict__ hot_ids, int* __restrict__ cold_ids) {
   __shared__ uint8_t s_routed[MAX_E];
   __shared__ int s_se[MAX_S];
   __shared__ long long s_st[MAX_S];
@@ -167,6 +168,16 @@ __global__ void __launch_bounds__(MT_THREADS) lru_manage_kernel(
   }
   for (int e = t; e < E; e += MT_THREADS) routed_out[e] = s_routed[e];
   if (t == 0) n_miss[0] = nact;
+  if (hot_ids) {
+    // the two passes' routing ids from the updated maps (the installs' global writes are ordered by the barrier)
+    __syncthreads();
+    for (int i = t; i < mk; i += MT_THREADS) {
+      const int e = ids[i];
+      const bool ok = e >= 0 && e < E;
+      hot_ids[i] = ok ? table[e] : -1;
+      cold_ids[i] = ok ? map_cold[e] : -1;
+    }
+  }
 }
 
 struct Slabs {
@@ -215,18 +226,27 @@ __global__ void __launch_bounds__(256) lru_map_ids_kernel(const int* __restrict_
 
 }  // namespace
 
-extern "C" int r4d_lru_manage(long ids, int mk, int E, int S, int max_distinct, int max_inserts, long table,
-                              long map_cold, long slot_expert, long slot_stamp, long routed, long step, long miss,
-                              long n_miss, long stream) {
+extern "C" int r9k_lru_manage_map(long ids, int mk, int E, int S, int max_distinct, int max_inserts, long table,
+                                  long map_cold, long slot_expert, long slot_stamp, long routed, long step, long miss,
+                                  long n_miss, long hot, long cold, long stream) {
   if (E <= 0 || E > MAX_E || S <= 0 || S > MAX_S || S > E || mk < 0) return -1;
   if (max_inserts < 0 || max_inserts > S) return -2;
   if ((mk && !ids) || !table || !map_cold || !slot_expert || !slot_stamp || !routed || !step || !miss || !n_miss)
     return -3;
   if ((slot_stamp | step) & 7) return -4;
+  if ((hot != 0) != (cold != 0)) return -3;
   hipLaunchKernelGGL(lru_manage_kernel, dim3(1), dim3(MT_THREADS), 0, (hipStream_t)stream, (const int*)ids, mk, E,
                      S, max_distinct, max_inserts, (int*)table, (int*)map_cold, (int*)slot_expert,
-                     (long long*)slot_stamp, (uint8_t*)routed, (long long*)step, (int*)miss, (int*)n_miss);
+                     (long long*)slot_stamp, (uint8_t*)routed, (long long*)step, (int*)miss, (int*)n_miss,
+                     (int*)hot, (int*)cold);
   return hipGetLastError() == hipSuccess ? 0 : -6;
+}
+
+extern "C" int r4d_lru_manage(long ids, int mk, int E, int S, int max_distinct, int max_inserts, long table,
+                              long map_cold, long slot_expert, long slot_stamp, long routed, long step, long miss,
+                              long n_miss, long stream) {
+  return r9k_lru_manage_map(ids, mk, E, S, max_distinct, max_inserts, table, map_cold, slot_expert, slot_stamp,
+                            routed, step, miss, n_miss, 0, 0, stream);
 }
 
 extern "C" int r4d_lru_gather(long d0, long s0, long b0, long d1, long s1, long b1, long d2, long s2, long b2,

@@ -50,6 +50,8 @@ def _L():
         L.r4d_lru_manage.argtypes = [l, i, i, i, i, i] + [l] * 8 + [l]
         L.r4d_lru_gather.restype = i
         L.r4d_lru_gather.argtypes = [l, l, l] * 6 + [l, l, i, i, l]
+        L.r9k_lru_manage_map.restype = i
+        L.r9k_lru_manage_map.argtypes = [l, i, i, i, i, i] + [l] * 10 + [l]
         L.r9k_lru_map_ids.restype = i
         L.r9k_lru_map_ids.argtypes = [l, i, i, l, l, l, l, l]
         L.r9k_host_alloc.restype = l
@@ -271,11 +273,14 @@ class LayerCache:
         if rc:
             raise RuntimeError(f"r4d_lru_gather failed ({rc})")
 
-    def _manage(self, ids: torch.Tensor) -> None:
-        rc = _L().r4d_lru_manage(ids.data_ptr(), ids.numel(), self.E, self.S, self.max_distinct, self.max_inserts,
-                                 self.table.data_ptr(), self.map_cold.data_ptr(), self.slot_expert.data_ptr(),
-                                 self.slot_stamp.data_ptr(), self.routed.data_ptr(), self.step.data_ptr(),
-                                 self.miss.data_ptr(), self.n_miss.data_ptr(), _stream())
+    def _manage(self, ids: torch.Tensor, hot: torch.Tensor | None = None, cold: torch.Tensor | None = None) -> None:
+        """LRU manage; with hot / cold given, the same launch also writes the two passes' mapped routing ids."""
+        rc = _L().r9k_lru_manage_map(ids.data_ptr(), ids.numel(), self.E, self.S, self.max_distinct,
+                                     self.max_inserts, self.table.data_ptr(), self.map_cold.data_ptr(),
+                                     self.slot_expert.data_ptr(), self.slot_stamp.data_ptr(), self.routed.data_ptr(),
+                                     self.step.data_ptr(), self.miss.data_ptr(), self.n_miss.data_ptr(),
+                                     hot.data_ptr() if hot is not None else 0,
+                                     cold.data_ptr() if cold is not None else 0, _stream())
         if rc:
             raise RuntimeError(f"r4d_lru_manage failed ({rc}) E={self.E} S={self.S}")
 
@@ -322,25 +327,23 @@ class LayerCache:
             self._one = o
         return (L, NB, o[2][:L], o[3][:NB], o[4], o[5][:L], o[6][:NB], o[7], o[8][:mk], o[9][:mk])
 
-    def update_fused(self, topk_ids: torch.Tensor, bs: int):
-        """LRU manage + gather, then both align outputs: the resident one over slot ids (ids through table) and the
-        host one over expert ids (through map_cold). Returns ((sorted, eids, ntpp) hot, (sorted, eids, ntpp) cold),
-        views of the layer's persistent buffers."""
+    def update_fused(self, topk_ids: torch.Tensor, bs: int, need_cold: bool = True):
+        """LRU manage (which also maps the routing ids) + gather, then both align outputs: the resident one over
+        slot ids (ids through table) and the host one over expert ids (through map_cold). Returns
+        ((sorted, eids, ntpp) hot, (sorted, eids, ntpp) cold), views of the layer's persistent buffers. need_cold =
+        False skips the host tables (their contents are then stale): for steps of at most no_cold_limit rows, whose
+        cold pass is provably empty."""
         ids = self._ids(topk_ids)
         mk = ids.numel()
         L_, NB, sh, eh, nh, sc, ec, nc, hid, cid = self._align_bufs(mk, bs)
-        self._manage(ids)
+        self._manage(ids, hid, cid)
         self._gather()
         if self.stats is not None:
             self._record()
         lib, st = _L(), _stream()
-        rc = lib.r9k_lru_map_ids(ids.data_ptr(), mk, self.E, self.table.data_ptr(), self.map_cold.data_ptr(),
-                                 hid.data_ptr(), cid.data_ptr(), st)
-        if rc:
-            raise RuntimeError(f"r9k_lru_map_ids failed ({rc})")
         n = lib.r9k_moe_align_scratch_ints(mk, self.E)
         scratch = K._align_scratch(ids.device, n)
-        for a, s_, e_, t_ in ((hid, sh, eh, nh), (cid, sc, ec, nc)):
+        for a, s_, e_, t_ in ((hid, sh, eh, nh), (cid, sc, ec, nc))[: 2 if need_cold else 1]:
             rc = lib.r9k_moe_align(a.data_ptr(), mk, self.E, bs, s_.data_ptr(), e_.data_ptr(), t_.data_ptr(),
                                    scratch.data_ptr(), scratch.numel(), st)
             if rc:

@@ -174,14 +174,15 @@ class R9700Mxfp4Experts(_experts_base()):
             if expert_map is not None or nv is not None:
                 raise RuntimeError("r9k expert cache: MXFP4 experts without an expert map only")
             (h1, h2), (c1, c2) = cache.hot(), cache.cold()
+            need_cold = numel > cache.no_cold_limit
             if cache.fused:
-                hot_al, cold_al = cache.update_fused(topk_ids, blk)
+                hot_al, cold_al = cache.update_fused(topk_ids, blk, need_cold)
             else:
                 cache.update(topk_ids)
                 hot_al = K.moe_align(topk_ids, blk, E, cache.table)
-                cold_al = K.moe_align(topk_ids, blk, E, cache.map_cold)
+                cold_al = K.moe_align(topk_ids, blk, E, cache.map_cold) if need_cold else None
             passes = [(h1, h2, hot_al)]
-            if numel > cache.no_cold_limit:
+            if need_cold:
                 passes.append((c1, c2, cold_al))
         else:
             tabs = route.take(getattr(self, "r9k_layer", None), topk_ids, blk, numel) if expert_map is None else None

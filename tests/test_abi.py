@@ -92,6 +92,8 @@ def test_shape_errors_before_launch():
     assert Lc.r4d_lru_gather(*([16, 16, 24] + [16, 16, 16] * 5), 16, 16, 64, 16, z) == -4
     assert Lc.r4d_lru_gather(*([16, 24, 16] + [16, 16, 16] * 5), 16, 16, 64, 16, z) == -4
     assert Lc.r4d_lru_gather(*([0, 16, 16] + [16, 16, 16] * 5), 16, 16, 64, 16, z) == -3
+    assert Lc.r9k_lru_manage_map(8, 4, 64, 16, 1, 4, *p8, 8, 0, z) == -3          # hot without cold
+    assert Lc.r9k_lru_manage_map(8, 4, 64, 16, 1, 17, *p8, 8, 8, z) == -2
     assert Lc.r9k_lru_map_ids(16, 0, 64, 16, 16, 16, 16, z) == 0
     assert Lc.r9k_lru_map_ids(16, -1, 64, 16, 16, 16, 16, z) == -1
     assert Lc.r9k_lru_map_ids(0, 4, 64, 16, 16, 16, 16, z) == -3

@@ -47,13 +47,19 @@ class DevState:
         self.miss = torch.full((max(1, max_ins), 2), -1, **i32)
         self.n_miss = torch.zeros((1,), **i32)
 
-    def manage(self, ids, max_distinct, max_ins):
-        rc = C._L().r4d_lru_manage(ids.data_ptr(), ids.numel(), self.E, self.S, max_distinct, max_ins,
-                                   self.table.data_ptr(), self.map_cold.data_ptr(), self.slot_expert.data_ptr(),
-                                   self.slot_stamp.data_ptr(), self.routed.data_ptr(), self.step.data_ptr(),
-                                   self.miss.data_ptr(), self.n_miss.data_ptr(),
-                                   torch.cuda.current_stream().cuda_stream)
-        assert rc == 0, rc
+    def manage(self, ids, max_distinct, max_ins, mapped=False):
+        """r4d_lru_manage, or with mapped=True r9k_lru_manage_map (returns the hot / cold routing ids)."""
+        args = (ids.data_ptr(), ids.numel(), self.E, self.S, max_distinct, max_ins, self.table.data_ptr(),
+                self.map_cold.data_ptr(), self.slot_expert.data_ptr(), self.slot_stamp.data_ptr(),
+                self.routed.data_ptr(), self.step.data_ptr(), self.miss.data_ptr(), self.n_miss.data_ptr())
+        st = torch.cuda.current_stream().cuda_stream
+        if not mapped:
+            assert C._L().r4d_lru_manage(*args, st) == 0
+            return None
+        hot = torch.full_like(ids, -9)
+        cold = torch.full_like(ids, -9)
+        assert C._L().r9k_lru_manage_map(*args, hot.data_ptr(), cold.data_ptr(), st) == 0
+        return hot, cold
 
 
 def same_state(d: DevState, st: O.LruState):
@@ -81,8 +87,13 @@ def test_lru_manage_matches_oracle(dev, E, S, thresh, max_ins, M, k, seed):
         if step % 5 == 0:
             ids = np.concatenate([ids, [-1, E, E + 3]])
         routed, misses = O.lru_manage(st, ids, max_distinct, max_ins)
-        d.manage(torch.from_numpy(ids.astype(np.int32)).to(dev), max_distinct, max_ins)
+        hc = d.manage(torch.from_numpy(ids.astype(np.int32)).to(dev), max_distinct, max_ins, mapped=step % 2 == 1)
         torch.cuda.synchronize()
+        if hc is not None:                                # the ids through the updated maps, -1 outside [0, E)
+            ok = (ids >= 0) & (ids < E)
+            safe = np.where(ok, ids, 0)
+            assert np.array_equal(hc[0].cpu().numpy(), np.where(ok, st.table[safe], -1)), step
+            assert np.array_equal(hc[1].cpu().numpy(), np.where(ok, st.map_cold[safe], -1)), step
         n = int(d.n_miss.item())
         got = [tuple(x) for x in d.miss[:n].cpu().tolist()]
         assert got == misses, (step, got, misses)
