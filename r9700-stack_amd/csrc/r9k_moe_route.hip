@@ -374,6 +374,54 @@ __device__ __forceinline__ int wave_incl_scan(int v, int lane) {
   return v + (row > 0 ? r0 : 0) + (row > 1 ? r1 : 0) + (row > 2 ? r2 : 0);
 }
 
+// The table build of the small routing kernels, after every thread t < numel holds e = the expert of flat row t
+// and the LDS layout is set up (mask zeroed, tab = numel, eids = -1): LDS mask[e] |= 1 << row, block-padded counts
+// scanned over the experts (one per thread), rows placed at offs[e] + the number of earlier rows of e, then the
+// tables written out. Every thread of the ST-thread workgroup calls it.
+__device__ __forceinline__ void small_tables(int e, int numel, int topk, int E, int blk, int cap,
+                                             unsigned long long* mask, int* offs, int* scan, int* tab, int* eids,
+                                             int* __restrict__ sorted_ids, int* __restrict__ expert_ids,
+                                             int* __restrict__ ntpp) {
+  const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
+  const int nblk = cap / blk;
+  const int trow = tid < numel ? tid / topk : 0;
+  if (tid < numel) atomicOr(&mask[e], 1ull << trow);
+  lds_barrier();
+
+  // block-padded counts, scanned over the experts (one per thread)
+  const int c = tid < E ? __popcll(mask[tid]) : 0;
+  const int n = (c + blk - 1) & ~(blk - 1);
+  const int incl = wave_incl_scan(n, lane);
+  if (lane == WAVE - 1) scan[wave] = incl;
+  lds_barrier();
+  int wbase = 0, total = 0;
+#pragma unroll
+  for (int w = 0; w < SW; w++) {
+    const int t = scan[w];
+    wbase += w < wave ? t : 0;
+    total += t;
+  }
+  if (tid < E) {
+    const int o = wbase + incl - n;
+    offs[tid] = o;
+    for (int b = o / blk; b < (o + n) / blk; b++) eids[b] = tid;
+  }
+  if (tid == 0) ntpp[0] = total;
+  lds_barrier();
+  if (tid < numel) tab[offs[e] + __popcll(mask[e] & ((1ull << trow) - 1ull))] = tid;
+  lds_barrier();
+
+  // write-out: 16-byte stores where the destination allows, the rest one int at a time
+  int done = 0;
+  if ((reinterpret_cast<uintptr_t>(sorted_ids) & 15) == 0) {
+    const int n4 = cap / 4;
+    for (int i = tid; i < n4; i += ST) reinterpret_cast<int4*>(sorted_ids)[i] = reinterpret_cast<const int4*>(tab)[i];
+    done = n4 * 4;
+  }
+  for (int i = done + tid; i < cap; i += ST) sorted_ids[i] = tab[i];
+  for (int b = tid; b < nblk; b += ST) expert_ids[b] = eids[b];
+}
+
 // Top-k of NR rows per wave, interleaved so that their reduction chains overlap (same order and numerics as
 // topk_core). The selection loop only finds keys; lane k then rebuilds its entry's exp from the key (the key holds
 // the bf16 logit) and forms p_k = e_k / sum, and the selected sum is accumulated in k order as before. Returns,
@@ -506,42 +554,7 @@ __global__ void __launch_bounds__(ST) route_small_kernel(
     lds_barrier();
     if (tid < numel) e = lids[tid];
   }
-  const int trow = tid < numel ? tid / topk : 0;
-  if (tid < numel) atomicOr(&mask[e], 1ull << trow);
-  lds_barrier();
-
-  // block-padded counts, scanned over the experts (one per thread)
-  const int c = tid < E ? __popcll(mask[tid]) : 0;
-  const int n = (c + blk - 1) & ~(blk - 1);
-  const int incl = wave_incl_scan(n, lane);
-  if (lane == WAVE - 1) scan[wave] = incl;
-  lds_barrier();
-  int wbase = 0, total = 0;
-#pragma unroll
-  for (int w = 0; w < SW; w++) {
-    const int t = scan[w];
-    wbase += w < wave ? t : 0;
-    total += t;
-  }
-  if (tid < E) {
-    const int o = wbase + incl - n;
-    offs[tid] = o;
-    for (int b = o / blk; b < (o + n) / blk; b++) eids[b] = tid;
-  }
-  if (tid == 0) ntpp[0] = total;
-  lds_barrier();
-  if (tid < numel) tab[offs[e] + __popcll(mask[e] & ((1ull << trow) - 1ull))] = tid;
-  lds_barrier();
-
-  // write-out: 16-byte stores where the destination allows, the rest one int at a time
-  int done = 0;
-  if ((reinterpret_cast<uintptr_t>(sorted_ids) & 15) == 0) {
-    const int n4 = cap / 4;
-    for (int i = tid; i < n4; i += ST) reinterpret_cast<int4*>(sorted_ids)[i] = reinterpret_cast<const int4*>(tab)[i];
-    done = n4 * 4;
-  }
-  for (int i = done + tid; i < cap; i += ST) sorted_ids[i] = tab[i];
-  for (int b = tid; b < nblk; b += ST) expert_ids[b] = eids[b];
+  small_tables(e, numel, topk, E, blk, cap, mask, offs, scan, tab, eids, sorted_ids, expert_ids, ntpp);
 }
 
 template <int EPL>

@@ -16,47 +16,14 @@
 // act_cols > 0 applies the hyper-connection epilogue (reference kernels/r9k_router.hip:34-40) to the first act_cols
 // columns: s = bf16(v) / hc, out = s / (1 + exp(-s)).
 #include "r9k_common.h"
+#include "r9k_router_tile.h"
 
 namespace {
 
 using namespace r9k;
 
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-
 constexpr int ROUTER_MAX_M = 32;
 constexpr int ROUTER_MAX_WAVES = 8;
-
-__device__ __forceinline__ float dot8(uint4 a, uint4 b, float c) {
-  c = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a.x), __builtin_bit_cast(bf16x2, b.x), c, false);
-  c = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a.y), __builtin_bit_cast(bf16x2, b.y), c, false);
-  c = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a.z), __builtin_bit_cast(bf16x2, b.z), c, false);
-  c = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a.w), __builtin_bit_cast(bf16x2, b.w), c, false);
-  return c;
-}
-
-// N values (a power of two <= 64) held by every lane -> lane l returns the wave-wide sum of value l / (64 / N).
-// Each halving step keeps one half of the values and trades the other half with the lane `o` away, so the work is
-// N - 1 exchanges plus log2(64 / N) for the lanes that still share a value.
-template <int N>
-__device__ __forceinline__ float wave_transpose_sum(float (&v)[N], int lane) {
-  static_assert(N >= 1 && N <= WAVE && (N & (N - 1)) == 0, "N: a power of two <= 64");
-  int o = WAVE / 2;
-#pragma unroll
-  for (int h = N / 2; h >= 1; h /= 2) {
-    const bool up = lane & o;
-#pragma unroll
-    for (int i = 0; i < h; i++) {
-      const float send = up ? v[i] : v[i + h];
-      const float keep = up ? v[i + h] : v[i];
-      v[i] = keep + __shfl_xor(send, o, WAVE);
-    }
-    o >>= 1;
-  }
-  float s = v[0];
-#pragma unroll
-  for (; o >= 1; o >>= 1) s += __shfl_xor(s, o, WAVE);
-  return s;
-}
 
 template <int EPT, int MT, bool BF>
 __global__ void __launch_bounds__(ROUTER_MAX_WAVES * WAVE) router_rows_kernel(const uint16_t* __restrict__ x, long sx,
@@ -65,31 +32,10 @@ __global__ void __launch_bounds__(ROUTER_MAX_WAVES * WAVE) router_rows_kernel(co
                                                                               int E, int K, int act_cols, float hc) {
   constexpr int N = EPT * MT;
   __shared__ float part[ROUTER_MAX_WAVES][N];
-  const int tid = threadIdx.x, lane = tid % WAVE, wave = tid / WAVE, nw = blockDim.x / WAVE;
+  const int tid = threadIdx.x, nw = blockDim.x / WAVE;
   const int e0 = blockIdx.x * EPT, m0 = blockIdx.y * MT;
-  const int nch = K / 8;                    // 16-byte chunks a row (K % 8 == 0)
-  float acc[N];
-#pragma unroll
-  for (int i = 0; i < N; i++) acc[i] = 0.f;
-#pragma unroll 2
-  for (int c = tid; c < nch; c += blockDim.x) {
-    uint4 wv[EPT], xv[MT];
-#pragma unroll
-    for (int i = 0; i < EPT; i++) wv[i] = reinterpret_cast<const uint4*>(w + (long)min(e0 + i, E - 1) * sw)[c];
-#pragma unroll
-    for (int m = 0; m < MT; m++) xv[m] = reinterpret_cast<const uint4*>(x + (long)min(m0 + m, M - 1) * sx)[c];
-#pragma unroll
-    for (int i = 0; i < EPT; i++)
-#pragma unroll
-      for (int m = 0; m < MT; m++) acc[i * MT + m] = dot8(wv[i], xv[m], acc[i * MT + m]);
-  }
-  const float s = wave_transpose_sum<N>(acc, lane);
-  constexpr int G = WAVE / N;               // lanes sharing one value after the transpose
-  if (lane % G == 0) part[wave][lane / G] = s;
-  __syncthreads();
+  float v = router_tile<EPT, MT>(x, sx, w, sw, M, E, K, e0, m0, nw, part);
   if (tid >= N) return;
-  float v = part[0][tid];
-  for (int q = 1; q < nw; q++) v += part[q][tid];
   const int e = e0 + tid / MT, m = m0 + tid % MT;
   if (e >= E || m >= M) return;
   if (e < act_cols) {
@@ -133,20 +79,6 @@ int router_launch(const RouterArgs& a, bool bf, int ept, int mt, int nw, hipStre
     case 204: launch_shape<2, 4>(a, bf, nw, st); return 0;
     default: return -5;
   }
-}
-
-// Launch shape, measured on the gates served (E 256-512, K 2048-7168, M 1-32): many small workgroups beat few
-// large ones (the loads in flight across the chip, not the bytes, bound the time), so a workgroup takes 1-2 experts x
-// 1-4 tokens and 1-4 waves, each lane about `cpl` chunks of K (two at a time: the chunk loop is unrolled twice).
-void router_shape(int M, int K, int* ept, int* mt, int* nw) {
-  int cpl;
-  if (M <= 2) *ept = 1, *mt = 1, cpl = 2;
-  else if (M <= 4) *ept = 1, *mt = 2, cpl = 2;
-  else if (M <= 8) *ept = 2, *mt = 2, cpl = 3;
-  else if (M <= 16) *ept = 2, *mt = 2, cpl = 6;
-  else *ept = 2, *mt = 4, cpl = 8;
-  const int nch = K / 8;
-  *nw = min(4, max(1, (nch + WAVE * cpl - 1) / (WAVE * cpl)));
 }
 
 }  // namespace
