@@ -149,6 +149,13 @@ int r9k_nvfp4_to_mxfp4(long packed, long s16, long row_div, long out_packed, lon
 /* The same MSE search on fp32 weights [N][K] (r9700_vllm/quant/nvfp4.py:54-75, quantize_mxfp4_search). */
 int r9k_quantize_mxfp4_search(long w, long out_packed, long out_e8m0, int N, int K, long stream);
 
+/* Device-side block-size choice for one routed step whose tables were built in both layouts (16 * MT-row decode
+ * blocks, big_blk-row prefill blocks): keeps the big layout when numel >= min_rows * (ntpp_big / big_blk) (the
+ * touched experts' average rows, estimated from the big layout's block count), else the small one; the other gets
+ * ntpp = 0, so the GEMMs launched over it exit at once. No reference counterpart (the reference picks on the host
+ * from the row count, r9700_vllm/kernels/moe.py:532-535). 0, -1 bad arguments, -6 launch error. */
+int r9k_moe_pick_blocks(long ntpp_small, long ntpp_big, int numel, int big_blk, int min_rows, long stream);
+
 /* ---- Host-offloaded experts: device LRU cache (reference r9700_vllm/moe/cache.py:1-20, 182-395) ---- */
 
 /* One manage step (replaces kernels/third_party/davetha/r4d_lru.hip:187-274, bound at moe/cache.py:39-41):

@@ -557,6 +557,19 @@ __global__ void __launch_bounds__(ST) route_small_kernel(
   small_tables(e, numel, topk, E, blk, cap, mask, offs, scan, tab, eids, sorted_ids, expert_ids, ntpp);
 }
 
+// Device-side choice between the two table layouts of one routed step, built side by side: 16 * MT-row decode
+// blocks (ntpp_small) and big_blk-row prefill blocks (ntpp_big). The big layout's block count estimates the touched
+// experts (one block each up to big_blk rows); min_rows or more routed rows per such block keeps the big layout,
+// else the small one. The layout not kept gets ntpp = 0, so every GEMM launched over it exits at once.
+__global__ void __launch_bounds__(64) pick_blocks_kernel(int* __restrict__ ntpp_small, int* __restrict__ ntpp_big,
+                                                         int numel, int big_blk, int min_rows) {
+  if (threadIdx.x) return;
+  const int nbig = ntpp_big[0] / big_blk;
+  const bool big = nbig > 0 && (long)numel >= (long)min_rows * nbig;
+  if (big) ntpp_small[0] = 0;
+  else ntpp_big[0] = 0;
+}
+
 template <int EPL>
 __global__ void __launch_bounds__(RW * WAVE) topk_kernel(const uint16_t* __restrict__ logits, int ldl,
                                                          float* __restrict__ weights, int* __restrict__ ids, int M,
@@ -961,4 +974,14 @@ extern "C" int r9k_moe_align(long ids, int numel, int E, int blk, long sorted_id
                    (hipStream_t)stream))
     return 1;
   return (int)hipGetLastError();
+}
+
+// Keep one of two table layouts of a routed step on the device (pick_blocks_kernel): no reference counterpart (the
+// reference picks its block size on the host from the row count). 0, -1 bad arguments, -6 launch error.
+extern "C" int r9k_moe_pick_blocks(long ntpp_small, long ntpp_big, int numel, int big_blk, int min_rows,
+                                   long stream) {
+  if (!ntpp_small || !ntpp_big || numel < 0 || big_blk <= 0 || min_rows < 0) return -1;
+  hipLaunchKernelGGL(pick_blocks_kernel, dim3(1), dim3(64), 0, (hipStream_t)stream, (int*)ntpp_small,
+                     (int*)ntpp_big, numel, big_blk, min_rows);
+  return hipGetLastError() == hipSuccess ? 0 : -6;
 }

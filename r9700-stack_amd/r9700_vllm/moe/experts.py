@@ -181,9 +181,9 @@ class R9700Mxfp4Experts(_experts_base()):
                 cache.update(topk_ids)
                 hot_al = K.moe_align(topk_ids, blk, E, cache.table)
                 cold_al = K.moe_align(topk_ids, blk, E, cache.map_cold) if need_cold else None
-            passes = [(h1, h2, hot_al)]
+            passes = [(h1, h2, hot_al, (MT, pf_gate, pf_down))]
             if need_cold:
-                passes.append((c1, c2, cold_al))
+                passes.append((c1, c2, cold_al, (MT, pf_gate, pf_down)))
         else:
             tabs = route.take(getattr(self, "r9k_layer", None), topk_ids, blk, numel) if expert_map is None else None
             if tabs is None:
@@ -194,7 +194,14 @@ class R9700Mxfp4Experts(_experts_base()):
             else:
                 W1 = K.Mxfp4Experts(w1, self.w1_scale, N1, K1)
                 W2 = K.Mxfp4Experts(w2, self.w2_scale, N2, K2)
-            passes = [(W1, W2, tabs)]
+            passes = [(W1, W2, tabs, (MT, pf_gate, pf_down))]
+            bc = K.big_block_cfg(K1, K2)
+            if (big is None and nv is None and expert_map is None and not MOE_FUSE and bc is not None
+                    and K.DEVICE_BLOCKS_MIN > 0 and numel >= K.DEVICE_BLOCKS_MIN):
+                # skew the host cannot see: the 256-row layout too, the device keeps one (the other's GEMMs exit)
+                tabs_big = K.moe_align(topk_ids, bc[1], E)
+                K.pick_blocks(tabs[2], tabs_big[2], numel, bc[1])
+                passes.append((W1, W2, tabs_big, (1, bc[0], bc[0])))
 
         # the router's fp8 quant of this input, when it made one (with its tables at decode, alone at prefill)
         q = route.take_quant(getattr(self, "r9k_layer", None), topk_ids, hidden_states) if expert_map is None else None
@@ -202,14 +209,14 @@ class R9700Mxfp4Experts(_experts_base()):
         fused = MOE_FUSE and nv is None and MT == 1 and pf_gate is None and pf_down is None
         if fused:
             aq = torch.empty((numel, N1 // 2), dtype=torch.float32, device=dev)
-            for W1, _, (sid, eid, ntpp) in passes:
+            for W1, _, (sid, eid, ntpp), _ in passes:
                 K.moe_gemm(xq, xs, W1, aq, sid, eid, ntpp, numel, topk, None, num_experts=E, MT=1, fuse=1)
             as_ = None
         else:
             gate_up = torch.empty((numel, N1), dtype=torch.bfloat16, device=dev)
-            for W1, _, (sid, eid, ntpp) in passes:
-                K.moe_gemm(xq, xs, W1, gate_up, sid, eid, ntpp, numel, topk, None, num_experts=E, MT=MT,
-                           prefill=pf_gate)
+            for W1, _, (sid, eid, ntpp), (mt, pfg, _) in passes:
+                K.moe_gemm(xq, xs, W1, gate_up, sid, eid, ntpp, numel, topk, None, num_experts=E, MT=mt,
+                           prefill=pfg)
             aq, as_ = K.silu_mul_quant_fp8(gate_up)
         # Rows no table places (experts on other ranks under an expert map) must not feed moe_sum garbage.
         if expert_map is not None or ZERO_DOWN:
@@ -217,8 +224,8 @@ class R9700Mxfp4Experts(_experts_base()):
         else:
             down = torch.empty((numel, N2), dtype=torch.bfloat16, device=dev)
         tw = topk_weights.reshape(-1).to(torch.float32).contiguous()
-        for _, W2, (sid, eid, ntpp) in passes:
-            K.moe_gemm(aq, as_, W2, down, sid, eid, ntpp, numel, 1, tw, num_experts=E, MT=MT, prefill=pf_down,
+        for _, W2, (sid, eid, ntpp), (mt, _, pfd) in passes:
+            K.moe_gemm(aq, as_, W2, down, sid, eid, ntpp, numel, 1, tw, num_experts=E, MT=mt, prefill=pfd,
                        fuse=2 if fused else 0)
         K.moe_sum(down.view(M, topk, N2), None, output)
         return output

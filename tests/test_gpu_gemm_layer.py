@@ -261,6 +261,46 @@ def test_layer_config2_decode_fused(dev, monkeypatch):
         run_layer(dev, 288, 2048, 512, T, 8, seed=20261201 + 2000 + T)
 
 
+@pytest.mark.parametrize("zipf", [True, False])
+def test_device_block_choice(dev, monkeypatch, zipf):
+    """From R9K_MOE_DEVICE_BLOCKS_MIN routed rows a step the host would put on decode blocks gets its tables in both
+    layouts and r9k_moe_pick_blocks keeps one on the device: 256-row blocks when numel >= DEVICE_MIN_ROWS x the
+    256-row layout's block count (skewed routing), else the decode blocks. The output equals, bit for bit, the same layer run on that
+    layout alone (forced from the host)."""
+    E, H, I, T, topk = 128, 512, 256, 256, 8
+    print(f"device block choice zipf={zipf}", flush=True)
+    (_, _), (_, _), W13, W2 = make_layer(dev, E, H, I, 20261201 + 8000 + zipf)
+    g = torch.Generator().manual_seed(8001 + zipf)
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16).to(dev)
+    logits = torch.randn(T, E, generator=g)
+    if zipf:
+        logits += -2.5 * torch.log(torch.arange(1, E + 1).float())
+    logits = logits.to(torch.bfloat16).to(dev)
+    w, ids = K.moe_topk(logits, topk, True)
+    counts = torch.bincount(ids.reshape(-1).long().cpu(), minlength=E)
+    nbig = int(((counts + 255) // 256).sum())
+    want_big = T * topk >= K.DEVICE_MIN_ROWS * nbig
+    assert want_big == zipf, (nbig, int((counts > 0).sum()))
+    ex = R9700Mxfp4Experts.standalone(W13.wsr, W2.wsr)
+
+    def run():
+        o = torch.full((T, H), float("nan"), dtype=torch.bfloat16, device=dev)
+        ex.apply(o, x, W13.wq, W2.wq, w, ids, "silu", E, None, None, None, None, None, None, False)
+        torch.cuda.synchronize()
+        return o
+
+    dual = run()
+    monkeypatch.setattr(K, "DEVICE_BLOCKS_MIN", 0)
+    small = run()
+    monkeypatch.setattr(K, "PREFILL_MOE_ROWS", 1)              # the host picks the 256-row blocks
+    big = run()
+    ref = big if want_big else small
+    same = torch.equal(dual.view(torch.int16), ref.view(torch.int16))
+    print(f"  touched {int((counts > 0).sum())}, 256-row blocks {nbig}: kept {'big' if want_big else 'small'}, "
+          f"bit-equal {same}", flush=True)
+    assert same
+
+
 def test_fused_entry_rejects_bad_args(dev):
     L = K.lib()
     # fuse values other than 1 / 2 -> -8; multi-tile routing blocks -> -7 (checked before any launch)
