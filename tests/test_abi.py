@@ -73,6 +73,10 @@ def test_shape_errors_before_launch():
     assert Lr.r9k_router_gemm(16, 64, 16, 64, 16, 64, 1, 64, 72, 2, 1, 0, 1.0, z) == -3
     assert Lr.r9k_router_gemm(16, 60, 16, 64, 16, 64, 1, 64, 64, 1, 1, 0, 1.0, z) == -4
     assert Lr.r9k_router_gemm(24, 64, 16, 64, 16, 64, 1, 64, 64, 1, 1, 0, 1.0, z) == -4
+    # device block choice: null table counts, negative sizes (before any launch)
+    assert L.r9k_moe_pick_blocks(0, 16, 64, 256, 22, z) == -1
+    assert L.r9k_moe_pick_blocks(16, 16, 64, 0, 22, z) == -1
+    assert L.r9k_moe_pick_blocks(16, 16, -1, 256, 22, z) == -1
     # expert cache: E / S / mk, the insert cap, pointers, int64 alignment; gather grid, slab sizes and alignment;
     # map ids with nothing to do; host allocation of nothing (all return before a HIP call)
     from r9700_vllm.moe import cache as C
