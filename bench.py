@@ -138,8 +138,13 @@ class Step:
         return self.out
 
 
-def graph_time(step: Step, steps: int, warmup: int):
-    """ms per step over `steps` steps replayed from a HIP graph that cycles the weight copies."""
+def graph_time(step: Step, steps: int, warmup: int, windows: int = 1, min_warm_ms: float = 40.0):
+    """ms per step from a HIP graph that cycles the weight copies (one replay = `copies` steps).
+
+    Warm-up: `warmup` eager steps, then graph replays until at least max(warmup steps, min_warm_ms of replays) have
+    run, so every point starts from steady state (clocks, caches, allocator) whatever --warmup says. windows == 1 (the
+    headline): exactly `steps` steps (a multiple of the copy count) in one timed window. windows > 1 (side lines):
+    the median of `windows` windows of `steps` steps each. Returns (ms per step, steps in one window)."""
     copies = len(step.layer.W13)
     for i in range(max(2, warmup)):
         step(i % copies)
@@ -150,22 +155,33 @@ def graph_time(step: Step, steps: int, warmup: int):
     with torch.cuda.graph(g):
         for c in range(copies):
             step(c)
-    for _ in range(max(1, warmup // copies)):
-        g.replay()
+    g.replay()
     torch.cuda.synchronize()
     if not torch.equal(step.out, ref):
         raise RuntimeError("graph replay output differs from the eager step")
+    t_w = time.perf_counter()
+    n_w = 1
+    while n_w * copies < warmup or (time.perf_counter() - t_w) * 1e3 < min_warm_ms:
+        g.replay()
+        n_w += 1
+        if n_w % 8 == 0:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
     reps = max(1, steps // copies)
     t0 = torch.cuda.Event(enable_timing=True)
     t1 = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t0.record()
-    for _ in range(reps):
-        g.replay()
-    t1.record()
-    torch.cuda.synchronize()
-    ms = t0.elapsed_time(t1) / (reps * copies)
-    return ms, reps * copies
+    times = []
+    for _ in range(windows):
+        torch.cuda.synchronize()
+        t0.record()
+        for _ in range(reps):
+            g.replay()
+        t1.record()
+        torch.cuda.synchronize()
+        times.append(t0.elapsed_time(t1) / (reps * copies))
+    if not torch.equal(step.out, ref):
+        raise RuntimeError("graph replay output differs from the eager step")
+    return float(np.median(times)), reps * copies
 
 
 def gate_up_kernel_time(step: Step, reps: int = 40):
@@ -315,7 +331,7 @@ def cfg5_lines(dev, steps: int, warmup: int) -> dict:
     out = {}
     for T in (1, 32, 256, 4096):
         st = Step(layer, T, 8, dev, SEED + 5000 + T, zipf=True)
-        ms, n = graph_time(st, steps if T < 4096 else max(8, steps // 10), warmup)
+        ms, n = graph_time(st, max(40, steps) if T < 4096 else 8, warmup, windows=5)
         nbytes, touched = layer_bytes(st)
         counts = torch.bincount(st.ids.reshape(-1).long(), minlength=layer.E).float()
         flops = 6 * T * 8 * layer.H * layer.I
@@ -482,6 +498,18 @@ def layer_bytes(step: Step) -> tuple[int, int]:
     return touched * L.bytes_per_expert() + T * L.H * 2 + T * L.E * 2 + T * L.H * 2, touched
 
 
+def cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo), or "unknown"."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(step: Step, budget_s: float = 10.0) -> dict:
     """The oracle's CPU layer (route, quant, per-expert dequant + fp32 matmul, SiLU quant, down, sum) on this host's
     cores, on the first tokens of the same workload; tokens/s."""
@@ -504,7 +532,8 @@ def cpu_baseline(step: Step, budget_s: float = 10.0) -> dict:
         el = time.perf_counter() - t0
         if el > budget_s or n >= 30:
             break
-    return {"value": round(n * T / el, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
+    return {"value": round(n * T / el, 3), "unit": "tokens/s", "cores": threads, "cpu_model": cpu_model(),
+            "kind": "port",
             "sample": f"{n} full layer forward(s) of the T={T} workload (E={L.E}, H={L.H}, I={L.I}, top-{step.topk}),"
                       f" oracle dequant-then-matmul in fp32 on {threads} host threads, {el:.1f} s"}
 
@@ -530,7 +559,9 @@ def main():
     main_step = None
     for T in (1, 8, 16, 64):
         st = Step(layer, T, topk, dev, SEED + 2000 + T)
-        ms, n = graph_time(st, args.steps, args.warmup)
+        # the headline point (T = 64) is exactly --steps steps in one window; the others a median of 5 windows
+        ms, n = (graph_time(st, args.steps, args.warmup) if T == 64
+                 else graph_time(st, max(40, args.steps), args.warmup, windows=5))
         nbytes, touched = layer_bytes(st)
         sweep[str(T)] = {"ms_per_step": round(ms, 5), "tokens_per_s": round(T / (ms * 1e-3), 1),
                          "experts_touched": touched, "layer_GBps": round(nbytes / (ms * 1e-3) / 1e9, 1),
@@ -548,7 +579,7 @@ def main():
     prefill = None
     if not args.no_prefill:
         pl = Step(layer, 8192, topk, dev, SEED + 3000 + 8192)
-        ms, n = graph_time(pl, max(8, args.steps // 10), max(4, args.warmup // 4))
+        ms, n = graph_time(pl, 8, max(4, args.warmup // 4), windows=5)
         flops = 6 * 8192 * topk * layer.H * layer.I
         tf = flops / (ms * 1e-3) / 1e12
         prefill = {"workload": "cfg3 prefill T=8192", "ms_per_step": round(ms, 4), "tokens_per_s": round(8192 / (ms * 1e-3)),
@@ -579,8 +610,13 @@ def main():
                    "weight_copies_rotated": COPIES},
         "roofline": {"bound": "hbm", "kernel": "r9k_moe_mxfp4a8 gate_up (T=64)", "achieved": round(k_gbs, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(k_gbs / HBM_PEAK_GBS, 4),
-                     "traffic": measured_traffic(), "kernel_us": round(k_ms * 1e3, 2),
-                     "bytes_per_launch": k_bytes},
+                     "traffic": measured_traffic(),
+                     "traffic_source": "not measured in this run: the committed PMC summary "
+                                       "profiles/moe_gate_up_t64_pmc_traffic.md (rocprofv3 --pmc FETCH_SIZE, then "
+                                       "WRITE_SIZE, scaled by this script's 256 MiB calibration copy)",
+                     "kernel_us": round(k_ms * 1e3, 2), "bytes_per_launch": k_bytes,
+                     "layer": {"what": "whole T=64 layer (all launches), algorithmic bytes / ms_per_step",
+                               "achieved": sweep["64"]["layer_GBps"], "frac": sweep["64"]["hbm_frac"]}},
         "cpu_baseline": cpu,
         "decode_sweep": sweep,
         "prefill": prefill,

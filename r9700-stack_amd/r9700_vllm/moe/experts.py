@@ -31,6 +31,24 @@ ZERO_DOWN = os.environ.get("R9K_MOE_ZERO_DOWN", "0") == "1"
 MOE_FUSE = os.environ.get("R9K_MOE_FUSE", "0") == "1"
 
 
+# A launch of the 256-row prefill GEMM addresses its activations, one expert's codes and its output through 32-bit
+# buffer ranges, so no buffer one launch touches may reach 2 GiB. A step whose routed rows would cross that runs as
+# token chunks (each a complete layer step over its own tables), planned by chunk_tokens.
+BUF_LIMIT = (1 << 31) - 1
+
+
+def chunk_tokens(M: int, topk: int, N1: int, K1: int, N2: int, K2: int, limit: int = BUF_LIMIT) -> list:
+    """Token ranges [(t0, t1), ...] covering 0..M, as few and as even as possible, such that in each range every
+    per-step buffer stays <= `limit` bytes: the gate_up output [rows*topk, N1] and the down output [rows*topk, N2]
+    (bf16), the fp8 activations of both GEMMs ([rows, K1] and [rows*topk, K2]) and the fp32 row scales."""
+    per_token = max(topk * N1 * 2, topk * N2 * 2, K1, topk * K2, topk * 4)
+    n = -(-M // max(1, limit // per_token))
+    if n == 0:
+        return []
+    bounds = [M * i // n for i in range(n + 1)]
+    return list(zip(bounds[:-1], bounds[1:]))
+
+
 def r9k_available() -> bool:
     """ROCm torch with a gfx950 device and the kernel library loadable."""
     try:
@@ -155,6 +173,14 @@ class R9700Mxfp4Experts(_experts_base()):
         dev = hidden_states.device
         if M == 0:
             return
+
+        chunks = chunk_tokens(M, topk, N1, K1, N2, K2)
+        if len(chunks) > 1:
+            for t0, t1 in chunks:
+                self.apply(output[t0:t1], hidden_states[t0:t1], w1, w2, topk_weights[t0:t1], topk_ids[t0:t1],
+                           activation, global_num_experts, expert_map, a1q_scale, a2_scale, workspace13, workspace2,
+                           expert_tokens_meta, apply_router_weight_on_input)
+            return output
 
         nv = self.nv
         MT = K.pick_mt(numel, global_num_experts)

@@ -334,3 +334,99 @@ def test_shared_expert(dev, M):
     r, c = rel_err(a, b), cosine(a, b)
     print(f"shared expert M={M}: rel {r:.2e} cos {c:.7f}", flush=True)
     assert r <= 1e-2 and c >= 0.9999
+
+
+def test_layer_config5_T256_router_handoff(dev, monkeypatch):
+    """BASELINE config 5 at T = 256 (E=384, hidden 4096, intermediate 2048, Zipf(1.1) logits) through the default
+    apply() with the router's hand-off: the tables come from route.moe_route on the router's own persistent buffers
+    (route.Tables on the layer, as R9kTopKRouter leaves them), so the device-side block choice runs on them (the
+    256-row layout built beside them, r9k_moe_pick_blocks keeping one). Checked against the oracle on 32 sampled
+    tokens, and bit for bit against the layout the host-side counts say must be kept, run alone."""
+    from r9700_vllm.moe import route
+    E, H, I, T, topk = 384, 4096, 2048, 256, 8
+    seed = 20261201 + 5000 + T
+    (p13, e13), (p2, e2), W13, W2 = make_layer(dev, E, H, I, seed, 116, 126)
+    g = torch.Generator().manual_seed(seed + 1)
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    rank = torch.randperm(E, generator=g).float() + 1
+    logits = (torch.randn(T, E, generator=g) - 1.1 * torch.log(rank)[None, :]).to(torch.bfloat16)
+    xd, ld = x.to(dev), logits.to(dev)
+    numel = T * topk
+    blk = K.MOE_BLOCK * K.pick_mt(numel, E)
+    assert numel >= K.DEVICE_BLOCKS_MIN and K.pick_moe_prefill_block(numel, E, H, I) is None
+    cap = route.capacity(numel, E, blk)
+    sid = torch.empty(cap, dtype=torch.int32, device=dev)
+    eid = torch.empty(cap // blk, dtype=torch.int32, device=dev)
+    ntpp = torch.zeros(1, dtype=torch.int32, device=dev)
+    scratch = torch.zeros(route.scratch_ints(E), dtype=torch.int32, device=dev)
+    w, ids = route.moe_route(ld, topk, True, blk, sid, eid, ntpp, scratch)
+
+    class Routed:
+        _r9k_tables = route.Tables(ids, sid, eid, ntpp, blk, numel)
+
+    ex = R9700Mxfp4Experts.standalone(W13.wsr, W2.wsr)
+    ex.r9k_layer = Routed()
+    assert route.take(ex.r9k_layer, ids, blk, numel) is not None, "the hand-off must be taken"
+
+    def run(e):
+        o = torch.full((T, H), float("nan"), dtype=torch.bfloat16, device=dev)
+        e.apply(o, xd, W13.wq, W2.wq, w, ids, "silu", E, None, None, None, None, None, None, False)
+        torch.cuda.synchronize()
+        return o
+
+    out = run(ex)
+    counts = torch.bincount(ids.reshape(-1).long().cpu(), minlength=E)
+    nbig = int(((counts + 255) // 256).sum())
+    want_big = numel >= K.DEVICE_MIN_ROWS * nbig
+    plain = R9700Mxfp4Experts.standalone(W13.wsr, W2.wsr)
+    if want_big:
+        monkeypatch.setattr(K, "PREFILL_MOE_ROWS", 1)
+    else:
+        monkeypatch.setattr(K, "DEVICE_BLOCKS_MIN", 0)
+    alone = run(plain)
+    same = torch.equal(out.view(torch.int16), alone.view(torch.int16))
+    print(f"cfg5 T=256 hand-off: touched {int((counts > 0).sum())}, 256-row blocks {nbig}, kept "
+          f"{'256-row' if want_big else '16-row'} layout, bit-equal to it alone: {same}", flush=True)
+    assert same
+    tokens = np.sort(np.random.default_rng(256).choice(T, 32, replace=False))
+    ro = O.route(logits, topk, True)
+    assert np.array_equal(ids.cpu().numpy(), ro[1]), "routing ids"
+    need = np.unique(ro[1][tokens])
+    sub = lambda p: {int(e): p[int(e)].cpu() for e in need}
+    ref = O.moe_layer(x, logits, (_Lazy(sub(p13)), _Lazy(sub(e13))), (_Lazy(sub(p2)), _Lazy(sub(e2))), topk, True,
+                      tokens=tokens, route_out=ro)
+    a, b = bf16_bits_to_f64(O.bf16_bits(out)[ref["tokens"]]), bf16_bits_to_f64(ref["out"])
+    r, c = rel_err(a, b), cosine(a, b)
+    print(f"  vs oracle on {len(tokens)} tokens: rel {r:.2e} cos {c:.7f}", flush=True)
+    assert r < 1e-2 and c >= 0.9999
+
+
+@pytest.mark.parametrize("M", [4, 16])
+def test_dense_mxfp4_linear_config4_decode_full(dev, M):
+    """BASELINE config 4 decode widths on the full [17408, 5120] weight through ops.mxfp4_linear."""
+    N, Kd = 17408, 5120
+    g = torch.Generator().manual_seed(20261201 + 4000 + M)
+    packed, e8 = make_experts(1, N, Kd, g)
+    W = K.prepare_mxfp4_weights(packed.to(dev), e8.to(dev))
+    x = torch.randn(M, Kd, generator=g).to(torch.bfloat16)
+    out = ops.mxfp4_linear(x.to(dev), W.wq, W.wsr, N, Kd)
+    qo, so = O.quant_rows_fp8(x)
+    ref = O.grouped_gemm(qo, so, {0: O.mxfp4_dequant(packed[0], e8[0], torch.float32)}, np.zeros(M, dtype=np.int32),
+                         1, acc_dtype=torch.float32)
+    got = O.bf16_bits(out)
+    a, b = bf16_bits_to_f64(got), bf16_bits_to_f64(ref)
+    r, c = rel_err(a, b), cosine(a, b)
+    print(f"dense cfg4 M={M}: rel {r:.2e} cos {c:.7f} exact {(got == ref).mean():.4f}", flush=True)
+    assert r < 2e-3 and c > 0.99999
+
+
+def test_layer_past_the_buffer_limit_chunks(dev):
+    """A routed step whose gate_up output would reach 2 GiB (E=8, hidden 256, intermediate 2048, T = 32768, top-8:
+    262144 routed rows x 4096 bf16 columns = 2^31 bytes), which one launch of the 256-row prefill GEMM cannot
+    address: apply() runs it as token chunks and the output matches the oracle on sampled tokens."""
+    from r9700_vllm.moe.experts import chunk_tokens
+    E, H, I, T, topk = 8, 256, 2048, 32768, 8
+    assert len(chunk_tokens(T, topk, 2 * I, H, H, I)) == 2
+    tokens = np.unique(np.concatenate([[0, T // 2 - 1, T // 2, T - 1],       # both chunks' ends
+                                       np.random.default_rng(7).choice(T, 24, replace=False)]))
+    run_layer(dev, E, H, I, T, topk, seed=20261201 + 32768, tokens=tokens)

@@ -107,3 +107,29 @@ def test_nvfp4_layout_places_checkpoint_bytes():
                         gi = kt * 8 + 2 * gg + h
                         want = int(s8[e, n, gi]) if gi < Kd // 16 else 0
                         assert int(ws[e, n // 16, kt, lane, h]) == want, (e, n, kt, gg, h)
+
+
+@pytest.mark.parametrize("M,topk,N1,K1,N2,K2", [(1, 8, 1024, 2048, 2048, 512), (8192, 8, 1024, 2048, 2048, 512),
+                                                 (32768, 8, 4096, 4096, 4096, 2048), (65536, 8, 4096, 4096, 4096, 2048),
+                                                 (40000, 16, 8192, 7168, 7168, 4096), (32768, 8, 4096, 256, 256, 2048),
+                                                 (3, 1, 1 << 30, 64, 64, 1 << 29), (0, 8, 1024, 2048, 2048, 512)])
+def test_chunk_tokens_plan(M, topk, N1, K1, N2, K2):
+    """The token chunks of a routed step cover 0..M once, in order, as evenly as possible, with every per-step buffer
+    of each chunk within the 32-bit buffer range the 256-row prefill GEMM addresses (< 2 GiB), and as few chunks
+    as that allows."""
+    from r9700_vllm.moe.experts import BUF_LIMIT, chunk_tokens
+    ch = chunk_tokens(M, topk, N1, K1, N2, K2)
+    if M == 0:
+        assert ch == []
+        return
+    assert ch[0][0] == 0 and ch[-1][1] == M and all(a[1] == b[0] for a, b in zip(ch, ch[1:]))
+    sizes = [t1 - t0 for t0, t1 in ch]
+    assert max(sizes) - min(sizes) <= 1 and min(sizes) >= 1
+    for t0, t1 in ch:
+        rows = t1 - t0
+        bufs = [rows * topk * N1 * 2, rows * topk * N2 * 2, rows * K1, rows * topk * K2, rows * topk * 4]
+        assert max(bufs) <= BUF_LIMIT or rows == 1
+    per_token = max(topk * N1 * 2, topk * N2 * 2, K1, topk * K2, topk * 4)
+    assert len(ch) == -(-M // max(1, BUF_LIMIT // per_token))
+    if M * per_token <= BUF_LIMIT:
+        assert ch == [(0, M)]

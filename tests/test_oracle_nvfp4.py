@@ -155,3 +155,46 @@ def test_config4_scale_generator_roundtrip():
     pm, em = O.nvfp4_to_mxfp4(p16, s16, div)
     pt, et = torch_search(torch.from_numpy(O.dequant_nvfp4(p16, s16, div)))
     assert np.array_equal(pm, pt) and np.array_equal(em, et)
+
+
+def _mismatches(w: torch.Tensor) -> tuple[int, int]:
+    pm, em = O.quantize_mxfp4_search(w.numpy())
+    pt, et = torch_search(w)
+    N = w.shape[0]
+    bad = (em != et) | (pm.reshape(N, -1, 16) != pt.reshape(N, -1, 16)).any(-1)
+    return int(bad.sum()), bad.size
+
+
+def test_search_matches_torch_restatement_on_arbitrary_fp32():
+    """quantize_mxfp4_search (exact exponent rule, fp64 error sums) against the fp32 torch restatement
+    (torch.log2, exp2, bucketize, fp32 sums: the reference's operations) on weights that are NOT NVFP4-derived:
+      * wide-range random blocks (per-row magnitudes spread over ~6 binades);
+      * block maxima 1..8 ulp above 6 * 2^k for k in [-100, 98], where fp32 ceil(log2(amax / 6)) can land one
+        below the exact exponent -- the result still agrees, because both candidate pairs contain e = k and the
+        coarser exponent never wins for a block whose maximum sits on 6 * 2^k;
+      * the 2048 blocks (of 200K) whose two candidate errors are closest, exact ties included (ties keep e0 in both).
+    The mismatch count is 0 on every set."""
+    g = torch.Generator().manual_seed(11)
+    wide = torch.randn(256, 2048, generator=g) * torch.exp(torch.randn(256, 1, generator=g) * 2)
+    rng = np.random.default_rng(0)
+    rows = []
+    for k in range(-100, 100, 3):
+        for d in range(1, 9):
+            b = rng.standard_normal(32).astype(np.float32)
+            b = (b / np.abs(b).max() * np.float32(3.0) * np.float32(2.0 ** k)).astype(np.float32)
+            b[d] = np.float32(6.0 * 2.0 ** k) * np.float32(1 + d * 2.0 ** -23)
+            rows.append(b)
+    edge = torch.from_numpy(np.stack(rows[: len(rows) // 8 * 8]).reshape(-1, 256).copy())
+    x = torch.randn(200000, 32, generator=g)
+    e0 = torch.ceil(torch.log2(x.abs().amax(-1, keepdim=True) / 6))
+    errs = []
+    for d in (0, -1):
+        s = torch.exp2(e0 + d)
+        v = E2M1_T[torch.bucketize((x / s).abs(), MID_T)].double() * torch.sign(x).double() * s.double()
+        errs.append(((v - x.double()) ** 2).sum(-1))
+    near = x[torch.argsort(((errs[0] - errs[1]).abs() / errs[0]))[:2048]].reshape(-1, 256).contiguous()
+    assert float(((errs[0] - errs[1]).abs() / errs[0]).min()) == 0.0      # the set really holds exact ties
+    for name, w in (("wide-range", wide), ("log2 edge", edge), ("near-tie", near)):
+        bad, n = _mismatches(w)
+        print(f"{name}: {bad} of {n} blocks differ from the fp32 torch restatement", flush=True)
+        assert bad == 0, name
