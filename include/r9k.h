@@ -141,6 +141,17 @@ int r9k_moe_align(long ids, int numel, int E, int blk, long sorted_ids, long exp
                   long scratch_ints, long stream);
 long r9k_moe_align_scratch_ints(int numel, int E);
 
+/* No counterpart in the reference. r9k_moe_align for callers that cannot allocate (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc): no scratch argument, nothing allocated; the multi-workgroup
+ * path uses the library's own file-scope device array (r9k_moe_align_noalloc_max_ints() int32 = 1 MiB per GPU, held
+ * until the process ends; its arrival counter starts zero and every call leaves it zero). Every call on one GPU
+ * shares that array: calls that overlap on one GPU race. Tables bit-identical to r9k_moe_align's. 0; 1 bad arguments
+ * or HIP error; -9 the step needs more than r9k_moe_align_noalloc_max_ints() scratch ints (see
+ * r9k_moe_align_scratch_ints); -6 the array's device address could not be obtained. */
+int r9k_moe_align_noalloc(long ids, int numel, int E, int blk, long sorted_ids, long expert_ids, long ntpp,
+                          long stream);
+long r9k_moe_align_noalloc_max_ints(void);
+
 /* Load-time NVFP4 -> MXFP4 with MSE-searched block exponents (the reference does this with torch:
  * r9700_vllm/quant/nvfp4.py:39-90). packed u8 [N][K/2], s16 e4m3 [N][K/16], row_div fp32 [N] -> out_packed u8
  * [N][K/2], out_e8m0 u8 [N][K/32] (checkpoint layout). -2 K % 32, -3 bad pointer / alignment, -6 launch error. */

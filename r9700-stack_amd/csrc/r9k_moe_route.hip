@@ -35,6 +35,8 @@
 //                        per-chunk histogram launch plus a scatter launch (bases from the histograms), caller scratch.
 #include "r9k_common.h"
 
+#include <mutex>
+
 namespace {
 
 using namespace r9k;
@@ -971,6 +973,60 @@ extern "C" int r9k_moe_align(long ids, int numel, int E, int blk, long sorted_id
   if (numel < 1 || E < 1 || E > MAX_E || blk < 1 || (blk & (blk - 1))) return 1;
   if (numel > SMALL_MAX && (!scratch || scratch_ints < r9k_moe_align_scratch_ints(numel, E))) return 1;
   if (launch_align((const int*)ids, numel, E, blk, (int*)sorted_ids, (int*)expert_ids, (int*)ntpp, (int*)scratch,
+                   (hipStream_t)stream))
+    return 1;
+  return (int)hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------------- align without allocation
+// r9k_moe_align's multi-workgroup path needs scratch (the histograms' arrival counter and the per-chunk histograms /
+// bases). Callers that cannot allocate (code under HIP graph capture, tight serving loops, harnesses that forbid
+// hipMalloc) use r9k_moe_align_noalloc, whose scratch is this file-scope device array: 1 MiB per GPU, held by every
+// GPU the library runs on until the process ends. Its first int is the arrival counter: zero when the code object is
+// loaded (device globals start zeroed) and left zero by every call (the last-arriving histogram workgroup resets
+// it), so it is zero at the start of each call; the rest is fully written before it is read within a call. All
+// calls on one GPU share the array and keep the last call's contents: calls that overlap on one GPU (other streams,
+// concurrent graph replays) race on it.
+namespace {
+
+constexpr long NOALLOC_SCRATCH_INTS = 1L << 18;
+static __device__ __align__(256) int scratch[NOALLOC_SCRATCH_INTS];
+
+constexpr int MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+int* g_scratch_ptr[MAX_DEVICES] = {};
+
+// The device address of `scratch` on the current device, looked up once per device (with that device current) by
+// hipGetSymbolAddress: in host code the array's name is only a host-side stand-in. nullptr on failure.
+int* noalloc_scratch() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES) return nullptr;
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return nullptr;
+    g_scratch_ptr[dev] = static_cast<int*>(p);
+  }
+  return g_scratch_ptr[dev];
+}
+
+}  // namespace
+
+// No counterpart in the reference: r9k_moe_align for callers that cannot allocate (graph capture, tight serving
+// loops, allocation-free harnesses). The scratch is the library's own 1 MiB device array per GPU (see above), so
+// the caller passes only ids and the three tables; overlapping calls on one GPU race. Tables as r9k_moe_align's, bit
+// for bit. 0; 1 bad arguments or a HIP error (as r9k_moe_align); -9 when the step needs more scratch than the array
+// holds (r9k_moe_align_scratch_ints(numel, E) > r9k_moe_align_noalloc_max_ints()); -6 the array's address could not
+// be had.
+extern "C" long r9k_moe_align_noalloc_max_ints(void) { return NOALLOC_SCRATCH_INTS; }
+
+extern "C" int r9k_moe_align_noalloc(long ids, int numel, int E, int blk, long sorted_ids, long expert_ids,
+                                     long ntpp, long stream) {
+  if (numel < 1 || E < 1 || E > MAX_E || blk < 1 || (blk & (blk - 1))) return 1;
+  if (align_scratch_ints(numel, E) > NOALLOC_SCRATCH_INTS) return -9;
+  int* sp = nullptr;
+  if (numel > SMALL_MAX && !(sp = noalloc_scratch())) return -6;
+  if (launch_align((const int*)ids, numel, E, blk, (int*)sorted_ids, (int*)expert_ids, (int*)ntpp, sp,
                    (hipStream_t)stream))
     return 1;
   return (int)hipGetLastError();

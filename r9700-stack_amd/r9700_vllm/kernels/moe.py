@@ -59,6 +59,10 @@ def lib() -> ctypes.CDLL:
         L.r9k_moe_align.restype = i
         L.r9k_moe_align.argtypes = [l, i, i, i, l, l, l, l, l, l]
         L.r9k_moe_align_scratch_ints.restype = l
+        L.r9k_moe_align_noalloc.restype = i
+        L.r9k_moe_align_noalloc.argtypes = [l, i, i, i, l, l, l, l]
+        L.r9k_moe_align_noalloc_max_ints.restype = l
+        L.r9k_moe_align_noalloc_max_ints.argtypes = []
         L.r9k_moe_pick_blocks.restype = i
         L.r9k_moe_pick_blocks.argtypes = [l, l, i, i, i, l]
         L.r9k_moe_align_scratch_ints.argtypes = [i, i]
@@ -614,6 +618,33 @@ def moe_align(topk_ids: torch.Tensor, block: int, num_experts: int, expert_map: 
                          ntpp.data_ptr(), scratch.data_ptr(), scratch.numel(), _stream())
     if rc:
         raise RuntimeError(f"r9k_moe_align failed ({rc}) numel={numel} E={num_experts} block={block}")
+    return sorted_ids, expert_ids, ntpp
+
+
+def moe_align_noalloc(topk_ids: torch.Tensor, block: int, num_experts: int, out=None):
+    """moe_align's tables from r9k_moe_align_noalloc, which allocates nothing on the device (its scratch is the
+    library's own fixed 1 MiB array per GPU; overlapping calls on one GPU race on it). `out` = (sorted_ids,
+    expert_ids, ntpp) int32 buffers of at least capacity(numel, num_experts, block), that / block and 1 entries, or
+    None to allocate them here. Raises RuntimeError when the step needs more scratch than the array holds."""
+    ids = topk_ids.reshape(-1)
+    assert ids.dtype == torch.int32 and ids.is_contiguous()
+    numel = ids.numel()
+    cap = capacity(numel, num_experts, block)
+    if out is None:
+        out = (torch.empty(cap, dtype=torch.int32, device=ids.device),
+               torch.empty(cap // block, dtype=torch.int32, device=ids.device),
+               torch.empty(1, dtype=torch.int32, device=ids.device))
+    sorted_ids, expert_ids, ntpp = out
+    assert sorted_ids.numel() >= cap and expert_ids.numel() >= cap // block and ntpp.numel() >= 1
+    L = lib()
+    rc = L.r9k_moe_align_noalloc(ids.data_ptr(), numel, num_experts, block, sorted_ids.data_ptr(),
+                                 expert_ids.data_ptr(), ntpp.data_ptr(), _stream())
+    if rc == -9:
+        raise RuntimeError(f"r9k_moe_align_noalloc: numel={numel} E={num_experts} needs "
+                           f"{L.r9k_moe_align_scratch_ints(numel, num_experts)} scratch ints, more than the "
+                           f"{L.r9k_moe_align_noalloc_max_ints()} it holds")
+    if rc:
+        raise RuntimeError(f"r9k_moe_align_noalloc failed ({rc}) numel={numel} E={num_experts} block={block}")
     return sorted_ids, expert_ids, ntpp
 
 
