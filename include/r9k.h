@@ -152,6 +152,19 @@ int r9k_moe_align_noalloc(long ids, int numel, int E, int blk, long sorted_ids, 
                           long stream);
 long r9k_moe_align_noalloc_max_ints(void);
 
+/* The tail of a decode-width MoE layer in one launch: SiLU-gating + per-row fp8 quant of the gate_up output, the
+ * grouped down GEMM with the router weight in its epilogue, and the weighted top-k sum (+ an optional shared-expert
+ * term). Replaces, as one entry, kernels/r9k_moe_mxfp4a8.hip:550 (r9k_silu_mul_quant_fp8) + :631-638 (the down
+ * r9k_moe_mxfp4a8 with a_row_div 1 and topk_w) + kernels/r9k_moe_sum.hip:62 (r9k_moe_sum). Token-major: no routing
+ * tables, the expert of routed row t * topk + j is ids[t * topk + j] (outside [0, E): contributes 0).
+ * gu bf16 [T * topk][2I]; ids int32 [T * topk]; tw fp32 [T * topk]; wq / ws the down weights (N = hidden, K = I) in
+ * the r9k_moe_mxfp4a8 layout, ws_estride bytes per expert; shared bf16 [T][N] (row stride ld_shared) or 0; out bf16
+ * [T][N] (row stride ld_out). Equals the three launches bit for bit for I < 1024. Served: I % 128 == 0, I <= 2048,
+ * N % 16 == 0, topk <= 16 (I > 1024 with topk > 8 not); else 2 with nothing launched. 0, -3 bad argument, -6 launch
+ * error. */
+int r9k_moe_down_sum(long gu, long ids, long tw, long wq, long ws, long ws_estride, long shared, long ld_shared,
+                     long out, long ld_out, int T, int topk, int E, int I, int N, long stream);
+
 /* Load-time NVFP4 -> MXFP4 with MSE-searched block exponents (the reference does this with torch:
  * r9700_vllm/quant/nvfp4.py:39-90). packed u8 [N][K/2], s16 e4m3 [N][K/16], row_div fp32 [N] -> out_packed u8
  * [N][K/2], out_e8m0 u8 [N][K/32] (checkpoint layout). -2 K % 32, -3 bad pointer / alignment, -6 launch error. */

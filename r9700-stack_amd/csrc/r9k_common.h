@@ -132,6 +132,52 @@ __device__ __forceinline__ void quant_row_wave(const uint16_t* __restrict__ xrow
   }
 }
 
+// One wave turns one row of the gate_up output (gate = the first I bf16 values, up = the next I; I % 8 == 0,
+// I <= 512 * R, the row 16-byte aligned, the code row 8-byte aligned) into silu(gate) * up quantised to OCP e4m3 with
+// a per-row scale, the rule of the per-token quant: amax = max(max |h|, 1e-12), inv = 448 / amax, q = e4m3(h * inv),
+// s = amax / 448 (returned to every lane). Lane chunks c = lane + 64 i of 8 values stay in registers. The standalone
+// SiLU kernel and every fused consumer of the gate_up output use this one routine, so their codes are the same bytes.
+template <int R>
+__device__ __forceinline__ float silu_quant_row_wave(const uint16_t* __restrict__ grow, int I, uint8_t* qrow,
+                                                     int lane) {
+  const int nvec = I / 8;
+  const uint4* gr = reinterpret_cast<const uint4*>(grow);
+  const uint4* ur = reinterpret_cast<const uint4*>(grow + I);
+  uint4 gv[R], uv[R];
+#pragma unroll
+  for (int i = 0; i < R; i++) {
+    const int c = lane + i * WAVE;
+    gv[i] = c < nvec ? gr[c] : make_uint4(0u, 0u, 0u, 0u);
+    uv[i] = c < nvec ? ur[c] : make_uint4(0u, 0u, 0u, 0u);
+  }
+  float a[R][8];
+  float m = 0.f;
+#pragma unroll
+  for (int i = 0; i < R; i++) {
+    const uint32_t gw[4] = {gv[i].x, gv[i].y, gv[i].z, gv[i].w}, uw[4] = {uv[i].x, uv[i].y, uv[i].z, uv[i].w};
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      a[i][2 * j] = silu_mul(lo16(gw[j]), lo16(uw[j]));
+      a[i][2 * j + 1] = silu_mul(hi16(gw[j]), hi16(uw[j]));
+    }
+#pragma unroll
+    for (int j = 0; j < 8; j++) m = fmaxf(m, fabsf(a[i][j]));      // zero padding lanes give silu(0) * 0 = 0
+  }
+  const float amax = fmaxf(wave_max(m), 1e-12f);
+  const float inv = 448.f / amax;
+  uint2* qr = reinterpret_cast<uint2*>(qrow);
+#pragma unroll
+  for (int i = 0; i < R; i++) {
+    const int c = lane + i * WAVE;
+    if (c < nvec) {
+      const uint32_t lo = pack4_e4m3(a[i][0] * inv, a[i][1] * inv, a[i][2] * inv, a[i][3] * inv);
+      const uint32_t hi = pack4_e4m3(a[i][4] * inv, a[i][5] * inv, a[i][6] * inv, a[i][7] * inv);
+      qr[c] = make_uint2(lo, hi);
+    }
+  }
+  return amax / 448.f;
+}
+
 // Block-wide max of a float; `sh` holds one float per wave. Every thread gets the result.
 template <int NT>
 __device__ __forceinline__ float block_max(float v, float* sh) {

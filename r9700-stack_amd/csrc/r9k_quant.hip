@@ -178,43 +178,10 @@ template <int R>
 __global__ void __launch_bounds__(WR * WAVE) silu_mul_quant_wave_kernel(const uint16_t* __restrict__ gu,
                                                                         uint8_t* __restrict__ q,
                                                                         float* __restrict__ s, int M, int I) {
-  const int row = blockIdx.x * WR + threadIdx.x / WAVE, lane = threadIdx.x % WAVE, nvec = I / 8;
+  const int row = blockIdx.x * WR + threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
   if (row >= M) return;
-  const uint4* gr = reinterpret_cast<const uint4*>(gu + (size_t)row * 2 * I);
-  const uint4* ur = reinterpret_cast<const uint4*>(gu + (size_t)row * 2 * I + I);
-  uint4 gv[R], uv[R];
-#pragma unroll
-  for (int i = 0; i < R; i++) {
-    const int c = lane + i * WAVE;
-    gv[i] = c < nvec ? gr[c] : make_uint4(0u, 0u, 0u, 0u);
-    uv[i] = c < nvec ? ur[c] : make_uint4(0u, 0u, 0u, 0u);
-  }
-  float a[R][8];
-  float m = 0.f;
-#pragma unroll
-  for (int i = 0; i < R; i++) {
-    const uint32_t gw[4] = {gv[i].x, gv[i].y, gv[i].z, gv[i].w}, uw[4] = {uv[i].x, uv[i].y, uv[i].z, uv[i].w};
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-      a[i][2 * j] = silu_mul(lo16(gw[j]), lo16(uw[j]));
-      a[i][2 * j + 1] = silu_mul(hi16(gw[j]), hi16(uw[j]));
-    }
-#pragma unroll
-    for (int j = 0; j < 8; j++) m = fmaxf(m, fabsf(a[i][j]));      // zero padding lanes give silu(0) * 0 = 0
-  }
-  const float amax = fmaxf(wave_max(m), 1e-12f);
-  const float inv = 448.f / amax;
-  if (lane == 0) s[row] = amax / 448.f;
-  uint2* qr = reinterpret_cast<uint2*>(q + (size_t)row * I);
-#pragma unroll
-  for (int i = 0; i < R; i++) {
-    const int c = lane + i * WAVE;
-    if (c < nvec) {
-      const uint32_t lo = pack4_e4m3(a[i][0] * inv, a[i][1] * inv, a[i][2] * inv, a[i][3] * inv);
-      const uint32_t hi = pack4_e4m3(a[i][4] * inv, a[i][5] * inv, a[i][6] * inv, a[i][7] * inv);
-      qr[c] = make_uint2(lo, hi);
-    }
-  }
+  const float sc = silu_quant_row_wave<R>(gu + (size_t)row * 2 * I, I, q + (size_t)row * I, lane);
+  if (lane == 0) s[row] = sc;
 }
 
 // One row per workgroup; each thread keeps its activations (I <= QT * 8 * QR) in registers between the max pass

@@ -71,6 +71,8 @@ def lib() -> ctypes.CDLL:
         L.r9k_quantize_mxfp4_search.restype = i
         L.r9k_quantize_mxfp4_search.argtypes = [l] * 3 + [i] * 2 + [l]
         L.r9k_fold_supported.restype = i
+        L.r9k_moe_down_sum.restype = i
+        L.r9k_moe_down_sum.argtypes = [l] * 10 + [i] * 5 + [l]
         assert L.r9k_moe_block() == MOE_BLOCK
         _LIB = L
     return _LIB
@@ -564,6 +566,45 @@ def pick_moe_prefill(MT: int, K_down: int, gate_up: bool = False) -> int | None:
     if cfg < 0 or 16 * MT != prefill_block(cfg) or K_down % prefill_bk(cfg):
         return None
     return cfg
+
+
+# At decode widths the SiLU + re-quant, the down GEMM and the top-k sum run as one token-major launch
+# (r9k_moe_down_sum), which saves two launches but reads an expert's down weights once per routed row instead of
+# once per routing block. It is used while the routed rows' down weight bytes (numel * N2 * K2 / 2, re-reads
+# included) stay within DOWN_SUM_MAX_BYTES. Measured on MI355X: config 2 (E=288, 0.5 MB of down weights an expert)
+# T = 1 / 8 / 16 / 32: 21.2 -> 14.4, 35.3 -> 27.8, 47.4 -> 40.5, 62.0 -> 59.5 us a layer, T = 64 81.0 -> 90.6 (not
+# taken); config 5 (4 MB an expert, Zipf routing) T = 1 / 2: 36.7 -> 30.0, 43.7 -> 39.5, T = 4 even, T = 8 68.9 ->
+# 84.3 (not taken).
+DOWN_SUM_MAX_BYTES = int(os.environ.get("R9K_MOE_DOWN_SUM_MAX_BYTES", str(128 << 20)))
+
+
+def down_sum_fits(numel: int, N2: int, K2: int) -> bool:
+    """Whether a decode step of `numel` routed rows takes the token-major tail (r9k_moe_down_sum)."""
+    return numel * N2 * K2 // 2 <= DOWN_SUM_MAX_BYTES
+
+
+def moe_down_sum(gate_up: torch.Tensor, topk_ids: torch.Tensor, topk_w: torch.Tensor, w: Mxfp4Experts,
+                 out: torch.Tensor, shared: torch.Tensor | None = None) -> bool:
+    """out[t] = sum_j bf16(silu-quant(gate_up[t*k+j]) @ W2[ids[t, j]]^T * (as * topk_w[t*k+j])) (+ shared[t]) in one
+    launch (r9k_moe_down_sum): the three-launch tail's values (bit for bit when K2 < 1024). gate_up bf16 [T*k, 2*K2]
+    contiguous; topk_ids int32 [T, k]; topk_w fp32 [T*k]. False when the shape is not served (nothing launched:
+    run silu_mul_quant_fp8, the down moe_gemm and moe_sum)."""
+    T, k = topk_ids.shape
+    assert gate_up.is_contiguous() and gate_up.dtype == torch.bfloat16 and gate_up.shape == (T * k, 2 * w.K)
+    assert topk_ids.dtype == torch.int32 and topk_ids.is_contiguous()
+    assert topk_w.dtype == torch.float32 and topk_w.is_contiguous() and topk_w.numel() == T * k
+    assert out.dtype == torch.bfloat16 and out.shape == (T, w.N) and out.stride(1) == 1
+    if shared is not None:
+        assert shared.dtype == torch.bfloat16 and shared.shape == (T, w.N) and shared.stride(1) == 1
+    rc = lib().r9k_moe_down_sum(gate_up.data_ptr(), topk_ids.data_ptr(), topk_w.data_ptr(), w.wq.data_ptr(),
+                                w.wsr.data_ptr(), w.estride, shared.data_ptr() if shared is not None else 0,
+                                shared.stride(0) if shared is not None else 0, out.data_ptr(), out.stride(0), T, k,
+                                w.wq.shape[0], w.K, w.N, _stream())
+    if rc == 2:
+        return False
+    if rc:
+        raise RuntimeError(f"r9k_moe_down_sum failed ({rc}) T={T} topk={k} N={w.N} K={w.K}")
+    return True
 
 
 # ------------------------------------------------------------------------------------- routing and sum

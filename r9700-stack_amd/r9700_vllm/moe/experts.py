@@ -243,6 +243,12 @@ class R9700Mxfp4Experts(_experts_base()):
             for W1, _, (sid, eid, ntpp), (mt, pfg, _) in passes:
                 K.moe_gemm(xq, xs, W1, gate_up, sid, eid, ntpp, numel, topk, None, num_experts=E, MT=mt,
                            prefill=pfg)
+            if (len(passes) == 1 and cache is None and nv is None and expert_map is None and MT == 1
+                    and pf_gate is None and K.down_sum_fits(numel, N2, K2) and not ZERO_DOWN):
+                # decode widths: SiLU + quant, down and the top-k sum in one token-major launch
+                tw = topk_weights.reshape(-1).to(torch.float32).contiguous()
+                if K.moe_down_sum(gate_up, topk_ids.to(torch.int32).contiguous(), tw, passes[0][1], output):
+                    return output
             aq, as_ = K.silu_mul_quant_fp8(gate_up)
         # Rows no table places (experts on other ranks under an expert map) must not feed moe_sum garbage.
         if expert_map is not None or ZERO_DOWN:

@@ -430,3 +430,55 @@ def test_layer_past_the_buffer_limit_chunks(dev):
     tokens = np.unique(np.concatenate([[0, T // 2 - 1, T // 2, T - 1],       # both chunks' ends
                                        np.random.default_rng(7).choice(T, 24, replace=False)]))
     run_layer(dev, E, H, I, T, topk, seed=20261201 + 32768, tokens=tokens)
+
+
+@pytest.mark.parametrize("E,T,H,I,topk,shared", [(288, 1, 2048, 512, 8, False), (288, 8, 2048, 512, 8, True),
+                                                 (288, 16, 2048, 512, 8, False), (64, 5, 1024, 1024, 6, False),
+                                                 (32, 3, 512, 512, 16, True), (16, 2, 256, 512, 1, False),
+                                                 (24, 4, 4096, 2048, 8, False), (12, 3, 320, 1024, 12, True)])
+def test_down_sum_equals_three_launches(dev, E, T, H, I, topk, shared):
+    """r9k_moe_down_sum (SiLU + quant, down GEMM and top-k sum in one token-major launch) against the three launches
+    it replaces on the same gate_up output: bit for bit when K2 = I < 1024 (the down GEMM's single-wave K chain),
+    else within fp32 accumulation order (the down GEMM splits K over waves); optional shared-expert term."""
+    seed = 20261201 + 9100 + E + T + H + I
+    (_, _), (_, _), W13, W2 = make_layer(dev, E, H, I, seed)
+    g = torch.Generator().manual_seed(seed + 1)
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16).to(dev)
+    logits = torch.randn(T, E, generator=g).to(torch.bfloat16).to(dev)
+    sh = torch.randn(T, H, generator=g).to(torch.bfloat16).to(dev) if shared else None
+    w, ids = K.moe_topk(logits, topk, True)
+    numel = T * topk
+    sid, eid, ntpp = K.moe_align(ids, 16, E)
+    xq, xs = K.quant_rows_fp8(x)
+    tw = w.reshape(-1).float().contiguous()
+    gu = torch.empty(numel, 2 * I, dtype=torch.bfloat16, device=dev)
+    K.moe_gemm(xq, xs, W13, gu, sid, eid, ntpp, numel, topk, None, num_experts=E, MT=1)
+    aq, as_ = K.silu_mul_quant_fp8(gu)
+    down = torch.empty(numel, H, dtype=torch.bfloat16, device=dev)
+    K.moe_gemm(aq, as_, W2, down, sid, eid, ntpp, numel, 1, tw, num_experts=E, MT=1)
+    o3 = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
+    K.moe_sum(down.view(T, topk, H), sh, o3)
+    o1 = torch.full((T, H), float("nan"), dtype=torch.bfloat16, device=dev)
+    assert K.moe_down_sum(gu, ids, tw, W2, o1, sh), "shape not served"
+    torch.cuda.synchronize()
+    same = torch.equal(o1.view(torch.int16), o3.view(torch.int16))
+    a, b = o1.double(), o3.double()
+    r = float((a - b).norm() / b.norm())
+    print(f"down_sum E={E} T={T} H={H} I={I} k={topk} shared={shared}: bit-equal {same}, rel {r:.2e}", flush=True)
+    if I < 1024:
+        assert same
+    else:
+        assert r < 1e-3 and (o1 != o3).float().mean() < 0.05
+
+
+def test_down_sum_refuses_unserved_shapes(dev):
+    """Shapes the token-major tail does not take return False with nothing launched (apply() then runs the three
+    launches): K2 not a multiple of 128 or past 2048, more than 16 slots."""
+    E, H = 4, 256
+    for I, topk in ((320, 2), (4096, 2), (512, 17)):
+        W2 = K.Mxfp4Experts(torch.zeros(E, H * I // 8, dtype=torch.int32, device=dev),
+                            torch.zeros(E, I // 32 + 1, H, dtype=torch.uint8, device=dev), H, I)
+        gu = torch.zeros(topk, 2 * I, dtype=torch.bfloat16, device=dev)
+        ids = torch.zeros(1, topk, dtype=torch.int32, device=dev)
+        out = torch.zeros(1, H, dtype=torch.bfloat16, device=dev)
+        assert not K.moe_down_sum(gu, ids, torch.ones(topk, device=dev), W2, out)
