@@ -165,6 +165,14 @@ long r9k_moe_align_noalloc_max_ints(void);
 int r9k_moe_down_sum(long gu, long ids, long tw, long wq, long ws, long ws_estride, long shared, long ld_shared,
                      long out, long ld_out, int T, int topk, int E, int I, int N, long stream);
 
+/* The dense MXFP4 weight-only linear at decode widths in one launch: the per-row fp8 quant of the bf16 activations
+ * (each workgroup quantises the M <= 16 rows into LDS) and the GEMM. Replaces, as one entry, the reference's
+ * r9k_quant_rows_fp8 + r9k_moe_mxfp4a8 over identity tables (r9700_vllm/ops.py:89-117; kernels/r9k_moe_mxfp4a8.hip
+ * :1745-1760, :631-638). x bf16 [M][K] (row stride ldx, 16-byte aligned); wq / ws one expert in the r9k_moe_mxfp4a8
+ * layout; out bf16 [M][N] (row stride ldo). Bit-equal to the two launches. Served: 1 <= M <= 16, K % 128 == 0,
+ * K <= 8192, N % 16 == 0; else 2 with nothing launched. 0, -3 bad argument, -6 launch error. */
+int r9k_dense_mxfp4_qa(long x, long ldx, long wq, long ws, long out, long ldo, int M, int N, int K, long stream);
+
 /* Load-time NVFP4 -> MXFP4 with MSE-searched block exponents (the reference does this with torch:
  * r9700_vllm/quant/nvfp4.py:39-90). packed u8 [N][K/2], s16 e4m3 [N][K/16], row_div fp32 [N] -> out_packed u8
  * [N][K/2], out_e8m0 u8 [N][K/32] (checkpoint layout). -2 K % 32, -3 bad pointer / alignment, -6 launch error. */

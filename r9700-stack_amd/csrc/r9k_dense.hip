@@ -1,0 +1,211 @@
+// r9k_dense.hip -- the dense MXFP4 weight-only linear at decode widths (M <= 16 rows) in one launch: the per-token
+// fp8 (e4m3) quant of the bf16 activations and the MXFP4 x fp8 GEMM.
+//
+//   out[m, n] = bf16( (sum_k q[m, k] * W[n, k]) * s[m] ),   q, s = the per-row quant of x (quant_row_wave)
+//
+// The reference runs it as r9k_quant_rows_fp8 then r9k_moe_mxfp4a8 over identity routing tables
+// (r9700_vllm/ops.py:89-117; kernels/r9k_moe_mxfp4a8.hip:1683-1743 and :187-485). At decode widths the quant launch
+// costs about as much as a third of the GEMM (its launch and memory latency), so here every workgroup quantises the
+// M activation rows itself into LDS (each row read once from L2 per workgroup, M * K * 2 bytes) while its first weight
+// loads are in flight, then runs the weight stream against the LDS codes.
+//
+// Work split: a workgroup owns NPW 16-column tiles (1 KB of codes + 64 exponent bytes per 128-K tile, the
+// r9k_moe_mxfp4a8 weight layout), SK waves split the K-tiles in contiguous ranges, each wave issues the loads of up
+// to U K-tiles at once (all of its range when it fits) and runs the 16x16x128 scaled MFMAs: activations as the fp8 A
+// operand (rows m < M live, the other rows zero), weights as the fp4 B operand with their e8m0 exponent as the B
+// scale. The SK partial tiles meet in LDS and are summed in wave order. With the entry's SK rule (the decode GEMM's:
+// 4 waves from 8 K-tiles) the result equals the two-launch path's bit for bit.
+#include "r9k_common.h"
+
+#include <cstdlib>
+
+namespace {
+
+using namespace r9k;
+
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int KT = 128;
+constexpr int E8M0_ONE = 127;
+constexpr int MAXM = 16;          // activation rows: one MFMA M-tile
+constexpr int APAD = 16;          // bytes of padding per LDS code row (row stride K + 16: no bank aliasing of rows)
+
+// One wave quantises one row like quant_row_wave (the same amax, 448 / amax and per-element encode, so the same
+// bytes) in two passes of 4 chunks a lane at a time -- the row maximum, then the codes -- so the row is never held
+// in registers beside the weight loads in flight. The second pass re-reads the row from L2.
+__device__ __forceinline__ void quant_row_two_pass(const uint16_t* __restrict__ xrow, int K, uint8_t* qrow,
+                                                   float* s_out, int lane) {
+  const uint4* xr = reinterpret_cast<const uint4*>(xrow);
+  const int nvec = K / 8;
+  float m = 0.f;
+  for (int c0 = 0; c0 < nvec; c0 += 4 * WAVE) {
+    uint4 v[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int c = c0 + lane + i * WAVE;
+      v[i] = c < nvec ? xr[c] : make_uint4(0u, 0u, 0u, 0u);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const uint32_t w[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
+#pragma unroll
+      for (int j = 0; j < 4; j++) m = fmaxf(m, fmaxf(fabsf(lo16(w[j])), fabsf(hi16(w[j]))));
+    }
+  }
+  const float amax = fmaxf(wave_max(m), 1e-12f);
+  const float inv = 448.f / amax;
+  if (lane == 0) *s_out = amax / 448.f;
+  uint2* qr = reinterpret_cast<uint2*>(qrow);
+  for (int c0 = 0; c0 < nvec; c0 += 4 * WAVE) {
+    uint4 v[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int c = c0 + lane + i * WAVE;
+      v[i] = c < nvec ? xr[c] : make_uint4(0u, 0u, 0u, 0u);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int c = c0 + lane + i * WAVE;
+      if (c < nvec) {
+        const uint32_t lo = pack4_e4m3(lo16(v[i].x) * inv, hi16(v[i].x) * inv, lo16(v[i].y) * inv, hi16(v[i].y) * inv);
+        const uint32_t hi = pack4_e4m3(lo16(v[i].z) * inv, hi16(v[i].z) * inv, lo16(v[i].w) * inv, hi16(v[i].w) * inv);
+        qr[c] = make_uint2(lo, hi);
+      }
+    }
+  }
+}
+
+// LDS: codes [M][K + APAD] (fp8), row scales [MAXM] fp32, partial tiles [SK][NPW][256] fp32 (sized by M, so small M
+// leaves room for several workgroups a CU).
+template <int NPW, int SK, int U>
+__global__ void __launch_bounds__(WAVE * SK) dense_mxfp4_qa_kernel(
+    const uint16_t* __restrict__ x, long ldx, const uint8_t* __restrict__ Wq, const uint8_t* __restrict__ Ws,
+    uint16_t* __restrict__ out, long ldo, int M, int N, int K) {
+  extern __shared__ __align__(16) uint8_t lds[];
+  const int lda = K + APAD;
+  uint8_t* A = lds;
+  float* s_row = reinterpret_cast<float*>(lds + (size_t)M * lda);
+  float* red = s_row + MAXM;
+  const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
+  const int g = lane >> 4, r = lane & 15;
+  const int NT = N / 16, nkt = K / KT, KB = K / 32;
+
+  const uint8_t* wtile[NPW];
+  const uint8_t* stile[NPW];
+#pragma unroll
+  for (int j = 0; j < NPW; j++) {
+    const int nt = min((int)blockIdx.x * NPW + j, NT - 1);     // a tile past N computes a copy, never stored
+    wtile[j] = Wq + (size_t)nt * (size_t)(8 * K) + lane * 16;
+    stile[j] = Ws + (size_t)nt * (size_t)(16 * KB) + lane;
+  }
+  const int kt0 = wave * nkt / SK, kt1 = (wave + 1) * nkt / SK;
+
+  // the first batch of weight loads goes out before the activation quant, so its latency overlaps it
+  u32x4 bf[U][NPW];
+  uint32_t sb[U][NPW];
+  auto issue = [&](int kb) {
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const int k = min(kb + u, kt1 - 1);
+#pragma unroll
+      for (int j = 0; j < NPW; j++) {
+        bf[u][j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wtile[j] + (size_t)k * 1024));
+        sb[u][j] = __builtin_nontemporal_load(stile[j] + k * 64);
+      }
+    }
+  };
+  issue(kt0);
+  for (int m = wave; m < M; m += SK) quant_row_two_pass(x + (size_t)m * ldx, K, A + (size_t)m * lda, s_row + m, lane);
+  __syncthreads();
+
+  v4f acc[NPW];
+#pragma unroll
+  for (int j = 0; j < NPW; j++) acc[j] = (v4f){0.f, 0.f, 0.f, 0.f};
+  const bool arow = r < M;
+  const uint8_t* ar = A + (size_t)(arow ? r : 0) * lda + 16 * g;
+  for (int kb = kt0; kb < kt1; kb += U) {
+    if (kb != kt0) issue(kb);
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const int k = kb + u;
+      if (k < kt1) {                                         // wave-uniform
+        uint4 lo = *reinterpret_cast<const uint4*>(ar + k * KT);
+        uint4 hi = *reinterpret_cast<const uint4*>(ar + k * KT + 64);
+        if (!arow) lo = hi = make_uint4(0u, 0u, 0u, 0u);
+        const v8i a = (v8i){(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+#pragma unroll
+        for (int j = 0; j < NPW; j++) {
+          const v8i b = (v8i){(int)bf[u][j].x, (int)bf[u][j].y, (int)bf[u][j].z, (int)bf[u][j].w, 0, 0, 0, 0};
+          acc[j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, acc[j], 0, 4, 0, E8M0_ONE, 0, (int)sb[u][j]);
+        }
+      }
+    }
+  }
+
+  // C layout: lane holds column r, rows 4g .. 4g + 3. The partial tiles always go through LDS (no branch on the
+  // MFMA results, so the compiler cannot move the MFMAs under a partial exec mask), then are summed in wave order.
+#pragma unroll
+  for (int j = 0; j < NPW; j++) {
+    float* t = red + (size_t)(wave * NPW + j) * 256;
+#pragma unroll
+    for (int q = 0; q < 4; q++) t[(4 * g + q) * 16 + r] = acc[j][q];
+  }
+  __syncthreads();
+  constexpr int TOT = NPW * 256;
+  for (int idx = tid; idx < TOT; idx += WAVE * SK) {
+    const int col = idx & 15, m = (idx >> 4) & 15, j = idx >> 8;
+    const int n = (blockIdx.x * NPW + j) * 16 + col;
+    if (m >= M || n >= N) continue;
+    float v = 0.f;
+#pragma unroll
+    for (int s = 0; s < SK; s++) v += red[(size_t)s * TOT + idx];
+    out[(size_t)m * ldo + n] = f2bf(v * s_row[m]);
+  }
+}
+
+int env_int(const char* name, int dflt) {
+  const char* v = getenv(name);
+  return v && *v ? atoi(v) : dflt;
+}
+
+}  // namespace
+
+// No counterpart as one entry in the reference: r9k_quant_rows_fp8 + r9k_moe_mxfp4a8 over identity tables
+// (r9700_vllm/ops.py:89-117 calls them back to back) in one launch, for M <= 16 rows. x bf16 [M][K] (row stride
+// ldx elements, rows 16-byte aligned); wq / ws one expert's weights in the r9k_moe_mxfp4a8 layout (N columns, K);
+// out bf16 [M][N] (row stride ldo). Served: 1 <= M <= 16, K % 128 == 0, K <= 8192, N % 16 == 0; 2 (nothing launched)
+// otherwise. 0, -3 bad argument, -6 launch error. The K split (SK waves) follows the decode GEMM's rule, so the
+// output equals r9k_quant_rows_fp8 + r9k_moe_mxfp4a8's bit for bit.
+extern "C" int r9k_dense_mxfp4_qa(long x, long ldx, long wq, long ws, long out, long ldo, int M, int N, int K,
+                                  long stream) {
+  if (M <= 0) return 0;
+  if (!x || !wq || !ws || !out || N <= 0 || K <= 0) return -3;
+  if (M > MAXM || K % KT || K > 8192 || N % 16 || (x & 15) || (ldx & 7) || (wq & 15)) return 2;
+  const int nkt = K / KT, NT = N / 16;
+  const int NPW = env_int("R9K_DENSE_NPW", NT >= 2 ? 2 : 1);
+  const int SK = env_int("R9K_DENSE_SK", nkt >= 8 ? 4 : 1);
+  const int per = (nkt + SK - 1) / SK;
+  // loads in flight a wave: its whole K range up to 5 K-tiles, else two batches (all of a 10-tile range at once
+  // needs ~165 VGPRs, two waves a SIMD, and 544 workgroups of config 4 no longer fit the chip in one round:
+  // measured 20.2 us against 14.2 us in two batches of 5)
+  const int U = env_int("R9K_DENSE_U", per <= 4 ? 4 : (per <= 5 ? 5 : (per <= 8 ? 4 : (per <= 10 ? 5 : 8))));
+  const size_t smem = (size_t)M * (K + APAD) + MAXM * sizeof(float) + (size_t)SK * NPW * 256 * sizeof(float);
+  const dim3 grid((NT + NPW - 1) / NPW), block(WAVE * SK);
+  const hipStream_t st = (hipStream_t)stream;
+#define DQ(NPWv, SKv, Uv)                                                                                          \
+  if (NPW == NPWv && SK == SKv && U == Uv) {                                                                       \
+    static const hipError_t a = hipFuncSetAttribute(reinterpret_cast<const void*>(dense_mxfp4_qa_kernel<NPWv, SKv, Uv>), \
+                                                    hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);       \
+    if (a != hipSuccess) return -6;                                                                                \
+    hipLaunchKernelGGL((dense_mxfp4_qa_kernel<NPWv, SKv, Uv>), grid, block, smem, st, (const uint16_t*)x, ldx,     \
+                       (const uint8_t*)wq, (const uint8_t*)ws, (uint16_t*)out, ldo, M, N, K);                      \
+    return hipGetLastError() == hipSuccess ? 0 : -6;                                                               \
+  }
+#define DQU(NPWv, SKv) DQ(NPWv, SKv, 4) DQ(NPWv, SKv, 5) DQ(NPWv, SKv, 8) DQ(NPWv, SKv, 10) DQ(NPWv, SKv, 16)
+  DQU(1, 1) DQU(2, 1) DQU(1, 4) DQU(2, 4) DQU(2, 8) DQU(4, 4) DQU(1, 8) DQU(4, 8)
+#undef DQU
+#undef DQ
+  return 2;
+}

@@ -72,6 +72,8 @@ def lib() -> ctypes.CDLL:
         L.r9k_quantize_mxfp4_search.argtypes = [l] * 3 + [i] * 2 + [l]
         L.r9k_fold_supported.restype = i
         L.r9k_moe_down_sum.restype = i
+        L.r9k_dense_mxfp4_qa.restype = i
+        L.r9k_dense_mxfp4_qa.argtypes = [l] * 6 + [i] * 3 + [l]
         L.r9k_moe_down_sum.argtypes = [l] * 10 + [i] * 5 + [l]
         assert L.r9k_moe_block() == MOE_BLOCK
         _LIB = L
@@ -604,6 +606,28 @@ def moe_down_sum(gate_up: torch.Tensor, topk_ids: torch.Tensor, topk_w: torch.Te
         return False
     if rc:
         raise RuntimeError(f"r9k_moe_down_sum failed ({rc}) T={T} topk={k} N={w.N} K={w.K}")
+    return True
+
+
+# ops.mxfp4_linear runs the one-launch dense path (r9k_dense_mxfp4_qa) up to this many rows. Measured on MI355X at
+# config 4 ([17408, 5120]): M = 1 15.8 -> 14.2 us, M = 4 16.4 -> 16.2 us; at M = 16 every workgroup's quant of 16
+# rows (160 KB from L2) costs more than the quant launch it saves (20.5 -> 32+ us), so M > 4 keeps two launches.
+DENSE_QA_MAX_M = int(os.environ.get("R9K_DENSE_QA_MAX_M", "4"))
+
+
+def dense_mxfp4_qa(x: torch.Tensor, w: Mxfp4Experts, out: torch.Tensor) -> bool:
+    """out [M, N] = bf16(quant_rows_fp8(x) @ W^T) for one dense MXFP4 weight (w.wq / w.wsr of a single expert) in ONE
+    launch (r9k_dense_mxfp4_qa: every workgroup quantises the <= 16 activation rows into LDS itself), the values of
+    quant_rows_fp8 + moe_gemm over identity tables bit for bit. False when not served (nothing launched)."""
+    M = x.shape[0]
+    assert x.dtype == torch.bfloat16 and x.dim() == 2 and x.stride(1) == 1 and x.shape[1] == w.K
+    assert out.dtype == torch.bfloat16 and out.shape == (M, w.N) and out.stride(1) == 1
+    rc = lib().r9k_dense_mxfp4_qa(x.data_ptr(), x.stride(0), w.wq.data_ptr(), w.wsr.data_ptr(), out.data_ptr(),
+                                  out.stride(0), M, w.N, w.K, _stream())
+    if rc == 2:
+        return False
+    if rc:
+        raise RuntimeError(f"r9k_dense_mxfp4_qa failed ({rc}) M={M} N={w.N} K={w.K}")
     return True
 
 

@@ -54,8 +54,10 @@ def _mxfp4_linear(x: torch.Tensor, wq: torch.Tensor, wsr: torch.Tensor, N: int, 
     out = torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
     if M == 0:
         return out
-    cfg = KM.pick_cfg(N, K, M=M, kind="mxfp4", fold=fold)
     W = KM.Mxfp4Experts(wq, wsr, N, K, fold)
+    if M <= KM.DENSE_QA_MAX_M and KM.dense_mxfp4_qa(x, W, out):   # decode widths: the quant inside the GEMM launch
+        return out
+    cfg = KM.pick_cfg(N, K, M=M, kind="mxfp4", fold=fold)
     q, s = KM.quant_rows_fp8(x)
     mxfp4_gemm_q(q, s, W, out, M, cfg)
     return out

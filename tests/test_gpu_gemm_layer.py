@@ -482,3 +482,42 @@ def test_down_sum_refuses_unserved_shapes(dev):
         ids = torch.zeros(1, topk, dtype=torch.int32, device=dev)
         out = torch.zeros(1, H, dtype=torch.bfloat16, device=dev)
         assert not K.moe_down_sum(gu, ids, torch.ones(topk, device=dev), W2, out)
+
+
+@pytest.mark.parametrize("M,N,Kd", [(1, 17408, 5120), (4, 17408, 5120), (16, 17408, 5120), (7, 1024, 2048),
+                                    (16, 1024, 2048), (3, 48, 1024), (2, 272, 384), (5, 64, 8192)])
+def test_dense_qa_equals_two_launches(dev, M, N, Kd):
+    """r9k_dense_mxfp4_qa (the activation quant inside the dense GEMM launch, M <= 16) against quant_rows_fp8 + the
+    decode GEMM over identity tables: bit for bit (same K split over waves), and within the GEMM tolerance of the
+    oracle."""
+    g = torch.Generator().manual_seed(20261201 + 4100 + M + N + Kd)
+    packed, e8 = make_experts(1, N, Kd, g)
+    W = K.prepare_mxfp4_weights(packed.to(dev), e8.to(dev))
+    x = torch.randn(M, Kd, generator=g).to(torch.bfloat16)
+    xd = x.to(dev)
+    one = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=dev)
+    assert K.dense_mxfp4_qa(xd, W, one), "shape not served"
+    q, s = K.quant_rows_fp8(xd)
+    two = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+    ops.mxfp4_gemm_q(q, s, W, two, M, K.pick_cfg(N, Kd, M=M, kind="mxfp4"))
+    torch.cuda.synchronize()
+    same = torch.equal(one.view(torch.int16), two.view(torch.int16))
+    qo, so = O.quant_rows_fp8(x)
+    ref = O.grouped_gemm(qo, so, {0: O.mxfp4_dequant(packed[0], e8[0], torch.float32)}, np.zeros(M, dtype=np.int32),
+                         1, acc_dtype=torch.float32)
+    a, b = bf16_bits_to_f64(O.bf16_bits(one)), bf16_bits_to_f64(ref)
+    r = rel_err(a, b)
+    print(f"dense qa M={M} N={N} K={Kd}: bit-equal to two launches {same}, rel {r:.2e}", flush=True)
+    assert same and r < 2e-3 and cosine(a, b) > 0.99999
+
+
+def test_dense_qa_refuses_unserved(dev):
+    """M > 16, K not a multiple of 128 or unaligned activations: False, nothing launched (ops falls back)."""
+    W = K.Mxfp4Experts(torch.zeros(1, 64 * 320 // 8, dtype=torch.int32, device=dev),
+                       torch.zeros(1, 320 // 32 + 1, 64, dtype=torch.uint8, device=dev), 64, 320)
+    assert not K.dense_mxfp4_qa(torch.zeros(2, 320, dtype=torch.bfloat16, device=dev), W,
+                                torch.empty(2, 64, dtype=torch.bfloat16, device=dev))
+    W2 = K.Mxfp4Experts(torch.zeros(1, 64 * 256 // 8, dtype=torch.int32, device=dev),
+                        torch.zeros(1, 256 // 32 + 1, 64, dtype=torch.uint8, device=dev), 64, 256)
+    assert not K.dense_mxfp4_qa(torch.zeros(17, 256, dtype=torch.bfloat16, device=dev), W2,
+                                torch.empty(17, 64, dtype=torch.bfloat16, device=dev))
