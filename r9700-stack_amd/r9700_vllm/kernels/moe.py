@@ -155,8 +155,9 @@ def prepare_nvfp4_weights(packed: torch.Tensor, scale16: torch.Tensor, row_mult:
     return Nvfp4Experts(wq.view(torch.int32), ws, row_mult.float().reshape(E, N).contiguous(), N, K)
 
 
-def permute_fragments(packed: torch.Tensor) -> torch.Tensor:
-    """[E, N, K/2] uint8 checkpoint order -> [E, N*K/8] int32 fragment order (same bytes, same size).
+def permute_fragments(packed: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """[E, N, K/2] uint8 checkpoint order -> [E, N*K/8] int32 fragment order (same bytes, same size); written into
+    `out` (any tensor of E * N * K/2 bytes, not overlapping `packed`) when given.
 
     Column tile nt (16 rows) occupies 8*K bytes. Its K-tile kt (128 K) is 1 KB at kt*1024: lane l = g*16 + r of the
     V_MFMA_SCALE_F32_16X16X128_F8F6F4 B operand holds row nt*16 + r, K elements kt*128 + g*32 .. +32, i.e. the 16
@@ -166,16 +167,17 @@ def permute_fragments(packed: torch.Tensor) -> torch.Tensor:
     K = Kh * 2
     assert N % 16 == 0 and K % GROUP == 0, (N, K)
     nt, nkf, G = N // 16, K // KTILE, (K % KTILE) // GROUP
+    if out is None:
+        out = torch.empty((E, N * Kh // 4), dtype=torch.int32, device=packed.device)
+    dst = out.view(torch.uint8).reshape(E, nt, 8 * K)
     w = packed.reshape(E, nt, 16, Kh)
-    parts = []
     if nkf:
         f = w[..., : nkf * 64].reshape(E, nt, 16, nkf, 4, 16).permute(0, 1, 3, 4, 2, 5)   # [E, nt, kt, g, r, 16]
-        parts.append(f.reshape(E, nt, nkf * 1024))
+        dst[..., : nkf * 1024].view(E, nt, nkf, 4, 16, 16).copy_(f)
     if G:
         t = w[..., nkf * 64:].reshape(E, nt, 16, G, 16).permute(0, 1, 3, 2, 4)              # [E, nt, g, r, 16]
-        parts.append(t.reshape(E, nt, G * 256))
-    out = parts[0] if len(parts) == 1 else torch.cat(parts, dim=2)
-    return out.reshape(E, -1).contiguous().view(torch.int32)
+        dst[..., nkf * 1024:].view(E, nt, G, 16, 16).copy_(t)
+    return out.view(torch.uint8).reshape(E, -1).view(torch.int32)
 
 
 def unpermute_fragments(wq: torch.Tensor, N: int, K: int) -> torch.Tensor:
@@ -202,9 +204,9 @@ def prepare_mxfp4_weights(packed: torch.Tensor, scale: torch.Tensor) -> Mxfp4Exp
     return Mxfp4Experts(permute_fragments(packed.view(torch.uint8)), pack_scales(scale), N, K)
 
 
-def pack_scales(scale: torch.Tensor) -> torch.Tensor:
-    """[E, N, K/32] E8M0 -> [E, K/32 + 1, N] uint8: the first (K/32)*N bytes of each expert are the exponents in
-    the kernels' fragment order, the last N bytes the per-row maximum exponent.
+def pack_scales(scale: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """[E, N, K/32] E8M0 -> [E, K/32 + 1, N] uint8 (into `out` when given): the first (K/32)*N bytes of each expert
+    are the exponents in the kernels' fragment order, the last N bytes the per-row maximum exponent.
 
     Column tile nt owns 16*K/32 bytes at nt*16*K/32. K-tile kt (128 K, four 32-blocks) is 64 bytes at kt*64: lane
     l = g*16 + r has the exponent of row r, block 4*kt + g at byte l -- the scale operand of one MFMA tile, one byte
@@ -212,15 +214,15 @@ def pack_scales(scale: torch.Tensor) -> torch.Tensor:
     scale = scale.view(torch.uint8)
     E, N, KB = scale.shape
     nt, nkf, G = N // 16, KB // 4, KB % 4
+    if out is None:
+        out = torch.empty((E, KB + 1, N), dtype=torch.uint8, device=scale.device)
+    body = out.view(E, -1)[:, : KB * N].view(E, nt, 16 * KB)
     s = scale.reshape(E, nt, 16, KB)                                                     # [E, nt, r, kb]
-    parts = []
     if nkf:
-        parts.append(s[..., : nkf * 4].reshape(E, nt, 16, nkf, 4).permute(0, 1, 3, 4, 2).reshape(E, nt, nkf * 64))
+        body[..., : nkf * 64].view(E, nt, nkf, 4, 16).copy_(
+            s[..., : nkf * 4].reshape(E, nt, 16, nkf, 4).permute(0, 1, 3, 4, 2))         # [E, nt, kt, g, r]
     if G:
-        parts.append(s[..., nkf * 4:].permute(0, 1, 3, 2).reshape(E, nt, G * 16))    # [E, nt, g, r]
-    body = parts[0] if len(parts) == 1 else torch.cat(parts, dim=2)
-    out = torch.empty((E, KB + 1, N), dtype=torch.uint8, device=scale.device)
-    out.view(E, -1)[:, : KB * N].copy_(body.reshape(E, KB * N))
+        body[..., nkf * 64:].view(E, nt, G, 16).copy_(s[..., nkf * 4:].permute(0, 1, 3, 2))   # [E, nt, g, r]
     out[:, KB] = scale.max(dim=2).values
     return out
 

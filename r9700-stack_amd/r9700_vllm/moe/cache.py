@@ -39,6 +39,7 @@ _BOUND = False
 _PROFILE: torch.Tensor | None = None
 _PROFILE_LOADED = False
 _HOST_BUFFERS: list = []          # (pointer, bytes) of every mapped host buffer: held until the process ends
+HOST_COPY_BYTES = 512 << 20       # largest single device -> host transfer of to_host
 
 
 def _L():
@@ -90,11 +91,13 @@ def is_host(t: torch.Tensor) -> bool:
 
 
 def to_host(t: torch.Tensor) -> torch.Tensor:
-    """Copy a (device) tensor into a fresh mapped host tensor, chunked along dim 0."""
+    """A mapped host copy of `t` (uva_empty). The destination is pinned, so each copy is one DMA; a device source is
+    copied a slab of whole experts (dim-0 slices) at a time so no single transfer exceeds HOST_COPY_BYTES."""
     h = uva_empty(t.shape, t.dtype)
-    step = max(1, (256 << 20) // max(1, t[0].numel() * t.element_size()))
-    for i in range(0, t.shape[0], step):
-        h[i:i + step].copy_(t[i:i + step])
+    per = max(1, t[0].numel() * t.element_size()) if t.dim() and t.shape[0] else 1
+    rows = max(1, HOST_COPY_BYTES // per)
+    for lo in range(0, t.shape[0] if t.dim() else 1, rows):
+        h[lo:lo + rows].copy_(t[lo:lo + rows])
     return h
 
 
@@ -137,51 +140,62 @@ def stats_enabled() -> bool:
 
 
 STAT_FIELDS = ("steps", "distinct", "inserts", "read_through", "wide")
-_STATS: list = []
-_STATS_THREAD = None
+
+
+class _StatsReporter:
+    """Per-layer cache counters (each cached layer's device tensor `stats`, STAT_FIELDS) and one daemon thread that
+    logs the change over every R9K_EXPERT_CACHE_STATS_SEC seconds (0 = no thread). A reporter that fails stops
+    itself: a diagnostic never takes the worker down."""
+
+    def __init__(self):
+        self.layers: list = []
+        self.thread = None
+
+    def add(self, cache) -> None:
+        self.layers.append(cache)
+        period = float(os.environ.get("R9K_EXPERT_CACHE_STATS_SEC", "10") or 0)
+        if self.thread is None and period > 0:
+            import threading
+            self.thread = threading.Thread(target=self._run, args=(period,), name="r9k-cache-stats", daemon=True)
+            self.thread.start()
+
+    def snapshot(self) -> torch.Tensor:
+        if not self.layers:
+            return torch.zeros((0, len(STAT_FIELDS)), dtype=torch.int64)
+        return torch.stack([c.stats for c in self.layers]).cpu()
+
+    def _run(self, period: float) -> None:
+        import time
+        prev = None
+        while True:
+            time.sleep(period)
+            try:
+                now = self.snapshot()
+                if prev is not None and now.shape == prev.shape and int((now - prev)[:, 0].sum()) > 0:
+                    c = self.layers[0]
+                    logger.info("r9700: expert cache over %.0f s (S=%d, threshold %d, insert cap %d): %s", period,
+                                c.S, c.max_distinct, c.max_inserts, stats_line(now - prev, sum(c.bytes) / 2**20))
+                prev = now
+            except Exception as e:
+                logger.warning("r9700: expert cache stats reporter stopped: %s", e)
+                return
+
+
+_REPORTER = _StatsReporter()
 
 
 def stats_snapshot() -> torch.Tensor:
     """[layers, 5] int64 on the host: per cached layer, totals since load of STAT_FIELDS."""
-    if not _STATS:
-        return torch.zeros((0, len(STAT_FIELDS)), dtype=torch.int64)
-    return torch.stack([c.stats for c in _STATS]).cpu()
+    return _REPORTER.snapshot()
 
 
 def stats_line(delta: torch.Tensor, mib_per_expert: float) -> str:
-    """One line for a [layers, 5] difference of two snapshots; per layer-step means over the layers that stepped."""
-    t = delta.sum(0).tolist()
-    n = max(t[0], 1)
-    return (f"{t[0]} layer-steps: routed {t[1] / n:.1f} distinct experts, {t[2] / n:.1f} inserted, "
-            f"{t[3] / n:.1f} read through from host ({t[3] / n * mib_per_expert:.0f} MiB), "
-            f"{100.0 * t[4] / n:.0f}% of steps over the insert threshold")
-
-
-def _stats_loop(period: float):
-    import time
-    last = None
-    while True:
-        time.sleep(period)
-        try:
-            cur = stats_snapshot()
-            if last is not None and cur.shape == last.shape and int((cur - last)[:, 0].sum()) > 0:
-                c = _STATS[0]
-                logger.info("r9700: expert cache, last %.0f s (S=%d, threshold %d, insert cap %d): %s", period, c.S,
-                            c.max_distinct, c.max_inserts, stats_line(cur - last, sum(c.bytes) / 2**20))
-            last = cur
-        except Exception as e:                   # a diagnostic must never take the worker down
-            logger.warning("r9700: expert cache stats reader stopped: %s", e)
-            return
-
-
-def _stats_register(cache) -> None:
-    global _STATS_THREAD
-    _STATS.append(cache)
-    period = float(os.environ.get("R9K_EXPERT_CACHE_STATS_SEC", "10") or 0)
-    if _STATS_THREAD is None and period > 0:
-        import threading
-        _STATS_THREAD = threading.Thread(target=_stats_loop, args=(period,), name="r9k-cache-stats", daemon=True)
-        _STATS_THREAD.start()
+    """One line for a [layers, 5] difference of two snapshots: per layer-step means over the layers that stepped."""
+    steps, distinct, inserts, through, wide = delta.sum(0).tolist()
+    n = max(steps, 1)
+    return (f"{steps} layer-steps: routed {distinct / n:.1f} distinct experts, {inserts / n:.1f} inserted, "
+            f"{through / n:.1f} read through from host ({through / n * mib_per_expert:.0f} MiB), "
+            f"{100.0 * wide / n:.0f}% of steps over the insert threshold")
 
 
 class LayerCache:
@@ -201,43 +215,50 @@ class LayerCache:
         self.fold = (False, False)
         if not (is_host(w13) and is_host(w2)):
             raise ValueError("LayerCache: w13 / w2 must be mapped host tensors (to_host / uva_empty)")
+        # host store (the backing copy of every expert) and the VRAM arena of S slots with the same slab shapes
         self.h_w13, self.h_w2 = w13, w2
-        self.h_s13 = s13 if is_host(s13) else to_host(s13.contiguous())
-        self.h_s2 = s2 if is_host(s2) else to_host(s2.contiguous())
-        S = self.S
-        self.a_w13 = torch.empty((S, *w13.shape[1:]), dtype=w13.dtype, device=dev)
-        self.a_w2 = torch.empty((S, *w2.shape[1:]), dtype=w2.dtype, device=dev)
-        self.a_s13 = torch.empty((S, *self.h_s13.shape[1:]), dtype=torch.uint8, device=dev)
-        self.a_s2 = torch.empty((S, *self.h_s2.shape[1:]), dtype=torch.uint8, device=dev)
-        self.bytes = [w13[0].numel() * w13.element_size(), w2[0].numel() * w2.element_size(),
-                      self.h_s13[0].numel(), self.h_s2[0].numel()]
-        for b in self.bytes:
-            if b % 16:
-                raise ValueError(f"LayerCache: per-expert slab sizes must be multiples of 16 bytes: {self.bytes}")
-        i32 = dict(dtype=torch.int32, device=dev)
-        self.table = torch.full((E,), -1, **i32)
-        self.map_cold = torch.arange(E, **i32)
-        self.slot_expert = torch.full((S,), -1, **i32)
-        self.slot_stamp = torch.zeros((S,), dtype=torch.int64, device=dev)
-        self.routed = torch.zeros((E,), dtype=torch.uint8, device=dev)
-        self.step = torch.zeros((1,), dtype=torch.int64, device=dev)
-        self.max_inserts = min(int(os.environ.get("R9K_LRU_MAX_INSERTS", "64")), S)
-        self.max_distinct = int(S * float(os.environ.get("R9K_LRU_THRESH", "0.99")))
-        self.miss = torch.full((max(1, self.max_inserts), 2), -1, **i32)
-        # rows per step up to which the cold pass cannot have work: distinct <= rows <= both limits
-        self.no_cold_limit = min(self.max_distinct, self.max_inserts) if S > self.max_distinct else 0
-        self.n_miss = torch.zeros((1,), **i32)
-        self.fused = os.environ.get("R9K_LRU_FUSED", "1") == "1"
-        self._one = None
-        self._one_old: list = []
-        g = os.environ.get("R9K_LRU_GATHER", "64,16").split(",")
-        self.chunks, self.lanes = int(g[0]), int(g[1])
-        self.stage = None
+        self.h_s13, self.h_s2 = (s if is_host(s) else to_host(s.contiguous()) for s in (s13, s2))
+        store = (self.h_w13, self.h_w2, self.h_s13, self.h_s2)
+        self.a_w13, self.a_w2, self.a_s13, self.a_s2 = (
+            torch.empty((self.S, *h.shape[1:]), dtype=h.dtype, device=dev) for h in store)
+        self.bytes = [h[0].numel() * h.element_size() for h in store]
+        if any(b % 16 for b in self.bytes):
+            raise ValueError(f"LayerCache: per-expert slab sizes must be multiples of 16 bytes: {self.bytes}")
+        self._init_lru_state(dev)
+        self._init_policy()
         self._warm_start()
         self.stats = None
         if stats_enabled():
             self.stats = torch.zeros((len(STAT_FIELDS),), dtype=torch.int64, device=dev)
-            _stats_register(self)
+            _REPORTER.add(self)
+
+    def _init_lru_state(self, dev) -> None:
+        """table [E] (expert -> slot, -1 = host), map_cold [E] (expert -> itself when not resident, else -1),
+        slot_expert [S], slot_stamp [S] (step of last use), routed [E] flags, the step counter."""
+        E, S = self.E, self.S
+        self.table = torch.full((E,), -1, dtype=torch.int32, device=dev)
+        self.map_cold = torch.arange(E, dtype=torch.int32, device=dev)
+        self.slot_expert = torch.full((S,), -1, dtype=torch.int32, device=dev)
+        self.slot_stamp = torch.zeros((S,), dtype=torch.int64, device=dev)
+        self.routed = torch.zeros((E,), dtype=torch.uint8, device=dev)
+        self.step = torch.zeros((1,), dtype=torch.int64, device=dev)
+
+    def _init_policy(self) -> None:
+        """Insert cap and read-through threshold (R9K_LRU_MAX_INSERTS, R9K_LRU_THRESH), the miss list they size,
+        the gather launch shape (R9K_LRU_GATHER = "chunks,lanes") and the fused manage + align switch."""
+        S, dev = self.S, self.table.device
+        self.max_inserts = min(int(os.environ.get("R9K_LRU_MAX_INSERTS", "64")), S)
+        self.max_distinct = int(S * float(os.environ.get("R9K_LRU_THRESH", "0.99")))
+        self.miss = torch.full((max(1, self.max_inserts), 2), -1, dtype=torch.int32, device=dev)
+        self.n_miss = torch.zeros((1,), dtype=torch.int32, device=dev)
+        # a step of at most this many routed rows cannot need the cold pass: its distinct experts fit both limits
+        self.no_cold_limit = min(self.max_distinct, self.max_inserts) if S > self.max_distinct else 0
+        self.fused = os.environ.get("R9K_LRU_FUSED", "1") == "1"
+        chunks, lanes = os.environ.get("R9K_LRU_GATHER", "64,16").split(",")
+        self.chunks, self.lanes = int(chunks), int(lanes)
+        self._one = None
+        self._one_old: list = []
+        self.stage = None
 
     def _warm_start(self):
         prof = _profile()
@@ -353,26 +374,30 @@ class LayerCache:
     def stage_cold(self, topk_ids: torch.Tensor):
         raise RuntimeError("LayerCache.stage_cold: bulk staging of cold experts is not built for gfx950")
 
+    def _experts(self, w13, s13, w2, s2):
+        return (K.Mxfp4Experts(w13, s13, self.N1, self.K1, self.fold[0]),
+                K.Mxfp4Experts(w2, s2, self.N2, self.K2, self.fold[1]))
+
     def hot(self):
-        return (K.Mxfp4Experts(self.a_w13, self.a_s13, self.N1, self.K1, self.fold[0]),
-                K.Mxfp4Experts(self.a_w2, self.a_s2, self.N2, self.K2, self.fold[1]))
+        """(w13, w2) experts over the VRAM arena: the pass whose ids go through `table`."""
+        return self._experts(self.a_w13, self.a_s13, self.a_w2, self.a_s2)
 
     def cold(self):
-        return (K.Mxfp4Experts(self.h_w13, self.h_s13, self.N1, self.K1, self.fold[0]),
-                K.Mxfp4Experts(self.h_w2, self.h_s2, self.N2, self.K2, self.fold[1]))
+        """(w13, w2) experts over the mapped host store: the pass whose ids go through `map_cold`."""
+        return self._experts(self.h_w13, self.h_s13, self.h_w2, self.h_s2)
 
 
 def slots_per_layer(bytes_per_expert: int) -> int:
-    """Slots per cached layer: R9K_EXPERT_CACHE_SLOTS if set, else the R9K_EXPERT_CACHE_GB budget spread over the
-    layers that will be cached (R9K_EXPERT_CACHE_LAYERS, default all MoE layers)."""
-    slots = int(os.environ.get("R9K_EXPERT_CACHE_SLOTS", "0") or 0)
-    if slots > 0:
-        return slots
-    gb = budget_gb()
-    if gb <= 0:
+    """VRAM slots of each cached layer: R9K_EXPERT_CACHE_SLOTS when set; else the R9K_EXPERT_CACHE_GB budget shared
+    by the cached layers (R9K_EXPERT_CACHE_LAYERS, default every MoE layer of the model), in whole experts; 0 = off."""
+    fixed = int(os.environ.get("R9K_EXPERT_CACHE_SLOTS", "0") or 0)
+    if fixed > 0:
+        return fixed
+    budget = int(budget_gb() * 2**30)
+    if budget <= 0:
         return 0
-    nl = int(os.environ.get("R9K_EXPERT_CACHE_LAYERS", "0") or 0) or _num_moe_layers()
-    return int(gb * 2**30 // (nl * bytes_per_expert))
+    layers = int(os.environ.get("R9K_EXPERT_CACHE_LAYERS", "0") or 0) or _num_moe_layers()
+    return budget // layers // bytes_per_expert
 
 
 def host_only() -> bool:

@@ -1,10 +1,14 @@
-"""torch.library custom ops around libr9k's ctypes kernels, so they can sit inside a torch.compile'd graph and be
-captured into HIP graphs (reference: r9700_vllm/ops.py:1-170, MXFP4 path).
+"""torch.library custom ops over libr9k's ctypes kernels, so the dense linears can sit inside a torch.compile'd
+graph (Dynamo cannot trace a ctypes call) and be captured into HIP graphs. The reference's r9700_vllm/ops.py surface
+for the 4-bit path:
 
-  torch.ops.r9700.mxfp4_linear(x[M,K] bf16, wq, wsr, N, K, fold) -> [M,N] bf16   MXFP4 weight x per-token fp8 act
-  torch.ops.r9700.nvfp4_linear(x[M,K] bf16, wq, ws, wg, N, K) -> [M,N] bf16      native NVFP4 weight (exact bits)
+  torch.ops.r9700.mxfp4_linear(x [M, K] bf16, wq, wsr, N, K, fold) -> [M, N] bf16   MXFP4 weight, per-token fp8 act
+  torch.ops.r9700.nvfp4_linear(x [M, K] bf16, wq, ws, wg, N, K) -> [M, N] bf16      native NVFP4 weight (exact bits)
 
-The reference's fp8_linear / fp8_block_linear (dense fp8 GEMMs) are not part of the gfx950 MoE build.
+plus `mxfp4_gemm_q` (the GEMM on already-quantised rows, which the shared expert uses). A dense linear is the grouped
+MoE GEMM with one expert and identity routing tables (`IdentityTables`); at decode widths the MXFP4 linear is one
+launch with the activation quant inside (kernels.moe.dense_mxfp4_qa). The reference's fp8_linear / fp8_block_linear
+(dense fp8 GEMMs) are outside this build.
 """
 from __future__ import annotations
 
@@ -13,38 +17,44 @@ import torch
 from ._compat import register_custom_op
 
 _LIB = torch.library.Library("r9700", "FRAGMENT")
-_DONE = False
-
-_MX_TABLES: dict[tuple, tuple] = {}
+_registered = False
 
 
-def _identity_tables(x, M, MT=None):
-    """Routing tables for a dense GEMM: sorted ids 0..Mpad-1, every block on expert 0 (cached per shape)."""
-    from .kernels import moe as KM
-    if MT is None:
-        MT = 4 if M >= 64 else (2 if M >= 32 else 1)
-    blk = KM.MOE_BLOCK * MT
-    mpad = (M + blk - 1) // blk * blk
-    key = (x.device.index, mpad, blk)
-    t = _MX_TABLES.get(key)
-    if t is None:
-        t = (torch.arange(mpad, dtype=torch.int32, device=x.device),
-             torch.zeros(mpad // blk, dtype=torch.int32, device=x.device),
-             torch.full((1,), mpad, dtype=torch.int32, device=x.device))
-        _MX_TABLES[key] = t
-    return t, MT
+class IdentityTables:
+    """Routing tables that make the grouped GEMM a dense one: rows 0..Mpad-1 in order, every block on expert 0,
+    Mpad = M rounded up to the block. Built once per (device, Mpad, block) and reused (graph capture needs fixed
+    addresses, and a decode step asks for the same few shapes every time)."""
+
+    _cache: dict = {}
+
+    @classmethod
+    def get(cls, device: torch.device, M: int, block: int):
+        mpad = -(-M // block) * block
+        key = (device.type, device.index, mpad, block)
+        t = cls._cache.get(key)
+        if t is None:
+            i32 = dict(dtype=torch.int32, device=device)
+            t = cls._cache[key] = (torch.arange(mpad, **i32), torch.zeros(mpad // block, **i32),
+                                   torch.tensor([mpad], **i32))
+        return t
+
+
+def _decode_mt(M: int) -> int:
+    """M-tiles per routing block of a dense decode GEMM: 16-row blocks up to 31 rows, 32 up to 63, then 64."""
+    return 4 if M >= 64 else (2 if M >= 32 else 1)
 
 
 def mxfp4_gemm_q(q: torch.Tensor, s: torch.Tensor, W, out: torch.Tensor, M: int, cfg, topk_w=None) -> None:
-    """out [M, W.N] bf16 = dequant(q * s) @ W^T (* topk_w[row]) for a dense MXFP4 weight on the kernel `cfg` names:
-    the prefill entry ("P", cfg) or the decode kernel (a (WV, SK, NPW[, MT]) tuple)."""
+    """out [M, W.N] bf16 = dequant(q, s) @ W^T (* topk_w[row]) for one dense MXFP4 weight, on the kernel `cfg` names:
+    ("P", prefill cfg) or a decode tuple (WV, SK, NPW[, MT]) whose only meaning here is the optional MT."""
     from .kernels import moe as KM
     if KM.is_prefill_cfg(cfg):
-        t, _ = _identity_tables(q, M, KM.prefill_block(cfg[1]) // KM.MOE_BLOCK)
-        KM.moe_gemm(q, s, W, out, *t, M, 1, topk_w, num_experts=1, prefill=cfg[1])
-    else:
-        t, MT = _identity_tables(q, M, cfg[3] if len(cfg) > 3 else None)
-        KM.moe_gemm(q, s, W, out, *t, M, 1, topk_w, *cfg[:3], num_experts=1, MT=MT)
+        tabs = IdentityTables.get(q.device, M, KM.prefill_block(cfg[1]))
+        KM.moe_gemm(q, s, W, out, *tabs, M, 1, topk_w, num_experts=1, prefill=cfg[1])
+        return
+    MT = cfg[3] if len(cfg) > 3 else _decode_mt(M)
+    tabs = IdentityTables.get(q.device, M, KM.MOE_BLOCK * MT)
+    KM.moe_gemm(q, s, W, out, *tabs, M, 1, topk_w, *cfg[:3], num_experts=1, MT=MT)
 
 
 def _mxfp4_linear(x: torch.Tensor, wq: torch.Tensor, wsr: torch.Tensor, N: int, K: int, fold: bool = False
@@ -57,22 +67,15 @@ def _mxfp4_linear(x: torch.Tensor, wq: torch.Tensor, wsr: torch.Tensor, N: int, 
     W = KM.Mxfp4Experts(wq, wsr, N, K, fold)
     if M <= KM.DENSE_QA_MAX_M and KM.dense_mxfp4_qa(x, W, out):   # decode widths: the quant inside the GEMM launch
         return out
-    cfg = KM.pick_cfg(N, K, M=M, kind="mxfp4", fold=fold)
     q, s = KM.quant_rows_fp8(x)
-    mxfp4_gemm_q(q, s, W, out, M, cfg)
+    mxfp4_gemm_q(q, s, W, out, M, KM.pick_cfg(N, K, M=M, kind="mxfp4", fold=fold))
     return out
-
-
-def _mxfp4_linear_fake(x: torch.Tensor, wq: torch.Tensor, wsr: torch.Tensor, N: int, K: int, fold: bool = False
-                       ) -> torch.Tensor:
-    return x.new_empty((x.shape[0], N))
 
 
 def _nvfp4_linear(x: torch.Tensor, wq: torch.Tensor, ws: torch.Tensor, wg: torch.Tensor, N: int, K: int
                   ) -> torch.Tensor:
-    """x [M, K] bf16 -> [M, N] bf16 over native NVFP4 weights (prepare_nvfp4_weights of one expert) with per-row fp8
-    activations (reference: r9700_vllm/ops.py nvfp4_linear): the decode-family kernel below NV_PREFILL_MIN_M rows,
-    the 128 x 128-tile prefill kernel (r9k_moe_4bit_prefill nv = 1) from there."""
+    """Native NVFP4 weights (prepare_nvfp4_weights of one expert) with per-row fp8 activations: the decode-family
+    kernel below NV_PREFILL_MIN_M rows, the 128 x 128-tile prefill kernel (r9k_moe_4bit_prefill nv = 1) from there."""
     from .kernels import moe as KM
     M = x.shape[0]
     out = torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
@@ -81,41 +84,54 @@ def _nvfp4_linear(x: torch.Tensor, wq: torch.Tensor, ws: torch.Tensor, wg: torch
     W = KM.Nvfp4Experts(wq, ws, wg, N, K)
     q, s = KM.quant_rows_fp8(x)
     if M >= KM.NV_PREFILL_MIN_M and K % 32 == 0:
-        t, _ = _identity_tables(q, M, KM.prefill_block(KM.NV_PREFILL_CFG) // KM.MOE_BLOCK)
-        KM.moe_gemm(q, s, W, out, *t, M, 1, None, num_experts=1, prefill=KM.NV_PREFILL_CFG)
+        tabs = IdentityTables.get(x.device, M, KM.prefill_block(KM.NV_PREFILL_CFG))
+        KM.moe_gemm(q, s, W, out, *tabs, M, 1, None, num_experts=1, prefill=KM.NV_PREFILL_CFG)
     else:
-        t, MT = _identity_tables(q, M)
-        KM.moe_gemm(q, s, W, out, *t, M, 1, None, num_experts=1, MT=MT)
+        MT = _decode_mt(M)
+        tabs = IdentityTables.get(x.device, M, KM.MOE_BLOCK * MT)
+        KM.moe_gemm(q, s, W, out, *tabs, M, 1, None, num_experts=1, MT=MT)
     return out
+
+
+def _rows_out_fake(x: torch.Tensor, N: int) -> torch.Tensor:
+    return torch.empty((x.shape[0], N), dtype=torch.bfloat16, device=x.device)
+
+
+def _mxfp4_linear_fake(x: torch.Tensor, wq: torch.Tensor, wsr: torch.Tensor, N: int, K: int, fold: bool = False
+                       ) -> torch.Tensor:
+    return _rows_out_fake(x, N)
 
 
 def _nvfp4_linear_fake(x: torch.Tensor, wq: torch.Tensor, ws: torch.Tensor, wg: torch.Tensor, N: int, K: int
                        ) -> torch.Tensor:
-    return x.new_empty((x.shape[0], N))
+    return _rows_out_fake(x, N)
+
+
+_OPS = (("mxfp4_linear", _mxfp4_linear, _mxfp4_linear_fake), ("nvfp4_linear", _nvfp4_linear, _nvfp4_linear_fake))
 
 
 def register() -> None:
-    global _DONE
-    if _DONE:
-        return
-    register_custom_op(_LIB, "mxfp4_linear", _mxfp4_linear, [], _mxfp4_linear_fake)
-    register_custom_op(_LIB, "nvfp4_linear", _nvfp4_linear, [], _nvfp4_linear_fake)
-    _DONE = True
+    global _registered
+    if not _registered:
+        for name, fn, fake in _OPS:
+            register_custom_op(_LIB, name, fn, [], fake)
+        _registered = True
+
+
+def _call_on_rows(op, x: torch.Tensor, K: int, N: int) -> torch.Tensor:
+    """op over x viewed as contiguous bf16 rows [-1, K], the result shaped back to x's leading dims + [N]."""
+    register()
+    rows = x.reshape(-1, K)
+    if rows.dtype != torch.bfloat16:
+        rows = rows.to(torch.bfloat16)
+    return op(rows.contiguous()).reshape(*x.shape[:-1], N)
 
 
 def mxfp4_linear(x: torch.Tensor, wq: torch.Tensor, wsr: torch.Tensor, N: int, K: int, fold: bool = False
                  ) -> torch.Tensor:
-    register()
-    lead = x.shape[:-1]
-    x2 = x.reshape(-1, K)
-    x2 = (x2 if x2.dtype == torch.bfloat16 else x2.to(torch.bfloat16)).contiguous()
-    return torch.ops.r9700.mxfp4_linear(x2, wq, wsr, N, K, fold).reshape(*lead, N)
+    return _call_on_rows(lambda r: torch.ops.r9700.mxfp4_linear(r, wq, wsr, N, K, fold), x, K, N)
 
 
 def nvfp4_linear(x: torch.Tensor, wq: torch.Tensor, ws: torch.Tensor, wg: torch.Tensor, N: int, K: int
                  ) -> torch.Tensor:
-    register()
-    lead = x.shape[:-1]
-    x2 = x.reshape(-1, K)
-    x2 = (x2 if x2.dtype == torch.bfloat16 else x2.to(torch.bfloat16)).contiguous()
-    return torch.ops.r9700.nvfp4_linear(x2, wq, ws, wg, N, K).reshape(*lead, N)
+    return _call_on_rows(lambda r: torch.ops.r9700.nvfp4_linear(r, wq, ws, wg, N, K), x, K, N)
