@@ -483,10 +483,6 @@ def pick_cfg(N: int, K: int, group: int = GROUP, M: int | None = None, kind: str
     The tuple's values are the reference's gfx1201 knobs (ignored by the gfx950 kernel, which sizes its own split);
     they are still returned legal for the shape so callers written against the reference keep working."""
     if kind and M:
-        from .tuned import lookup
-        t = lookup(kind, N, K, M)
-        if t:
-            return t
         if M >= PREFILL_MIN_M and K % prefill_bk(PREFILL_DEFAULT) == 0:
             return ("P", PREFILL_DEFAULT if M >= 512 else PREFILL_DEFAULT_SMALL)
     for WV, SK, NPW in ((2, 4, 2), (4, 2, 1), (2, 5, 2), (4, 1, 1)):
@@ -756,20 +752,25 @@ def moe_topk_quant(logits: torch.Tensor, topk: int, renorm: bool, x: torch.Tenso
 
 
 def align_block_size_ref(topk_ids: torch.Tensor, num_experts: int, block: int = MOE_BLOCK):
-    """Pure-torch equivalent of moe_align_block_size (tests and host-side table builds): pads each expert's rows
-    to a multiple of `block`, pad value = numel. Returns (sorted_ids, expert_ids, ntpp) sized to capacity."""
+    """Host-side moe_align_block_size in the canonical order (tests and host table builds): a stable sort of the
+    routed rows by expert, each expert's run padded to a multiple of `block` with the pad value numel, expert_ids
+    -1 past the used blocks; ids outside [0, num_experts) are left out. Returns (sorted_ids, expert_ids, ntpp) int32,
+    sized to capacity()."""
     flat = topk_ids.flatten().to(torch.int64).cpu()
     numel = flat.numel()
     cap = capacity(numel, num_experts, block)
+    keep = (flat >= 0) & (flat < num_experts)
+    order = torch.argsort(torch.where(keep, flat, num_experts), stable=True)[: int(keep.sum())]
+    counts = torch.bincount(flat[keep], minlength=num_experts)
+    padded = (counts + block - 1) // block * block
+    start = torch.cumsum(padded, 0) - padded                     # first slot of each expert
+    first_row = torch.cumsum(counts, 0) - counts                 # its first entry in `order`
+    e_of = flat[order]
+    slot = start[e_of] + (torch.arange(order.numel()) - first_row[e_of])
     sorted_ids = torch.full((cap,), numel, dtype=torch.int32)
+    sorted_ids[slot] = order.to(torch.int32)
+    total = int(padded.sum())
     expert_ids = torch.full((cap // block,), -1, dtype=torch.int32)
-    pos = 0
-    for e in range(num_experts):
-        rows = (flat == e).nonzero().flatten()
-        if rows.numel() == 0:
-            continue
-        n = (rows.numel() + block - 1) // block * block
-        sorted_ids[pos:pos + rows.numel()] = rows.to(torch.int32)
-        expert_ids[pos // block:(pos + n) // block] = e
-        pos += n
-    return sorted_ids, expert_ids, torch.tensor([pos], dtype=torch.int32)
+    expert_ids[: total // block] = torch.repeat_interleave(torch.arange(num_experts, dtype=torch.int32),
+                                                          padded // block)
+    return sorted_ids, expert_ids, torch.tensor([total], dtype=torch.int32)

@@ -133,3 +133,19 @@ def test_chunk_tokens_plan(M, topk, N1, K1, N2, K2):
     assert len(ch) == -(-M // max(1, BUF_LIMIT // per_token))
     if M * per_token <= BUF_LIMIT:
         assert ch == [(0, M)]
+
+
+def test_align_block_size_ref_matches_oracle_align():
+    """The host-side table builder (a vectorised stable sort) equals the oracle's align (C restatement of the
+    canonical moe_align_block_size order) on random shapes, block sizes and ids outside [0, E)."""
+    from oracle import oracle as O
+    rng = np.random.default_rng(0)
+    for _ in range(200):
+        E, n, blk = int(rng.integers(1, 40)), int(rng.integers(1, 300)), int(2 ** rng.integers(0, 6))
+        ids = torch.from_numpy(rng.integers(-2, E + 2, n).astype(np.int32))
+        s, e, t = K.align_block_size_ref(ids, E, blk)
+        rs, re_, rt = O.align(ids.numpy(), E, blk)
+        N = int(t[0])
+        assert N == int(rt[0])
+        assert np.array_equal(s[:N].numpy(), rs[:N]) and np.array_equal(e[: N // blk].numpy(), re_[: N // blk])
+        assert bool((s[N:] == n).all()) and bool((e[N // blk:] == -1).all())
