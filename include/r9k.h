@@ -141,6 +141,13 @@ int r9k_moe_align(long ids, int numel, int E, int blk, long sorted_ids, long exp
                   long scratch_ints, long stream);
 long r9k_moe_align_scratch_ints(int numel, int E);
 
+/* No counterpart in the reference: r9k_moe_align writing only the live tables (the expert blocks up to ntpp, with
+ * their padding entries); sorted_ids / expert_ids past ntpp are left as they were. For consumers that read no
+ * further than ntpp, as this library's GEMMs: a 256-row layout at decode widths (numel + E * 255 entries, mostly
+ * tail) costs a fraction to build. Arguments and return codes as r9k_moe_align. */
+int r9k_moe_align_live(long ids, int numel, int E, int blk, long sorted_ids, long expert_ids, long ntpp,
+                       long scratch, long scratch_ints, long stream);
+
 /* No counterpart in the reference. r9k_moe_align for callers that cannot allocate (code under HIP graph capture,
  * tight serving loops, harnesses that forbid hipMalloc): no scratch argument, nothing allocated; the multi-workgroup
  * path uses the library's own file-scope device array (r9k_moe_align_noalloc_max_ints() int32 = 1 MiB per GPU, held

@@ -45,6 +45,8 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 constexpr int KT = 128;           // K per MFMA
 constexpr int GROUP = 32;         // MXFP4 block
 constexpr int E8M0_ONE = 127;     // 2^0
+constexpr long MAX_WG = 16384;    // workgroups of one launch at most (64 for each of the 256 CUs); more tile rows
+                                  // are walked grid-stride
 
 template <bool NTL>
 __device__ __forceinline__ u32x4 ld16(const uint8_t* p) {
@@ -71,18 +73,22 @@ __device__ __forceinline__ uint32_t ld1(const uint8_t* p) {
 //   2: down with fp32 A rows [numel, K] (h) quantised on load: each lane group of a row first takes the row's
 //      absmax over all K, then every A chunk is encoded as e4m3(h * (448 / amax)) and the row scale amax / 448
 //      replaces As -- the per-row quant of the standalone SiLU kernel, so fused and unfused results are identical.
+//
+// One call of moe_tile computes the tile of grid row `by` (routing block by / subs, sub-block by % subs). It returns
+// false when that block lies at or past ntpp -- and so does every later one, blocks being in order -- true
+// otherwise (a tile done, or an expert-map hole / all-padding sub-block skipped).
 template <int MT, int NPW, int SK, int U, int FUSE>
-__global__ void __launch_bounds__(WAVE * SK) moe_mxfp4_kernel(
+__device__ __forceinline__ bool moe_tile(
     const uint8_t* __restrict__ A, const float* __restrict__ As, const uint8_t* __restrict__ Wq,
     const uint8_t* __restrict__ Ws, uint16_t* __restrict__ C, const int* __restrict__ sorted_ids,
     const int* __restrict__ expert_ids, const int* __restrict__ ntpp, const float* __restrict__ topk_w,
-    long wq_estride, long ws_estride, int numel, int a_row_div, int K, int N, int blk, int subs) {
+    long wq_estride, long ws_estride, int numel, int a_row_div, int K, int N, int blk, int subs, int by) {
   constexpr int BLK = 16 * MT;
   constexpr bool NTL = MT == 1;                            // decode: every weight byte is read once
   static_assert(FUSE == 0 || (MT == 1 && (FUSE == 2 || NPW == 2)), "fused variants: MT = 1; gate_up NPW = 2");
   extern __shared__ float red[];
 
-  const int rb = blockIdx.y / subs, sub = blockIdx.y - rb * subs;
+  const int rb = by / subs, sub = by - rb * subs;
   const int row0 = rb * blk + sub * BLK;
   const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
   const int g = lane >> 4, r = lane & 15;
@@ -94,8 +100,9 @@ __global__ void __launch_bounds__(WAVE * SK) moe_mxfp4_kernel(
   int fr_in[MT];
 #pragma unroll
   for (int i = 0; i < MT; i++) fr_in[i] = sorted_ids[row0 + i * 16 + r];
-  if (rb * blk >= np || e < 0) return;
-  if (first < 0 || first >= numel || __shfl(fr_in[0], 0, WAVE) >= numel) return;   // padding: end of a block
+  if (rb * blk >= np) return false;
+  if (e < 0) return true;
+  if (first < 0 || first >= numel || __shfl(fr_in[0], 0, WAVE) >= numel) return true;   // padding: end of a block
   const int NT = N / 16;
   const int nkt = (K + KT - 1) / KT, nkt_full = K / KT, tg = (K % KT) / GROUP;
   const int KB = K / GROUP;
@@ -294,7 +301,8 @@ __global__ void __launch_bounds__(WAVE * SK) moe_mxfp4_kernel(
         const float sc = s_sc[i * 16 + row];
         reinterpret_cast<float*>(C)[(size_t)fr * Nh + n] = silu_mul(bf2f(f2bf(vg * sc)), bf2f(f2bf(vu * sc)));
       }
-      return;
+      __syncthreads();                                     // LDS reused by the workgroup's next tile
+      return true;
     }
     for (int idx = tid; idx < TOT; idx += WAVE * SK) {
       const int col = idx & 15, row = (idx >> 4) & 15, ti = idx >> 8;   // ti = j * MT + i
@@ -308,7 +316,24 @@ __global__ void __launch_bounds__(WAVE * SK) moe_mxfp4_kernel(
       for (int s = 0; s < SK; s++) v += red[(size_t)s * TOT + idx];
       C[(size_t)fr * N + n] = f2bf(v * s_sc[i * 16 + row]);
     }
+    __syncthreads();                                       // LDS reused by the workgroup's next tile
   }
+  return true;
+}
+
+// The grid's rows walk the launch's ny = max_blocks * subs tile rows grid-stride (the host caps the grid at
+// MAX_WG workgroups), in ascending order, and a workgroup stops at the first row past ntpp: a launch over a layout
+// whose blocks all lie past ntpp (the table layout the device did not keep) ends after one table read a workgroup.
+template <int MT, int NPW, int SK, int U, int FUSE>
+__global__ void __launch_bounds__(WAVE * SK) moe_mxfp4_kernel(
+    const uint8_t* __restrict__ A, const float* __restrict__ As, const uint8_t* __restrict__ Wq,
+    const uint8_t* __restrict__ Ws, uint16_t* __restrict__ C, const int* __restrict__ sorted_ids,
+    const int* __restrict__ expert_ids, const int* __restrict__ ntpp, const float* __restrict__ topk_w,
+    long wq_estride, long ws_estride, int numel, int a_row_div, int K, int N, int blk, int subs, int ny) {
+  for (int by = blockIdx.y; by < ny; by += gridDim.y)
+    if (!moe_tile<MT, NPW, SK, U, FUSE>(A, As, Wq, Ws, C, sorted_ids, expert_ids, ntpp, topk_w, wq_estride,
+                                        ws_estride, numel, a_row_div, K, N, blk, subs, by))
+      break;
 }
 
 struct Pick { int MT, NPW, SK, U; };
@@ -353,12 +378,12 @@ Pick pick(int MT, int N, int K, int max_blocks) {
 template <int MT, int NPW, int SK, int U, int FUSE = 0>
 int launch_one(dim3 grid, hipStream_t st, long a, long as, long wq, long ws, long c, long sorted_ids,
                long expert_ids, long ntpp, long topk_w, long wq_estride, long ws_estride, int numel, int a_row_div,
-               int K, int N, int blk, int subs) {
+               int K, int N, int blk, int subs, int ny) {
   const size_t smem = SK > 1 ? (size_t)SK * NPW * MT * 256 * sizeof(float) : 0;
   hipLaunchKernelGGL((moe_mxfp4_kernel<MT, NPW, SK, U, FUSE>), grid, dim3(WAVE * SK), smem, st, (const uint8_t*)a,
                      (const float*)as, (const uint8_t*)wq, (const uint8_t*)ws, (uint16_t*)c, (const int*)sorted_ids,
                      (const int*)expert_ids, (const int*)ntpp, (const float*)topk_w, wq_estride, ws_estride, numel,
-                     a_row_div, K, N, blk, subs);
+                     a_row_div, K, N, blk, subs, ny);
   return 0;
 }
 
@@ -383,14 +408,16 @@ int moe_dispatch(long a, long as, long wq, long ws, long c, long sorted_ids, lon
   const int subs = blk / (16 * MT);
   const long ny = (long)max_blocks * subs;
   if (ny > 0x7fffffffL || p.NPW < 1) return -3;
-  const dim3 grid(fuse == 1 ? N / 32 : (N / 16 + p.NPW - 1) / p.NPW, (unsigned)ny);
+  const unsigned gx = fuse == 1 ? N / 32 : (N / 16 + p.NPW - 1) / p.NPW;
+  const long cap_y = MAX_WG / (long)gx > 0 ? MAX_WG / (long)gx : 1;
+  const dim3 grid(gx, (unsigned)(ny < cap_y ? ny : cap_y));
   const long wq_estride = (long)N * K / 2;
   const hipStream_t st = (hipStream_t)stream;
   if (fuse) {
 #define F(FV, NPWv, SKv, Uv)                                                                                      \
   if (fuse == FV && p.NPW == NPWv && p.SK == SKv && p.U == Uv)                                                    \
     return launch_one<1, NPWv, SKv, Uv, FV>(grid, st, a, as, wq, ws, c, sorted_ids, expert_ids, ntpp, topk_w,     \
-                                            wq_estride, ws_estride, numel, a_row_div, K, N, blk, subs);
+                                            wq_estride, ws_estride, numel, a_row_div, K, N, blk, subs, (int)ny);
 #define FU(FV, NPWv, SKv) F(FV, NPWv, SKv, 1) F(FV, NPWv, SKv, 2) F(FV, NPWv, SKv, 4)
 #define FS(FV, NPWv) FU(FV, NPWv, 1) FU(FV, NPWv, 2) FU(FV, NPWv, 4)
     FS(1, 2) FS(2, 1) FS(2, 2) FS(2, 4)
@@ -402,7 +429,7 @@ int moe_dispatch(long a, long as, long wq, long ws, long c, long sorted_ids, lon
 #define L(MTv, NPWv, SKv, Uv)                                                                               \
   if (p.MT == MTv && p.NPW == NPWv && p.SK == SKv && p.U == Uv)                                             \
     return launch_one<MTv, NPWv, SKv, Uv>(grid, st, a, as, wq, ws, c, sorted_ids, expert_ids, ntpp, topk_w, \
-                                          wq_estride, ws_estride, numel, a_row_div, K, N, blk, subs);
+                                          wq_estride, ws_estride, numel, a_row_div, K, N, blk, subs, (int)ny);
 #define LU(MTv, NPWv, SKv) L(MTv, NPWv, SKv, 1) L(MTv, NPWv, SKv, 2) L(MTv, NPWv, SKv, 4)
 #define LS(MTv, NPWv) LU(MTv, NPWv, 1) LU(MTv, NPWv, 2) LU(MTv, NPWv, 4)
   LS(1, 1) LS(1, 2) LS(1, 4) LS(2, 1) LS(2, 2) LS(2, 4) LS(4, 1) LS(4, 2)

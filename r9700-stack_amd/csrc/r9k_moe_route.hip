@@ -215,7 +215,7 @@ __device__ __forceinline__ int padded_scan(TabLds<NT>& sh, int E, int blk) {
 template <int NT>
 __device__ __forceinline__ void write_layout(TabLds<NT>& sh, int E, int blk, int numel, int total, int pre,
                                              int share, int nshare, int* __restrict__ sorted_ids,
-                                             int* __restrict__ expert_ids) {
+                                             int* __restrict__ expert_ids, bool write_tail = true) {
   constexpr int NW = NT / WAVE;
   const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
   if (tid < E) sh.cursor[tid] = sh.offs[tid] + pre;
@@ -227,6 +227,10 @@ __device__ __forceinline__ void write_layout(TabLds<NT>& sh, int E, int blk, int
       for (int b = o / blk + lane; b < (o + n) / blk; b += WAVE) expert_ids[b] = e;
       for (int i = o + c + lane; i < o + n; i += WAVE) sorted_ids[i] = numel;
     }
+  }
+  if (!write_tail) {                            // live entries only: the capacity past ntpp is left as it was
+    lds_barrier();
+    return;
   }
   const long cap = ((long)numel + (long)E * (blk - 1) + blk - 1) / blk * blk;
   const long tail = cap - total, per = (tail + nshare - 1) / nshare;
@@ -293,7 +297,7 @@ __device__ __forceinline__ void stable_round(TabLds<NT>& sh, const short* ids, i
 template <int NT>
 __device__ __forceinline__ void build_tables(TabLds<NT>& sh, const short* ids, int numel, int E, int blk,
                                              int* __restrict__ sorted_ids, int* __restrict__ expert_ids,
-                                             int* __restrict__ ntpp) {
+                                             int* __restrict__ ntpp, bool tail = true) {
   for (int t = threadIdx.x; t < numel; t += NT) {
     const int e = ids[t];
     if (e >= 0) atomicAdd(&sh.cnt[e], 1);
@@ -301,7 +305,7 @@ __device__ __forceinline__ void build_tables(TabLds<NT>& sh, const short* ids, i
   lds_barrier();
   const int total = padded_scan(sh, E, blk);
   if (threadIdx.x == 0) ntpp[0] = total;
-  write_layout(sh, E, blk, numel, total, 0, 0, 1, sorted_ids, expert_ids);
+  write_layout(sh, E, blk, numel, total, 0, 0, 1, sorted_ids, expert_ids, tail);
   for (int base = 0; base < numel; base += NT) stable_round(sh, ids, base, numel, 0, E, sorted_ids);
 }
 
@@ -609,7 +613,7 @@ __global__ void __launch_bounds__(RW * WAVE) topk_quant_kernel(const uint16_t* _
 // Tables from ids in global memory, one workgroup, numel <= SMALL_MAX.
 __global__ void __launch_bounds__(AT) align_single_kernel(const int* __restrict__ ids, int numel, int E, int blk,
                                                           int* __restrict__ sorted_ids, int* __restrict__ expert_ids,
-                                                          int* __restrict__ ntpp) {
+                                                          int* __restrict__ ntpp, int tail) {
   __shared__ TabLds<AT> sh;
   __shared__ short lids[SMALL_MAX];
   zero_counts(sh, E);
@@ -618,7 +622,7 @@ __global__ void __launch_bounds__(AT) align_single_kernel(const int* __restrict_
     lids[t] = (short)(e >= 0 && e < E ? e : -1);
   }
   lds_barrier();
-  build_tables(sh, lids, numel, E, blk, sorted_ids, expert_ids, ntpp);
+  build_tables(sh, lids, numel, E, blk, sorted_ids, expert_ids, ntpp, tail != 0);
 }
 
 // Tables from ids in global memory for any numel in one workgroup without scratch (the reference route entry's
@@ -724,7 +728,7 @@ __global__ void __launch_bounds__(AT) align_count_kernel(const int* __restrict__
 // rows.
 __global__ void __launch_bounds__(AT) align_scatter_kernel(const int* __restrict__ ids, int numel, int E, int blk,
                                                            int* __restrict__ sorted_ids, int* __restrict__ expert_ids,
-                                                           const int* __restrict__ scratch) {
+                                                           const int* __restrict__ scratch, int tail) {
   __shared__ TabLds<AT> sh;
   __shared__ short lids[CH];
   const int* __restrict__ hist = scratch + ALIGN_HIST;
@@ -743,7 +747,7 @@ __global__ void __launch_bounds__(AT) align_scatter_kernel(const int* __restrict
   }
   const int total = hist[(size_t)(nch + 2) * E];
   lds_barrier();
-  write_layout(sh, E, blk, numel, total, pre, c, nch, sorted_ids, expert_ids);
+  write_layout(sh, E, blk, numel, total, pre, c, nch, sorted_ids, expert_ids, tail != 0);
   for (int base = 0; base < n; base += AT) stable_round(sh, lids, base, n, t0, E, sorted_ids);
 }
 
@@ -779,17 +783,17 @@ long align_scratch_ints(int numel, int E) {
 }
 
 int launch_align(const int* ids, int numel, int E, int blk, int* sorted_ids, int* expert_ids, int* ntpp,
-                 int* scratch, hipStream_t st) {
+                 int* scratch, hipStream_t st, int tail = 1) {
   if (numel <= SMALL_MAX) {
     hipLaunchKernelGGL(align_single_kernel, dim3(1), dim3(AT), 0, st, ids, numel, E, blk, sorted_ids, expert_ids,
-                       ntpp);
+                       ntpp, tail);
     return 0;
   }
   if (!scratch) return 1;
   const int nch = (numel + CH - 1) / CH;
   hipLaunchKernelGGL(align_count_kernel, dim3(nch), dim3(AT), 0, st, ids, numel, E, blk, scratch, ntpp);
   hipLaunchKernelGGL(align_scatter_kernel, dim3(nch), dim3(AT), 0, st, ids, numel, E, blk, sorted_ids, expert_ids,
-                     (const int*)scratch);
+                     (const int*)scratch, tail);
   return 0;
 }
 
@@ -1011,6 +1015,21 @@ int* noalloc_scratch() {
 }
 
 }  // namespace
+
+// No counterpart in the reference: r9k_moe_align writing only the live part of the tables -- the expert blocks up to
+// ntpp with their padding entries -- and leaving the capacity past ntpp as it was, for consumers that read no
+// further than ntpp (this library's GEMMs do not). A capacity-sized layout whose tail dominates (256-row blocks over
+// many experts at decode widths: numel + E * 255 entries) costs a fraction to build. Arguments and codes as
+// r9k_moe_align.
+extern "C" int r9k_moe_align_live(long ids, int numel, int E, int blk, long sorted_ids, long expert_ids, long ntpp,
+                                  long scratch, long scratch_ints, long stream) {
+  if (numel < 1 || E < 1 || E > MAX_E || blk < 1 || (blk & (blk - 1))) return 1;
+  if (numel > SMALL_MAX && (!scratch || scratch_ints < r9k_moe_align_scratch_ints(numel, E))) return 1;
+  if (launch_align((const int*)ids, numel, E, blk, (int*)sorted_ids, (int*)expert_ids, (int*)ntpp, (int*)scratch,
+                   (hipStream_t)stream, 0))
+    return 1;
+  return (int)hipGetLastError();
+}
 
 // No counterpart in the reference: r9k_moe_align for callers that cannot allocate (graph capture, tight serving
 // loops, allocation-free harnesses). The scratch is the library's own 1 MiB device array per GPU (see above), so

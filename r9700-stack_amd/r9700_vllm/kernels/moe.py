@@ -58,6 +58,8 @@ def lib() -> ctypes.CDLL:
         L.r9k_moe_topk_quant.argtypes = [l, i, l, l, i, i, i, i, l, l, i, l, l, l]
         L.r9k_moe_align.restype = i
         L.r9k_moe_align.argtypes = [l, i, i, i, l, l, l, l, l, l]
+        L.r9k_moe_align_live.restype = i
+        L.r9k_moe_align_live.argtypes = [l, i, i, i, l, l, l, l, l, l]
         L.r9k_moe_align_scratch_ints.restype = l
         L.r9k_moe_align_noalloc.restype = i
         L.r9k_moe_align_noalloc.argtypes = [l, i, i, i, l, l, l, l]
@@ -660,10 +662,12 @@ def _align_scratch(device: torch.device, n: int) -> torch.Tensor:
     return t
 
 
-def moe_align(topk_ids: torch.Tensor, block: int, num_experts: int, expert_map: torch.Tensor | None = None):
+def moe_align(topk_ids: torch.Tensor, block: int, num_experts: int, expert_map: torch.Tensor | None = None,
+              live_only: bool = False):
     """GPU moe_align_block_size: (sorted_ids [cap], expert_ids [cap/block], ntpp [1]) int32, rows ascending within
     each expert (align_block_size_ref's canonical order). expert_map (global -> local id, -1 = not here) is
-    applied first; rows of experts outside [0, num_experts) are left out of the tables."""
+    applied first; rows of experts outside [0, num_experts) are left out of the tables. live_only writes the entries
+    up to ntpp only (r9k_moe_align_live; the rest of the capacity is left unset), enough for this library's GEMMs."""
     ids = topk_ids.reshape(-1)
     if expert_map is not None:
         ids = expert_map[ids.long()]
@@ -677,8 +681,9 @@ def moe_align(topk_ids: torch.Tensor, block: int, num_experts: int, expert_map: 
     L = lib()
     n = L.r9k_moe_align_scratch_ints(numel, num_experts)
     scratch = _align_scratch(dev, n)
-    rc = L.r9k_moe_align(ids.data_ptr(), numel, num_experts, block, sorted_ids.data_ptr(), expert_ids.data_ptr(),
-                         ntpp.data_ptr(), scratch.data_ptr(), scratch.numel(), _stream())
+    fn = L.r9k_moe_align_live if live_only else L.r9k_moe_align
+    rc = fn(ids.data_ptr(), numel, num_experts, block, sorted_ids.data_ptr(), expert_ids.data_ptr(), ntpp.data_ptr(),
+            scratch.data_ptr(), scratch.numel(), _stream())
     if rc:
         raise RuntimeError(f"r9k_moe_align failed ({rc}) numel={numel} E={num_experts} block={block}")
     return sorted_ids, expert_ids, ntpp

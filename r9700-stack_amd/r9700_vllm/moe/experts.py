@@ -225,7 +225,7 @@ class R9700Mxfp4Experts(_experts_base()):
             if (big is None and nv is None and expert_map is None and not MOE_FUSE and bc is not None
                     and K.DEVICE_BLOCKS_MIN > 0 and numel >= K.DEVICE_BLOCKS_MIN):
                 # skew the host cannot see: the 256-row layout too, the device keeps one (the other's GEMMs exit)
-                tabs_big = K.moe_align(topk_ids, bc[1], E)
+                tabs_big = K.moe_align(topk_ids, bc[1], E, live_only=True)
                 K.pick_blocks(tabs[2], tabs_big[2], numel, bc[1])
                 passes.append((W1, W2, tabs_big, (1, bc[0], bc[0])))
 

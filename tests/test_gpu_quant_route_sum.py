@@ -256,3 +256,29 @@ def test_moe_topk_quant(dev, M, E, topk, H):
     torch.cuda.synchronize()
     assert torch.equal(ids, ids0) and torch.equal(w, w0)
     assert torch.equal(xq.view(torch.uint8), xq0.view(torch.uint8)) and torch.equal(xs, xs0)
+
+
+@pytest.mark.parametrize("T,E,topk,blk", [(256, 384, 8, 256), (1, 288, 8, 256), (700, 64, 6, 16), (4096, 288, 8, 64)])
+def test_align_live_only(dev, T, E, topk, blk):
+    """r9k_moe_align_live: the tables up to ntpp equal r9k_moe_align's bit for bit, and nothing past ntpp is
+    written (the buffers' sentinel survives) -- one workgroup below 4097 routed rows, the multi-workgroup path
+    above."""
+    g = torch.Generator().manual_seed(20261201 + 13000 + T + E)
+    logits = torch.randn(T, E, generator=g).to(torch.bfloat16).to(dev)
+    ids = K.moe_topk(logits, topk, True)[1]
+    numel = T * topk
+    s0, e0, n0 = K.moe_align(ids, blk, E)
+    L = K.lib()
+    cap = K.capacity(numel, E, blk)
+    s1 = torch.full((cap,), -777, dtype=torch.int32, device=dev)
+    e1 = torch.full((cap // blk,), -777, dtype=torch.int32, device=dev)
+    n1 = torch.zeros(1, dtype=torch.int32, device=dev)
+    scratch = K._align_scratch(dev, L.r9k_moe_align_scratch_ints(numel, E))
+    assert L.r9k_moe_align_live(ids.data_ptr(), numel, E, blk, s1.data_ptr(), e1.data_ptr(), n1.data_ptr(),
+                                scratch.data_ptr(), scratch.numel(), torch.cuda.current_stream().cuda_stream) == 0
+    torch.cuda.synchronize()
+    n = int(n0.item())
+    print(f"align live T={T} E={E} k={topk} blk={blk}: ntpp {n} of capacity {cap}", flush=True)
+    assert int(n1.item()) == n
+    assert torch.equal(s1[:n], s0[:n]) and torch.equal(e1[: n // blk], e0[: n // blk])
+    assert bool((s1[n:] == -777).all()) and bool((e1[n // blk:] == -777).all())
