@@ -86,6 +86,36 @@ __device__ __forceinline__ uint32_t pack4_e4m3(float a, float b, float c, float 
   return f32_to_e4m3(a) | (f32_to_e4m3(b) << 8) | (f32_to_e4m3(c) << 16) | (f32_to_e4m3(d) << 24);
 }
 
+// Eight fp32 values times `inv` to e4m3 bytes (v[0] in the low byte of .x): pack4_e4m3's bytes. V_CVT_PK_FP8_F32
+// converts all eight; a product that is NaN or past 464 in magnitude (the hardware need not give it f32_to_e4m3's
+// code) then has its byte replaced by that code, sign | 0x7f, in one short block shared by the eight.
+__device__ __forceinline__ uint2 pack8_e4m3(const float (&v)[8], float inv) {
+  float x[8];
+  bool ok = true;
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    x[j] = v[j] * inv;
+    ok = ok && fabsf(x[j]) <= 464.f;
+  }
+  uint32_t w[2];
+#pragma unroll
+  for (int h = 0; h < 2; h++) {
+    const int r = __builtin_amdgcn_cvt_pk_fp8_f32(x[4 * h], x[4 * h + 1], 0, false);
+    w[h] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(x[4 * h + 2], x[4 * h + 3], r, true);
+  }
+  if (__builtin_expect(!ok, 0)) {
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      if (!(fabsf(x[j]) <= 464.f)) {
+        const uint32_t code = ((__float_as_uint(x[j]) >> 24) & 0x80u) | 0x7fu;
+        const int sh = 8 * (j & 3);
+        w[j >> 2] = (w[j >> 2] & ~(0xffu << sh)) | (code << sh);
+      }
+    }
+  }
+  return make_uint2(w[0], w[1]);
+}
+
 // silu(g) * u with g, u the stored bf16 values, evaluated as (g / (1 + exp(-g))) * u in fp32 with the hardware
 // exponential (__expf, as the reference: kernels/r9k_moe_mxfp4a8.hip:526) and a reciprocal-multiply division
 // (V_RCP_F32, 1 ulp; within 2 ulp of the reference's IEEE division, whose sequence is 10 instructions an element in a
@@ -132,25 +162,11 @@ __device__ __forceinline__ void quant_row_wave(const uint16_t* __restrict__ xrow
   }
 }
 
-// One wave turns one row of the gate_up output (gate = the first I bf16 values, up = the next I; I % 8 == 0,
-// I <= 512 * R, the row 16-byte aligned, the code row 8-byte aligned) into silu(gate) * up quantised to OCP e4m3 with
-// a per-row scale, the rule of the per-token quant: amax = max(max |h|, 1e-12), inv = 448 / amax, q = e4m3(h * inv),
-// s = amax / 448 (returned to every lane). Lane chunks c = lane + 64 i of 8 values stay in registers. The standalone
-// SiLU kernel and every fused consumer of the gate_up output use this one routine, so their codes are the same bytes.
+// The two halves of silu_quant_chunks, for callers that convert several rows at once and interleave their wave
+// reductions: silu_chunk_values gives a lane's products a[i][0..7] (chunk lane + 64 i) and their running max |a|;
+// quant_chunks_write takes the row's reduced max and writes the codes, returning the row scale.
 template <int R>
-__device__ __forceinline__ float silu_quant_row_wave(const uint16_t* __restrict__ grow, int I, uint8_t* qrow,
-                                                     int lane) {
-  const int nvec = I / 8;
-  const uint4* gr = reinterpret_cast<const uint4*>(grow);
-  const uint4* ur = reinterpret_cast<const uint4*>(grow + I);
-  uint4 gv[R], uv[R];
-#pragma unroll
-  for (int i = 0; i < R; i++) {
-    const int c = lane + i * WAVE;
-    gv[i] = c < nvec ? gr[c] : make_uint4(0u, 0u, 0u, 0u);
-    uv[i] = c < nvec ? ur[c] : make_uint4(0u, 0u, 0u, 0u);
-  }
-  float a[R][8];
+__device__ __forceinline__ float silu_chunk_values(const uint4 (&gv)[R], const uint4 (&uv)[R], float (&a)[R][8]) {
   float m = 0.f;
 #pragma unroll
   for (int i = 0; i < R; i++) {
@@ -163,19 +179,59 @@ __device__ __forceinline__ float silu_quant_row_wave(const uint16_t* __restrict_
 #pragma unroll
     for (int j = 0; j < 8; j++) m = fmaxf(m, fabsf(a[i][j]));      // zero padding lanes give silu(0) * 0 = 0
   }
-  const float amax = fmaxf(wave_max(m), 1e-12f);
+  return m;
+}
+
+template <int R>
+__device__ __forceinline__ float quant_chunks_write(const float (&a)[R][8], float row_max, int nvec, uint8_t* qrow,
+                                                    int lane) {
+  const float amax = fmaxf(row_max, 1e-12f);
   const float inv = 448.f / amax;
   uint2* qr = reinterpret_cast<uint2*>(qrow);
 #pragma unroll
   for (int i = 0; i < R; i++) {
     const int c = lane + i * WAVE;
-    if (c < nvec) {
-      const uint32_t lo = pack4_e4m3(a[i][0] * inv, a[i][1] * inv, a[i][2] * inv, a[i][3] * inv);
-      const uint32_t hi = pack4_e4m3(a[i][4] * inv, a[i][5] * inv, a[i][6] * inv, a[i][7] * inv);
-      qr[c] = make_uint2(lo, hi);
-    }
+    if (c < nvec) qr[c] = pack8_e4m3(a[i], inv);
   }
   return amax / 448.f;
+}
+
+// silu(gate) * up of one gate_up row held in registers (lane chunks c = lane + 64 i of 8 values: gv = gate, uv =
+// up, zero past the row's nvec chunks) quantised to OCP e4m3 with a per-row scale, the rule of the per-token quant:
+// amax = max(max |h|, 1e-12), inv = 448 / amax, q = e4m3(h * inv) written as 8-byte pieces at qrow + 8 c,
+// s = amax / 448 returned to every lane. Every consumer of the gate_up output goes through these routines (the
+// standalone SiLU kernel, the decode tail and the prefill down kernel), so their codes are the same bytes.
+template <int R>
+__device__ __forceinline__ float silu_quant_chunks(const uint4 (&gv)[R], const uint4 (&uv)[R], int nvec,
+                                                   uint8_t* qrow, int lane) {
+  float a[R][8];
+  const float m = silu_chunk_values<R>(gv, uv, a);
+  return quant_chunks_write<R>(a, wave_max(m), nvec, qrow, lane);
+}
+
+// Loads the lane chunks of one gate_up row for silu_quant_chunks (gate = the first I bf16 values, up = the next I;
+// I % 8 == 0, I <= 512 * R, the row 16-byte aligned).
+template <int R>
+__device__ __forceinline__ void load_gate_up_row(const uint16_t* __restrict__ grow, int I, int lane, uint4 (&gv)[R],
+                                                 uint4 (&uv)[R]) {
+  const int nvec = I / 8;
+  const uint4* gr = reinterpret_cast<const uint4*>(grow);
+  const uint4* ur = reinterpret_cast<const uint4*>(grow + I);
+#pragma unroll
+  for (int i = 0; i < R; i++) {
+    const int c = lane + i * WAVE;
+    gv[i] = c < nvec ? gr[c] : make_uint4(0u, 0u, 0u, 0u);
+    uv[i] = c < nvec ? ur[c] : make_uint4(0u, 0u, 0u, 0u);
+  }
+}
+
+// One wave turns one gate_up row into e4m3 codes (the code row 8-byte aligned) and returns its scale.
+template <int R>
+__device__ __forceinline__ float silu_quant_row_wave(const uint16_t* __restrict__ grow, int I, uint8_t* qrow,
+                                                     int lane) {
+  uint4 gv[R], uv[R];
+  load_gate_up_row<R>(grow, I, lane, gv, uv);
+  return silu_quant_chunks<R>(gv, uv, I / 8, qrow, lane);
 }
 
 // Block-wide max of a float; `sh` holds one float per wave. Every thread gets the result.

@@ -20,6 +20,7 @@
 // whose 32 rows are all padding skip their MFMAs. Live tiles are renumbered so that each XCD gets a contiguous range
 // (the column blocks of one routing block share an L2) and dead blocks past ntpp never occupy an XCD.
 #include "r9k_common.h"
+#include "r9k_dma.h"
 
 #include <cstdlib>
 
@@ -31,13 +32,6 @@ typedef int v8i __attribute__((ext_vector_type(8)));
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-
-// Two fp32 values to packed bf16, round to nearest even (v_cvt_pk_bf16_f32), a in the low half.
-__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
-  return __builtin_bit_cast(uint32_t, (bf16x2){(__bf16)a, (__bf16)b});
-}
-
 constexpr int BM = 256, BN = 256, KC = 128;   // rows, columns, K per chunk
 constexpr int NTH = 512;                       // 8 waves
 constexpr int NXCD = 8;
@@ -52,27 +46,6 @@ struct __align__(16) Stage {
 };
 constexpr size_t SMEM = sizeof(Stage) * NSTAGE;
 
-// global -> LDS DMA of 16 (4) bytes per lane: lane l's bytes land at LDS address `lds` + 16 l (4 l). M0 carries the
-// wave-uniform LDS base. Completion is tracked by vmcnt; the kernel waits for it explicitly.
-__device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds) : "memory", "m0");
-}
-__device__ __forceinline__ void dma4(const void* g, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(lds) : "memory", "m0");
-}
-// The same from a wave-uniform base (SGPR pair) plus a 32-bit per-lane byte offset.
-__device__ __forceinline__ void dma16s(const void* base, uint32_t off, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "s"(lds) : "memory", "m0");
-}
-__device__ __forceinline__ void dma4s(const void* base, uint32_t off, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dword %0, %1" ::"v"(off), "s"(base), "s"(lds) : "memory", "m0");
-}
-// A wave-uniform copy of a pointer computed from per-lane-equal values (kept in SGPRs).
-__device__ __forceinline__ const uint8_t* uniform_ptr(const void* p) {
-  const uint64_t v = (uint64_t)(uintptr_t)p;
-  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v), hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
-  return reinterpret_cast<const uint8_t*>(((uint64_t)hi << 32) | lo);
-}
 // n / d for 32-bit unsigned n by a divisor fixed per launch, as a multiply-high and shifts (Granlund & Montgomery,
 // "Division by invariant integers using multiplication", 1994, fig. 4.1): with l = ceil(log2 d) and
 // m = floor(2^32 (2^l - d) / d) + 1, n / d = (t + ((n - t) >> 1)) >> (l - 1), t = mulhi(n, m); l = 0 means d = 1.
@@ -100,9 +73,6 @@ int getenv_flag_off_pf(const char* name) {
   return v && v[0] == '0' ? 1 : 0;
 }
 
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-  return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)p);
-}
 
 __global__ void __launch_bounds__(NTH) moe_prefill_kernel(
     const uint8_t* __restrict__ A, const float* __restrict__ As, const uint8_t* __restrict__ Wq,

@@ -71,6 +71,35 @@ def test_silu_mul_quant_fp8(dev, M, I, scale):
     assert np.linalg.norm(deq - ref) / np.linalg.norm(ref) < 6e-2      # the reference's quant round-trip gate
 
 
+def test_silu_mul_quant_fp8_special_values(dev):
+    """Non-finite products take the encoder's fallback block: a NaN product encodes as sign | 0x7f, a row whose
+    maximum is inf quantises with inv = 0 (finite products -> +-0, inf * 0 -> NaN -> sign | 0x7f), a product past
+    the fp32 range overflows to inf. The codes of those positions match the oracle's bit routine exactly."""
+    g = torch.Generator().manual_seed(77)
+    M, I = 8, 512
+    gu = torch.randn(M, 2 * I, generator=g)
+    gu[0, 3] = float("nan"); gu[0, I + 9] = float("nan")          # NaN gate / NaN up in a finite row
+    gu[1, I + 5] = float("inf"); gu[1, I + 6] = float("-inf")     # inf up: the row maximum is inf
+    gu[2, 7] = 3e38; gu[2, I + 7] = 3e38                           # silu(3e38) * 3e38 overflows to inf
+    gu[3, :I] = float("-inf")                                      # silu(-inf) = -inf / (1 + inf) = NaN
+    gu[4, 11] = 200.0; gu[4, I + 11] = 2.0                         # an ordinary large product
+    gu = gu.to(torch.bfloat16)
+    q, s = K.silu_mul_quant_fp8(gu.to(dev))
+    qo, so, _ = O.silu_mul_quant_fp8(gu)
+    qd = u8(q)
+    # a NaN's sign bit is not specified (the GPU's default NaN is positive, x86's negative): compare NaN codes as
+    # 0x7f with either sign, everything else exactly where no exp() rounding can matter (rows with inv = 0 or a
+    # NaN-only row)
+    special = (qo & 0x7F) == 0x7F
+    assert special.sum() >= 4
+    assert np.array_equal(qd[special] & 0x7F, qo[special] & 0x7F)
+    for r in (1, 2, 3):
+        assert np.array_equal(qd[r][~special[r]], qo[r][~special[r]]), r
+    assert (qd == qo)[~special].mean() >= 0.99
+    sd = s.cpu().numpy()
+    assert np.array_equal(np.isnan(sd), np.isnan(so)) and np.array_equal(np.isinf(sd), np.isinf(so))
+
+
 @pytest.mark.parametrize("M,E,topk,blk", [(1, 288, 8, 16), (8, 288, 8, 16), (16, 288, 8, 16), (64, 288, 8, 16),
                                           (37, 512, 10, 32), (256, 384, 8, 64), (5, 48, 6, 16), (300, 100, 10, 16),
                                           (512, 288, 8, 16)])
