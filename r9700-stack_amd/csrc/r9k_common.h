@@ -74,21 +74,11 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
 __device__ __forceinline__ float lo16(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float hi16(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
-// Four fp32 values to e4m3 bytes, a in the low byte. V_CVT_PK_FP8_F32 (OCP e4m3 on gfx950, round to nearest even)
-// gives f32_to_e4m3's bytes for every |v| <= 464, signed zeros and the subnormal grid included; a lane holding a NaN
-// or a larger magnitude (codes 0x7f with the sign, which the hardware need not produce) takes the bit routine.
-__device__ __forceinline__ uint32_t pack4_e4m3(float a, float b, float c, float d) {
-  if (fabsf(a) <= 464.f && fabsf(b) <= 464.f && fabsf(c) <= 464.f && fabsf(d) <= 464.f) {
-    int r = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
-    r = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, r, true);
-    return (uint32_t)r;
-  }
-  return f32_to_e4m3(a) | (f32_to_e4m3(b) << 8) | (f32_to_e4m3(c) << 16) | (f32_to_e4m3(d) << 24);
-}
-
-// Eight fp32 values times `inv` to e4m3 bytes (v[0] in the low byte of .x): pack4_e4m3's bytes. V_CVT_PK_FP8_F32
-// converts all eight; a product that is NaN or past 464 in magnitude (the hardware need not give it f32_to_e4m3's
-// code) then has its byte replaced by that code, sign | 0x7f, in one short block shared by the eight.
+// Eight fp32 values times `inv` to e4m3 bytes (v[0] in the low byte of .x), f32_to_e4m3's bytes for each.
+// V_CVT_PK_FP8_F32 (OCP e4m3 on gfx950, round to nearest even) gives them for every |x| <= 464, signed zeros and the
+// subnormal grid included, and converts all eight; a product that is NaN or larger in magnitude (code sign | 0x7f,
+// which the hardware need not produce) then has its byte replaced, in one short block shared by the eight (kept
+// small because several kernels inline this routine once per row).
 __device__ __forceinline__ uint2 pack8_e4m3(const float (&v)[8], float inv) {
   float x[8];
   bool ok = true;
@@ -114,6 +104,12 @@ __device__ __forceinline__ uint2 pack8_e4m3(const float (&v)[8], float inv) {
     }
   }
   return make_uint2(w[0], w[1]);
+}
+
+// Eight packed bf16 values (one 16-byte chunk) times `inv` to e4m3 bytes.
+__device__ __forceinline__ uint2 pack8_bf16_e4m3(uint4 v, float inv) {
+  const float f[8] = {lo16(v.x), hi16(v.x), lo16(v.y), hi16(v.y), lo16(v.z), hi16(v.z), lo16(v.w), hi16(v.w)};
+  return pack8_e4m3(f, inv);
 }
 
 // silu(g) * u with g, u the stored bf16 values, evaluated as (g / (1 + exp(-g))) * u in fp32 with the hardware
@@ -155,9 +151,7 @@ __device__ __forceinline__ void quant_row_wave(const uint16_t* __restrict__ xrow
   for (int i = 0; i < RMAX; i++) {
     const int c = lane + i * WAVE;
     if (c < nvec) {
-      const uint32_t lo = pack4_e4m3(lo16(v[i].x) * inv, hi16(v[i].x) * inv, lo16(v[i].y) * inv, hi16(v[i].y) * inv);
-      const uint32_t hi = pack4_e4m3(lo16(v[i].z) * inv, hi16(v[i].z) * inv, lo16(v[i].w) * inv, hi16(v[i].w) * inv);
-      qr[c] = make_uint2(lo, hi);
+      qr[c] = pack8_bf16_e4m3(v[i], inv);
     }
   }
 }

@@ -1,4 +1,4 @@
-// r9k_dense.hip -- the dense MXFP4 weight-only linear at decode widths (M <= 16 rows) in one launch: the per-token
+// r9k_dense.hip -- the dense MXFP4 weight-only linear at decode widths (M <= 4 rows) in one launch: the per-token
 // fp8 (e4m3) quant of the bf16 activations and the MXFP4 x fp8 GEMM.
 //
 //   out[m, n] = bf16( (sum_k q[m, k] * W[n, k]) * s[m] ),   q, s = the per-row quant of x (quant_row_wave)
@@ -6,8 +6,9 @@
 // The reference runs it as r9k_quant_rows_fp8 then r9k_moe_mxfp4a8 over identity routing tables
 // (r9700_vllm/ops.py:89-117; kernels/r9k_moe_mxfp4a8.hip:1683-1743 and :187-485). At decode widths the quant launch
 // costs about as much as a third of the GEMM (its launch and memory latency), so here every workgroup quantises the
-// M activation rows itself into LDS (each row read once from L2 per workgroup, M * K * 2 bytes) while its first weight
-// loads are in flight, then runs the weight stream against the LDS codes.
+// M activation rows itself into LDS (each row read once from L2 per workgroup, M * K * 2 bytes, spread over all of
+// its threads and issued ahead of its weight loads, which then overlap the quant), then runs the weight stream
+// against the LDS codes.
 //
 // Work split: a workgroup owns NPW 16-column tiles (1 KB of codes + 64 exponent bytes per 128-K tile, the
 // r9k_moe_mxfp4a8 weight layout), SK waves split the K-tiles in contiguous ranges, each wave issues the loads of up
@@ -30,56 +31,78 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 constexpr int KT = 128;
 constexpr int E8M0_ONE = 127;
 constexpr int MAXM = 16;          // activation rows: one MFMA M-tile
+constexpr int MAXM_QA = 4;        // rows the one-launch entry serves (the quant holds them all in registers)
 constexpr int APAD = 16;          // bytes of padding per LDS code row (row stride K + 16: no bank aliasing of rows)
 
-// One wave quantises one row like quant_row_wave (the same amax, 448 / amax and per-element encode, so the same
-// bytes) in two passes of 4 chunks a lane at a time -- the row maximum, then the codes -- so the row is never held
-// in registers beside the weight loads in flight. The second pass re-reads the row from L2.
-__device__ __forceinline__ void quant_row_two_pass(const uint16_t* __restrict__ xrow, int K, uint8_t* qrow,
-                                                   float* s_out, int lane) {
-  const uint4* xr = reinterpret_cast<const uint4*>(xrow);
-  const int nvec = K / 8;
-  float m = 0.f;
-  for (int c0 = 0; c0 < nvec; c0 += 4 * WAVE) {
-    uint4 v[4];
+// The workgroup quantises the activation rows MG at a time, like quant_row_wave (the same amax, 448 / amax and
+// per-element encode, so the same bytes): thread t holds chunks t + T i (i < XC, T threads) of each row, read once,
+// so one row's read is spread over every wave of the workgroup and the reads of the first group go out ahead of the
+// weight stream instead of queueing behind it. The row maxima meet in LDS (any combination order of a max gives the
+// same value), then every thread encodes its own chunks.
+template <int T>
+constexpr int row_chunks() { return T >= 256 ? 4 : 2; }   // K / 8 <= chunks * T: K <= 8192 at 256 threads, < 1024 at 64
+
+template <int T, int MG, int XC>
+__device__ __forceinline__ void load_row_group(const uint16_t* __restrict__ x, long ldx, int m0, int M, int nvec,
+                                               int tid, uint4 (&v)[MG][XC]) {
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const int c = c0 + lane + i * WAVE;
-      v[i] = c < nvec ? xr[c] : make_uint4(0u, 0u, 0u, 0u);
-    }
+  for (int m = 0; m < MG; m++) {
+    const uint4* xr = reinterpret_cast<const uint4*>(x + (size_t)(m0 + m) * ldx);
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const uint32_t w[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
-#pragma unroll
-      for (int j = 0; j < 4; j++) m = fmaxf(m, fmaxf(fabsf(lo16(w[j])), fabsf(hi16(w[j]))));
-    }
-  }
-  const float amax = fmaxf(wave_max(m), 1e-12f);
-  const float inv = 448.f / amax;
-  if (lane == 0) *s_out = amax / 448.f;
-  uint2* qr = reinterpret_cast<uint2*>(qrow);
-  for (int c0 = 0; c0 < nvec; c0 += 4 * WAVE) {
-    uint4 v[4];
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const int c = c0 + lane + i * WAVE;
-      v[i] = c < nvec ? xr[c] : make_uint4(0u, 0u, 0u, 0u);
-    }
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const int c = c0 + lane + i * WAVE;
-      if (c < nvec) {
-        const uint32_t lo = pack4_e4m3(lo16(v[i].x) * inv, hi16(v[i].x) * inv, lo16(v[i].y) * inv, hi16(v[i].y) * inv);
-        const uint32_t hi = pack4_e4m3(lo16(v[i].z) * inv, hi16(v[i].z) * inv, lo16(v[i].w) * inv, hi16(v[i].w) * inv);
-        qr[c] = make_uint2(lo, hi);
-      }
+    for (int i = 0; i < XC; i++) {
+      const int c = tid + i * T;
+      v[m][i] = (m0 + m < M && c < nvec) ? xr[c] : make_uint4(0u, 0u, 0u, 0u);
     }
   }
 }
 
+// Ends with a barrier: the codes and scales of the group are visible, and `red` (MG floats a wave) is free again.
+template <int T, int MG, int XC>
+__device__ __forceinline__ void quant_row_group(const uint4 (&v)[MG][XC], int m0, int M, int nvec, uint8_t* A,
+                                                int lda, float* s_row, float* red, int tid) {
+  constexpr int NW = T / WAVE;
+  const int wave = tid / WAVE, lane = tid % WAVE;
+  float mx[MG];
+#pragma unroll
+  for (int m = 0; m < MG; m++) {
+    mx[m] = 0.f;
+#pragma unroll
+    for (int i = 0; i < XC; i++) {
+      const uint32_t w[4] = {v[m][i].x, v[m][i].y, v[m][i].z, v[m][i].w};
+#pragma unroll
+      for (int j = 0; j < 4; j++) mx[m] = fmaxf(mx[m], fmaxf(fabsf(lo16(w[j])), fabsf(hi16(w[j]))));
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < MG; m++) mx[m] = wave_max(mx[m]);
+  if (lane == 0) {
+#pragma unroll
+    for (int m = 0; m < MG; m++) red[wave * MG + m] = mx[m];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int m = 0; m < MG; m++) {
+    const int row = m0 + m;
+    if (row >= M) break;
+    float amax = red[m];
+#pragma unroll
+    for (int w = 1; w < NW; w++) amax = fmaxf(amax, red[w * MG + m]);
+    amax = fmaxf(amax, 1e-12f);
+    const float inv = 448.f / amax;
+    if (tid == 0) s_row[row] = amax / 448.f;
+    uint2* qr = reinterpret_cast<uint2*>(A + (size_t)row * lda);
+#pragma unroll
+    for (int i = 0; i < XC; i++) {
+      const int c = tid + i * T;
+      if (c < nvec) qr[c] = pack8_bf16_e4m3(v[m][i], inv);
+    }
+  }
+  __syncthreads();
+}
+
 // LDS: codes [M][K + APAD] (fp8), row scales [MAXM] fp32, partial tiles [SK][NPW][256] fp32 (sized by M, so small M
 // leaves room for several workgroups a CU).
-template <int NPW, int SK, int U>
+template <int NPW, int SK, int U, int MG>
 __global__ void __launch_bounds__(WAVE * SK) dense_mxfp4_qa_kernel(
     const uint16_t* __restrict__ x, long ldx, const uint8_t* __restrict__ Wq, const uint8_t* __restrict__ Ws,
     uint16_t* __restrict__ out, long ldo, int M, int N, int K) {
@@ -102,7 +125,6 @@ __global__ void __launch_bounds__(WAVE * SK) dense_mxfp4_qa_kernel(
   }
   const int kt0 = wave * nkt / SK, kt1 = (wave + 1) * nkt / SK;
 
-  // the first batch of weight loads goes out before the activation quant, so its latency overlaps it
   u32x4 bf[U][NPW];
   uint32_t sb[U][NPW];
   auto issue = [&](int kb) {
@@ -116,9 +138,16 @@ __global__ void __launch_bounds__(WAVE * SK) dense_mxfp4_qa_kernel(
       }
     }
   };
-  issue(kt0);
-  for (int m = wave; m < M; m += SK) quant_row_two_pass(x + (size_t)m * ldx, K, A + (size_t)m * lda, s_row + m, lane);
-  __syncthreads();
+  // the activation rows' reads (M <= MG), then the first batch of weight loads, then the rows' quant (whose latency
+  // the weight loads overlap)
+  {
+    constexpr int T = WAVE * SK, XC = row_chunks<T>();
+    const int nvec = K / 8;
+    uint4 xv[MG][XC];
+    load_row_group<T, MG, XC>(x, ldx, 0, M, nvec, tid, xv);
+    issue(kt0);
+    quant_row_group<T, MG, XC>(xv, 0, M, nvec, A, lda, s_row, red, tid);
+  }
 
   v4f acc[NPW];
 #pragma unroll
@@ -173,39 +202,47 @@ int env_int(const char* name, int dflt) {
 }  // namespace
 
 // No counterpart as one entry in the reference: r9k_quant_rows_fp8 + r9k_moe_mxfp4a8 over identity tables
-// (r9700_vllm/ops.py:89-117 calls them back to back) in one launch, for M <= 16 rows. x bf16 [M][K] (row stride
+// (r9700_vllm/ops.py:89-117 calls them back to back) in one launch, for M <= 4 rows. x bf16 [M][K] (row stride
 // ldx elements, rows 16-byte aligned); wq / ws one expert's weights in the r9k_moe_mxfp4a8 layout (N columns, K);
-// out bf16 [M][N] (row stride ldo). Served: 1 <= M <= 16, K % 128 == 0, K <= 8192, N % 16 == 0; 2 (nothing launched)
+// out bf16 [M][N] (row stride ldo). Served: 1 <= M <= 4, K % 128 == 0, K <= 8192, N % 16 == 0; 2 (nothing launched)
 // otherwise. 0, -3 bad argument, -6 launch error. The K split (SK waves) follows the decode GEMM's rule, so the
 // output equals r9k_quant_rows_fp8 + r9k_moe_mxfp4a8's bit for bit.
 extern "C" int r9k_dense_mxfp4_qa(long x, long ldx, long wq, long ws, long out, long ldo, int M, int N, int K,
                                   long stream) {
   if (M <= 0) return 0;
   if (!x || !wq || !ws || !out || N <= 0 || K <= 0) return -3;
-  if (M > MAXM || K % KT || K > 8192 || N % 16 || (x & 15) || (ldx & 7) || (wq & 15)) return 2;
+  if (M > MAXM_QA || K % KT || K > 8192 || N % 16 || (x & 15) || (ldx & 7) || (wq & 15)) return 2;
   const int nkt = K / KT, NT = N / 16;
-  const int NPW = env_int("R9K_DENSE_NPW", NT >= 2 ? 2 : 1);
+  // one 16-column tile a workgroup at M = 1 (every workgroup of config 4 resident at once), two from M = 2
+  // (measured at config 4: M = 1 12.2 us with two tiles, 10.7 us with one; M = 2 13.8 us with one, 12.9 us with two)
+  const int NPW = env_int("R9K_DENSE_NPW", (NT >= 2 && M >= 2) ? 2 : 1);
   const int SK = env_int("R9K_DENSE_SK", nkt >= 8 ? 4 : 1);
+  if (SK != 1 && SK != 4) return 2;
+  if (K / 8 > (SK == 4 ? row_chunks<256>() * 256 : row_chunks<64>() * 64)) return 2;   // chunks a thread holds
   const int per = (nkt + SK - 1) / SK;
   // loads in flight a wave: its whole K range up to 5 K-tiles, else two batches (all of a 10-tile range at once
   // needs ~165 VGPRs, two waves a SIMD, and 544 workgroups of config 4 no longer fit the chip in one round:
   // measured 20.2 us against 14.2 us in two batches of 5)
   const int U = env_int("R9K_DENSE_U", per <= 4 ? 4 : (per <= 5 ? 5 : (per <= 8 ? 4 : (per <= 10 ? 5 : 8))));
+  const int MG = M == 1 ? 1 : (M == 2 ? 2 : 4);
   const size_t smem = (size_t)M * (K + APAD) + MAXM * sizeof(float) + (size_t)SK * NPW * 256 * sizeof(float);
   const dim3 grid((NT + NPW - 1) / NPW), block(WAVE * SK);
   const hipStream_t st = (hipStream_t)stream;
-#define DQ(NPWv, SKv, Uv)                                                                                          \
-  if (NPW == NPWv && SK == SKv && U == Uv) {                                                                       \
-    static const hipError_t a = hipFuncSetAttribute(reinterpret_cast<const void*>(dense_mxfp4_qa_kernel<NPWv, SKv, Uv>), \
-                                                    hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);       \
+#define DQ(NPWv, SKv, Uv, MGv)                                                                                     \
+  if (NPW == NPWv && SK == SKv && U == Uv && MG == MGv) {                                                          \
+    static const hipError_t a = hipFuncSetAttribute(                                                               \
+        reinterpret_cast<const void*>(dense_mxfp4_qa_kernel<NPWv, SKv, Uv, MGv>),                                  \
+        hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);                                                    \
     if (a != hipSuccess) return -6;                                                                                \
-    hipLaunchKernelGGL((dense_mxfp4_qa_kernel<NPWv, SKv, Uv>), grid, block, smem, st, (const uint16_t*)x, ldx,     \
-                       (const uint8_t*)wq, (const uint8_t*)ws, (uint16_t*)out, ldo, M, N, K);                      \
+    hipLaunchKernelGGL((dense_mxfp4_qa_kernel<NPWv, SKv, Uv, MGv>), grid, block, smem, st, (const uint16_t*)x,     \
+                       ldx, (const uint8_t*)wq, (const uint8_t*)ws, (uint16_t*)out, ldo, M, N, K);                 \
     return hipGetLastError() == hipSuccess ? 0 : -6;                                                               \
   }
-#define DQU(NPWv, SKv) DQ(NPWv, SKv, 4) DQ(NPWv, SKv, 5) DQ(NPWv, SKv, 8) DQ(NPWv, SKv, 10) DQ(NPWv, SKv, 16)
-  DQU(1, 1) DQU(2, 1) DQU(1, 4) DQU(2, 4) DQU(2, 8) DQU(4, 4) DQU(1, 8) DQU(4, 8)
+#define DQM(NPWv, SKv, Uv) DQ(NPWv, SKv, Uv, 1) DQ(NPWv, SKv, Uv, 2) DQ(NPWv, SKv, Uv, 4)
+#define DQU(NPWv, SKv) DQM(NPWv, SKv, 4) DQM(NPWv, SKv, 5) DQM(NPWv, SKv, 8) DQM(NPWv, SKv, 10)
+  DQU(1, 1) DQU(2, 1) DQU(1, 4) DQU(2, 4)
 #undef DQU
+#undef DQM
 #undef DQ
   return 2;
 }

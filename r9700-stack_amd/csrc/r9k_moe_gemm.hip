@@ -212,8 +212,10 @@ __device__ __forceinline__ bool moe_tile(
 #pragma unroll
           for (int v = 0; v < 4; v++) {
             const float4 a = flo[u][i][v], b = fhi[u][i][v];
-            wl[v] = pack4_e4m3(a.x * s, a.y * s, a.z * s, a.w * s);
-            wh[v] = pack4_e4m3(b.x * s, b.y * s, b.z * s, b.w * s);
+            const float f[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+            const uint2 w = pack8_e4m3(f, s);
+            wl[v] = w.x;
+            wh[v] = w.y;
           }
           alo[u][i] = make_uint4(wl[0], wl[1], wl[2], wl[3]);
           ahi[u][i] = make_uint4(wh[0], wh[1], wh[2], wh[3]);

@@ -77,9 +77,7 @@ __global__ void __launch_bounds__(WR * WAVE) quant_rows_wave_kernel(const uint16
   for (int i = 0; i < R; i++) {
     const int c = lane + i * WAVE;
     if (c < nvec) {
-      const uint32_t lo = pack4_e4m3(lo16(v[i].x) * inv, hi16(v[i].x) * inv, lo16(v[i].y) * inv, hi16(v[i].y) * inv);
-      const uint32_t hi = pack4_e4m3(lo16(v[i].z) * inv, hi16(v[i].z) * inv, lo16(v[i].w) * inv, hi16(v[i].w) * inv);
-      qr[c] = make_uint2(lo, hi);
+      qr[c] = pack8_bf16_e4m3(v[i], inv);
     }
   }
 }
@@ -131,9 +129,7 @@ __global__ void __launch_bounds__(QT) quant_rows_vec_kernel(const uint16_t* __re
   for (int i = 0; i < QR; i++) {
     const int c = tid + i * QT;
     if (c >= nvec) break;
-    const uint32_t lo = pack4_e4m3(lo16(v[i].x) * inv, hi16(v[i].x) * inv, lo16(v[i].y) * inv, hi16(v[i].y) * inv);
-    const uint32_t hi = pack4_e4m3(lo16(v[i].z) * inv, hi16(v[i].z) * inv, lo16(v[i].w) * inv, hi16(v[i].w) * inv);
-    qr[c] = make_uint2(lo, hi);
+    qr[c] = pack8_bf16_e4m3(v[i], inv);
   }
 }
 
@@ -227,9 +223,7 @@ __global__ void __launch_bounds__(QT) silu_mul_quant_kernel(const uint16_t* __re
     for (int i = 0; i < QR; i++) {
       const int c = tid + i * QT;
       if (c >= nvec) break;
-      const uint32_t lo = pack4_e4m3(a[i][0] * inv, a[i][1] * inv, a[i][2] * inv, a[i][3] * inv);
-      const uint32_t hi = pack4_e4m3(a[i][4] * inv, a[i][5] * inv, a[i][6] * inv, a[i][7] * inv);
-      reinterpret_cast<uint2*>(qr)[c] = make_uint2(lo, hi);
+      reinterpret_cast<uint2*>(qr)[c] = pack8_e4m3(a[i], inv);
     }
   } else {
     for (int k = tid; k < I; k += QT) qr[k] = (uint8_t)f32_to_e4m3(silu_mul(bf2f(gr[k]), bf2f(ur[k])) * inv);

@@ -609,15 +609,16 @@ def moe_down_sum(gate_up: torch.Tensor, topk_ids: torch.Tensor, topk_w: torch.Te
     return True
 
 
-# ops.mxfp4_linear runs the one-launch dense path (r9k_dense_mxfp4_qa) up to this many rows. Measured on MI355X at
-# config 4 ([17408, 5120]): M = 1 15.8 -> 14.2 us, M = 4 16.4 -> 16.2 us; at M = 16 every workgroup's quant of 16
-# rows (160 KB from L2) costs more than the quant launch it saves (20.5 -> 32+ us), so M > 4 keeps two launches.
-DENSE_QA_MAX_M = int(os.environ.get("R9K_DENSE_QA_MAX_M", "4"))
+# ops.mxfp4_linear runs the one-launch dense path (r9k_dense_mxfp4_qa, M <= 4) up to this many rows. Measured on
+# MI355X at config 4 ([17408, 5120]), one launch against the two (quant + GEMM): M = 1 10.7 vs 16.3 us, M = 2 13.2
+# vs 16.4 us, M = 3 17.8 vs 16.5 us, M = 4 19.6 vs 16.6 us (from three rows the activation chunks the workgroup holds
+# in registers, 228 VGPRs at M = 4, leave two waves a SIMD), so M > 2 keeps two launches.
+DENSE_QA_MAX_M = int(os.environ.get("R9K_DENSE_QA_MAX_M", "2"))
 
 
 def dense_mxfp4_qa(x: torch.Tensor, w: Mxfp4Experts, out: torch.Tensor) -> bool:
     """out [M, N] = bf16(quant_rows_fp8(x) @ W^T) for one dense MXFP4 weight (w.wq / w.wsr of a single expert) in ONE
-    launch (r9k_dense_mxfp4_qa: every workgroup quantises the <= 16 activation rows into LDS itself), the values of
+    launch (r9k_dense_mxfp4_qa: every workgroup quantises the <= 4 activation rows into LDS itself), the values of
     quant_rows_fp8 + moe_gemm over identity tables bit for bit. False when not served (nothing launched)."""
     M = x.shape[0]
     assert x.dtype == torch.bfloat16 and x.dim() == 2 and x.stride(1) == 1 and x.shape[1] == w.K

@@ -484,10 +484,11 @@ def test_down_sum_refuses_unserved_shapes(dev):
         assert not K.moe_down_sum(gu, ids, torch.ones(topk, device=dev), W2, out)
 
 
-@pytest.mark.parametrize("M,N,Kd", [(1, 17408, 5120), (4, 17408, 5120), (16, 17408, 5120), (7, 1024, 2048),
-                                    (16, 1024, 2048), (3, 48, 1024), (2, 272, 384), (5, 64, 8192)])
+@pytest.mark.parametrize("M,N,Kd", [(1, 17408, 5120), (2, 17408, 5120), (4, 17408, 5120), (3, 1024, 2048),
+                                    (4, 1024, 2048), (3, 48, 1024), (2, 272, 384), (1, 64, 8192), (4, 64, 8192),
+                                    (1, 32, 256), (4, 16, 896)])
 def test_dense_qa_equals_two_launches(dev, M, N, Kd):
-    """r9k_dense_mxfp4_qa (the activation quant inside the dense GEMM launch, M <= 16) against quant_rows_fp8 + the
+    """r9k_dense_mxfp4_qa (the activation quant inside the dense GEMM launch, M <= 4) against quant_rows_fp8 + the
     decode GEMM over identity tables: bit for bit (same K split over waves), and within the GEMM tolerance of the
     oracle."""
     g = torch.Generator().manual_seed(20261201 + 4100 + M + N + Kd)
@@ -512,12 +513,13 @@ def test_dense_qa_equals_two_launches(dev, M, N, Kd):
 
 
 def test_dense_qa_refuses_unserved(dev):
-    """M > 16, K not a multiple of 128 or unaligned activations: False, nothing launched (ops falls back)."""
+    """M > 4, K not a multiple of 128 or unaligned activations: False, nothing launched (ops falls back)."""
     W = K.Mxfp4Experts(torch.zeros(1, 64 * 320 // 8, dtype=torch.int32, device=dev),
                        torch.zeros(1, 320 // 32 + 1, 64, dtype=torch.uint8, device=dev), 64, 320)
     assert not K.dense_mxfp4_qa(torch.zeros(2, 320, dtype=torch.bfloat16, device=dev), W,
                                 torch.empty(2, 64, dtype=torch.bfloat16, device=dev))
     W2 = K.Mxfp4Experts(torch.zeros(1, 64 * 256 // 8, dtype=torch.int32, device=dev),
                         torch.zeros(1, 256 // 32 + 1, 64, dtype=torch.uint8, device=dev), 64, 256)
-    assert not K.dense_mxfp4_qa(torch.zeros(17, 256, dtype=torch.bfloat16, device=dev), W2,
-                                torch.empty(17, 64, dtype=torch.bfloat16, device=dev))
+    for M in (5, 17):
+        assert not K.dense_mxfp4_qa(torch.zeros(M, 256, dtype=torch.bfloat16, device=dev), W2,
+                                    torch.empty(M, 64, dtype=torch.bfloat16, device=dev))
