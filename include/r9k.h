@@ -217,6 +217,28 @@ int r9k_lru_manage_map(long ids, int mk, int E, int S, int max_distinct, int max
                        long slot_expert, long slot_stamp, long routed, long step, long miss, long n_miss, long hot,
                        long cold, long stream);
 
+/* The reference's one-launch manage + both moe_align_block_size outputs (replaces r4d_lru.hip:596-610, bound at
+ * moe/cache.py:45-48 and called at :345-352): one manage step (as r4d_lru_manage), then the resident pass's tables
+ * over slot ids (ids through the updated table) and the host pass's over expert ids (through map_cold), block size
+ * bs, each in canonical order (rows ascending within an id). sorted_* int32 [L] (padding and tail = mk), eids_*
+ * int32 [NB] (-1 past the end), npad_* int32 [1] = padded total. L must cover the padded total's bound (min(mk * bs,
+ * mk + E (bs - 1)) while mk < E, else mk + E (bs - 1), vLLM's sizing) and NB * bs >= L. Served for E <= 1024 and
+ * mk <= 4096 (one workgroup builds the tables); 2 otherwise (nothing launched). -1 sizes, other codes as
+ * r4d_lru_manage. */
+int r4d_lru_fused(long ids, int mk, int E, int S, int max_distinct, int max_inserts, long table, long map_cold,
+                  long slot_expert, long slot_stamp, long routed, long step, long miss, long n_miss, int bs, int L,
+                  int NB, long sorted_hot, long eids_hot, long npad_hot, long sorted_cold, long eids_cold,
+                  long npad_cold, long stream);
+
+/* r4d_lru_fused with this library's table capacity (sorted capacity(mk, E, blk) = ceil((mk + E (blk - 1)) / blk)
+ * * blk entries, expert ids capacity / blk, as r9k_moe_align writes them); sorted_c = 0 skips the host pass's tables
+ * (steps whose host pass is provably empty). No counterpart of its own in the reference (the same step as
+ * r4d_lru_fused, bound by moe/cache.py LayerCache.update_fused). 2 when not served (E > 1024 or mk > 4096). */
+int r9k_lru_manage_tables(long ids, int mk, int E, int S, int max_distinct, int max_inserts, long table, long map_cold,
+                          long slot_expert, long slot_stamp, long routed, long step, long miss, long n_miss, int blk,
+                          long sorted_h, long eids_h, long ntpp_h, long sorted_c, long eids_c, long ntpp_c,
+                          long stream);
+
 /* Copy each listed expert's six per-expert slabs host -> slot (replaces r4d_lru.hip:276-303, bound at
  * moe/cache.py:42-44): slab i of expert e at s_i + e * b_i goes to d_i + slot * b_i for the first n_miss[0]
  * (expert, slot) pairs of miss. Bytes b_i multiples of 16 (0 = unused slab), pointers 16-byte aligned. Grid

@@ -20,6 +20,7 @@
 // atomics, so the evolution is deterministic (identical on every rank that sees the same routing). gather reads the
 // host store over PCIe with 16-byte loads; it is link-bound.
 #include "r9k_common.h"
+#include "r9k_tables.h"
 
 #include <climits>
 
@@ -62,18 +63,31 @@ __device__ __forceinline__ int block_exscan(int v, int* sh, int* total) {
   return before + x - v;
 }
 
-__global__ void __launch_bounds__(MT_THREADS) lru_manage_kernel(
-    const int* __restrict__ ids, int mk, int E, int S, int max_distinct, int max_inserts, int* __restrict__ table,
-    int* __restrict__ map_cold, int* __restrict__ slot_expert, long long* __restrict__ slot_stamp,
-    uint8_t* __restrict__ routed_out, long long* __restrict__ step, int* __restrict__ miss, int* __restrict__ n_miss,
-    int* __restrict__ hot_ids, int* __restrict__ cold_ids) {
-  __shared__ uint8_t s_routed[MAX_E];
-  __shared__ int s_se[MAX_S];
-  __shared__ long long s_st[MAX_S];
-  __shared__ long long s_key[MAX_S];
-  __shared__ int s_vic[MAX_S];
-  __shared__ int s_miss[MAX_S];
-  __shared__ int sh[2 * NWAVE];
+// LDS of one manage step: routed flags, the slot mirror (expert, stamp, eviction key), victims, misses, scan space.
+struct ManageLds {
+  long long st[MAX_S];
+  long long key[MAX_S];
+  int se[MAX_S];
+  int vic[MAX_S];
+  int miss[MAX_S];
+  int sh[2 * NWAVE];
+  uint8_t routed[MAX_E];
+};
+
+// One manage step by the whole (MT_THREADS) workgroup; with hot_ids / cold_ids given it also writes the two passes'
+// routing ids (ids through the updated table / map_cold).
+__device__ __forceinline__ void manage_step(
+    ManageLds& L, const int* __restrict__ ids, int mk, int E, int S, int max_distinct, int max_inserts,
+    int* __restrict__ table, int* __restrict__ map_cold, int* __restrict__ slot_expert,
+    long long* __restrict__ slot_stamp, uint8_t* __restrict__ routed_out, long long* __restrict__ step,
+    int* __restrict__ miss, int* __restrict__ n_miss, int* __restrict__ hot_ids, int* __restrict__ cold_ids) {
+  uint8_t* s_routed = L.routed;
+  int* s_se = L.se;
+  long long* s_st = L.st;
+  long long* s_key = L.key;
+  int* s_vic = L.vic;
+  int* s_miss = L.miss;
+  int* sh = L.sh;
   const int t = threadIdx.x;
 
   const long long st = step[0] + 1;                 // every lane reads before lane 0 writes (barrier below)
@@ -180,6 +194,53 @@ __global__ void __launch_bounds__(MT_THREADS) lru_manage_kernel(
   }
 }
 
+__global__ void __launch_bounds__(MT_THREADS) lru_manage_kernel(
+    const int* __restrict__ ids, int mk, int E, int S, int max_distinct, int max_inserts, int* __restrict__ table,
+    int* __restrict__ map_cold, int* __restrict__ slot_expert, long long* __restrict__ slot_stamp,
+    uint8_t* __restrict__ routed_out, long long* __restrict__ step, int* __restrict__ miss, int* __restrict__ n_miss,
+    int* __restrict__ hot_ids, int* __restrict__ cold_ids) {
+  __shared__ ManageLds L;
+  manage_step(L, ids, mk, E, S, max_distinct, max_inserts, table, map_cold, slot_expert, slot_stamp, routed_out, step,
+              miss, n_miss, hot_ids, cold_ids);
+}
+
+// Manage, then the two passes' moe_align_block_size tables in the same workgroup (E <= TAB_MAX_E, mk <=
+// TAB_SMALL_MAX): the routing ids mapped through the updated table (resident pass, ids = slots) and map_cold (host
+// pass, ids = experts) go to LDS, and each table set is built by the routing kernels' single-workgroup builder (the
+// canonical order, so the tables equal r9k_moe_align's over the same mapped ids). The manage LDS and the builder's
+// share one union (the build starts after the last manage read). sorted_c = 0 skips the host pass's tables.
+// cap < 0: this library's capacity; else sorted_ids hold cap entries and expert_ids cap_blocks.
+__global__ void __launch_bounds__(MT_THREADS) lru_manage_tables_kernel(
+    const int* __restrict__ ids, int mk, int E, int S, int max_distinct, int max_inserts, int* __restrict__ table,
+    int* __restrict__ map_cold, int* __restrict__ slot_expert, long long* __restrict__ slot_stamp,
+    uint8_t* __restrict__ routed_out, long long* __restrict__ step, int* __restrict__ miss, int* __restrict__ n_miss,
+    int blk, long cap, long cap_blocks, int* __restrict__ sorted_h, int* __restrict__ eids_h,
+    int* __restrict__ ntpp_h, int* __restrict__ sorted_c, int* __restrict__ eids_c, int* __restrict__ ntpp_c) {
+  __shared__ union {
+    ManageLds m;
+    TabLds<MT_THREADS> t;
+  } u;
+  __shared__ short lids_h[TAB_SMALL_MAX], lids_c[TAB_SMALL_MAX];
+  manage_step(u.m, ids, mk, E, S, max_distinct, max_inserts, table, map_cold, slot_expert, slot_stamp, routed_out,
+              step, miss, n_miss, nullptr, nullptr);
+  __syncthreads();                                   // the installs' global writes are ordered before the reads
+  for (int i = threadIdx.x; i < mk; i += MT_THREADS) {
+    const int e = ids[i];
+    const bool ok = e >= 0 && e < E;
+    lids_h[i] = (short)(ok ? table[e] : -1);
+    lids_c[i] = (short)(ok ? map_cold[e] : -1);
+  }
+  __syncthreads();                                   // every manage LDS read is done: the union turns over
+  zero_counts(u.t, E);
+  lds_barrier();
+  build_tables(u.t, lids_h, mk, E, blk, sorted_h, eids_h, ntpp_h, true, cap, cap_blocks);
+  if (sorted_c) {
+    zero_counts(u.t, E);
+    lds_barrier();
+    build_tables(u.t, lids_c, mk, E, blk, sorted_c, eids_c, ntpp_c, true, cap, cap_blocks);
+  }
+}
+
 struct Slabs {
   u32x4* d[6];
   const u32x4* s[6];
@@ -240,6 +301,58 @@ extern "C" int r9k_lru_manage_map(long ids, int mk, int E, int S, int max_distin
                      (long long*)slot_stamp, (uint8_t*)routed, (long long*)step, (int*)miss, (int*)n_miss,
                      (int*)hot, (int*)cold);
   return hipGetLastError() == hipSuccess ? 0 : -6;
+}
+
+namespace {
+
+int manage_tables_launch(long ids, int mk, int E, int S, int max_distinct, int max_inserts, long table, long map_cold,
+                         long slot_expert, long slot_stamp, long routed, long step, long miss, long n_miss, int blk,
+                         long cap, long cap_blocks, long sorted_h, long eids_h, long ntpp_h, long sorted_c,
+                         long eids_c, long ntpp_c, long stream) {
+  if (E <= 0 || E > MAX_E || S <= 0 || S > MAX_S || S > E || mk < 0 || blk <= 0) return -1;
+  if (max_inserts < 0 || max_inserts > S) return -2;
+  if ((mk && !ids) || !table || !map_cold || !slot_expert || !slot_stamp || !routed || !step || !miss || !n_miss ||
+      !sorted_h || !eids_h || !ntpp_h || (sorted_c && (!eids_c || !ntpp_c)))
+    return -3;
+  if ((slot_stamp | step) & 7) return -4;
+  if (E > TAB_MAX_E || mk > TAB_SMALL_MAX) return 2;          // one workgroup's tables: the composed path serves it
+  hipLaunchKernelGGL(lru_manage_tables_kernel, dim3(1), dim3(MT_THREADS), 0, (hipStream_t)stream, (const int*)ids, mk,
+                     E, S, max_distinct, max_inserts, (int*)table, (int*)map_cold, (int*)slot_expert,
+                     (long long*)slot_stamp, (uint8_t*)routed, (long long*)step, (int*)miss, (int*)n_miss, blk, cap,
+                     cap_blocks, (int*)sorted_h, (int*)eids_h, (int*)ntpp_h, (int*)sorted_c, (int*)eids_c,
+                     (int*)ntpp_c);
+  return hipGetLastError() == hipSuccess ? 0 : -6;
+}
+
+}  // namespace
+
+// The manage step and both passes' routing tables in one launch, tables of this library's capacity (sorted
+// capacity(mk, E, blk) entries, expert ids capacity / blk); sorted_c = 0 skips the host pass. 2 when not served
+// (E > 1024 or mk > 4096; nothing launched: manage_map + two aligns give the same result).
+extern "C" int r9k_lru_manage_tables(long ids, int mk, int E, int S, int max_distinct, int max_inserts, long table,
+                                     long map_cold, long slot_expert, long slot_stamp, long routed, long step,
+                                     long miss, long n_miss, int blk, long sorted_h, long eids_h, long ntpp_h,
+                                     long sorted_c, long eids_c, long ntpp_c, long stream) {
+  return manage_tables_launch(ids, mk, E, S, max_distinct, max_inserts, table, map_cold, slot_expert, slot_stamp,
+                              routed, step, miss, n_miss, blk, -1, -1, sorted_h, eids_h, ntpp_h, sorted_c, eids_c,
+                              ntpp_c, stream);
+}
+
+// The reference's one-launch manage + both moe_align_block_size outputs with its buffer lengths: sorted_* hold L
+// entries and eids_* NB (L must cover the padded total's bound: min(mk * bs, mk + E (bs - 1)) rows while mk < E,
+// else mk + E (bs - 1); NB >= ceil(L / bs)). The tails past the padded totals are written (numel / -1) up to L / NB.
+extern "C" int r4d_lru_fused(long ids, int mk, int E, int S, int max_distinct, int max_inserts, long table,
+                             long map_cold, long slot_expert, long slot_stamp, long routed, long step, long miss,
+                             long n_miss, int bs, int L, int NB, long sorted_hot, long eids_hot, long npad_hot,
+                             long sorted_cold, long eids_cold, long npad_cold, long stream) {
+  if (bs <= 0 || mk < 0 || L <= 0 || NB <= 0) return -1;
+  const long lo = (long)mk + (long)E * (bs - 1);
+  const long need = mk < E ? (lo < (long)mk * bs ? lo : (long)mk * bs) : lo;
+  if (L < need || (long)NB * bs < L) return -1;
+  if (!sorted_cold) return -3;
+  return manage_tables_launch(ids, mk, E, S, max_distinct, max_inserts, table, map_cold, slot_expert, slot_stamp,
+                              routed, step, miss, n_miss, bs, L, NB, sorted_hot, eids_hot, npad_hot, sorted_cold,
+                              eids_cold, npad_cold, stream);
 }
 
 extern "C" int r4d_lru_manage(long ids, int mk, int E, int S, int max_distinct, int max_inserts, long table,

@@ -1,0 +1,165 @@
+// r9k_tables.h -- the moe_align_block_size table build of one workgroup (LDS histogram, scan of the block-padded
+// counts, block layout and a stable placement: rows ascend within each expert), shared by the routing kernels and
+// the expert cache's one-launch manage + tables (reference contract: kernels/r9k_moe_route.hip:27-31,
+// r9700_vllm/kernels/moe.py:574-592).
+#pragma once
+#include "r9k_common.h"
+
+namespace r9k {
+
+constexpr int TAB_MAX_E = 1024;      // experts (ids) one workgroup's tables cover: E <= its thread count
+constexpr int TAB_SMALL_MAX = 4096;  // routed rows whose tables one workgroup builds from LDS
+
+// Workgroup barrier that orders LDS traffic only (global stores stay in flight).
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+template <int NT>
+struct TabLds {
+  static constexpr int NW = NT / WAVE;
+  int cnt[TAB_MAX_E];              // rows per expert
+  int offs[TAB_MAX_E];             // first padded position of each expert
+  int cursor[TAB_MAX_E];           // next slot of each expert during the placement
+  uint16_t wcnt[NW][TAB_MAX_E];    // rows per (wave, expert) in the current round of NT rows; zero between rounds
+  int scan[NW];
+};
+
+template <int NT>
+__device__ __forceinline__ void zero_counts(TabLds<NT>& sh, int E) {
+  for (int e = threadIdx.x; e < E; e += NT) sh.cnt[e] = 0;
+  uint32_t* p = reinterpret_cast<uint32_t*>(&sh.wcnt[0][0]);
+  for (int i = threadIdx.x; i < TabLds<NT>::NW * TAB_MAX_E / 2; i += NT) p[i] = 0u;
+}
+
+// Exclusive scan of the block-padded counts (one expert per thread, E <= NT): offs[], returns the padded total.
+template <int NT>
+__device__ __forceinline__ int padded_scan(TabLds<NT>& sh, int E, int blk) {
+  constexpr int NW = NT / WAVE;
+  const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
+  const int c = tid < E ? sh.cnt[tid] : 0;
+  const int n = ((c + blk - 1) / blk) * blk;
+  int x = n;
+#pragma unroll
+  for (int o = 1; o < WAVE; o <<= 1) {
+    const int y = __shfl_up(x, o, WAVE);
+    if (lane >= o) x += y;
+  }
+  if (lane == WAVE - 1) sh.scan[wave] = x;
+  lds_barrier();
+  int wbase = 0, total = 0;
+#pragma unroll
+  for (int w = 0; w < NW; w++) {
+    if (w < wave) wbase += sh.scan[w];
+    total += sh.scan[w];
+  }
+  if (tid < E) sh.offs[tid] = wbase + x - n;
+  lds_barrier();
+  return total;
+}
+
+// Expert blocks and padding entries of the experts e < E with e % nshare == share, every expert's cursor at its
+// first slot plus `pre` (the calling thread's expert's rows in earlier chunks), and this share's part of the
+// capacity tail: sorted_ids up to `cap` entries, expert_ids up to `cap_blocks` (cap < 0: this library's capacity,
+// ceil((numel + E (blk - 1)) / blk) * blk entries and cap / blk blocks). Ends with an LDS barrier.
+template <int NT>
+__device__ __forceinline__ void write_layout(TabLds<NT>& sh, int E, int blk, int numel, int total, int pre,
+                                             int share, int nshare, int* __restrict__ sorted_ids,
+                                             int* __restrict__ expert_ids, bool write_tail = true, long cap = -1,
+                                             long cap_blocks = -1) {
+  constexpr int NW = NT / WAVE;
+  const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
+  if (tid < E) sh.cursor[tid] = sh.offs[tid] + pre;
+  // a wave per expert of the share: its block ids and its padding entries (up to blk - 1) written by the wave's lanes
+  for (int e = share + wave * nshare; e < E; e += NW * nshare) {
+    const int c = sh.cnt[e], o = sh.offs[e];
+    if (c > 0) {
+      const int n = ((c + blk - 1) / blk) * blk;
+      for (int b = o / blk + lane; b < (o + n) / blk; b += WAVE) expert_ids[b] = e;
+      for (int i = o + c + lane; i < o + n; i += WAVE) sorted_ids[i] = numel;
+    }
+  }
+  if (!write_tail) {                            // live entries only: the capacity past ntpp is left as it was
+    lds_barrier();
+    return;
+  }
+  if (cap < 0) {
+    cap = ((long)numel + (long)E * (blk - 1) + blk - 1) / blk * blk;
+    cap_blocks = cap / blk;
+  }
+  const long tail = cap - total, per = (tail + nshare - 1) / nshare;
+  const long i1 = min(cap, total + (long)(share + 1) * per);
+  for (long i = total + (long)share * per + tid; i < i1; i += NT) sorted_ids[i] = numel;
+  const long btail = cap_blocks - total / blk, bper = (btail + nshare - 1) / nshare;
+  const long b1 = min(cap_blocks, total / blk + (long)(share + 1) * bper);
+  for (long b = total / blk + (long)share * bper + tid; b < b1; b += NT) expert_ids[b] = -1;
+  lds_barrier();
+}
+
+// The lanes of this wave whose id equals this lane's (ids in [0, 2^nbits), -1 = none): the valid lanes ANDed with,
+// per id bit, the ballot of that bit or its complement -- nbits + 1 ballots instead of a compare against every lane.
+__device__ __forceinline__ uint64_t same_id_lanes(int e, int nbits) {
+  uint64_t m = __ballot(e >= 0);
+  for (int b = 0; b < nbits; b++) {
+    const int bit = (e >> b) & 1;
+    const uint64_t B = __ballot(bit);
+    m &= bit ? B : ~B;
+  }
+  return m;
+}
+
+__device__ __forceinline__ int id_bits(int E) { return E <= 1 ? 0 : 32 - __builtin_clz((unsigned)(E - 1)); }
+
+// Stable placement of ids[base, base + NT) (LDS; -1 = not placed) at their experts' cursors: a lane's rank among
+// the equal ids of lower lanes in its wave is the count of same-id lanes below it (same_id_lanes), the rows of
+// earlier waves come from the per-wave counts. Advances the cursors; leaves wcnt zero.
+template <int NT>
+__device__ __forceinline__ void stable_round(TabLds<NT>& sh, const short* ids, int base, int n, int row0, int E,
+                                             int* __restrict__ sorted_ids) {
+  constexpr int NW = NT / WAVE;
+  const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
+  const int t = base + tid;
+  const int e = t < n ? ids[t] : -1;
+  int rank = 0, cw = 0;
+  if (base + wave * WAVE < n) {                                     // waves past the rows skip the ballots
+    const uint64_t m = same_id_lanes(e, id_bits(E));
+    rank = __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+    cw = __popcll(m);
+  }
+  if (e >= 0 && rank == cw - 1) sh.wcnt[wave][e] = (uint16_t)cw;     // the last of its expert in this wave
+  lds_barrier();
+  if (e >= 0) {
+    int pos = sh.cursor[e] + rank;
+    for (int w = 0; w < wave; w++) pos += sh.wcnt[w][e];
+    sorted_ids[pos] = row0 + t;
+  }
+  lds_barrier();
+  if (tid < E) {
+    int add = 0;
+#pragma unroll
+    for (int w = 0; w < NW; w++) {
+      add += sh.wcnt[w][tid];
+      sh.wcnt[w][tid] = 0;
+    }
+    sh.cursor[tid] += add;
+  }
+  lds_barrier();
+}
+
+// The whole table build in one workgroup from ids in LDS (numel <= SMALL_MAX, -1 = skipped; zero_counts and a
+// barrier done by the caller): histogram, scan, layout and the stable placement.
+template <int NT>
+__device__ __forceinline__ void build_tables(TabLds<NT>& sh, const short* ids, int numel, int E, int blk,
+                                             int* __restrict__ sorted_ids, int* __restrict__ expert_ids,
+                                             int* __restrict__ ntpp, bool tail = true, long cap = -1,
+                                             long cap_blocks = -1) {
+  for (int t = threadIdx.x; t < numel; t += NT) {
+    const int e = ids[t];
+    if (e >= 0) atomicAdd(&sh.cnt[e], 1);
+  }
+  lds_barrier();
+  const int total = padded_scan(sh, E, blk);
+  if (threadIdx.x == 0) ntpp[0] = total;
+  write_layout(sh, E, blk, numel, total, 0, 0, 1, sorted_ids, expert_ids, tail, cap, cap_blocks);
+  for (int base = 0; base < numel; base += NT) stable_round(sh, ids, base, numel, 0, E, sorted_ids);
+}
+
+}  // namespace r9k

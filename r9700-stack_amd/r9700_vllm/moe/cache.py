@@ -55,6 +55,10 @@ def _L():
         L.r9k_lru_manage_map.argtypes = [l, i, i, i, i, i] + [l] * 10 + [l]
         L.r9k_lru_map_ids.restype = i
         L.r9k_lru_map_ids.argtypes = [l, i, i, l, l, l, l, l]
+        L.r9k_lru_manage_tables.restype = i
+        L.r9k_lru_manage_tables.argtypes = [l, i, i, i, i, i] + [l] * 8 + [i] + [l] * 6 + [l]
+        L.r4d_lru_fused.restype = i
+        L.r4d_lru_fused.argtypes = [l, i, i, i, i, i] + [l] * 8 + [i, i, i] + [l] * 6 + [l]
         L.r9k_host_alloc.restype = l
         L.r9k_host_alloc.argtypes = [l]
         L.r9k_host_free.restype = i
@@ -349,19 +353,34 @@ class LayerCache:
         return (L, NB, o[2][:L], o[3][:NB], o[4], o[5][:L], o[6][:NB], o[7], o[8][:mk], o[9][:mk])
 
     def update_fused(self, topk_ids: torch.Tensor, bs: int, need_cold: bool = True):
-        """LRU manage (which also maps the routing ids) + gather, then both align outputs: the resident one over
-        slot ids (ids through table) and the host one over expert ids (through map_cold). Returns
+        """LRU manage and both align outputs -- the resident one over slot ids (ids through table), the host one
+        over expert ids (through map_cold) -- in one launch (r9k_lru_manage_tables; E <= 1024 and mk <= 4096, else
+        manage with the mapped ids, then two aligns: the same tables), then the gather. Returns
         ((sorted, eids, ntpp) hot, (sorted, eids, ntpp) cold), views of the layer's persistent buffers. need_cold =
         False skips the host tables (their contents are then stale): for steps of at most no_cold_limit rows, whose
         cold pass is provably empty."""
         ids = self._ids(topk_ids)
         mk = ids.numel()
         L_, NB, sh, eh, nh, sc, ec, nc, hid, cid = self._align_bufs(mk, bs)
+        lib, st = _L(), _stream()
+        # one launch (manage + both table sets) while one workgroup can build the tables, else manage + two aligns
+        rc = lib.r9k_lru_manage_tables(ids.data_ptr(), mk, self.E, self.S, self.max_distinct, self.max_inserts,
+                                       self.table.data_ptr(), self.map_cold.data_ptr(), self.slot_expert.data_ptr(),
+                                       self.slot_stamp.data_ptr(), self.routed.data_ptr(), self.step.data_ptr(),
+                                       self.miss.data_ptr(), self.n_miss.data_ptr(), bs, sh.data_ptr(), eh.data_ptr(),
+                                       nh.data_ptr(), sc.data_ptr() if need_cold else 0,
+                                       ec.data_ptr() if need_cold else 0, nc.data_ptr() if need_cold else 0, st)
+        if rc not in (0, 2):
+            raise RuntimeError(f"r9k_lru_manage_tables failed ({rc}) E={self.E} S={self.S} mk={mk}")
+        if rc == 0:
+            self._gather()
+            if self.stats is not None:
+                self._record()
+            return (sh, eh, nh), (sc, ec, nc)
         self._manage(ids, hid, cid)
         self._gather()
         if self.stats is not None:
             self._record()
-        lib, st = _L(), _stream()
         n = lib.r9k_moe_align_scratch_ints(mk, self.E)
         scratch = K._align_scratch(ids.device, n)
         for a, s_, e_, t_ in ((hid, sh, eh, nh), (cid, sc, ec, nc))[: 2 if need_cold else 1]:

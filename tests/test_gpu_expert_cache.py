@@ -101,6 +101,113 @@ def test_lru_manage_matches_oracle(dev, E, S, thresh, max_ins, M, k, seed):
         assert same_state(d, st), step
 
 
+def _tables_state(d: DevState):
+    return [d.table, d.map_cold, d.slot_expert, d.slot_stamp, d.routed, d.step, d.n_miss]
+
+
+@pytest.mark.parametrize("E,S,thresh,max_ins,M,k,blk,seed", [
+    (64, 48, 0.5, 48, 4, 6, 16, 11), (288, 64, 0.99, 64, 8, 8, 16, 12), (384, 256, 0.99, 64, 32, 8, 32, 13),
+    (1024, 512, 0.99, 256, 500, 8, 16, 14), (16, 16, 1.0, 16, 3, 4, 64, 15)])
+def test_manage_tables_one_launch_equals_composed(dev, E, S, thresh, max_ins, M, k, blk, seed):
+    """r9k_lru_manage_tables (manage + both passes' tables in one launch) against r9k_lru_manage_map + two
+    r9k_moe_align launches on a twin state: every state array and both table sets (the whole capacity) bit for bit
+    after every step, with the host tables skipped on some steps; the state also against the oracle's manager."""
+    print(f"manage+tables E={E} S={S} M={M} k={k} blk={blk}", flush=True)
+    rng = np.random.default_rng(seed)
+    a, b = DevState(dev, E, S, max_ins), DevState(dev, E, S, max_ins)
+    st = O.LruState(E, S)
+    max_distinct = int(S * thresh)
+    hot = rng.permutation(E)[: max(1, S // 2)]
+    L = C._L()
+    s_ = torch.cuda.current_stream().cuda_stream
+    for step in range(40):
+        if step == 25:
+            hot = rng.permutation(E)[: max(1, S // 2)]
+        pool = np.arange(E) if step % 7 == 0 else hot
+        ids_np = np.stack([rng.choice(pool, size=min(k, pool.size), replace=False) for _ in range(M)]).reshape(-1)
+        if step % 5 == 0:
+            ids_np = np.concatenate([ids_np, [-1, E, E + 3]])
+        O.lru_manage(st, ids_np, max_distinct, max_ins)
+        ids = torch.from_numpy(ids_np.astype(np.int32)).to(dev)
+        mk = ids.numel()
+        cap = K.capacity(mk, E, blk)
+        need_cold = step % 3 != 2
+        i32 = dict(dtype=torch.int32, device=dev)
+        ta = [torch.full((cap,), -7, **i32), torch.full((cap // blk,), -7, **i32), torch.full((1,), -7, **i32),
+              torch.full((cap,), -7, **i32), torch.full((cap // blk,), -7, **i32), torch.full((1,), -7, **i32)]
+        cold_ptrs = [t.data_ptr() for t in ta[3:]] if need_cold else [0, 0, 0]
+        rc = L.r9k_lru_manage_tables(ids.data_ptr(), mk, E, S, max_distinct, max_ins, a.table.data_ptr(),
+                                     a.map_cold.data_ptr(), a.slot_expert.data_ptr(), a.slot_stamp.data_ptr(),
+                                     a.routed.data_ptr(), a.step.data_ptr(), a.miss.data_ptr(), a.n_miss.data_ptr(),
+                                     blk, ta[0].data_ptr(), ta[1].data_ptr(), ta[2].data_ptr(), *cold_ptrs, s_)
+        assert rc == 0, rc
+        hid, cid = b.manage(ids, max_distinct, max_ins, mapped=True)
+        hb = K.moe_align(hid, blk, E)
+        cb = K.moe_align(cid, blk, E) if need_cold else None
+        torch.cuda.synchronize()
+        for x, y in zip(_tables_state(a), _tables_state(b)):
+            assert torch.equal(x, y), step
+        n = int(a.n_miss.item())
+        assert torch.equal(a.miss[:n], b.miss[:n]), step
+        assert same_state(a, st), step
+        for x, y in zip(ta[:3], hb):
+            assert torch.equal(x, y), step
+        if need_cold:
+            for x, y in zip(ta[3:], cb):
+                assert torch.equal(x, y), step
+        else:
+            assert bool((ta[3] == -7).all()) and bool((ta[5] == -7).all()), step
+
+
+def test_r4d_lru_fused_reference_sizing(dev):
+    """The reference's entry with vLLM's table lengths (L = min(mk * bs, mk + E (bs - 1)) while mk < E): the tables
+    equal this library's over their first L / NB entries and nothing past L / NB is written; E > 1024 is not served
+    (2, nothing changes)."""
+    E, S, max_ins, bs = 288, 64, 64, 16
+    rng = np.random.default_rng(21)
+    a, b = DevState(dev, E, S, max_ins), DevState(dev, E, S, max_ins)
+    L = C._L()
+    s_ = torch.cuda.current_stream().cuda_stream
+    for M in (1, 4, 40, 300):
+        ids = torch.from_numpy(np.stack([rng.choice(E, 8, replace=False) for _ in range(M)]).reshape(-1)
+                               .astype(np.int32)).to(dev)
+        mk = ids.numel()
+        Lr = min(mk * bs, mk + E * (bs - 1)) if mk < E else mk + E * (bs - 1)
+        NB = -(-Lr // bs)
+        i32 = dict(dtype=torch.int32, device=dev)
+        bufs = [torch.full((Lr + 64,), -7, **i32), torch.full((NB + 8,), -7, **i32), torch.full((1,), -7, **i32),
+                torch.full((Lr + 64,), -7, **i32), torch.full((NB + 8,), -7, **i32), torch.full((1,), -7, **i32)]
+        rc = L.r4d_lru_fused(ids.data_ptr(), mk, E, S, S, max_ins, a.table.data_ptr(), a.map_cold.data_ptr(),
+                             a.slot_expert.data_ptr(), a.slot_stamp.data_ptr(), a.routed.data_ptr(),
+                             a.step.data_ptr(), a.miss.data_ptr(), a.n_miss.data_ptr(), bs, Lr, NB,
+                             *[t.data_ptr() for t in bufs], s_)
+        assert rc == 0, rc
+        hid, cid = b.manage(ids, S, max_ins, mapped=True)
+        hb, cb = K.moe_align(hid, bs, E), K.moe_align(cid, bs, E)
+        torch.cuda.synchronize()
+        print(f"  r4d_lru_fused M={M}: L={Lr} NB={NB} npad hot {int(bufs[2].item())} cold {int(bufs[5].item())}",
+              flush=True)
+        for (so, eo, no), (sr, er, nr) in (((bufs[0], bufs[1], bufs[2]), hb), ((bufs[3], bufs[4], bufs[5]), cb)):
+            assert torch.equal(no, nr)
+            assert torch.equal(so[:Lr], sr[:Lr]) and bool((so[Lr:] == -7).all())
+            assert torch.equal(eo[:NB], er[:NB]) and bool((eo[NB:] == -7).all())
+        for x, y in zip(_tables_state(a), _tables_state(b)):
+            assert torch.equal(x, y)
+    big = DevState(dev, 2048, 64, 64)
+    before = [t.clone() for t in _tables_state(big)]
+    ids = torch.randint(0, 2048, (64,), dtype=torch.int32, device=dev)
+    mk, Lr = 64, 64 * bs
+    out = [torch.empty(Lr, dtype=torch.int32, device=dev) for _ in range(6)]
+    rc = L.r4d_lru_fused(ids.data_ptr(), mk, 2048, 64, 64, 64, big.table.data_ptr(), big.map_cold.data_ptr(),
+                         big.slot_expert.data_ptr(), big.slot_stamp.data_ptr(), big.routed.data_ptr(),
+                         big.step.data_ptr(), big.miss.data_ptr(), big.n_miss.data_ptr(), bs, Lr, Lr // bs,
+                         *[t.data_ptr() for t in out], s_)
+    torch.cuda.synchronize()
+    assert rc == 2
+    for x, y in zip(_tables_state(big), before):
+        assert torch.equal(x, y)
+
+
 def test_lru_gather_copies_listed_slabs(dev):
     E, S = 12, 5
     print("lru gather", flush=True)
