@@ -107,6 +107,10 @@ class Step:
         self.eid = torch.empty(cap // self.blk, dtype=torch.int32, device=dev)
         self.ntpp = torch.zeros(1, dtype=torch.int32, device=dev)
         self.scratch = torch.zeros(route.scratch_ints(E), dtype=torch.int32, device=dev)
+        # the router's second (256-row) layout for steps the device may route to big blocks (route.dual_wanted)
+        capb = route.capacity(self.numel, E, 256)
+        self.big = (torch.empty(capb, dtype=torch.int32, device=dev),
+                    torch.empty(capb // 256, dtype=torch.int32, device=dev), torch.zeros(1, dtype=torch.int32, device=dev))
         self.experts = [R9700Mxfp4Experts.standalone(w13.wsr, w2.wsr) for w13, w2 in zip(layer.W13, layer.W2)]
 
         class _Routed:
@@ -117,7 +121,14 @@ class Step:
 
     def __call__(self, c: int):
         K, route, L = self.K, self.route, self.layer
-        if self.fused:
+        bb = route.dual_wanted(self.routed, self.numel, L.E) if self.fused else 0
+        if bb == 256:
+            # as R9kTopKRouter for a wide decode step of a layer that runs the device-picked pair: both layouts
+            w, ids, xq, xs = route.moe_route_dual(self.logits, self.topk, True, self.blk, self.sid, self.eid,
+                                                  self.ntpp, self.scratch, self.x, bb, *self.big, K.DEVICE_MIN_ROWS)
+            self.routed._r9k_tables = route.Tables(ids, self.sid, self.eid, self.ntpp, self.blk, self.numel,
+                                                   self.x, self.x._version, xq, xs, big=(*self.big, bb))
+        elif self.fused:
             w, ids, xq, xs = route.moe_route_quant(self.logits, self.topk, True, self.blk, self.sid, self.eid,
                                                    self.ntpp, self.scratch, self.x)
             self.routed._r9k_tables = route.Tables(ids, self.sid, self.eid, self.ntpp, self.blk, self.numel,

@@ -126,12 +126,25 @@ int r9k_moe_topk_quant(long logits, int ldl, long weights, long ids, int M, int 
 /* r9k_moe_route plus the per-token fp8 quant of the layer's activations in the same launch (the work the reference
  * does in r9k_moe_route and then r9k_quant_rows_fp8, r9700_vllm/moe/experts.py:185): x bf16 [M][H] (row stride
  * ldx) -> xq e4m3fn [M][H], xs fp32 [M], the bytes of r9k_quant_rows_fp8. scratch as for r9k_moe_route (its first
- * int is the arrival counter, used above 16 rows). Decode widths only: M <= 64, E <= 512, the tables within 16384
- * entries, H % 8 == 0, H <= 4096, x 16-byte and xq 8-byte aligned; any other shape returns 2 with nothing launched
- * (run r9k_moe_route + r9k_quant_rows_fp8 instead). 0 / 1 bad arguments / 2 / HIP error. */
+ * int is the arrival counter, used above 16 rows). Served while the routing is one launch (M * topk <= 4096) for
+ * H % 8 == 0, H <= 4096, ldx % 8 == 0, x 16-byte and xq 8-byte aligned; any other shape returns 2 with nothing
+ * launched (run r9k_moe_route + r9k_quant_rows_fp8 instead). 0 / 1 bad arguments / 2 / HIP error. */
 int r9k_moe_route_quant(long logits, int ldl, long weights, long ids, long sorted_ids, long expert_ids, long ntpp,
                         long scratch, int M, int E, int topk, int renorm, int blk, long x, long ldx, int H, long xq,
                         long xs, long stream);
+
+/* r9k_moe_route(_quant) with the tables in two layouts of which the device keeps one. No counterpart in the
+ * reference, which picks the block size on the host from the row count (r9700_vllm/kernels/moe.py:532-535): a
+ * skewed step the host cannot see may take the 256-row blocks. The per-expert counts decide: with nbig the number of
+ * big_blk-row blocks, the big layout is kept when nbig > 0 and M * topk >= min_rows * nbig (r9k_moe_pick_blocks'
+ * rule); only the kept layout is written (blk rows: sorted_ids / expert_ids over the whole capacity, ntpp; big_blk
+ * rows: sorted_big / expert_big up to ntpp_big, the live entries), the other's ntpp is set to 0. x = 0: no
+ * activation quant (else as r9k_moe_route_quant). Served for M * topk <= 4096 and, with x, rows the wave quant
+ * takes; 2 otherwise (nothing launched). 0 / 1 bad arguments / 2 / HIP error. */
+int r9k_moe_route_dual(long logits, int ldl, long weights, long ids, long sorted_ids, long expert_ids, long ntpp,
+                       long scratch, int M, int E, int topk, int renorm, int blk, long x, long ldx, int H, long xq,
+                       long xs, int big_blk, long sorted_big, long expert_big, long ntpp_big, int min_rows,
+                       long stream);
 
 /* Align tables only, from ids int32 [numel] (the role of vLLM's moe_align_block_size, called at
  * r9700_vllm/moe/experts.py:172 of the reference). ids outside [0, E) are left out. scratch: at least

@@ -164,23 +164,50 @@ __device__ __forceinline__ void topk_core(const uint16_t* h, int E, int topk, bo
   }
 }
 
+// Optional outputs of the fused routing launch beyond the reference's: the per-token fp8 quant of the layer input
+// (x bf16 rows of stride ldx, H values -> xq e4m3 [M, H], xs fp32 [M], quant_row_wave's bytes; x == nullptr: none)
+// and a second table layout of the same ids in blocks of big_blk rows (sorted_big == nullptr: none), of which the
+// device keeps one: the big layout when its nbig blocks hold numel >= min_rows * nbig rows (pick_blocks_kernel's
+// rule), the other's ntpp then 0 and its entries left as they were. The big layout is written live-only (entries up
+// to its ntpp), the small one over its whole capacity.
+struct RouteExtras {
+  const uint16_t* x;
+  long ldx;
+  int H;
+  uint8_t* xq;
+  float* xs;
+  int big_blk;
+  int min_rows;
+  int* sorted_big;
+  int* expert_big;
+  int* ntpp_big;
+};
+
 // Fused routing + tables (reference: r9k_moe_route_kernel, kernels/r9k_moe_route.hip:67-210), numel <= SMALL_MAX:
 // one wave per token row over ceil(M / 8) workgroups of 8 waves (the rows' latency chains spread over CUs). Each
 // workgroup stores its ids as agent-scope atomics, waits for them (vmcnt) and counts itself in `arrive` (zero at
 // entry, left zero); the last to arrive reads every id back with agent-scope loads, 8 in flight a thread, into LDS
-// and builds the tables. With one workgroup the ids go straight to LDS.
-template <int EPL>
+// and builds the tables. With one workgroup the ids go straight to LDS. With R > 0 each wave then quantises its
+// rows of x (after the arrival, so the table build does not wait for it; R chunks of 8 values a lane).
+template <int EPL, int R>
 __global__ void __launch_bounds__(FT) route_fused_kernel(const uint16_t* __restrict__ logits, int ldl,
                                                          float* __restrict__ weights, int* __restrict__ ids,
                                                          int* __restrict__ sorted_ids, int* __restrict__ expert_ids,
                                                          int* __restrict__ ntpp, int* __restrict__ arrive, int M,
-                                                         int E, int topk, int renorm, int blk) {
+                                                         int E, int topk, int renorm, int blk, RouteExtras ex) {
   __shared__ TabLds<FT> sh;
   __shared__ short lids[SMALL_MAX];
   __shared__ int s_last;
+  __shared__ int s_nbig[FW];
   const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
   const int numel = M * topk;
   const bool single = gridDim.x == 1;
+  auto quant_rows = [&]() {
+    if constexpr (R > 0) {
+      for (int r = blockIdx.x * FW + wave; r < M; r += gridDim.x * FW)
+        quant_row_wave<R>(ex.x + (size_t)r * ex.ldx, ex.H, ex.xq + (size_t)r * ex.H, ex.xs + r, lane);
+    }
+  };
   zero_counts(sh, E);
   for (int r = blockIdx.x * FW + wave; r < M; r += gridDim.x * FW) {
     uint16_t h[EPL];
@@ -194,7 +221,10 @@ __global__ void __launch_bounds__(FT) route_fused_kernel(const uint16_t* __restr
     if (threadIdx.x == 0)
       s_last = __hip_atomic_fetch_add(arrive, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (int)gridDim.x - 1;
     lds_barrier();
-    if (!s_last) return;
+    if (!s_last) {
+      quant_rows();
+      return;
+    }
     if (threadIdx.x == 0) __hip_atomic_store(arrive, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     for (int t0 = 0; t0 < numel; t0 += 8 * FT) {                // other workgroups' ids, past this CU's caches
       int v[8];
@@ -210,7 +240,26 @@ __global__ void __launch_bounds__(FT) route_fused_kernel(const uint16_t* __restr
     }
   }
   lds_barrier();
-  build_tables(sh, lids, numel, E, blk, sorted_ids, expert_ids, ntpp);
+  count_ids(sh, lids, numel);
+  bool big = false;
+  if (ex.sorted_big) {
+    // the pick from the per-expert counts (the big layout's block count), then only the kept layout is built; the
+    // other's ntpp is 0 (its GEMMs exit before reading its stale entries)
+    int nb = 0;
+    for (int e = threadIdx.x; e < E; e += FT) nb += (sh.cnt[e] + ex.big_blk - 1) / ex.big_blk;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) nb += __shfl_xor(nb, o, WAVE);
+    if (lane == 0) s_nbig[wave] = nb;
+    lds_barrier();
+    int nbig = 0;
+#pragma unroll
+    for (int w = 0; w < FW; w++) nbig += s_nbig[w];
+    big = nbig > 0 && (long)numel >= (long)ex.min_rows * nbig;
+    if (threadIdx.x == 0) (big ? ntpp : ex.ntpp_big)[0] = 0;
+  }
+  if (big) build_from_counts(sh, lids, numel, E, ex.big_blk, ex.sorted_big, ex.expert_big, ex.ntpp_big, false);
+  else build_from_counts(sh, lids, numel, E, blk, sorted_ids, expert_ids, ntpp);
+  quant_rows();
 }
 
 // ------------------------------------------------------------------ small batches: M <= 64 rows in one workgroup
@@ -711,6 +760,47 @@ hipError_t launch_small(const uint16_t* logits, int ldl, float* w, int* ids, int
 #undef RS
 }
 
+// Chunks of 8 values a lane for quant_row_wave over H values (0: the rows do not suit the wave quant).
+int quant_chunks_for(int H, long ldx, const void* x, const void* xq) {
+  if (H < 8 || H % 8 || H > 512 * QRMAX || ldx < H || ldx % 8 || (reinterpret_cast<uintptr_t>(x) & 15) ||
+      (reinterpret_cast<uintptr_t>(xq) & 7))
+    return 0;
+  const int nv = (H / 8 + WAVE - 1) / WAVE;
+  return nv <= 1 ? 1 : nv <= 2 ? 2 : nv <= 4 ? 4 : 8;
+}
+
+// The one-wave-per-row routing launch (numel <= SMALL_MAX), with the extras R (quant chunks, 0 = none) and ex.
+int launch_fused(const uint16_t* logits, int ldl, float* w, int* ids, int* sorted_ids, int* expert_ids, int* ntpp,
+                 int* arrive, int M, int E, int topk, int renorm, int blk, int R, const RouteExtras& ex,
+                 hipStream_t st) {
+  const int nblk = (M + FW - 1) / FW;
+  if (nblk > 1 && !arrive) return 1;
+#define RF(EPLV, RV)                                                                                              \
+  hipLaunchKernelGGL((route_fused_kernel<EPLV, RV>), dim3(nblk), dim3(FT), 0, st, logits, ldl, w, ids,           \
+                     sorted_ids, expert_ids, ntpp, arrive, M, E, topk, renorm, blk, ex)
+#define RFR(EPLV)                    \
+  switch (R) {                       \
+    case 0: RF(EPLV, 0); break;      \
+    case 1: RF(EPLV, 1); break;      \
+    case 2: RF(EPLV, 2); break;      \
+    case 4: RF(EPLV, 4); break;      \
+    case 8: RF(EPLV, 8); break;      \
+    default: return 1;               \
+  }
+  switch (epl_for(E)) {
+    case 2: RFR(2); break;
+    case 4: RFR(4); break;
+    case 6: RFR(6); break;
+    case 8: RFR(8); break;
+    case 12: RFR(12); break;
+    case 16: RFR(16); break;
+    default: return 1;
+  }
+#undef RFR
+#undef RF
+  return (int)hipGetLastError();
+}
+
 }  // namespace
 
 // Reference: kernels/r9k_moe_route.hip:217-233. logits [M, E] bf16 (row stride ldl) -> weights fp32 [M, topk],
@@ -728,22 +818,9 @@ extern "C" int r9k_moe_route(long logits, int ldl, long weights, long ids, long 
                              (int*)expert_ids, (int*)ntpp, (int*)scratch, M, E, topk, renorm, blk, nullptr, 0, 0,
                              nullptr, nullptr, st);
   if (numel <= SMALL_MAX) {
-    const int nblk = (M + FW - 1) / FW;
-    if (nblk > 1 && !scratch) return 1;
-#define RF(EPLV)                                                                                                  \
-  hipLaunchKernelGGL(route_fused_kernel<EPLV>, dim3(nblk), dim3(FT), 0, st, (const uint16_t*)logits, ldl,        \
-                     (float*)weights, (int*)ids, (int*)sorted_ids, (int*)expert_ids, (int*)ntpp, (int*)scratch, M, E, \
-                     topk, renorm, blk)
-    switch (epl_for(E)) {
-      case 2: RF(2); break;
-      case 4: RF(4); break;
-      case 6: RF(6); break;
-      case 8: RF(8); break;
-      case 12: RF(12); break;
-      case 16: RF(16); break;
-      default: return 1;
-    }
-#undef RF
+    const RouteExtras none{};
+    return launch_fused((const uint16_t*)logits, ldl, (float*)weights, (int*)ids, (int*)sorted_ids, (int*)expert_ids,
+                        (int*)ntpp, (int*)scratch, M, E, topk, renorm, blk, 0, none, st);
   } else {
     if (numel > 0x7fffffffL) return 1;
     if (launch_topk((const uint16_t*)logits, ldl, (float*)weights, (int*)ids, M, E, topk, renorm, st)) return 1;
@@ -755,18 +832,63 @@ extern "C" int r9k_moe_route(long logits, int ldl, long weights, long ids, long 
 
 // r9k_moe_route plus the per-token fp8 quant of the layer's activations in the same launch (the quant of
 // r9k_quant_rows_fp8, same bytes): x bf16 [M, H] (row stride ldx) -> xq e4m3 [M, H], xs fp32 [M]. scratch as for
-// r9k_moe_route. Only at decode widths (M <= 64, E <= 512, the tables within 16384 entries) for rows that suit the
-// wave quant (H % 8 == 0, H <= 4096, x 16-byte and xq 8-byte aligned); returns 2 for any other shape, with
-// nothing launched, so the caller runs r9k_moe_route and r9k_quant_rows_fp8. 1 bad arguments, else the HIP error.
+// r9k_moe_route. Served while the routing is one launch (numel <= 4096) for rows that suit the wave quant (H % 8 ==
+// 0, H <= 4096, ldx % 8 == 0, x 16-byte and xq 8-byte aligned); returns 2 for any other shape, with nothing
+// launched, so the caller runs r9k_moe_route and r9k_quant_rows_fp8. 1 bad arguments, else the HIP error.
 extern "C" int r9k_moe_route_quant(long logits, int ldl, long weights, long ids, long sorted_ids, long expert_ids,
                                    long ntpp, long scratch, int M, int E, int topk, int renorm, int blk, long x,
                                    long ldx, int H, long xq, long xs, long stream) {
   if (!route_args_ok(M, E, topk, blk) || ldl < E || !x) return 1;
-  if (!small_fits(M, E, topk, blk, (const void*)scratch, (const void*)x, ldx, H, (const void*)xq, (const void*)xs))
-    return 2;
-  return (int)launch_small((const uint16_t*)logits, ldl, (float*)weights, (int*)ids, (int*)sorted_ids,
-                           (int*)expert_ids, (int*)ntpp, (int*)scratch, M, E, topk, renorm, blk, (const uint16_t*)x,
-                           ldx, H, (uint8_t*)xq, (float*)xs, (hipStream_t)stream);
+  if (small_fits(M, E, topk, blk, (const void*)scratch, (const void*)x, ldx, H, (const void*)xq, (const void*)xs))
+    return (int)launch_small((const uint16_t*)logits, ldl, (float*)weights, (int*)ids, (int*)sorted_ids,
+                             (int*)expert_ids, (int*)ntpp, (int*)scratch, M, E, topk, renorm, blk,
+                             (const uint16_t*)x, ldx, H, (uint8_t*)xq, (float*)xs, (hipStream_t)stream);
+  const int R = quant_chunks_for(H, ldx, (const void*)x, (const void*)xq);
+  if ((long)M * topk > SMALL_MAX || !R || !xs) return 2;
+  RouteExtras ex{};
+  ex.x = (const uint16_t*)x;
+  ex.ldx = ldx;
+  ex.H = H;
+  ex.xq = (uint8_t*)xq;
+  ex.xs = (float*)xs;
+  return launch_fused((const uint16_t*)logits, ldl, (float*)weights, (int*)ids, (int*)sorted_ids, (int*)expert_ids,
+                      (int*)ntpp, (int*)scratch, M, E, topk, renorm, blk, R, ex, (hipStream_t)stream);
+}
+
+// r9k_moe_route(_quant) with the tables in two layouts, of which the device keeps one (no reference counterpart:
+// the reference picks its block size on the host from the row count; here a skewed step the host cannot see may
+// take the big blocks): blocks of blk rows into sorted_ids / expert_ids / ntpp (the whole capacity) or of big_blk
+// rows into sorted_big / expert_big / ntpp_big (live entries only): the big layout is kept when its nbig blocks
+// hold numel >= min_rows * nbig rows (r9k_moe_pick_blocks' rule), only the kept layout is written, and the other's
+// ntpp is set to 0 (its entries are left as they were). x = 0:
+// no activation quant. Served for numel <= 4096 (one-wave-per-row launch) and, with x, rows that suit the wave
+// quant (as r9k_moe_route_quant); 2 otherwise (nothing launched). 1 bad arguments, else the HIP error.
+extern "C" int r9k_moe_route_dual(long logits, int ldl, long weights, long ids, long sorted_ids, long expert_ids,
+                                  long ntpp, long scratch, int M, int E, int topk, int renorm, int blk, long x,
+                                  long ldx, int H, long xq, long xs, int big_blk, long sorted_big, long expert_big,
+                                  long ntpp_big, int min_rows, long stream) {
+  if (!route_args_ok(M, E, topk, blk) || ldl < E || big_blk < 1 || (big_blk & (big_blk - 1)) || min_rows < 0 ||
+      !sorted_big || !expert_big || !ntpp_big)
+    return 1;
+  if ((long)M * topk > SMALL_MAX) return 2;
+  int R = 0;
+  RouteExtras ex{};
+  if (x) {
+    R = quant_chunks_for(H, ldx, (const void*)x, (const void*)xq);
+    if (!R || !xs) return 2;
+    ex.x = (const uint16_t*)x;
+    ex.ldx = ldx;
+    ex.H = H;
+    ex.xq = (uint8_t*)xq;
+    ex.xs = (float*)xs;
+  }
+  ex.big_blk = big_blk;
+  ex.min_rows = min_rows;
+  ex.sorted_big = (int*)sorted_big;
+  ex.expert_big = (int*)expert_big;
+  ex.ntpp_big = (int*)ntpp_big;
+  return launch_fused((const uint16_t*)logits, ldl, (float*)weights, (int*)ids, (int*)sorted_ids, (int*)expert_ids,
+                      (int*)ntpp, (int*)scratch, M, E, topk, renorm, blk, R, ex, (hipStream_t)stream);
 }
 
 extern "C" int r9k_moe_route_max_experts(void) { return MAX_E; }

@@ -7,7 +7,7 @@
 
 namespace r9k {
 
-constexpr int TAB_MAX_E = 1024;      // experts (ids) one workgroup's tables cover: E <= its thread count
+constexpr int TAB_MAX_E = 1024;      // experts (ids) one workgroup's tables cover
 constexpr int TAB_SMALL_MAX = 4096;  // routed rows whose tables one workgroup builds from LDS
 
 // Workgroup barrier that orders LDS traffic only (global stores stay in flight).
@@ -30,13 +30,16 @@ __device__ __forceinline__ void zero_counts(TabLds<NT>& sh, int E) {
   for (int i = threadIdx.x; i < TabLds<NT>::NW * TAB_MAX_E / 2; i += NT) p[i] = 0u;
 }
 
-// Exclusive scan of the block-padded counts (one expert per thread, E <= NT): offs[], returns the padded total.
+// Exclusive scan of the block-padded counts: offs[], returns the padded total. Thread t covers the experts
+// [t * ept, t * ept + ept), ept = ceil(E / NT) (one expert a thread while E <= NT), so offsets ascend with the expert.
 template <int NT>
 __device__ __forceinline__ int padded_scan(TabLds<NT>& sh, int E, int blk) {
   constexpr int NW = NT / WAVE;
   const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
-  const int c = tid < E ? sh.cnt[tid] : 0;
-  const int n = ((c + blk - 1) / blk) * blk;
+  const int ept = (E + NT - 1) / NT;
+  const int e0 = min(tid * ept, E), e1 = min(e0 + ept, E);
+  int n = 0;
+  for (int e = e0; e < e1; e++) n += (sh.cnt[e] + blk - 1) / blk * blk;
   int x = n;
 #pragma unroll
   for (int o = 1; o < WAVE; o <<= 1) {
@@ -51,7 +54,11 @@ __device__ __forceinline__ int padded_scan(TabLds<NT>& sh, int E, int blk) {
     if (w < wave) wbase += sh.scan[w];
     total += sh.scan[w];
   }
-  if (tid < E) sh.offs[tid] = wbase + x - n;
+  int o = wbase + x - n;
+  for (int e = e0; e < e1; e++) {
+    sh.offs[e] = o;
+    o += (sh.cnt[e] + blk - 1) / blk * blk;
+  }
   lds_barrier();
   return total;
 }
@@ -67,7 +74,7 @@ __device__ __forceinline__ void write_layout(TabLds<NT>& sh, int E, int blk, int
                                              long cap_blocks = -1) {
   constexpr int NW = NT / WAVE;
   const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
-  if (tid < E) sh.cursor[tid] = sh.offs[tid] + pre;
+  for (int e = tid; e < E; e += NT) sh.cursor[e] = sh.offs[e] + (e == tid ? pre : 0);   // pre: callers with E <= NT
   // a wave per expert of the share: its block ids and its padding entries (up to blk - 1) written by the wave's lanes
   for (int e = share + wave * nshare; e < E; e += NW * nshare) {
     const int c = sh.cnt[e], o = sh.offs[e];
@@ -132,34 +139,51 @@ __device__ __forceinline__ void stable_round(TabLds<NT>& sh, const short* ids, i
     sorted_ids[pos] = row0 + t;
   }
   lds_barrier();
-  if (tid < E) {
+  for (int ex = tid; ex < E; ex += NT) {
     int add = 0;
 #pragma unroll
     for (int w = 0; w < NW; w++) {
-      add += sh.wcnt[w][tid];
-      sh.wcnt[w][tid] = 0;
+      add += sh.wcnt[w][ex];
+      sh.wcnt[w][ex] = 0;
     }
-    sh.cursor[tid] += add;
+    sh.cursor[ex] += add;
   }
   lds_barrier();
 }
 
-// The whole table build in one workgroup from ids in LDS (numel <= SMALL_MAX, -1 = skipped; zero_counts and a
-// barrier done by the caller): histogram, scan, layout and the stable placement.
+// The table layout and stable placement from per-expert counts already in sh.cnt (a barrier after the counting;
+// wcnt zero): scan, layout and the rounds. The counts stay in sh.cnt, so a second layout of the same rows (another
+// block size) can follow with no recount.
 template <int NT>
-__device__ __forceinline__ void build_tables(TabLds<NT>& sh, const short* ids, int numel, int E, int blk,
-                                             int* __restrict__ sorted_ids, int* __restrict__ expert_ids,
-                                             int* __restrict__ ntpp, bool tail = true, long cap = -1,
-                                             long cap_blocks = -1) {
+__device__ __forceinline__ void build_from_counts(TabLds<NT>& sh, const short* ids, int numel, int E, int blk,
+                                                  int* __restrict__ sorted_ids, int* __restrict__ expert_ids,
+                                                  int* __restrict__ ntpp, bool tail = true, long cap = -1,
+                                                  long cap_blocks = -1) {
+  const int total = padded_scan(sh, E, blk);
+  if (threadIdx.x == 0) ntpp[0] = total;
+  write_layout(sh, E, blk, numel, total, 0, 0, 1, sorted_ids, expert_ids, tail, cap, cap_blocks);
+  for (int base = 0; base < numel; base += NT) stable_round(sh, ids, base, numel, 0, E, sorted_ids);
+}
+
+// The whole table build in one workgroup from ids in LDS (numel <= TAB_SMALL_MAX, -1 = skipped; zero_counts and a
+// barrier done by the caller): histogram, scan, layout and the stable placement.
+// Per-id row counts into sh.cnt (zero_counts and a barrier done by the caller); ends with a barrier.
+template <int NT>
+__device__ __forceinline__ void count_ids(TabLds<NT>& sh, const short* ids, int numel) {
   for (int t = threadIdx.x; t < numel; t += NT) {
     const int e = ids[t];
     if (e >= 0) atomicAdd(&sh.cnt[e], 1);
   }
   lds_barrier();
-  const int total = padded_scan(sh, E, blk);
-  if (threadIdx.x == 0) ntpp[0] = total;
-  write_layout(sh, E, blk, numel, total, 0, 0, 1, sorted_ids, expert_ids, tail, cap, cap_blocks);
-  for (int base = 0; base < numel; base += NT) stable_round(sh, ids, base, numel, 0, E, sorted_ids);
+}
+
+template <int NT>
+__device__ __forceinline__ void build_tables(TabLds<NT>& sh, const short* ids, int numel, int E, int blk,
+                                             int* __restrict__ sorted_ids, int* __restrict__ expert_ids,
+                                             int* __restrict__ ntpp, bool tail = true, long cap = -1,
+                                             long cap_blocks = -1) {
+  count_ids(sh, ids, numel);
+  build_from_counts(sh, ids, numel, E, blk, sorted_ids, expert_ids, ntpp, tail, cap, cap_blocks);
 }
 
 }  // namespace r9k

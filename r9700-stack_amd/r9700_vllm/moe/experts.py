@@ -211,7 +211,15 @@ class R9700Mxfp4Experts(_experts_base()):
             if need_cold:
                 passes.append((c1, c2, cold_al, (MT, pf_gate, pf_down)))
         else:
-            tabs = route.take(getattr(self, "r9k_layer", None), topk_ids, blk, numel) if expert_map is None else None
+            layer = getattr(self, "r9k_layer", None)
+            bc = K.big_block_cfg(K1, K2)
+            dual_ok = (nv is None and expert_map is None and not MOE_FUSE and bc is not None
+                       and K.DEVICE_BLOCKS_MIN > 0)
+            if layer is not None:
+                # tells the router (route.dual_wanted) to build both layouts for this layer's wide decode steps
+                layer._r9k_dual_blk = bc[1] if dual_ok else 0
+            tabs = route.take(layer, topk_ids, blk, numel) if expert_map is None else None
+            tabs_big = route.take_big(layer, topk_ids, blk, numel) if tabs is not None else None
             if tabs is None:
                 tabs = K.moe_align(topk_ids, blk, E, expert_map)
             if nv is not None:
@@ -221,9 +229,12 @@ class R9700Mxfp4Experts(_experts_base()):
                 W1 = K.Mxfp4Experts(w1, self.w1_scale, N1, K1)
                 W2 = K.Mxfp4Experts(w2, self.w2_scale, N2, K2)
             passes = [(W1, W2, tabs, (MT, pf_gate, pf_down))]
-            bc = K.big_block_cfg(K1, K2)
-            if (big is None and nv is None and expert_map is None and not MOE_FUSE and bc is not None
-                    and K.DEVICE_BLOCKS_MIN > 0 and numel >= K.DEVICE_BLOCKS_MIN):
+            if tabs_big is not None:
+                # the router built both layouts and the device kept one: both passes run (the other's GEMMs exit)
+                if big is not None or not dual_ok or tabs_big[3] != bc[1]:
+                    raise RuntimeError("r9k MoE: the router's second table layout does not fit this layer's pass")
+                passes.append((W1, W2, tabs_big[:3], (1, bc[0], bc[0])))
+            elif big is None and dual_ok and numel >= K.DEVICE_BLOCKS_MIN:
                 # skew the host cannot see: the 256-row layout too, the device keeps one (the other's GEMMs exit)
                 tabs_big = K.moe_align(topk_ids, bc[1], E, live_only=True)
                 K.pick_blocks(tabs[2], tabs_big[2], numel, bc[1])

@@ -28,7 +28,7 @@ from ..kernels import moe as KM
 logger = get_logger(__name__)
 
 MAX_ROWS = int(os.environ.get("R9K_MOE_ROUTE_MAX_ROWS", "256"))
-QUANT_MAX_ROWS = 64                 # r9k_moe_route_quant's row limit (one routing row a wave in one launch)
+QUANT_MAX_NUMEL = 4096              # routed rows (M * topk) r9k_moe_route_quant and _dual take in one launch
 _LIB = torch.library.Library("r9700", "FRAGMENT")
 _bound = None
 _registered = False
@@ -46,6 +46,8 @@ def lib() -> ctypes.CDLL:
         L.r9k_moe_route.argtypes, L.r9k_moe_route.restype = common + [l], i
         L.r9k_moe_route_quant.argtypes = common + [l, l, i, l, l, l]
         L.r9k_moe_route_quant.restype = i
+        L.r9k_moe_route_dual.argtypes = common + [l, l, i, l, l, i, l, l, l, i, l]
+        L.r9k_moe_route_dual.restype = i
         L.r9k_moe_route_max_experts.restype = i
         L.r9k_moe_route_max_topk.restype = i
         _bound = L
@@ -119,6 +121,57 @@ def moe_route_quant(logits: torch.Tensor, topk: int, renorm: bool, blk: int, sor
     return w, ids, xq, xs
 
 
+def moe_route_dual(logits: torch.Tensor, topk: int, renorm: bool, blk: int, sorted_ids: torch.Tensor,
+                   expert_ids: torch.Tensor, ntpp: torch.Tensor, scratch: torch.Tensor, x: torch.Tensor | None,
+                   big_blk: int, sorted_big: torch.Tensor, expert_big: torch.Tensor, ntpp_big: torch.Tensor,
+                   min_rows: int) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+    """moe_route(_quant) with the tables in two layouts -- blocks of blk rows and of big_blk rows (live entries) --
+    of which the device keeps one (the big one when its blocks average >= min_rows rows; the other's ntpp is set
+    to 0), in one launch (r9k_moe_route_dual). Returns (weights, ids, xq, xs); without x, xq and xs are empty.
+    The caller keeps to the served shapes (dual_wanted, quant_suits): anything else raises."""
+    M, E = logits.shape
+    assert logits.dtype == torch.bfloat16 and logits.stride(1) == 1
+    dev = logits.device
+    w = torch.empty((M, topk), dtype=torch.float32, device=dev)
+    ids = torch.empty((M, topk), dtype=torch.int32, device=dev)
+    xq = torch.empty((0,), dtype=torch.float8_e4m3fn, device=dev)
+    xs = torch.empty((0,), dtype=torch.float32, device=dev)
+    xa = (0, 0, 0, 0, 0)
+    if x is not None:
+        if not (x.dim() == 2 and x.dtype == torch.bfloat16 and x.stride(1) == 1 and x.shape[0] == M):
+            raise ValueError("moe_route_dual: x must be bf16 [M, H] with unit column stride")
+        H = x.shape[1]
+        xq = torch.empty((M, H), dtype=torch.float8_e4m3fn, device=dev)
+        xs = torch.empty((M,), dtype=torch.float32, device=dev)
+        xa = (x.data_ptr(), x.stride(0), H, xq.data_ptr(), xs.data_ptr())
+    rc = lib().r9k_moe_route_dual(logits.data_ptr(), logits.stride(0), w.data_ptr(), ids.data_ptr(),
+                                  sorted_ids.data_ptr(), expert_ids.data_ptr(), ntpp.data_ptr(), scratch.data_ptr(),
+                                  M, E, topk, int(renorm), blk, *xa, big_blk, sorted_big.data_ptr(),
+                                  expert_big.data_ptr(), ntpp_big.data_ptr(), min_rows,
+                                  torch.cuda.current_stream().cuda_stream)
+    if rc:
+        raise RuntimeError(f"r9k_moe_route_dual failed ({rc}) M={M} E={E} topk={topk} blk={blk} big={big_blk}")
+    return w, ids, xq, xs
+
+
+def quant_suits(x: torch.Tensor) -> bool:
+    """Rows the routing launch's wave quant takes: H % 8 == 0, H <= 4096, 16-byte aligned rows."""
+    H = x.shape[1]
+    return H % 8 == 0 and 8 <= H <= 4096 and x.stride(0) % 8 == 0 and x.data_ptr() % 16 == 0
+
+
+def _moe_route_dual_fake(logits, topk: int, renorm: bool, blk: int, sorted_ids, expert_ids, ntpp, scratch, x,
+                         big_blk: int, sorted_big, expert_big, ntpp_big, min_rows: int):
+    M = logits.shape[0]
+    dev = logits.device
+    w, ids = _moe_route_fake(logits, topk, renorm, blk, sorted_ids, expert_ids, ntpp, scratch)
+    if x is None:
+        return (w, ids, torch.empty((0,), dtype=torch.float8_e4m3fn, device=dev),
+                torch.empty((0,), dtype=torch.float32, device=dev))
+    return (w, ids, torch.empty(x.shape, dtype=torch.float8_e4m3fn, device=dev),
+            torch.empty((M,), dtype=torch.float32, device=dev))
+
+
 def _moe_route_fake(logits, topk: int, renorm: bool, blk: int, sorted_ids, expert_ids, ntpp, scratch):
     M = logits.shape[0]
     return (torch.empty((M, topk), dtype=torch.float32, device=logits.device),
@@ -139,6 +192,8 @@ def register() -> None:
     mut = ["sorted_ids", "expert_ids", "ntpp", "scratch"]
     register_custom_op(_LIB, "moe_route", moe_route, mut, _moe_route_fake)
     register_custom_op(_LIB, "moe_route_quant", moe_route_quant, mut, _moe_route_quant_fake)
+    register_custom_op(_LIB, "moe_route_dual", moe_route_dual, mut + ["sorted_big", "expert_big", "ntpp_big"],
+                       _moe_route_dual_fake)
     _registered = True
 
 
@@ -157,6 +212,7 @@ class Tables:
     x_version: int = -1
     xq: torch.Tensor | None = None
     xs: torch.Tensor | None = None
+    big: tuple | None = None          # (sorted_ids, expert_ids, ntpp, big_blk): the second layout (moe_route_dual)
 
     def matches(self, topk_ids: torch.Tensor, blk: int, numel: int) -> bool:
         return (self.sorted_ids is not None and self.blk == blk and self.numel == numel
@@ -175,6 +231,25 @@ def take(layer, topk_ids: torch.Tensor, blk: int, numel: int):
     return (t.sorted_ids, t.expert_ids, t.ntpp) if t is not None and t.matches(topk_ids, blk, numel) else None
 
 
+def take_big(layer, topk_ids: torch.Tensor, blk: int, numel: int):
+    """The second table layout (sorted_ids, expert_ids, ntpp, big_blk) the router built for this call, of which the
+    device kept one (the small layout's tables, take(), carry the other ntpp), or None. A caller that takes the
+    small tables of a call with a second layout must run both layouts' GEMMs."""
+    t = getattr(layer, "_r9k_tables", None)
+    return t.big if t is not None and t.big is not None and t.matches(topk_ids, blk, numel) else None
+
+
+def dual_wanted(layer, numel: int, E: int) -> int:
+    """The big block size when the router should build both layouts for a call of `numel` routed rows: the experts
+    of `layer` signalled they run the device-picked pair (their `_r9k_dual_blk`), the step has at least
+    DEVICE_BLOCKS_MIN rows and the host would keep small blocks (touched experts average below PREFILL_MOE_ROWS);
+    else 0."""
+    bb = getattr(layer, "_r9k_dual_blk", 0) if layer is not None else 0
+    if not bb or KM.DEVICE_BLOCKS_MIN <= 0 or numel < KM.DEVICE_BLOCKS_MIN or numel > QUANT_MAX_NUMEL:
+        return 0
+    return bb if numel / max(1, min(E, numel)) < KM.PREFILL_MOE_ROWS else 0
+
+
 def take_quant(layer, topk_ids: torch.Tensor, x: torch.Tensor):
     """The (xq, xs) fp8 quant of `x` the router made with this call's ids, or None."""
     t = getattr(layer, "_r9k_tables", None)
@@ -188,13 +263,19 @@ class RouteBuffers:
     decode path uses, plus the zero-once routing scratch. Allocated once (outside graph capture) and reused by every
     call, so captured graphs keep valid addresses."""
 
-    def __init__(self, device: torch.device, E: int, topk: int):
+    def __init__(self, device: torch.device, E: int, topk: int, big_blk: int = 256):
         cap = max(capacity(m * topk, E, KM.MOE_BLOCK * KM.pick_mt(m * topk, E)) for m in range(1, MAX_ROWS + 1))
         i32 = dict(dtype=torch.int32, device=device)
         self.sorted_ids = torch.empty(cap, **i32)
         self.expert_ids = torch.empty(cap // KM.MOE_BLOCK, **i32)
         self.ntpp = torch.zeros(1, **i32)
         self.scratch = torch.zeros(scratch_ints(E), **i32)
+        # the second (big-block) layout of moe_route_dual: live entries only, so sized by the routed rows
+        capb = capacity(min(MAX_ROWS * topk, QUANT_MAX_NUMEL), E, big_blk)
+        self.big_blk = big_blk
+        self.sorted_big = torch.empty(capb, **i32)
+        self.expert_big = torch.empty(capb // big_blk, **i32)
+        self.ntpp_big = torch.zeros(1, **i32)
 
 
 def plan_route(logits: torch.Tensor, topk: int, E: int, x, indices_type=None) -> str:
@@ -214,17 +295,18 @@ def plan_route(logits: torch.Tensor, topk: int, E: int, x, indices_type=None) ->
     return "stock"
 
 
-def _quantisable(x, M: int) -> bool:
+def _quantisable(x, M: int, topk: int) -> bool:
     """A layer input the decode routing launch can quantise alongside (the kernel checks its alignment)."""
     return (isinstance(x, torch.Tensor) and x.dim() == 2 and x.dtype == torch.bfloat16 and x.shape[0] == M
-            and x.is_contiguous() and M <= QUANT_MAX_ROWS)
+            and x.is_contiguous() and M * topk <= QUANT_MAX_NUMEL)
 
 
 def route_step(logits: torch.Tensor, x, topk: int, renorm: bool, E: int, bufs: RouteBuffers | None,
-               indices_type=None, use_ops: bool = True):
+               indices_type=None, use_ops: bool = True, dual_blk: int = 0):
     """Route one call: (weights, ids, Tables) on the decode / wide paths, or None when the stock router must run.
     At decode widths `bufs` holds the tables; use_ops routes the launch through the torch.ops.r9700 custom ops
-    (the compiled-graph path), else the plain functions."""
+    (the compiled-graph path), else the plain functions. dual_blk (dual_wanted): also the big-block layout, of which
+    the device keeps one (moe_route_dual)."""
     path = plan_route(logits, topk, E, x, indices_type)
     if path == "stock":
         return None
@@ -240,7 +322,17 @@ def route_step(logits: torch.Tensor, x, topk: int, renorm: bool, E: int, bufs: R
     args = (logits, topk, renorm, blk, bufs.sorted_ids, bufs.expert_ids, bufs.ntpp, bufs.scratch)
     if use_ops:
         register()
-    if _quantisable(x, M):
+    if dual_blk and dual_blk == bufs.big_blk and numel <= QUANT_MAX_NUMEL:
+        xd = x if _quantisable(x, M, topk) and quant_suits(x) else None
+        fn = torch.ops.r9700.moe_route_dual if use_ops else moe_route_dual
+        w, ids, xq, xs = fn(*args, xd, dual_blk, bufs.sorted_big, bufs.expert_big, bufs.ntpp_big,
+                            KM.DEVICE_MIN_ROWS)
+        big = (bufs.sorted_big, bufs.expert_big, bufs.ntpp_big, dual_blk)
+        if xd is None:
+            return w, ids, Tables(ids, bufs.sorted_ids, bufs.expert_ids, bufs.ntpp, blk, numel, big=big)
+        return w, ids, Tables(ids, bufs.sorted_ids, bufs.expert_ids, bufs.ntpp, blk, numel, x, x._version, xq, xs,
+                              big=big)
+    if _quantisable(x, M, topk):
         fn = torch.ops.r9700.moe_route_quant if use_ops else moe_route_quant
         w, ids, xq, xs = fn(*args, x)
         return w, ids, Tables(ids, bufs.sorted_ids, bufs.expert_ids, bufs.ntpp, blk, numel, x, x._version, xq, xs)
@@ -273,8 +365,10 @@ def make_router(stock, routed_experts):
             return b
 
         def _compute_routing(self, hidden_states, router_logits, indices_type, *, input_ids=None):
+            numel = router_logits.shape[0] * self.top_k
             r = route_step(router_logits, hidden_states, self.top_k, self.renormalize, self.global_num_experts,
-                           self._bufs_for(router_logits.device), indices_type)
+                           self._bufs_for(router_logits.device), indices_type,
+                           dual_blk=dual_wanted(self.routed_experts, numel, self.global_num_experts))
             if r is None:
                 self.routed_experts._r9k_tables = None
                 return super()._compute_routing(hidden_states, router_logits, indices_type, input_ids=input_ids)

@@ -401,6 +401,59 @@ def test_layer_config5_T256_router_handoff(dev, monkeypatch):
     assert r < 1e-2 and c >= 0.9999
 
 
+@pytest.mark.parametrize("E,H,I,T,zipf", [(384, 4096, 2048, 256, True), (384, 4096, 2048, 256, False),
+                                        (288, 2048, 512, 128, False), (288, 2048, 512, 256, True)])
+def test_layer_router_dual_layout(dev, E, H, I, T, zipf):
+    """The router's one-launch dual layout (route.route_step with dual_blk: routing, input quant, both table
+    layouts and the device's pick in r9k_moe_route_dual) through apply(): bit for bit the output of the same call
+    whose experts build the second layout themselves (moe_align + r9k_moe_pick_blocks), whichever layout the
+    device keeps; apply() signals the router through the layer object (route.dual_wanted)."""
+    from r9700_vllm.moe import route
+    topk = 8
+    seed = 20261201 + 7000 + E + T + int(zipf)
+    (_, _), (_, _), W13, W2 = make_layer(dev, E, H, I, seed, 116, 126)
+    g = torch.Generator().manual_seed(seed + 1)
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16).to(dev)
+    logits = torch.randn(T, E, generator=g)
+    if zipf:
+        rank = torch.randperm(E, generator=g).float() + 1
+        logits = logits - 1.1 * torch.log(rank)[None, :]
+    logits = logits.to(torch.bfloat16).to(dev)
+    numel = T * topk
+    assert numel >= K.DEVICE_BLOCKS_MIN and K.pick_moe_prefill_block(numel, E, H, I) is None
+
+    class Routed:
+        _r9k_tables = None
+
+    def run(layer_obj, tables):
+        layer_obj._r9k_tables = tables
+        ex = R9700Mxfp4Experts.standalone(W13.wsr, W2.wsr)
+        ex.r9k_layer = layer_obj
+        o = torch.full((T, H), float("nan"), dtype=torch.bfloat16, device=dev)
+        ex.apply(o, x, W13.wq, W2.wq, w, ids, "silu", E, None, None, None, None, None, None, False)
+        torch.cuda.synchronize()
+        return o
+
+    bufs = route.RouteBuffers(dev, E, topk)
+    lay = Routed()
+    # first call: apply() has not spoken yet -> single layout from the router, the experts build the second one
+    w, ids, t1 = route.route_step(logits, x, topk, True, E, bufs, use_ops=False,
+                                  dual_blk=route.dual_wanted(lay, numel, E))
+    assert t1.big is None
+    o1 = run(lay, t1)
+    assert route.dual_wanted(lay, numel, E) == 256, "apply() must ask the router for both layouts"
+    w, ids, t2 = route.route_step(logits, x, topk, True, E, bufs, use_ops=False,
+                                  dual_blk=route.dual_wanted(lay, numel, E))
+    assert t2.big is not None and t2.xq is not None
+    kept_big = int(t2.big[2].item()) > 0
+    o2 = run(lay, t2)
+    same = torch.equal(o1.view(torch.int16), o2.view(torch.int16))
+    print(f"router dual E={E} T={T} zipf={zipf}: kept {'256-row' if kept_big else '16-row'} layout, bit-equal {same}",
+          flush=True)
+    assert same
+    assert not bool(torch.isnan(o2.float()).any())
+
+
 @pytest.mark.parametrize("M", [4, 16])
 def test_dense_mxfp4_linear_config4_decode_full(dev, M):
     """BASELINE config 4 decode widths on the full [17408, 5120] weight through ops.mxfp4_linear."""

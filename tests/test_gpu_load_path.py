@@ -209,8 +209,8 @@ def test_mxfp4_linearize(dev, M):
 
 
 def test_route_step_paths(dev):
-    """route.route_step (the R9kTopKRouter body, vLLM-free): decode widths fill the persistent buffers and, up to 64
-    rows, quantise the input (bytes of quant_rows_fp8); wide calls return the top-k + quant and no tables; the ids
+    """route.route_step (the R9kTopKRouter body, vLLM-free): decode widths fill the persistent buffers and, up to
+    4096 routed rows, quantise the input (bytes of quant_rows_fp8); wide calls return the top-k + quant and no tables; the ids
     equal the oracle's and the hand-off helpers find exactly this call's data."""
     from r9700_vllm.moe import route
     E, H, topk = 288, 2048, 8
@@ -230,7 +230,7 @@ def test_route_step_paths(dev):
         got_tabs = route.take(Layer, ids, blk, numel)
         got_q = route.take_quant(Layer, ids, x)
         assert (got_tabs is not None) == (T <= route.MAX_ROWS)
-        assert (got_q is not None) == (T <= route.QUANT_MAX_ROWS or T > route.MAX_ROWS)
+        assert (got_q is not None) == (T * topk <= route.QUANT_MAX_NUMEL or T > route.MAX_ROWS)
         if got_q is not None:
             q, s = K.quant_rows_fp8(x)
             assert torch.equal(got_q[0].view(torch.uint8), q.view(torch.uint8)) and torch.equal(got_q[1], s)

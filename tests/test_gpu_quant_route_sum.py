@@ -102,7 +102,7 @@ def test_silu_mul_quant_fp8_special_values(dev):
 
 @pytest.mark.parametrize("M,E,topk,blk", [(1, 288, 8, 16), (8, 288, 8, 16), (16, 288, 8, 16), (64, 288, 8, 16),
                                           (37, 512, 10, 32), (256, 384, 8, 64), (5, 48, 6, 16), (300, 100, 10, 16),
-                                          (512, 288, 8, 16)])
+                                          (512, 288, 8, 16), (300, 1024, 8, 16), (100, 700, 16, 32)])
 @pytest.mark.parametrize("renorm", [True, False])
 def test_moe_route_fused(dev, M, E, topk, blk, renorm):
     print(f"route M={M} E={E} topk={topk} blk={blk} renorm={renorm}", flush=True)
@@ -127,10 +127,62 @@ def test_moe_route_fused(dev, M, E, topk, blk, renorm):
     check_tables(so, eo, no, ido, blk, numel, E)
 
 
+@pytest.mark.parametrize("M,E,topk,zipf,quant", [(128, 288, 8, False, True), (256, 384, 8, True, True),
+                                                 (256, 384, 8, True, False), (512, 64, 8, False, True),
+                                                 (300, 1024, 8, True, True), (130, 288, 8, True, False)])
+def test_moe_route_dual(dev, M, E, topk, zipf, quant):
+    """r9k_moe_route_dual: routing (bit-exact ids against the oracle), both table layouts and the device's pick
+    (r9k_moe_pick_blocks' rule on the oracle's counts), the kept layout's tables bit-exact against the oracle's align
+    (the 256-row one over its live entries), the other's ntpp 0, and the activation quant's bytes."""
+    print(f"route_dual M={M} E={E} topk={topk} zipf={zipf} quant={quant}", flush=True)
+    g = torch.Generator().manual_seed(M * 13 + E)
+    logits = torch.randn(M, E, generator=g)
+    if zipf:
+        rank = torch.randperm(E, generator=g).float() + 1
+        logits = logits - 1.1 * torch.log(rank)[None, :]
+    logits = logits.to(torch.bfloat16)
+    H = 2048
+    x = (torch.randn(M, H, generator=g) * 2.0).to(torch.bfloat16).to(dev)
+    numel = M * topk
+    blk, bb, min_rows = 16, 256, K.DEVICE_MIN_ROWS
+    i32 = dict(dtype=torch.int32, device=dev)
+    cap, capb = route.capacity(numel, E, blk), route.capacity(numel, E, bb)
+    s_, e_, n_ = torch.full((cap,), -9, **i32), torch.full((cap // blk,), -9, **i32), torch.full((1,), -9, **i32)
+    sb, eb, nb = torch.full((capb,), -9, **i32), torch.full((capb // bb,), -9, **i32), torch.full((1,), -9, **i32)
+    scratch = torch.zeros(route.scratch_ints(E), **i32)
+    w, ids, xq, xs = route.moe_route_dual(logits.to(dev), topk, True, blk, s_, e_, n_, scratch, x if quant else None,
+                                          bb, sb, eb, nb, min_rows)
+    torch.cuda.synchronize()
+    wo, ido = O.route(logits, topk, True)
+    assert np.array_equal(ids.cpu().numpy(), ido)
+    assert np.abs(w.cpu().numpy() - wo).max() < 2e-6
+    counts = np.bincount(ido.reshape(-1), minlength=E)
+    nbig = int(((counts + bb - 1) // bb).sum())
+    want_big = nbig > 0 and numel >= min_rows * nbig
+    so, eo, no = O.align(ido, E, blk)
+    sbo, ebo, nbo = O.align(ido, E, bb)
+    print(f"  nbig {nbig} -> {'256-row' if want_big else '16-row'} layout", flush=True)
+    if want_big:
+        assert n_.item() == 0 and nb.item() == nbo[0]
+        assert np.array_equal(sb.cpu().numpy()[:nbo[0]], sbo[:nbo[0]])
+        assert np.array_equal(eb.cpu().numpy()[:nbo[0] // bb], ebo[:nbo[0] // bb])
+    else:
+        assert nb.item() == 0 and n_.item() == no[0]
+        assert np.array_equal(s_.cpu().numpy(), so) and np.array_equal(e_.cpu().numpy(), eo)
+    assert not scratch.any()
+    if quant:
+        q, s2 = K.quant_rows_fp8(x)
+        assert torch.equal(xq.view(torch.uint8), q.view(torch.uint8)) and torch.equal(xs, s2)
+    else:
+        assert xq.numel() == 0 and xs.numel() == 0
+
+
 @pytest.mark.parametrize("M,E,topk,blk,H,ldx", [(1, 288, 8, 16, 2048, 2048), (64, 288, 8, 16, 2048, 2048),
                                                  (37, 384, 8, 16, 4096, 4096), (13, 100, 6, 32, 520, 528),
                                                  (16, 512, 10, 16, 2048, 2560),
-                                                 (100, 288, 8, 16, 2048, 2048),     # M > 64: two launches
+                                                 (100, 288, 8, 16, 2048, 2048),     # M > 64: one wave a row
+                                                 (512, 288, 8, 16, 2048, 2048), (300, 384, 8, 32, 4096, 4104),
+                                                 (600, 288, 8, 16, 2048, 2048),     # numel > 4096: two launches
                                                  (8, 288, 8, 16, 8192, 8192)])      # H > 4096: two launches
 def test_moe_route_quant(dev, M, E, topk, blk, H, ldx):
     """Routing + tables + the activation quant in one launch: every output bit-exact against the oracle, and the
