@@ -165,8 +165,6 @@ __device__ __forceinline__ void build_from_counts(TabLds<NT>& sh, const short* i
   for (int base = 0; base < numel; base += NT) stable_round(sh, ids, base, numel, 0, E, sorted_ids);
 }
 
-// The whole table build in one workgroup from ids in LDS (numel <= TAB_SMALL_MAX, -1 = skipped; zero_counts and a
-// barrier done by the caller): histogram, scan, layout and the stable placement.
 // Per-id row counts into sh.cnt (zero_counts and a barrier done by the caller); ends with a barrier.
 template <int NT>
 __device__ __forceinline__ void count_ids(TabLds<NT>& sh, const short* ids, int numel) {
@@ -177,6 +175,8 @@ __device__ __forceinline__ void count_ids(TabLds<NT>& sh, const short* ids, int 
   lds_barrier();
 }
 
+// The whole table build in one workgroup from ids in LDS (numel <= TAB_SMALL_MAX, -1 = skipped; zero_counts and a
+// barrier done by the caller): histogram, scan, layout and the stable placement.
 template <int NT>
 __device__ __forceinline__ void build_tables(TabLds<NT>& sh, const short* ids, int numel, int E, int blk,
                                              int* __restrict__ sorted_ids, int* __restrict__ expert_ids,
