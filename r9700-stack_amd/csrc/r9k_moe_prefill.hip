@@ -581,10 +581,304 @@ __global__ void __launch_bounds__(NTH) moe_prefill_persistent_kernel(
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
+
+// ------------------------------------------------------------------------------ row-resident variant (K = 512)
+// For the down GEMM at K = 512 (configs 2 and 3): each wave holds its 32 rows' activation fragments for the whole K
+// in registers (64 VGPRs), so a routing block's activations are read once per workgroup instead of once per
+// 256-column tile, and the LDS holds only a ring of four 34 KB stages. Work items are (routing block, 128-column
+// step) pairs, block-major; XCD x owns a contiguous range of them and each of its workgroups a contiguous sub-range,
+// so consecutive items of a workgroup are mostly columns of the same block. The workgroup walks a list of ring
+// steps: per block it touches, four activation steps (64 rows x 512 B each, plus their As and topk_w; waves 2c and
+// 2c + 1 copy theirs into registers) and then its column steps (the prepared layout's contiguous run of 8 column
+// tiles x 4 K-tiles of codes, 32 KB, plus 2 KB of exponents). DMA runs three steps ahead. Every load of the loop is
+// a global -> LDS DMA with an explicit wait, none a compiler-tracked load, so no compiler-inserted vmcnt wait drains
+// the ring (vmcnt completes in order, and a load issued after the output stores would wait for them). Per column
+// step and wave: 8 K-steps x 4 column tiles of the 32x32x64 scaled MFMA (weights as the fp4 A operand with their
+// block exponent, activations as the fp8 B operand), then the persistent kernel's epilogue (bf16(acc * As *
+// topk_w), permlane32 pairs, 16-byte buffer stores, padding rows and columns past N sent to the dropped offset).
+// Every step issues the same DMA count per wave, column steps 8 stores and activation steps none, so the vmcnt
+// waits are exact counts.
+constexpr int RR_K = 512;
+constexpr int RR_KS = RR_K / 64;                 // K-steps of one MFMA
+constexpr int RR_NTS = 8;                        // 16-column weight tiles per step (128 columns)
+constexpr int RR_NS = 4;                         // weight stages
+constexpr int RR_MAXB = 8;                       // routing blocks a workgroup's item range may touch
+constexpr int RR_TB = RR_K * 8;                  // code bytes of one 16-column tile over K (4 KB)
+constexpr int RR_SB = 16 * (RR_K / 32);          // exponent bytes of one 16-column tile over K (256 B)
+
+struct __align__(16) RRStage {
+  uint8_t b[RR_NTS * RR_TB];                     // 32 KB of codes
+  uint8_t s[RR_NTS * RR_SB];                     // 2 KB of exponents
+};
+struct __align__(16) RRMeta {
+  int rows[RR_MAXB][BM];                         // sorted_ids of the workgroup's blocks
+  int eid[RR_MAXB];
+  int nlive[RR_MAXB];                            // live rows (a prefix of the block); 0 for a block with no expert
+};
+constexpr size_t SMEM_RR = sizeof(RRStage) * RR_NS + sizeof(RRMeta);
+static_assert(SMEM_RR <= 160 * 1024, "LDS");
+
+constexpr int RR_DMA_OPS = 5;                    // weight DMA instructions per wave and step
+constexpr int RR_STORES = 8;                     // output stores per wave and column step
+constexpr int RR_ACH = BM / 64;                  // activation steps per block (64 rows x 512 B each)
+
+// s_waitcnt vmcnt(min(v, 40)) (waiting on fewer outstanding operations than there are is always safe).
+__device__ __forceinline__ void rr_wait_vm(int v) {
+#define RR_W(c)                                          \
+  case c:                                                \
+    asm volatile("s_waitcnt vmcnt(" #c ")" ::: "memory"); \
+    break;
+  switch (v < 0 ? 0 : v > 40 ? 40 : v) {
+    RR_W(0) RR_W(1) RR_W(2) RR_W(3) RR_W(4) RR_W(5) RR_W(6) RR_W(7) RR_W(8) RR_W(9) RR_W(10) RR_W(11) RR_W(12)
+    RR_W(13) RR_W(14) RR_W(15) RR_W(16) RR_W(17) RR_W(18) RR_W(19) RR_W(20) RR_W(21) RR_W(22) RR_W(23) RR_W(24)
+    RR_W(25) RR_W(26) RR_W(27) RR_W(28) RR_W(29) RR_W(30) RR_W(31) RR_W(32) RR_W(33) RR_W(34) RR_W(35) RR_W(36)
+    RR_W(37) RR_W(38) RR_W(39) RR_W(40)
+  }
+#undef RR_W
+}
+
+__global__ void __launch_bounds__(NTH) moe_prefill_rowres_kernel(
+    const uint8_t* __restrict__ A, const float* __restrict__ As, const uint8_t* __restrict__ Wq,
+    const uint8_t* __restrict__ Ws, uint16_t* __restrict__ C, const int* __restrict__ sorted_ids,
+    const int* __restrict__ expert_ids, const int* __restrict__ ntpp, const float* __restrict__ topk_w,
+    long wq_estride, long ws_estride, int numel, DivMagic rdiv, int N, int nsteps) {
+  extern __shared__ __align__(16) uint8_t smem[];
+  RRStage* st = reinterpret_cast<RRStage*>(smem);
+  RRMeta& mt = *reinterpret_cast<RRMeta*>(smem + RR_NS * sizeof(RRStage));
+
+  const int G = gridDim.x, wg = blockIdx.x, x = wg % NXCD, jj = wg / NXCD;
+  const int S = (G - x + NXCD - 1) / NXCD;                     // workgroups on XCD x
+  const int total = (ntpp[0] / BM) * nsteps;
+  const int q = total / NXCD, rem = total % NXCD;
+  const int xs = x * q + min(x, rem), xc = q + (x < rem ? 1 : 0);
+  const int i0 = xs + (int)((long)xc * jj / S), i1 = xs + (int)((long)xc * (jj + 1) / S);
+  if (i1 <= i0) return;
+  const int rb0 = i0 / nsteps, nblk = (i1 - 1) / nsteps - rb0 + 1;   // <= RR_MAXB, checked by the host
+  const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
+  const int NTt = N / 16;
+
+  {
+    // the blocks' tables, all loads in flight together (the kernel's only loads into registers)
+    int rv[RR_MAXB];
+#pragma unroll
+    for (int b = 0; b < RR_MAXB; b++) rv[b] = (b < nblk && tid < BM) ? sorted_ids[(size_t)(rb0 + b) * BM + tid] : 0;
+    const int ev = tid < nblk ? expert_ids[rb0 + tid] : 0;
+#pragma unroll
+    for (int b = 0; b < RR_MAXB; b++)
+      if (b < nblk && tid < BM) mt.rows[b][tid] = rv[b];
+    if (tid < nblk) mt.eid[tid] = ev;
+  }
+  __syncthreads();
+  if (wave < nblk) {
+    int nl = 0;
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      const int fr = mt.rows[wave][u * WAVE + lane];
+      nl += __popcll(__ballot(fr >= 0 && fr < numel));
+    }
+    if (lane == 0) mt.nlive[wave] = mt.eid[wave] < 0 ? 0 : nl;
+  }
+  __syncthreads();
+
+  // Steps: per touched block, RR_ACH activation steps (64 rows each, for waves 2c and 2c + 1) then its column steps
+  // in this workgroup's range. A cursor walks them in order; items(b) = the block's column steps here.
+  auto items = [&](int b) {
+    const int lo = max(i0, (rb0 + b) * nsteps), hi = min(i1, (rb0 + b + 1) * nsteps);
+    return hi - lo;
+  };
+  auto first_cs = [&](int b) { return max(i0 - (rb0 + b) * nsteps, 0); };
+  int nst = 0;
+  for (int b = 0; b < nblk; b++) nst += RR_ACH + items(b);
+  struct Cursor {
+    int b, off, len;
+  };
+  auto advance = [&](Cursor& c) {
+    if (++c.off == c.len) {
+      c.b++;
+      c.off = 0;
+      c.len = c.b < nblk ? RR_ACH + items(c.b) : 0;
+    }
+  };
+
+  // DMA of step s into stage sg, RR_DMA_OPS instructions a wave whatever the step: a column step's 32 KB run of codes
+  // (tiles past N re-read the last tile; their columns are never stored) and 2 KB of exponents; an activation step's
+  // 64 rows x 512 B (16-byte piece p of chunk row r at position p ^ (r & 31), so the fragment reads are conflict-free)
+  // and their scales (wave 0: As of each row, wave 1: topk_w, others a dummy dword).
+  const uint32_t lb0 = lds_addr(&st[0].b[wave * WAVE * 16]);
+  const uint32_t ls0 = lds_addr(&st[0].s[wave * WAVE * 4]);
+  const uint32_t doff = (uint32_t)lane * 4;                    // dummy loads read sorted_ids[lane]
+  auto issue = [&](const Cursor& c, int sg) {
+    const uint32_t so = (uint32_t)(sg * (int)sizeof(RRStage));
+    const int b = c.b;
+    if (c.off < RR_ACH) {
+      const int nl = mt.nlive[b];
+      int first = mt.rows[b][0];
+      first = (first >= 0 && first < numel) ? first : 0;
+#pragma unroll
+      for (int p = 0; p < 4; p++) {
+        const int r = p * 16 + (tid >> 5), row = c.off * 64 + r;  // row of the block
+        const int fr = row < nl ? mt.rows[b][row] : first;
+        const int piece = (tid & 31) ^ (r & 31);
+        dma16s(A, div_by((uint32_t)fr, rdiv) * (uint32_t)RR_K + (uint32_t)piece * 16, lb0 + so + p * NTH * 16);
+      }
+      const int row = c.off * 64 + lane;
+      const int fr = row < nl ? mt.rows[b][row] : first;
+      if (wave == 0) dma4s(As, div_by((uint32_t)fr, rdiv) * 4, ls0 + so);
+      else if (wave == 1 && topk_w) dma4s(topk_w, (uint32_t)fr * 4, ls0 + so);
+      else dma4s(sorted_ids, doff, ls0 + so);
+    } else {
+      int e = mt.eid[b];
+      e = __builtin_amdgcn_readfirstlane(e < 0 ? 0 : e);
+      const int cs = first_cs(b) + c.off - RR_ACH;
+      const uint8_t* wb = uniform_ptr(Wq + (size_t)e * wq_estride);
+      const uint8_t* sb = uniform_ptr(Ws + (size_t)e * ws_estride);
+#pragma unroll
+      for (int p = 0; p < 4; p++) {
+        const int piece = p * NTH + tid;                       // 16-byte piece of the step's 32 KB run
+        const int nt = min(cs * RR_NTS + (piece >> 8), NTt - 1);
+        dma16s(wb, (uint32_t)nt * RR_TB + (uint32_t)(piece & 255) * 16, lb0 + so + p * NTH * 16);
+      }
+      const int nt = min(cs * RR_NTS + (tid >> 6), NTt - 1);
+      dma4s(sb, (uint32_t)nt * RR_SB + (uint32_t)(tid & 63) * 4, ls0 + so);
+    }
+  };
+
+  const int g = lane >> 5, c32 = lane & 31;
+  // LDS offsets of this lane's weight fragment (column tile j, K-step t: + j * 8192 + t * 512) and exponent byte
+  // (+ j * 512 + t * 32)
+  const int fb = (c32 >> 4) * RR_TB + g * 256 + (c32 & 15) * 16;
+  const int fs = (c32 >> 4) * RR_SB + g * 16 + (c32 & 15);
+  const uint32_t cbytes = (uint32_t)numel * (uint32_t)N * 2u;
+  const auto crs = __builtin_amdgcn_make_buffer_rsrc(C, (short)0, (int)cbytes, 0x00020000);
+
+  Cursor ci{0, 0, RR_ACH + items(0)};                         // the step whose DMA goes out next
+  for (int s = 0; s < 3 && s < nst; s++) {
+    issue(ci, s);
+    advance(ci);
+  }
+  Cursor cc{0, 0, RR_ACH + items(0)};                         // the step being computed
+  // stores of the three steps before step s (a column step issues RR_STORES, an activation step none)
+  int st1 = 0, st2 = 0, st3 = 0;
+
+  u32x4 alo[RR_KS], ahi[RR_KS];
+  float sc = 0.f;
+  uint32_t rowoff = 0;
+  bool rlive = false, wlive = false;
+  int sidx = 0;
+  for (int s = 0; s < nst; s++) {
+    // DMA of step s: younger are the stores of steps s - 3 .. s - 1 and the DMA of steps s + 1 and s + 2
+    rr_wait_vm(st1 + st2 + st3 + (s + 1 < nst ? RR_DMA_OPS : 0) + (s + 2 < nst ? RR_DMA_OPS : 0));
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    const RRStage& Sg = st[sidx];
+    const int snext = sidx == 0 ? RR_NS - 1 : sidx - 1;       // stage read in the previous step
+    int nstores = 0;
+    if (cc.off < RR_ACH) {
+      if (s + 3 < nst) {
+        issue(ci, snext);
+        advance(ci);
+      }
+      if ((wave >> 1) == cc.off) {
+        // this wave's 32 rows of the block: activation fragments for all of K, scale, output row
+        const int b = cc.b, nl = mt.nlive[b];
+        const int r = (wave & 1) * 32 + c32, row = cc.off * 64 + r;
+        rlive = row < nl;
+        wlive = wave * 32 < nl;
+        const uint8_t* ab = &Sg.b[r * RR_K];
+#pragma unroll
+        for (int t = 0; t < RR_KS; t++) {
+          alo[t] = *reinterpret_cast<const u32x4*>(ab + (((4 * t + g) ^ (r & 31)) * 16));
+          ahi[t] = *reinterpret_cast<const u32x4*>(ab + (((4 * t + 2 + g) ^ (r & 31)) * 16));
+        }
+        const float* sf = reinterpret_cast<const float*>(Sg.s);
+        sc = sf[r];
+        if (topk_w) sc *= sf[WAVE + r];
+        rowoff = rlive ? (uint32_t)mt.rows[b][row] * (uint32_t)N : 0u;
+      }
+    } else {
+      const int cs = first_cs(cc.b) + cc.off - RR_ACH;
+      v16f acc[4];
+#pragma unroll
+      for (int j = 0; j < 4; j++) acc[j] = (v16f){};
+      if (wlive) {
+        u32x4 wf[2][4];
+        int sbv[2][4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          wf[0][j] = *reinterpret_cast<const u32x4*>(&Sg.b[fb + j * 8192]);
+          sbv[0][j] = Sg.s[fs + j * 512];
+        }
+#pragma unroll
+        for (int t = 0; t < RR_KS; t++) {
+          const int cb = t & 1, nbuf = cb ^ 1;
+          if (t + 1 < RR_KS) {
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+              wf[nbuf][j] = *reinterpret_cast<const u32x4*>(&Sg.b[fb + j * 8192 + (t + 1) * 512]);
+              sbv[nbuf][j] = Sg.s[fs + j * 512 + (t + 1) * 32];
+            }
+          }
+          const v8i af = (v8i){(int)alo[t].x, (int)alo[t].y, (int)alo[t].z, (int)alo[t].w,
+                               (int)ahi[t].x, (int)ahi[t].y, (int)ahi[t].z, (int)ahi[t].w};
+#pragma unroll
+          for (int j = 0; j < 4; j++) {
+            const v8i w8 = (v8i){(int)wf[cb][j].x, (int)wf[cb][j].y, (int)wf[cb][j].z, (int)wf[cb][j].w, 0, 0, 0, 0};
+            acc[j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(w8, af, acc[j], 4, 0, 0, sbv[cb][j], 0,
+                                                                      E8M0_ONE);
+          }
+          if (t == 0) {
+            __builtin_amdgcn_sched_barrier(0);
+            if (s + 3 < nst) {
+              issue(ci, snext);
+              advance(ci);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        }
+      } else if (s + 3 < nst) {
+        issue(ci, snext);
+        advance(ci);
+      }
+      // epilogue: as the persistent kernel's (lanes l and l + 32 hold row c32; permlane32 pairs make 16-byte runs),
+      // RR_STORES stores a wave (padding rows and columns past N to the dropped offset)
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        uint32_t pk[4][2];
+#pragma unroll
+        for (int qb = 0; qb < 4; qb++) {
+          pk[qb][0] = pack_bf16x2(acc[j][4 * qb] * sc, acc[j][4 * qb + 1] * sc);
+          pk[qb][1] = pack_bf16x2(acc[j][4 * qb + 2] * sc, acc[j][4 * qb + 3] * sc);
+        }
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+          uint32_t got[2];
+#pragma unroll
+          for (int kk = 0; kk < 2; kk++) {
+            const auto pr = __builtin_amdgcn_permlane32_swap(pk[2 * h][kk], pk[2 * h + 1][kk], false, false);
+            got[kk] = g == 0 ? pr[1] : pr[0];
+          }
+          const v4i v = g == 0 ? (v4i){(int)pk[2 * h][0], (int)pk[2 * h][1], (int)got[0], (int)got[1]}
+                               : (v4i){(int)got[0], (int)got[1], (int)pk[2 * h + 1][0], (int)pk[2 * h + 1][1]};
+          const int col = cs * RR_NTS * 16 + j * 32 + 16 * h + 8 * g;
+          const uint32_t off = (rlive && col < N) ? (rowoff + (uint32_t)col) * 2u : cbytes;
+          __builtin_amdgcn_raw_buffer_store_b128(v, crs, (int)off, 0, 0);
+        }
+      }
+      nstores = RR_STORES;
+    }
+    st3 = st2;
+    st2 = st1;
+    st1 = nstores;
+    advance(cc);
+    sidx = sidx == RR_NS - 1 ? 0 : sidx + 1;
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
+
 }  // namespace
 
 // Internal entry used by the prefill dispatch in r9k_moe_gemm.hip: tables with blocks of 256 rows, K % 128 == 0.
-// K >= 384 runs the persistent kernel (one workgroup per CU), K = 128 and 256 the one-tile-per-workgroup kernel.
+// K = 512 runs the row-resident kernel, other K >= 384 the persistent kernel (both one workgroup per CU), K = 128
+// and 256 the one-tile-per-workgroup kernel.
 int r9k_prefill_launch(long a, long as, long wq, long ws, long c, long sorted_ids, long expert_ids, long ntpp,
                        long topk_w, long ws_estride, int max_blocks, int numel, int a_row_div, int K, int N,
                        long stream) {
@@ -598,6 +892,28 @@ int r9k_prefill_launch(long a, long as, long wq, long ws, long c, long sorted_id
   if (a_rows * K >= (1L << 31) || (long)N * K / 2 >= (1L << 31) || (long)numel * 4 >= (1L << 31) ||
       (long)numel * N * 2 >= (1L << 31))
     return -3;
+  if (K == RR_K && getenv_flag_off_pf("R9K_PREFILL_ROWRES") == 0) {
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+      return -6;
+    const int nsteps = (N + RR_NTS * 16 - 1) / (RR_NTS * 16);
+    const long items = (long)max_blocks * nsteps;
+    const int grid = (int)(items < cus ? items : cus);
+    // a workgroup's item range (at most ceil(ceil(items / 8) / (grid / 8)) items) must touch <= RR_MAXB blocks
+    const long wpx = grid / NXCD > 1 ? grid / NXCD : 1;
+    const long per_wg = ((items + NXCD - 1) / NXCD + wpx - 1) / wpx;
+    if ((per_wg + nsteps - 2) / nsteps + 1 <= RR_MAXB) {
+      static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(moe_prefill_rowres_kernel),
+                                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)SMEM_RR);
+      if (attr != hipSuccess) return -4;
+      hipLaunchKernelGGL(moe_prefill_rowres_kernel, dim3(grid), dim3(NTH), SMEM_RR, (hipStream_t)stream,
+                         (const uint8_t*)a, (const float*)as, (const uint8_t*)wq, (const uint8_t*)ws, (uint16_t*)c,
+                         (const int*)sorted_ids, (const int*)expert_ids, (const int*)ntpp, (const float*)topk_w,
+                         (long)N * K / 2, ws_estride, numel, div_magic((uint32_t)a_row_div), N, nsteps);
+      return hipGetLastError() == hipSuccess ? 0 : -6;
+    }
+  }
   if (K / KC >= 3 && getenv_flag_off_pf("R9K_PREFILL_PERSIST") == 0) {
     static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(moe_prefill_persistent_kernel),
                                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)SMEM_P);

@@ -75,6 +75,52 @@ def test_grouped_gemm_prefill_256(dev, E, M, topk, N, Kd, down):
     gemm_case(dev, E, M, topk, N, Kd, seed=E + M + N + Kd, prefill=12, down=down)
 
 
+@pytest.mark.parametrize("E,M,topk,N,gate_up,zipf", [
+    (288, 8192, 8, 2048, False, False),   # config 3's down GEMM (65536 routed rows, 16 column steps a block)
+    (8, 900, 2, 2048, False, False),      # several blocks per expert
+    (16, 1200, 4, 2000, False, True),     # a partial last column step (N % 128 = 80), skewed expert sizes
+    (4, 300, 1, 272, False, False),       # three column steps, the last one mostly past N
+    (8, 700, 2, 512, True, False),        # activation rows shared by the top-k rows of a token (row divisor 2)
+    (3, 20, 1, 128, False, False),        # fewer work items than XCDs
+    (64, 6000, 8, 128, False, False),     # more blocks per workgroup than the row-resident kernel preloads
+])
+def test_prefill_row_resident_equals_persistent(dev, monkeypatch, E, M, topk, N, gate_up, zipf):
+    """K = 512 prefill GEMM (256-row blocks): the row-resident kernel (each wave's rows held in registers across the
+    column steps) against the persistent tile kernel, bit for bit, every routed row written."""
+    Kd = 512
+    g = torch.Generator().manual_seed(E * 7 + M + N)
+    packed, e8 = make_experts(E, N, Kd, g)
+    W = K.prepare_mxfp4_weights(packed.to(dev), e8.to(dev))
+    numel = M * topk
+    rows_a = M if gate_up else numel
+    x = (torch.randn(rows_a, Kd, generator=g) * 0.5).to(torch.bfloat16)
+    if zipf:
+        p = 1.0 / torch.arange(1, E + 1, dtype=torch.float64) ** 1.1
+        ids = torch.stack([torch.multinomial(p, topk, replacement=False, generator=g) for _ in range(M)])
+    else:
+        ids = torch.stack([torch.randperm(E, generator=g)[:topk] for _ in range(M)])
+    ids = ids.to(torch.int32)
+    tw = None if gate_up else torch.rand(numel, generator=g).float().to(dev)
+    sid, eid, ntpp = (t.to(dev) for t in K.align_block_size_ref(ids, E, K.prefill_block(12)))
+    xq, xs = K.quant_rows_fp8(x.to(dev))
+    outs = []
+    for flag in (None, "0"):
+        if flag is None:
+            monkeypatch.delenv("R9K_PREFILL_ROWRES", raising=False)
+        else:
+            monkeypatch.setenv("R9K_PREFILL_ROWRES", flag)
+        out = torch.full((numel, N), float("nan"), dtype=torch.bfloat16, device=dev)
+        K.moe_gemm(xq, xs, W, out, sid, eid, ntpp, numel, topk if gate_up else 1, tw, num_experts=E, prefill=12)
+        torch.cuda.synchronize()
+        outs.append(out)
+    rr, ps = outs
+    assert not torch.isnan(rr.float()).any(), "a routed row was not written"
+    diff = (rr.view(torch.int16) != ps.view(torch.int16)).sum().item()
+    print(f"row-resident E={E} M={M} k={topk} N={N} gate_up={gate_up}: {diff} of {rr.numel()} values differ",
+          flush=True)
+    assert diff == 0
+
+
 @pytest.mark.parametrize("M,N,Kd", [(16, 1024, 2048), (1, 17408, 5120), (4, 1024, 5120), (300, 512, 1024)])
 def test_dense_mxfp4_linear(dev, M, N, Kd):
     """BASELINE config 1 (and small slices of config 4): identity routing tables through ops.mxfp4_linear."""
