@@ -215,7 +215,8 @@ __global__ void __launch_bounds__(MT_THREADS) lru_manage_tables_kernel(
     int* __restrict__ map_cold, int* __restrict__ slot_expert, long long* __restrict__ slot_stamp,
     uint8_t* __restrict__ routed_out, long long* __restrict__ step, int* __restrict__ miss, int* __restrict__ n_miss,
     int blk, long cap, long cap_blocks, int* __restrict__ sorted_h, int* __restrict__ eids_h,
-    int* __restrict__ ntpp_h, int* __restrict__ sorted_c, int* __restrict__ eids_c, int* __restrict__ ntpp_c) {
+    int* __restrict__ ntpp_h, int* __restrict__ sorted_c, int* __restrict__ eids_c, int* __restrict__ ntpp_c,
+    int* __restrict__ hot_ids) {
   __shared__ union {
     ManageLds m;
     TabLds<MT_THREADS> t;
@@ -227,8 +228,10 @@ __global__ void __launch_bounds__(MT_THREADS) lru_manage_tables_kernel(
   for (int i = threadIdx.x; i < mk; i += MT_THREADS) {
     const int e = ids[i];
     const bool ok = e >= 0 && e < E;
-    lids_h[i] = (short)(ok ? table[e] : -1);
+    const int h = ok ? table[e] : -1;
+    lids_h[i] = (short)h;
     lids_c[i] = (short)(ok ? map_cold[e] : -1);
+    if (hot_ids) hot_ids[i] = h;                      // the resident pass's slot ids, for token-major consumers
   }
   __syncthreads();                                   // every manage LDS read is done: the union turns over
   zero_counts(u.t, E);
@@ -308,7 +311,7 @@ namespace {
 int manage_tables_launch(long ids, int mk, int E, int S, int max_distinct, int max_inserts, long table, long map_cold,
                          long slot_expert, long slot_stamp, long routed, long step, long miss, long n_miss, int blk,
                          long cap, long cap_blocks, long sorted_h, long eids_h, long ntpp_h, long sorted_c,
-                         long eids_c, long ntpp_c, long stream) {
+                         long eids_c, long ntpp_c, long hot_ids, long stream) {
   if (E <= 0 || E > MAX_E || S <= 0 || S > MAX_S || S > E || mk < 0 || blk <= 0) return -1;
   if (max_inserts < 0 || max_inserts > S) return -2;
   if ((mk && !ids) || !table || !map_cold || !slot_expert || !slot_stamp || !routed || !step || !miss || !n_miss ||
@@ -320,22 +323,23 @@ int manage_tables_launch(long ids, int mk, int E, int S, int max_distinct, int m
                      E, S, max_distinct, max_inserts, (int*)table, (int*)map_cold, (int*)slot_expert,
                      (long long*)slot_stamp, (uint8_t*)routed, (long long*)step, (int*)miss, (int*)n_miss, blk, cap,
                      cap_blocks, (int*)sorted_h, (int*)eids_h, (int*)ntpp_h, (int*)sorted_c, (int*)eids_c,
-                     (int*)ntpp_c);
+                     (int*)ntpp_c, (int*)hot_ids);
   return hipGetLastError() == hipSuccess ? 0 : -6;
 }
 
 }  // namespace
 
 // The manage step and both passes' routing tables in one launch, tables of this library's capacity (sorted
-// capacity(mk, E, blk) entries, expert ids capacity / blk); sorted_c = 0 skips the host pass. 2 when not served
-// (E > 1024 or mk > 4096; nothing launched: manage_map + two aligns give the same result).
+// capacity(mk, E, blk) entries, expert ids capacity / blk); sorted_c = 0 skips the host pass; hot_ids (int32 [mk],
+// 0 = not wanted) receives each routed row's slot (-1 not resident), as r9k_lru_manage_map's `hot`. 2 when not
+// served (E > 1024 or mk > 4096; nothing launched: manage_map + two aligns give the same result).
 extern "C" int r9k_lru_manage_tables(long ids, int mk, int E, int S, int max_distinct, int max_inserts, long table,
                                      long map_cold, long slot_expert, long slot_stamp, long routed, long step,
                                      long miss, long n_miss, int blk, long sorted_h, long eids_h, long ntpp_h,
-                                     long sorted_c, long eids_c, long ntpp_c, long stream) {
+                                     long sorted_c, long eids_c, long ntpp_c, long hot_ids, long stream) {
   return manage_tables_launch(ids, mk, E, S, max_distinct, max_inserts, table, map_cold, slot_expert, slot_stamp,
                               routed, step, miss, n_miss, blk, -1, -1, sorted_h, eids_h, ntpp_h, sorted_c, eids_c,
-                              ntpp_c, stream);
+                              ntpp_c, hot_ids, stream);
 }
 
 // The reference's one-launch manage + both moe_align_block_size outputs with its buffer lengths: sorted_* hold L
@@ -352,7 +356,7 @@ extern "C" int r4d_lru_fused(long ids, int mk, int E, int S, int max_distinct, i
   if (!sorted_cold) return -3;
   return manage_tables_launch(ids, mk, E, S, max_distinct, max_inserts, table, map_cold, slot_expert, slot_stamp,
                               routed, step, miss, n_miss, bs, L, NB, sorted_hot, eids_hot, npad_hot, sorted_cold,
-                              eids_cold, npad_cold, stream);
+                              eids_cold, npad_cold, 0, stream);
 }
 
 extern "C" int r4d_lru_manage(long ids, int mk, int E, int S, int max_distinct, int max_inserts, long table,

@@ -56,7 +56,7 @@ def _L():
         L.r9k_lru_map_ids.restype = i
         L.r9k_lru_map_ids.argtypes = [l, i, i, l, l, l, l, l]
         L.r9k_lru_manage_tables.restype = i
-        L.r9k_lru_manage_tables.argtypes = [l, i, i, i, i, i] + [l] * 8 + [i] + [l] * 6 + [l]
+        L.r9k_lru_manage_tables.argtypes = [l, i, i, i, i, i] + [l] * 8 + [i] + [l] * 7 + [l]
         L.r4d_lru_fused.restype = i
         L.r4d_lru_fused.argtypes = [l, i, i, i, i, i] + [l] * 8 + [i, i, i] + [l] * 6 + [l]
         L.r9k_host_alloc.restype = l
@@ -263,6 +263,7 @@ class LayerCache:
         self._one = None
         self._one_old: list = []
         self.stage = None
+        self.hot_ids = None                      # set by update_fused: the last step's slot per routed row
 
     def _warm_start(self):
         prof = _profile()
@@ -369,7 +370,9 @@ class LayerCache:
                                        self.slot_stamp.data_ptr(), self.routed.data_ptr(), self.step.data_ptr(),
                                        self.miss.data_ptr(), self.n_miss.data_ptr(), bs, sh.data_ptr(), eh.data_ptr(),
                                        nh.data_ptr(), sc.data_ptr() if need_cold else 0,
-                                       ec.data_ptr() if need_cold else 0, nc.data_ptr() if need_cold else 0, st)
+                                       ec.data_ptr() if need_cold else 0, nc.data_ptr() if need_cold else 0,
+                                       hid.data_ptr(), st)
+        self.hot_ids = hid                       # each routed row's slot (-1 not resident), both paths below
         if rc not in (0, 2):
             raise RuntimeError(f"r9k_lru_manage_tables failed ({rc}) E={self.E} S={self.S} mk={mk}")
         if rc == 0:

@@ -193,6 +193,7 @@ class R9700Mxfp4Experts(_experts_base()):
             pf_down = None if nv is not None else K.pick_moe_prefill(MT, K2)
             pf_gate = None if nv is not None else K.pick_moe_prefill(MT, K1, gate_up=True)
         cache = getattr(self, "r9k_cache", None)
+        slot_ids = None
         if cache is not None:
             # host-offloaded experts (moe/cache.py): LRU manage + gather, then a pass over the VRAM slots (ids
             # through table) and, unless provably empty, one over the host store (ids through map_cold); every
@@ -203,6 +204,8 @@ class R9700Mxfp4Experts(_experts_base()):
             need_cold = numel > cache.no_cold_limit
             if cache.fused:
                 hot_al, cold_al = cache.update_fused(topk_ids, blk, need_cold)
+                if not need_cold:
+                    slot_ids = cache.hot_ids.view(M, topk)   # every routed expert resident: each row's slot
             else:
                 cache.update(topk_ids)
                 hot_al = K.moe_align(topk_ids, blk, E, cache.table)
@@ -254,11 +257,14 @@ class R9700Mxfp4Experts(_experts_base()):
             for W1, _, (sid, eid, ntpp), (mt, pfg, _) in passes:
                 K.moe_gemm(xq, xs, W1, gate_up, sid, eid, ntpp, numel, topk, None, num_experts=E, MT=mt,
                            prefill=pfg)
-            if (len(passes) == 1 and cache is None and nv is None and expert_map is None and MT == 1
+            # the token-major tail's expert ids: the routing ids, or each row's slot when every routed expert is
+            # resident (the cache's one-launch manage wrote them; the host pass is provably empty)
+            ds_ids = topk_ids.to(torch.int32).contiguous() if cache is None else slot_ids
+            if (ds_ids is not None and len(passes) == 1 and nv is None and expert_map is None and MT == 1
                     and pf_gate is None and K.down_sum_fits(numel, N2, K2) and not ZERO_DOWN):
                 # decode widths: SiLU + quant, down and the top-k sum in one token-major launch
                 tw = topk_weights.reshape(-1).to(torch.float32).contiguous()
-                if K.moe_down_sum(gate_up, topk_ids.to(torch.int32).contiguous(), tw, passes[0][1], output):
+                if K.moe_down_sum(gate_up, ds_ids, tw, passes[0][1], output):
                     return output
             aq, as_ = K.silu_mul_quant_fp8(gate_up)
         # Rows no table places (experts on other ranks under an expert map) must not feed moe_sum garbage.

@@ -136,10 +136,12 @@ def test_manage_tables_one_launch_equals_composed(dev, E, S, thresh, max_ins, M,
         ta = [torch.full((cap,), -7, **i32), torch.full((cap // blk,), -7, **i32), torch.full((1,), -7, **i32),
               torch.full((cap,), -7, **i32), torch.full((cap // blk,), -7, **i32), torch.full((1,), -7, **i32)]
         cold_ptrs = [t.data_ptr() for t in ta[3:]] if need_cold else [0, 0, 0]
+        hot_out = torch.full((mk,), -7, **i32)
         rc = L.r9k_lru_manage_tables(ids.data_ptr(), mk, E, S, max_distinct, max_ins, a.table.data_ptr(),
                                      a.map_cold.data_ptr(), a.slot_expert.data_ptr(), a.slot_stamp.data_ptr(),
                                      a.routed.data_ptr(), a.step.data_ptr(), a.miss.data_ptr(), a.n_miss.data_ptr(),
-                                     blk, ta[0].data_ptr(), ta[1].data_ptr(), ta[2].data_ptr(), *cold_ptrs, s_)
+                                     blk, ta[0].data_ptr(), ta[1].data_ptr(), ta[2].data_ptr(), *cold_ptrs,
+                                     hot_out.data_ptr(), s_)
         assert rc == 0, rc
         hid, cid = b.manage(ids, max_distinct, max_ins, mapped=True)
         hb = K.moe_align(hid, blk, E)
@@ -147,6 +149,7 @@ def test_manage_tables_one_launch_equals_composed(dev, E, S, thresh, max_ins, M,
         torch.cuda.synchronize()
         for x, y in zip(_tables_state(a), _tables_state(b)):
             assert torch.equal(x, y), step
+        assert torch.equal(hot_out, hid), step
         n = int(a.n_miss.item())
         assert torch.equal(a.miss[:n], b.miss[:n]), step
         assert same_state(a, st), step
