@@ -83,6 +83,8 @@ def test_grouped_gemm_prefill_256(dev, E, M, topk, N, Kd, down):
     (8, 700, 2, 512, True, False),        # activation rows shared by the top-k rows of a token (row divisor 2)
     (3, 20, 1, 128, False, False),        # fewer work items than XCDs
     (64, 6000, 8, 128, False, False),     # more blocks per workgroup than the row-resident kernel preloads
+    (2, 3, 1, 16, False, False),          # one 16-column tile: every step's other tiles past N
+    (5, 700, 2, 2064, False, False),      # 17 column steps, the last one 16 columns wide
 ])
 def test_prefill_row_resident_equals_persistent(dev, monkeypatch, E, M, topk, N, gate_up, zipf):
     """K = 512 prefill GEMM (256-row blocks): the row-resident kernel (each wave's rows held in registers across the
