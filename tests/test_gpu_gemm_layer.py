@@ -67,11 +67,12 @@ def test_grouped_gemm_prefill_entry(dev, cfg):
 
 
 @pytest.mark.parametrize("E,M,topk,N,Kd", [(16, 1200, 4, 1024, 2048), (8, 900, 2, 2048, 512), (4, 300, 1, 272, 384),
-                                           (32, 2000, 8, 512, 256)])
+                                           (32, 2000, 8, 512, 256), (64, 200, 8, 1024, 1024)])
 @pytest.mark.parametrize("down", [False, True])
 def test_grouped_gemm_prefill_256(dev, E, M, topk, N, Kd, down):
     """256-row blocks with K % 128 == 0: the LDS-tiled 32x32x64 kernel (ragged expert sizes, padded M tiles,
-    a column block past N, one and several 256-row blocks per expert)."""
+    a column block past N, one and several 256-row blocks per expert, blocks of ~25 live rows whose other 64-row
+    pieces are never loaded)."""
     gemm_case(dev, E, M, topk, N, Kd, seed=E + M + N + Kd, prefill=12, down=down)
 
 
