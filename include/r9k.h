@@ -186,12 +186,21 @@ int r9k_moe_down_sum(long gu, long ids, long tw, long wq, long ws, long ws_estri
                      long out, long ld_out, int T, int topk, int E, int I, int N, long stream);
 
 /* The dense MXFP4 weight-only linear at decode widths in one launch: the per-row fp8 quant of the bf16 activations
- * (each workgroup quantises the M <= 16 rows into LDS) and the GEMM. Replaces, as one entry, the reference's
+ * (each workgroup quantises the M <= 4 rows into LDS) and the GEMM. Replaces, as one entry, the reference's
  * r9k_quant_rows_fp8 + r9k_moe_mxfp4a8 over identity tables (r9700_vllm/ops.py:89-117; kernels/r9k_moe_mxfp4a8.hip
  * :1745-1760, :631-638). x bf16 [M][K] (row stride ldx, 16-byte aligned); wq / ws one expert in the r9k_moe_mxfp4a8
- * layout; out bf16 [M][N] (row stride ldo). Bit-equal to the two launches. Served: 1 <= M <= 16, K % 128 == 0,
+ * layout; out bf16 [M][N] (row stride ldo). Bit-equal to the two launches. Served: 1 <= M <= 4, K % 128 == 0,
  * K <= 8192, N % 16 == 0; else 2 with nothing launched. 0, -3 bad argument, -6 launch error. */
 int r9k_dense_mxfp4_qa(long x, long ldx, long wq, long ws, long out, long ldo, int M, int N, int K, long stream);
+
+/* The GEMM of the same dense linear from activations already quantised (r9k_quant_rows_fp8's codes and row scales),
+ * 1 <= M <= 16 rows, on the dense kernel's weight stream: the reference runs it as r9k_moe_mxfp4a8 over identity
+ * tables (r9700_vllm/ops.py:89-117; kernels/r9k_moe_mxfp4a8.hip:631-638). q fp8 [M][K] (row stride ldq bytes, both
+ * 16-byte aligned), s fp32 [M]; wq / ws one expert in the r9k_moe_mxfp4a8 layout; out bf16 [M][N] (row stride ldo).
+ * Bit-equal to r9k_moe_mxfp4a8. Served: 1 <= M <= 16, K % 128 == 0, N % 16 == 0; else 2 with nothing launched.
+ * 0, -3 bad argument, -6 launch error. */
+int r9k_dense_mxfp4_a8(long q, long ldq, long s, long wq, long ws, long out, long ldo, int M, int N, int K,
+                       long stream);
 
 /* Load-time NVFP4 -> MXFP4 with MSE-searched block exponents (the reference does this with torch:
  * r9700_vllm/quant/nvfp4.py:39-90). packed u8 [N][K/2], s16 e4m3 [N][K/16], row_div fp32 [N] -> out_packed u8

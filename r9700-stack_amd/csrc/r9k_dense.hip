@@ -194,6 +194,89 @@ __global__ void __launch_bounds__(WAVE * SK) dense_mxfp4_qa_kernel(
   }
 }
 
+// The same weight stream, K split over waves and partial-tile sum as dense_mxfp4_qa_kernel, from activations already
+// quantised (r9k_quant_rows_fp8's codes q [M][K] and row scales s [M]) for up to 16 rows: no quant and no rows in
+// registers, so the LDS holds only the partial tiles. Each wave loads its A fragments (row r = lane % 16, 2 x 16
+// bytes a K-tile; M * K bytes in all, L2-resident) in the same batches as its weight tiles.
+template <int NPW, int SK, int U>
+__global__ void __launch_bounds__(WAVE * SK) dense_mxfp4_a8_kernel(
+    const uint8_t* __restrict__ q, long ldq, const float* __restrict__ s, const uint8_t* __restrict__ Wq,
+    const uint8_t* __restrict__ Ws, uint16_t* __restrict__ out, long ldo, int M, int N, int K) {
+  __shared__ float red[SK * NPW * 256];
+  const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
+  const int g = lane >> 4, r = lane & 15;
+  const int NT = N / 16, nkt = K / KT, KB = K / 32;
+
+  const uint8_t* wtile[NPW];
+  const uint8_t* stile[NPW];
+#pragma unroll
+  for (int j = 0; j < NPW; j++) {
+    const int nt = min((int)blockIdx.x * NPW + j, NT - 1);     // a tile past N computes a copy, never stored
+    wtile[j] = Wq + (size_t)nt * (size_t)(8 * K) + lane * 16;
+    stile[j] = Ws + (size_t)nt * (size_t)(16 * KB) + lane;
+  }
+  const int kt0 = wave * nkt / SK, kt1 = (wave + 1) * nkt / SK;
+  const bool arow = r < M;
+  const uint8_t* ar = q + (size_t)(arow ? r : 0) * ldq + 16 * g;
+
+  u32x4 bf[U][NPW];
+  uint32_t sb[U][NPW];
+  uint4 alo[U], ahi[U];
+  auto issue = [&](int kb) {
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const int k = min(kb + u, kt1 - 1);
+#pragma unroll
+      for (int j = 0; j < NPW; j++) {
+        bf[u][j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wtile[j] + (size_t)k * 1024));
+        sb[u][j] = __builtin_nontemporal_load(stile[j] + k * 64);
+      }
+      alo[u] = *reinterpret_cast<const uint4*>(ar + k * KT);
+      ahi[u] = *reinterpret_cast<const uint4*>(ar + k * KT + 64);
+    }
+  };
+
+  v4f acc[NPW];
+#pragma unroll
+  for (int j = 0; j < NPW; j++) acc[j] = (v4f){0.f, 0.f, 0.f, 0.f};
+  for (int kb = kt0; kb < kt1; kb += U) {
+    issue(kb);
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const int k = kb + u;
+      if (k < kt1) {                                         // wave-uniform
+        uint4 lo = alo[u], hi = ahi[u];
+        if (!arow) lo = hi = make_uint4(0u, 0u, 0u, 0u);
+        const v8i a = (v8i){(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+#pragma unroll
+        for (int j = 0; j < NPW; j++) {
+          const v8i b = (v8i){(int)bf[u][j].x, (int)bf[u][j].y, (int)bf[u][j].z, (int)bf[u][j].w, 0, 0, 0, 0};
+          acc[j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, acc[j], 0, 4, 0, E8M0_ONE, 0, (int)sb[u][j]);
+        }
+      }
+    }
+  }
+
+  // the partial tiles through LDS, summed in wave order (as dense_mxfp4_qa_kernel)
+#pragma unroll
+  for (int j = 0; j < NPW; j++) {
+    float* t = red + (size_t)(wave * NPW + j) * 256;
+#pragma unroll
+    for (int qq = 0; qq < 4; qq++) t[(4 * g + qq) * 16 + r] = acc[j][qq];
+  }
+  __syncthreads();
+  constexpr int TOT = NPW * 256;
+  for (int idx = tid; idx < TOT; idx += WAVE * SK) {
+    const int col = idx & 15, m = (idx >> 4) & 15, j = idx >> 8;
+    const int n = (blockIdx.x * NPW + j) * 16 + col;
+    if (m >= M || n >= N) continue;
+    float v = 0.f;
+#pragma unroll
+    for (int w = 0; w < SK; w++) v += red[(size_t)w * TOT + idx];
+    out[(size_t)m * ldo + n] = f2bf(v * s[m]);
+  }
+}
+
 int env_int(const char* name, int dflt) {
   const char* v = getenv(name);
   return v && *v ? atoi(v) : dflt;
@@ -244,5 +327,38 @@ extern "C" int r9k_dense_mxfp4_qa(long x, long ldx, long wq, long ws, long out, 
 #undef DQU
 #undef DQM
 #undef DQ
+  return 2;
+}
+
+// No counterpart as one entry in the reference: the GEMM half of r9k_quant_rows_fp8 + r9k_moe_mxfp4a8 over identity
+// tables (r9700_vllm/ops.py:89-117) for 1 <= M <= 16 pre-quantised rows, on the dense kernel's weight stream. q fp8
+// [M][K] (row stride ldq bytes, rows 16-byte aligned), s fp32 [M]; wq / ws one expert in the r9k_moe_mxfp4a8 layout;
+// out bf16 [M][N] (row stride ldo). Served: 1 <= M <= 16, K % 128 == 0, N % 16 == 0; 2 (nothing launched) otherwise.
+// 0, -3 bad argument, -6 launch error. Same K split as r9k_dense_mxfp4_qa, so the same bits as r9k_moe_mxfp4a8.
+extern "C" int r9k_dense_mxfp4_a8(long q, long ldq, long s, long wq, long ws, long out, long ldo, int M, int N, int K,
+                                  long stream) {
+  if (M <= 0) return 0;
+  if (!q || !s || !wq || !ws || !out || N <= 0 || K <= 0) return -3;
+  if (M > MAXM || K % KT || N % 16 || (q & 15) || (ldq & 15) || (wq & 15)) return 2;
+  const int nkt = K / KT, NT = N / 16;
+  // one 16-column tile a workgroup up to 8 rows, two above (each workgroup reads all M rows' codes from L2, so more
+  // rows favour more columns a workgroup). Config 4 GEMM (quant launch excluded): M = 4 12.1 us (NPW 1) / 13.2 (2),
+  // M = 8 13.6 / 13.6, M = 16 18.3 / 16.7; 5 K-tiles a batch beat 4, 8 and 10 at every M.
+  const int NPW = env_int("R9K_DENSE_A8_NPW", M > 8 ? 2 : 1);
+  const int SK = nkt >= 8 ? 4 : 1;
+  const int per = (nkt + SK - 1) / SK;
+  const int U = env_int("R9K_DENSE_A8_U", per <= 4 ? 4 : (per <= 5 ? 5 : (per <= 8 ? 4 : (per <= 10 ? 5 : 8))));
+  const dim3 grid((NT + NPW - 1) / NPW), block(WAVE * SK);
+  const hipStream_t st = (hipStream_t)stream;
+#define DA(NPWv, SKv, Uv)                                                                                          \
+  if (NPW == NPWv && SK == SKv && U == Uv) {                                                                       \
+    hipLaunchKernelGGL((dense_mxfp4_a8_kernel<NPWv, SKv, Uv>), grid, block, 0, st, (const uint8_t*)q, ldq,         \
+                       (const float*)s, (const uint8_t*)wq, (const uint8_t*)ws, (uint16_t*)out, ldo, M, N, K);     \
+    return hipGetLastError() == hipSuccess ? 0 : -6;                                                               \
+  }
+#define DAU(NPWv, SKv) DA(NPWv, SKv, 4) DA(NPWv, SKv, 5) DA(NPWv, SKv, 8) DA(NPWv, SKv, 10)
+  DAU(1, 1) DAU(2, 1) DAU(1, 4) DAU(2, 4)
+#undef DAU
+#undef DA
   return 2;
 }

@@ -68,6 +68,8 @@ def _mxfp4_linear(x: torch.Tensor, wq: torch.Tensor, wsr: torch.Tensor, N: int, 
     if M <= KM.DENSE_QA_MAX_M and KM.dense_mxfp4_qa(x, W, out):   # decode widths: the quant inside the GEMM launch
         return out
     q, s = KM.quant_rows_fp8(x)
+    if M <= KM.DENSE_A8_MAX_M and not fold and KM.dense_mxfp4_a8(q, s, W, out):   # the dense weight stream
+        return out
     mxfp4_gemm_q(q, s, W, out, M, KM.pick_cfg(N, K, M=M, kind="mxfp4", fold=fold))
     return out
 

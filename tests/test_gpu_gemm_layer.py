@@ -614,6 +614,48 @@ def test_dense_qa_equals_two_launches(dev, M, N, Kd):
     assert same and r < 2e-3 and cosine(a, b) > 0.99999
 
 
+@pytest.mark.parametrize("M,N,Kd", [(1, 17408, 5120), (4, 17408, 5120), (16, 17408, 5120), (3, 1024, 2048),
+                                    (7, 1024, 2048), (16, 48, 1024), (5, 272, 384), (9, 64, 8192), (16, 32, 256),
+                                    (12, 16, 896), (2, 2064, 640)])
+def test_dense_a8_equals_decode_gemm(dev, M, N, Kd):
+    """r9k_dense_mxfp4_a8 (the dense weight stream on pre-quantised rows, M <= 16) against the decode GEMM over
+    identity tables on the same codes: bit for bit, every row written, and within the GEMM tolerance of the oracle."""
+    g = torch.Generator().manual_seed(20261201 + 4200 + M + N + Kd)
+    packed, e8 = make_experts(1, N, Kd, g)
+    W = K.prepare_mxfp4_weights(packed.to(dev), e8.to(dev))
+    x = torch.randn(M, Kd, generator=g).to(torch.bfloat16)
+    q, s = K.quant_rows_fp8(x.to(dev))
+    one = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=dev)
+    assert K.dense_mxfp4_a8(q, s, W, one), "shape not served"
+    two = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+    ops.mxfp4_gemm_q(q, s, W, two, M, K.pick_cfg(N, Kd, M=M, kind="mxfp4"))
+    torch.cuda.synchronize()
+    assert not torch.isnan(one.float()).any(), "an output was not written"
+    same = torch.equal(one.view(torch.int16), two.view(torch.int16))
+    qo, so = O.quant_rows_fp8(x)
+    ref = O.grouped_gemm(qo, so, {0: O.mxfp4_dequant(packed[0], e8[0], torch.float32)}, np.zeros(M, dtype=np.int32),
+                         1, acc_dtype=torch.float32)
+    a, b = bf16_bits_to_f64(O.bf16_bits(one)), bf16_bits_to_f64(ref)
+    r = rel_err(a, b)
+    print(f"dense a8 M={M} N={N} K={Kd}: bit-equal to the decode GEMM {same}, rel {r:.2e}", flush=True)
+    assert same and r < 2e-3 and cosine(a, b) > 0.99999
+
+
+def test_dense_a8_refuses_unserved(dev):
+    """M > 16, K not a multiple of 128 or a row stride that is not 16-byte aligned: False, nothing launched."""
+    W = K.Mxfp4Experts(torch.zeros(1, 64 * 320 // 8, dtype=torch.int32, device=dev),
+                       torch.zeros(1, 320 // 32 + 1, 64, dtype=torch.uint8, device=dev), 64, 320)
+    s = torch.ones(17, dtype=torch.float32, device=dev)
+    assert not K.dense_mxfp4_a8(torch.zeros(2, 320, dtype=torch.uint8, device=dev), s, W,
+                                torch.empty(2, 64, dtype=torch.bfloat16, device=dev))
+    W2 = K.Mxfp4Experts(torch.zeros(1, 64 * 256 // 8, dtype=torch.int32, device=dev),
+                        torch.zeros(1, 256 // 32 + 1, 64, dtype=torch.uint8, device=dev), 64, 256)
+    assert not K.dense_mxfp4_a8(torch.zeros(17, 256, dtype=torch.uint8, device=dev), s, W2,
+                                torch.empty(17, 64, dtype=torch.bfloat16, device=dev))
+    qs = torch.zeros(2, 264, dtype=torch.uint8, device=dev)[:, :256]          # row stride 264: not 16-byte aligned
+    assert not K.dense_mxfp4_a8(qs, s, W2, torch.empty(2, 64, dtype=torch.bfloat16, device=dev))
+
+
 def test_dense_qa_refuses_unserved(dev):
     """M > 4, K not a multiple of 128 or unaligned activations: False, nothing launched (ops falls back)."""
     W = K.Mxfp4Experts(torch.zeros(1, 64 * 320 // 8, dtype=torch.int32, device=dev),
