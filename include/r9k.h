@@ -196,10 +196,11 @@ int r9k_dense_mxfp4_qa(long x, long ldx, long wq, long ws, long out, long ldo, i
 /* The GEMM of the same dense linear from activations already quantised (r9k_quant_rows_fp8's codes and row scales),
  * 1 <= M <= 16 rows, on the dense kernel's weight stream: the reference runs it as r9k_moe_mxfp4a8 over identity
  * tables (r9700_vllm/ops.py:89-117; kernels/r9k_moe_mxfp4a8.hip:631-638). q fp8 [M][K] (row stride ldq bytes, both
- * 16-byte aligned), s fp32 [M]; wq / ws one expert in the r9k_moe_mxfp4a8 layout; out bf16 [M][N] (row stride ldo).
- * Bit-equal to r9k_moe_mxfp4a8. Served: 1 <= M <= 16, K % 128 == 0, N % 16 == 0; else 2 with nothing launched.
- * 0, -3 bad argument, -6 launch error. */
-int r9k_dense_mxfp4_a8(long q, long ldq, long s, long wq, long ws, long out, long ldo, int M, int N, int K,
+ * 16-byte aligned), s fp32 [M], tw fp32 [M] row weights or 0 (r9k_moe_mxfp4a8's topk_w: the shared expert's gate);
+ * wq / ws one expert in the r9k_moe_mxfp4a8 layout; out bf16 [M][N] (row stride ldo). Bit-equal to r9k_moe_mxfp4a8.
+ * Served: 1 <= M <= 16, K % 128 == 0, N % 16 == 0; else 2 with nothing launched. 0, -3 bad argument, -6 launch
+ * error. */
+int r9k_dense_mxfp4_a8(long q, long ldq, long s, long tw, long wq, long ws, long out, long ldo, int M, int N, int K,
                        long stream);
 
 /* Load-time NVFP4 -> MXFP4 with MSE-searched block exponents (the reference does this with torch:

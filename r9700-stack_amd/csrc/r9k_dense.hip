@@ -195,13 +195,15 @@ __global__ void __launch_bounds__(WAVE * SK) dense_mxfp4_qa_kernel(
 }
 
 // The same weight stream, K split over waves and partial-tile sum as dense_mxfp4_qa_kernel, from activations already
-// quantised (r9k_quant_rows_fp8's codes q [M][K] and row scales s [M]) for up to 16 rows: no quant and no rows in
-// registers, so the LDS holds only the partial tiles. Each wave loads its A fragments (row r = lane % 16, 2 x 16
+// quantised (r9k_quant_rows_fp8's codes q [M][K] and row scales s [M]; optional row weights tw [M], applied as the
+// decode GEMM's epilogue does: v * (s * tw)) for up to 16 rows: no quant and no rows in registers, so the LDS holds
+// only the partial tiles. Each wave loads its A fragments (row r = lane % 16, 2 x 16
 // bytes a K-tile; M * K bytes in all, L2-resident) in the same batches as its weight tiles.
 template <int NPW, int SK, int U>
 __global__ void __launch_bounds__(WAVE * SK) dense_mxfp4_a8_kernel(
-    const uint8_t* __restrict__ q, long ldq, const float* __restrict__ s, const uint8_t* __restrict__ Wq,
-    const uint8_t* __restrict__ Ws, uint16_t* __restrict__ out, long ldo, int M, int N, int K) {
+    const uint8_t* __restrict__ q, long ldq, const float* __restrict__ s, const float* __restrict__ tw,
+    const uint8_t* __restrict__ Wq, const uint8_t* __restrict__ Ws, uint16_t* __restrict__ out, long ldo, int M, int N,
+    int K) {
   __shared__ float red[SK * NPW * 256];
   const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
   const int g = lane >> 4, r = lane & 15;
@@ -273,7 +275,9 @@ __global__ void __launch_bounds__(WAVE * SK) dense_mxfp4_a8_kernel(
     float v = 0.f;
 #pragma unroll
     for (int w = 0; w < SK; w++) v += red[(size_t)w * TOT + idx];
-    out[(size_t)m * ldo + n] = f2bf(v * s[m]);
+    float sc = s[m];
+    if (tw) sc *= tw[m];
+    out[(size_t)m * ldo + n] = f2bf(v * sc);
   }
 }
 
@@ -332,11 +336,11 @@ extern "C" int r9k_dense_mxfp4_qa(long x, long ldx, long wq, long ws, long out, 
 
 // No counterpart as one entry in the reference: the GEMM half of r9k_quant_rows_fp8 + r9k_moe_mxfp4a8 over identity
 // tables (r9700_vllm/ops.py:89-117) for 1 <= M <= 16 pre-quantised rows, on the dense kernel's weight stream. q fp8
-// [M][K] (row stride ldq bytes, rows 16-byte aligned), s fp32 [M]; wq / ws one expert in the r9k_moe_mxfp4a8 layout;
-// out bf16 [M][N] (row stride ldo). Served: 1 <= M <= 16, K % 128 == 0, N % 16 == 0; 2 (nothing launched) otherwise.
+// [M][K] (row stride ldq bytes, rows 16-byte aligned), s fp32 [M], tw fp32 [M] row weights or 0 (the decode GEMM's
+// topk_w); wq / ws one expert in the r9k_moe_mxfp4a8 layout; out bf16 [M][N] (row stride ldo). Served: 1 <= M <= 16, K % 128 == 0, N % 16 == 0; 2 (nothing launched) otherwise.
 // 0, -3 bad argument, -6 launch error. Same K split as r9k_dense_mxfp4_qa, so the same bits as r9k_moe_mxfp4a8.
-extern "C" int r9k_dense_mxfp4_a8(long q, long ldq, long s, long wq, long ws, long out, long ldo, int M, int N, int K,
-                                  long stream) {
+extern "C" int r9k_dense_mxfp4_a8(long q, long ldq, long s, long tw, long wq, long ws, long out, long ldo, int M,
+                                  int N, int K, long stream) {
   if (M <= 0) return 0;
   if (!q || !s || !wq || !ws || !out || N <= 0 || K <= 0) return -3;
   if (M > MAXM || K % KT || N % 16 || (q & 15) || (ldq & 15) || (wq & 15)) return 2;
@@ -353,7 +357,8 @@ extern "C" int r9k_dense_mxfp4_a8(long q, long ldq, long s, long wq, long ws, lo
 #define DA(NPWv, SKv, Uv)                                                                                          \
   if (NPW == NPWv && SK == SKv && U == Uv) {                                                                       \
     hipLaunchKernelGGL((dense_mxfp4_a8_kernel<NPWv, SKv, Uv>), grid, block, 0, st, (const uint8_t*)q, ldq,         \
-                       (const float*)s, (const uint8_t*)wq, (const uint8_t*)ws, (uint16_t*)out, ldo, M, N, K);     \
+                       (const float*)s, (const float*)tw, (const uint8_t*)wq, (const uint8_t*)ws, (uint16_t*)out,  \
+                       ldo, M, N, K);                                                                              \
     return hipGetLastError() == hipSuccess ? 0 : -6;                                                               \
   }
 #define DAU(NPWv, SKv) DA(NPWv, SKv, 4) DA(NPWv, SKv, 5) DA(NPWv, SKv, 8) DA(NPWv, SKv, 10)

@@ -77,7 +77,7 @@ def lib() -> ctypes.CDLL:
         L.r9k_dense_mxfp4_qa.restype = i
         L.r9k_dense_mxfp4_qa.argtypes = [l] * 6 + [i] * 3 + [l]
         L.r9k_dense_mxfp4_a8.restype = i
-        L.r9k_dense_mxfp4_a8.argtypes = [l] * 7 + [i] * 3 + [l]
+        L.r9k_dense_mxfp4_a8.argtypes = [l] * 8 + [i] * 3 + [l]
         L.r9k_moe_down_sum.argtypes = [l] * 10 + [i] * 5 + [l]
         assert L.r9k_moe_block() == MOE_BLOCK
         _LIB = L
@@ -634,20 +634,26 @@ def dense_mxfp4_qa(x: torch.Tensor, w: Mxfp4Experts, out: torch.Tensor) -> bool:
     return True
 
 
-# ops.mxfp4_linear runs the dense kernel on pre-quantised rows (r9k_dense_mxfp4_a8) from DENSE_QA_MAX_M + 1 rows up
-# to this many (the kernel serves up to 16); above it the decode-family GEMM.
+# ops.mxfp4_gemm_q (the dense GEMM on quantised rows: the MXFP4 linear from DENSE_QA_MAX_M + 1 rows, the shared
+# expert) runs the dense kernel (r9k_dense_mxfp4_a8) up to this many rows (the kernel serves up to 16); above it the
+# decode-family GEMM. Measured at config 4 ([17408, 5120]), quant + GEMM against quant + decode GEMM: M = 4 15.0 vs
+# 16.7 us, M = 8 16.6 vs 18.1, M = 16 19.9 vs 21.1.
 DENSE_A8_MAX_M = int(os.environ.get("R9K_DENSE_A8_MAX_M", "16"))
 
 
-def dense_mxfp4_a8(q: torch.Tensor, s: torch.Tensor, w: Mxfp4Experts, out: torch.Tensor) -> bool:
-    """out [M, N] = bf16(dequant(q, s) @ W^T) for one dense MXFP4 weight and M <= 16 rows already quantised
-    (quant_rows_fp8's codes and scales), on the dense kernel's weight stream (r9k_dense_mxfp4_a8): the values of
-    moe_gemm over identity tables bit for bit. False when not served (nothing launched)."""
+def dense_mxfp4_a8(q: torch.Tensor, s: torch.Tensor, w: Mxfp4Experts, out: torch.Tensor,
+                   topk_w: torch.Tensor | None = None) -> bool:
+    """out [M, N] = bf16(dequant(q, s) @ W^T (* topk_w[row])) for one dense MXFP4 weight and M <= 16 rows already
+    quantised (quant_rows_fp8's codes and scales), on the dense kernel's weight stream (r9k_dense_mxfp4_a8): the values
+    of moe_gemm over identity tables bit for bit. False when not served (nothing launched)."""
     M = q.shape[0]
     assert q.dtype in (torch.uint8, torch.float8_e4m3fn) and q.dim() == 2 and q.stride(1) == 1 and q.shape[1] == w.K
     assert s.dtype == torch.float32 and s.is_contiguous() and s.numel() >= M
     assert out.dtype == torch.bfloat16 and out.shape == (M, w.N) and out.stride(1) == 1
-    rc = lib().r9k_dense_mxfp4_a8(q.data_ptr(), q.stride(0), s.data_ptr(), w.wq.data_ptr(), w.wsr.data_ptr(),
+    if topk_w is not None:
+        assert topk_w.dtype == torch.float32 and topk_w.is_contiguous() and topk_w.numel() >= M
+    rc = lib().r9k_dense_mxfp4_a8(q.data_ptr(), q.stride(0), s.data_ptr(),
+                                  topk_w.data_ptr() if topk_w is not None else 0, w.wq.data_ptr(), w.wsr.data_ptr(),
                                   out.data_ptr(), out.stride(0), M, w.N, w.K, _stream())
     if rc == 2:
         return False

@@ -7,7 +7,8 @@ for the 4-bit path:
 
 plus `mxfp4_gemm_q` (the GEMM on already-quantised rows, which the shared expert uses). A dense linear is the grouped
 MoE GEMM with one expert and identity routing tables (`IdentityTables`); at decode widths the MXFP4 linear is one
-launch with the activation quant inside (kernels.moe.dense_mxfp4_qa). The reference's fp8_linear / fp8_block_linear
+launch with the activation quant inside (kernels.moe.dense_mxfp4_qa), and up to 16 rows the GEMM on quantised rows
+is the dense kernel's weight stream (kernels.moe.dense_mxfp4_a8). The reference's fp8_linear / fp8_block_linear
 (dense fp8 GEMMs) are outside this build.
 """
 from __future__ import annotations
@@ -46,8 +47,12 @@ def _decode_mt(M: int) -> int:
 
 def mxfp4_gemm_q(q: torch.Tensor, s: torch.Tensor, W, out: torch.Tensor, M: int, cfg, topk_w=None) -> None:
     """out [M, W.N] bf16 = dequant(q, s) @ W^T (* topk_w[row]) for one dense MXFP4 weight, on the kernel `cfg` names:
-    ("P", prefill cfg) or a decode tuple (WV, SK, NPW[, MT]) whose only meaning here is the optional MT."""
+    ("P", prefill cfg) or a decode tuple (WV, SK, NPW[, MT]) whose only meaning here is the optional MT. A decode cfg
+    with at most KM.DENSE_A8_MAX_M rows runs on the dense kernel (r9k_dense_mxfp4_a8), the decode GEMM's bits."""
     from .kernels import moe as KM
+    if (not KM.is_prefill_cfg(cfg) and M <= KM.DENSE_A8_MAX_M and not W.fold
+            and KM.dense_mxfp4_a8(q, s, W, out, topk_w)):
+        return
     if KM.is_prefill_cfg(cfg):
         tabs = IdentityTables.get(q.device, M, KM.prefill_block(cfg[1]))
         KM.moe_gemm(q, s, W, out, *tabs, M, 1, topk_w, num_experts=1, prefill=cfg[1])
@@ -68,8 +73,6 @@ def _mxfp4_linear(x: torch.Tensor, wq: torch.Tensor, wsr: torch.Tensor, N: int, 
     if M <= KM.DENSE_QA_MAX_M and KM.dense_mxfp4_qa(x, W, out):   # decode widths: the quant inside the GEMM launch
         return out
     q, s = KM.quant_rows_fp8(x)
-    if M <= KM.DENSE_A8_MAX_M and not fold and KM.dense_mxfp4_a8(q, s, W, out):   # the dense weight stream
-        return out
     mxfp4_gemm_q(q, s, W, out, M, KM.pick_cfg(N, K, M=M, kind="mxfp4", fold=fold))
     return out
 

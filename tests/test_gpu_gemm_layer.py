@@ -586,6 +586,14 @@ def test_down_sum_refuses_unserved_shapes(dev):
         assert not K.moe_down_sum(gu, ids, torch.ones(topk, device=dev), W2, out)
 
 
+def decode_gemm(q, s, W, out, M, topk_w=None):
+    """The decode-family GEMM (r9k_moe_mxfp4a8) over identity tables, 16-row blocks: the two-launch dense path's GEMM
+    as the reference runs it (ops.mxfp4_gemm_q itself takes the dense kernel up to 16 rows)."""
+    tabs = ops.IdentityTables.get(q.device, M, K.MOE_BLOCK)
+    cfg = K.pick_cfg(W.N, W.K, M=M, kind="mxfp4")
+    K.moe_gemm(q, s, W, out, *tabs, M, 1, topk_w, *cfg[:3], num_experts=1, MT=1)
+
+
 @pytest.mark.parametrize("M,N,Kd", [(1, 17408, 5120), (2, 17408, 5120), (4, 17408, 5120), (3, 1024, 2048),
                                     (4, 1024, 2048), (3, 48, 1024), (2, 272, 384), (1, 64, 8192), (4, 64, 8192),
                                     (1, 32, 256), (4, 16, 896)])
@@ -602,7 +610,7 @@ def test_dense_qa_equals_two_launches(dev, M, N, Kd):
     assert K.dense_mxfp4_qa(xd, W, one), "shape not served"
     q, s = K.quant_rows_fp8(xd)
     two = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
-    ops.mxfp4_gemm_q(q, s, W, two, M, K.pick_cfg(N, Kd, M=M, kind="mxfp4"))
+    decode_gemm(q, s, W, two, M)
     torch.cuda.synchronize()
     same = torch.equal(one.view(torch.int16), two.view(torch.int16))
     qo, so = O.quant_rows_fp8(x)
@@ -614,30 +622,37 @@ def test_dense_qa_equals_two_launches(dev, M, N, Kd):
     assert same and r < 2e-3 and cosine(a, b) > 0.99999
 
 
-@pytest.mark.parametrize("M,N,Kd", [(1, 17408, 5120), (4, 17408, 5120), (16, 17408, 5120), (3, 1024, 2048),
-                                    (7, 1024, 2048), (16, 48, 1024), (5, 272, 384), (9, 64, 8192), (16, 32, 256),
-                                    (12, 16, 896), (2, 2064, 640)])
-def test_dense_a8_equals_decode_gemm(dev, M, N, Kd):
-    """r9k_dense_mxfp4_a8 (the dense weight stream on pre-quantised rows, M <= 16) against the decode GEMM over
-    identity tables on the same codes: bit for bit, every row written, and within the GEMM tolerance of the oracle."""
+@pytest.mark.parametrize("M,N,Kd,rw", [(1, 17408, 5120, False), (4, 17408, 5120, False), (16, 17408, 5120, False),
+                                       (3, 1024, 2048, True), (7, 1024, 2048, False), (16, 48, 1024, True),
+                                       (5, 272, 384, False), (9, 64, 8192, False), (16, 32, 256, False),
+                                       (12, 16, 896, True), (2, 2064, 640, False), (1, 2048, 512, True)])
+def test_dense_a8_equals_decode_gemm(dev, M, N, Kd, rw):
+    """r9k_dense_mxfp4_a8 (the dense weight stream on pre-quantised rows, M <= 16; with row weights as the shared
+    expert's down GEMM passes its gate) against the decode GEMM over identity tables on the same codes: bit for bit,
+    every row written, and within the GEMM tolerance of the oracle."""
     g = torch.Generator().manual_seed(20261201 + 4200 + M + N + Kd)
     packed, e8 = make_experts(1, N, Kd, g)
     W = K.prepare_mxfp4_weights(packed.to(dev), e8.to(dev))
     x = torch.randn(M, Kd, generator=g).to(torch.bfloat16)
+    tw = torch.rand(M, generator=g).float() if rw else None
+    twd = tw.to(dev) if rw else None
     q, s = K.quant_rows_fp8(x.to(dev))
     one = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=dev)
-    assert K.dense_mxfp4_a8(q, s, W, one), "shape not served"
+    assert K.dense_mxfp4_a8(q, s, W, one, twd), "shape not served"
     two = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
-    ops.mxfp4_gemm_q(q, s, W, two, M, K.pick_cfg(N, Kd, M=M, kind="mxfp4"))
+    decode_gemm(q, s, W, two, M, twd)
+    three = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=dev)
+    ops.mxfp4_gemm_q(q, s, W, three, M, K.pick_cfg(N, Kd, M=M, kind="mxfp4"), topk_w=twd)   # dispatches to a8
     torch.cuda.synchronize()
     assert not torch.isnan(one.float()).any(), "an output was not written"
     same = torch.equal(one.view(torch.int16), two.view(torch.int16))
+    assert torch.equal(one.view(torch.int16), three.view(torch.int16))
     qo, so = O.quant_rows_fp8(x)
     ref = O.grouped_gemm(qo, so, {0: O.mxfp4_dequant(packed[0], e8[0], torch.float32)}, np.zeros(M, dtype=np.int32),
-                         1, acc_dtype=torch.float32)
+                         1, tw.numpy() if rw else None, acc_dtype=torch.float32)
     a, b = bf16_bits_to_f64(O.bf16_bits(one)), bf16_bits_to_f64(ref)
     r = rel_err(a, b)
-    print(f"dense a8 M={M} N={N} K={Kd}: bit-equal to the decode GEMM {same}, rel {r:.2e}", flush=True)
+    print(f"dense a8 M={M} N={N} K={Kd} rw={rw}: bit-equal to the decode GEMM {same}, rel {r:.2e}", flush=True)
     assert same and r < 2e-3 and cosine(a, b) > 0.99999
 
 
