@@ -203,6 +203,15 @@ int r9k_dense_mxfp4_qa(long x, long ldx, long wq, long ws, long out, long ldo, i
 int r9k_dense_mxfp4_a8(long q, long ldq, long s, long tw, long wq, long ws, long out, long ldo, int M, int N, int K,
                        long stream);
 
+/* The native NVFP4 dense linear at decode widths in one launch: the per-row fp8 quant of the bf16 activations (each
+ * workgroup quantises the M <= 2 rows into LDS) and the NVFP4 x fp8 GEMM. Replaces, as one entry, the reference's
+ * r9k_quant_rows_fp8 + r9k_moe_nvfp4a8 over identity tables (r9700_vllm/ops.py:66-83; kernels/r9k_moe_mxfp4a8.hip
+ * :641-647). x bf16 [M][K] (row stride ldx, 16-byte aligned); wq / ws / wg one expert in the layout of
+ * r9k_moe_nvfp4a8; out bf16 [M][N] (row stride ldo). Bit-equal to the two launches. Served: 1 <= M <= 2,
+ * K % 128 == 0, K <= 8192, N % 16 == 0; else 2 with nothing launched. 0, -3 bad argument, -6 launch error. */
+int r9k_dense_nvfp4_qa(long x, long ldx, long wq, long ws, long wg, long out, long ldo, int M, int N, int K,
+                       long stream);
+
 /* Load-time NVFP4 -> MXFP4 with MSE-searched block exponents (the reference does this with torch:
  * r9700_vllm/quant/nvfp4.py:39-90). packed u8 [N][K/2], s16 e4m3 [N][K/16], row_div fp32 [N] -> out_packed u8
  * [N][K/2], out_e8m0 u8 [N][K/32] (checkpoint layout). -2 K % 32, -3 bad pointer / alignment, -6 launch error. */

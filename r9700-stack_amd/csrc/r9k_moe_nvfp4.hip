@@ -28,6 +28,7 @@
 //   A partial last K-tile (K % 128 = 16 G) is stored whole, codes and scales zero past group G.
 //   Wg     : fp32 [N] (wg_estride floats per expert).
 #include "r9k_common.h"
+#include "r9k_rowquant.h"
 
 namespace {
 
@@ -250,17 +251,27 @@ __global__ void __launch_bounds__(WAVE * SK) moe_nvfp4_kernel(
 
 struct NvPick { int NPW, SK, U; };
 
-// Launch shape from the host-known shape: two column tiles a workgroup; K split over SK waves for long K; each wave
-// issues its K range in as few load batches as 4 K-tiles a batch allow.
-NvPick nv_pick(int N, int K, int max_blocks) {
+// Launch shape from the host-known shape: two column tiles a workgroup (one for a dense linear of up to 8 rows); K
+// split over SK waves for long K; each wave issues its K range in as few load batches as 4 K-tiles a batch allow (5
+// for a dense linear of more than 8 rows).
+NvPick nv_pick(int N, int K, int max_blocks, int rows) {
   const int nkt = (K + NV_KT - 1) / NV_KT;
   const int NT = N / 16;
   const int NPW = NT >= 2 ? 2 : 1;
   const long tiles = (long)max_blocks * ((NT + NPW - 1) / NPW);
   const int SK = nkt >= 8 ? (tiles >= 12288 ? 2 : 4) : 1;
   const int per = (nkt + SK - 1) / SK;
-  const int U = per >= 4 ? 4 : (per >= 2 ? 2 : 1);
-  return {NPW, SK, U};
+  int U = per >= 4 ? 4 : (per >= 2 ? 2 : 1);
+  int npw = NPW;
+  if (max_blocks <= 2 && SK == 4 && per >= 5) {
+    // at most two routing blocks (a dense linear at decode widths: moe_gemm sizes the grid at ceil(numel / 16) +
+    // min(numel, E) blocks): one column tile a workgroup up to 8 rows, two and 5-tile
+    // batches above (config 4, [17408, 5120], quant + GEMM: M = 1 19.6 -> 18.4 us, M = 4 19.5 -> 18.8, M = 16
+    // 23.6 -> 22.8; the K split is unchanged, so the bits are too)
+    npw = rows > 8 ? 2 : 1;
+    U = rows > 8 ? 5 : 4;
+  }
+  return {npw, SK, U};
 }
 
 template <int MT, int NPW, int SK, int U>
@@ -428,6 +439,109 @@ __global__ void __launch_bounds__(PV_THREADS, 2) nvfp4_prefill_kernel(
   }
 }
 
+// ------------------------------------------------------------------- dense linear at decode widths, one launch
+// The native NVFP4 dense linear for M <= 2 rows with the per-row fp8 activation quant inside the GEMM launch: every
+// workgroup quantises the rows into LDS (r9k_rowquant.h: quant_rows_fp8's bytes), then runs moe_nvfp4_kernel's
+// weight stream for one routing block of identity rows -- its widening, MFMA order, K split over SK waves and partial-
+// tile sum -- so the output equals r9k_quant_rows_fp8 + r9k_moe_nvfp4a8 over identity tables bit for bit. The weight
+// loads of the wave's first batch go out before the quant, whose latency they overlap.
+constexpr int NQ_APAD = 16;       // bytes of padding per LDS code row
+
+template <int NPW, int SK, int U, int MG>
+__global__ void __launch_bounds__(WAVE * SK) dense_nvfp4_qa_kernel(
+    const uint16_t* __restrict__ x, long ldx, const uint8_t* __restrict__ Wq, const uint8_t* __restrict__ Ws,
+    const float* __restrict__ Wg, uint16_t* __restrict__ out, long ldo, int M, int N, int K) {
+  extern __shared__ __align__(16) uint8_t lds[];
+  const int lda = K + NQ_APAD;
+  uint8_t* A = lds;
+  float* s_row = reinterpret_cast<float*>(lds + (size_t)M * lda);
+  float* red = s_row + 16;
+  const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
+  const int g = lane >> 4, c = lane & 15;
+  const int NT = N / 16, nkt = K / NV_KT;
+
+  const uint8_t* wtile[NPW];
+  const uint8_t* stile[NPW];
+#pragma unroll
+  for (int j = 0; j < NPW; j++) {
+    const int nt = min((int)blockIdx.x * NPW + j, NT - 1);     // a tile past N computes a copy, never stored
+    wtile[j] = Wq + (size_t)nt * nkt * 1024 + lane * 16;
+    stile[j] = Ws + (size_t)nt * nkt * 128 + lane * 2;
+  }
+  const int kt0 = wave * nkt / SK, kt1 = (wave + 1) * nkt / SK;
+
+  u32x4 bw[U][NPW];
+  uint32_t sw[U][NPW];
+  auto issue = [&](int kt) {
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const int k = min(kt + u, kt1 - 1);
+#pragma unroll
+      for (int j = 0; j < NPW; j++) {
+        bw[u][j] = ld16_nt(wtile[j] + (size_t)k * 1024);
+        sw[u][j] = ld2_nt(stile[j] + (size_t)k * 128);
+      }
+    }
+  };
+  {
+    constexpr int T = WAVE * SK, XC = row_chunks<T>();
+    const int nvec = K / 8;
+    uint4 xv[MG][XC];
+    load_row_group<T, MG, XC>(x, ldx, 0, M, nvec, tid, xv);
+    issue(kt0);
+    quant_row_group<T, MG, XC>(xv, 0, M, nvec, A, lda, s_row, red, tid);
+  }
+
+  v4f acc[NPW];
+#pragma unroll
+  for (int j = 0; j < NPW; j++) acc[j] = (v4f){0.f, 0.f, 0.f, 0.f};
+  const bool arow = c < M;
+  const uint8_t* ar = A + (size_t)(arow ? c : 0) * lda + 32 * g;   // lane group g: K values 32 g .. + 31 of a tile
+  for (int kt = kt0; kt < kt1; kt += U) {
+    if (kt != kt0) issue(kt);
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const int k = kt + u;
+      if (k < kt1) {                                         // wave-uniform
+        uint4 l = *reinterpret_cast<const uint4*>(ar + k * NV_KT);
+        uint4 h = *reinterpret_cast<const uint4*>(ar + k * NV_KT + 16);
+        if (!arow) l = h = make_uint4(0u, 0u, 0u, 0u);
+        const h8 a[4] = {e4m3x8_f16(l.x, l.y), e4m3x8_f16(l.z, l.w), e4m3x8_f16(h.x, h.y), e4m3x8_f16(h.z, h.w)};
+#pragma unroll
+        for (int j = 0; j < NPW; j++) {
+          const GroupScale s0 = group_scale(sw[u][j] & 0xffu), s1 = group_scale((sw[u][j] >> 8) & 0xffu);
+#pragma unroll
+          for (int st = 0; st < 4; st++) {
+            const h8 b = e2m1x8_f16(bw[u][j][st], st < 2 ? s0 : s1);
+            acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[st], b, acc[j], 0, 0, 0);
+          }
+        }
+      }
+    }
+  }
+
+  // partial tiles through LDS (the quant's scratch is free again after its closing barrier), summed in wave order;
+  // out = bf16(v * (Wg[n] * s[m])), moe_nvfp4_kernel's epilogue
+#pragma unroll
+  for (int j = 0; j < NPW; j++) {
+    float* t = red + (size_t)(wave * NPW + j) * 256;
+#pragma unroll
+    for (int q = 0; q < 4; q++) t[(4 * g + q) * 16 + c] = acc[j][q];
+  }
+  __syncthreads();
+  constexpr int TOT = NPW * 256;
+  for (int idx = tid; idx < TOT; idx += WAVE * SK) {
+    const int col = idx & 15, m = (idx >> 4) & 15, j = idx >> 8;
+    const int n = (blockIdx.x * NPW + j) * 16 + col;
+    if (m >= M || n >= N) continue;
+    float v = 0.f;
+#pragma unroll
+    for (int s = 0; s < SK; s++) v += red[(size_t)s * TOT + idx];
+    const float sc = Wg[n] * s_row[m];
+    out[(size_t)m * ldo + n] = f2bf(v * sc);
+  }
+}
+
 }  // namespace
 
 // The prefill entry's native-NVFP4 case (r9k_moe_4bit_prefill with nv = 1; reference kernels/r9k_moe_mxfp4a8.hip:
@@ -468,7 +582,7 @@ extern "C" int r9k_moe_nvfp4a8(long a, long as, long wq, long ws, long wg, long 
   if (max_blocks <= 0 || numel <= 0) return 0;
   if (!a || !as || !wq || !ws || !wg || !c || !sorted_ids || !expert_ids || !ntpp) return -3;
   const int blk = 16 * MT;
-  const NvPick p = nv_pick(N, K, max_blocks);
+  const NvPick p = nv_pick(N, K, max_blocks, numel);
   const dim3 grid((N / 16 + p.NPW - 1) / p.NPW, (unsigned)max_blocks);
   const long wq_estride = (long)N * ((K + NV_KT - 1) / NV_KT) * 64;
   const hipStream_t st = (hipStream_t)stream;
@@ -481,8 +595,43 @@ extern "C" int r9k_moe_nvfp4a8(long a, long as, long wq, long ws, long wg, long 
 #define NVU(MTv, NPWv, SKv) NVL(MTv, NPWv, SKv, 1) NVL(MTv, NPWv, SKv, 2) NVL(MTv, NPWv, SKv, 4)
 #define NVS(MTv, NPWv) NVU(MTv, NPWv, 1) NVU(MTv, NPWv, 2) NVU(MTv, NPWv, 4)
   NVS(1, 1) NVS(1, 2) NVS(2, 1) NVS(2, 2) NVS(4, 1) NVS(4, 2)
+  NVL(1, 2, 4, 5)
 #undef NVS
 #undef NVU
 #undef NVL
   return -3;
+}
+
+// No counterpart as one entry in the reference: r9k_quant_rows_fp8 + r9k_moe_nvfp4a8 over identity tables (the native
+// NVFP4 dense linear, r9700_vllm/ops.py:66-83) in one launch, for M <= 2 rows. x bf16 [M][K] (row stride ldx
+// elements, rows 16-byte aligned); wq / ws / wg one expert in this kernel's layout (prepare_nvfp4_weights); out bf16
+// [M][N] (row stride ldo). Served: 1 <= M <= 2, K % 128 == 0, K <= 8192, N % 16 == 0; 2 (nothing launched) otherwise.
+// 0, -3 bad argument, -6 launch error. Bit-equal to the two launches (the decode kernel's launch shape for one block).
+extern "C" int r9k_dense_nvfp4_qa(long x, long ldx, long wq, long ws, long wg, long out, long ldo, int M, int N, int K,
+                                  long stream) {
+  if (M <= 0) return 0;
+  if (!x || !wq || !ws || !wg || !out || N <= 0 || K <= 0) return -3;
+  if (M > 2 || K % NV_KT || K > 8192 || N % 16 || (x & 15) || (ldx & 7) || (wq & 15)) return 2;
+  const NvPick p = nv_pick(N, K, 1, M);
+  if (p.SK != 1 && p.SK != 4) return 2;
+  const int T = WAVE * p.SK;
+  if (K / 8 > (p.SK == 4 ? row_chunks<256>() : row_chunks<64>()) * T) return 2;
+  // LDS: codes, 16 row scales, then the partial tiles (which also hold the quant's SK x M row maxima before them)
+  const size_t smem = (size_t)M * (K + NQ_APAD) + 16 * sizeof(float) + (size_t)p.SK * p.NPW * 256 * sizeof(float);
+  const dim3 grid((N / 16 + p.NPW - 1) / p.NPW), block(T);
+  const hipStream_t st = (hipStream_t)stream;
+  const int MG = M;
+#define NQ(NPWv, SKv, Uv, MGv)                                                                                     \
+  if (p.NPW == NPWv && p.SK == SKv && p.U == Uv && MG == MGv) {                                                    \
+    hipLaunchKernelGGL((dense_nvfp4_qa_kernel<NPWv, SKv, Uv, MGv>), grid, block, smem, st, (const uint16_t*)x, ldx, \
+                       (const uint8_t*)wq, (const uint8_t*)ws, (const float*)wg, (uint16_t*)out, ldo, M, N, K);      \
+    return hipGetLastError() == hipSuccess ? 0 : -6;                                                               \
+  }
+#define NQM(NPWv, SKv, Uv) NQ(NPWv, SKv, Uv, 1) NQ(NPWv, SKv, Uv, 2)
+#define NQU(NPWv, SKv) NQM(NPWv, SKv, 1) NQM(NPWv, SKv, 2) NQM(NPWv, SKv, 4)
+  NQU(1, 1) NQU(2, 1) NQU(1, 4) NQU(2, 4)
+#undef NQU
+#undef NQM
+#undef NQ
+  return 2;
 }

@@ -77,6 +77,8 @@ def lib() -> ctypes.CDLL:
         L.r9k_dense_mxfp4_qa.restype = i
         L.r9k_dense_mxfp4_qa.argtypes = [l] * 6 + [i] * 3 + [l]
         L.r9k_dense_mxfp4_a8.restype = i
+        L.r9k_dense_nvfp4_qa.restype = i
+        L.r9k_dense_nvfp4_qa.argtypes = [l] * 7 + [i] * 3 + [l]
         L.r9k_dense_mxfp4_a8.argtypes = [l] * 8 + [i] * 3 + [l]
         L.r9k_moe_down_sum.argtypes = [l] * 10 + [i] * 5 + [l]
         assert L.r9k_moe_block() == MOE_BLOCK
@@ -659,6 +661,28 @@ def dense_mxfp4_a8(q: torch.Tensor, s: torch.Tensor, w: Mxfp4Experts, out: torch
         return False
     if rc:
         raise RuntimeError(f"r9k_dense_mxfp4_a8 failed ({rc}) M={M} N={w.N} K={w.K}")
+    return True
+
+
+# ops.nvfp4_linear runs the one-launch native NVFP4 path (r9k_dense_nvfp4_qa: the activation quant inside the GEMM
+# launch) up to this many rows (the kernel serves up to 2). Measured at config 4 ([17408, 5120]), one launch against
+# quant + GEMM: M = 1 15.2 vs 19.7 us, M = 2 18.7 vs 18.7 us.
+DENSE_NV_QA_MAX_M = int(os.environ.get("R9K_DENSE_NV_QA_MAX_M", "1"))
+
+
+def dense_nvfp4_qa(x: torch.Tensor, w: Nvfp4Experts, out: torch.Tensor) -> bool:
+    """out [M, N] = bf16(quant_rows_fp8(x) @ W^T) for one native NVFP4 weight (w.wq / w.ws / w.wg of a single expert)
+    in ONE launch (r9k_dense_nvfp4_qa: every workgroup quantises the <= 2 activation rows into LDS itself), the values
+    of quant_rows_fp8 + moe_gemm over identity tables bit for bit. False when not served (nothing launched)."""
+    M = x.shape[0]
+    assert x.dtype == torch.bfloat16 and x.dim() == 2 and x.stride(1) == 1 and x.shape[1] == w.K
+    assert out.dtype == torch.bfloat16 and out.shape == (M, w.N) and out.stride(1) == 1
+    rc = lib().r9k_dense_nvfp4_qa(x.data_ptr(), x.stride(0), w.wq.data_ptr(), w.ws.data_ptr(), w.wg.data_ptr(),
+                                  out.data_ptr(), out.stride(0), M, w.N, w.K, _stream())
+    if rc == 2:
+        return False
+    if rc:
+        raise RuntimeError(f"r9k_dense_nvfp4_qa failed ({rc}) M={M} N={w.N} K={w.K}")
     return True
 
 

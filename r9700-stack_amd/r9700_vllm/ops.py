@@ -79,14 +79,17 @@ def _mxfp4_linear(x: torch.Tensor, wq: torch.Tensor, wsr: torch.Tensor, N: int, 
 
 def _nvfp4_linear(x: torch.Tensor, wq: torch.Tensor, ws: torch.Tensor, wg: torch.Tensor, N: int, K: int
                   ) -> torch.Tensor:
-    """Native NVFP4 weights (prepare_nvfp4_weights of one expert) with per-row fp8 activations: the decode-family
-    kernel below NV_PREFILL_MIN_M rows, the 128 x 128-tile prefill kernel (r9k_moe_4bit_prefill nv = 1) from there."""
+    """Native NVFP4 weights (prepare_nvfp4_weights of one expert) with per-row fp8 activations: one launch with the
+    quant inside up to DENSE_NV_QA_MAX_M rows, the decode-family kernel below NV_PREFILL_MIN_M rows, the 128 x 128-tile
+    prefill kernel (r9k_moe_4bit_prefill nv = 1) from there."""
     from .kernels import moe as KM
     M = x.shape[0]
     out = torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
     if M == 0:
         return out
     W = KM.Nvfp4Experts(wq, ws, wg, N, K)
+    if M <= KM.DENSE_NV_QA_MAX_M and KM.dense_nvfp4_qa(x, W, out):   # decode widths: the quant inside the GEMM launch
+        return out
     q, s = KM.quant_rows_fp8(x)
     if M >= KM.NV_PREFILL_MIN_M and K % 32 == 0:
         tabs = IdentityTables.get(x.device, M, KM.prefill_block(KM.NV_PREFILL_CFG))

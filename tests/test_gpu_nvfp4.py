@@ -109,6 +109,45 @@ def test_nvfp4_linear(dev, M, N, Kd):
     check(O.bf16_bits(out), ref)
 
 
+@pytest.mark.parametrize("M,N,Kd", [(1, 17408, 5120), (2, 17408, 5120), (1, 1024, 2048), (2, 48, 1024),
+                                    (1, 272, 384), (2, 64, 8192), (1, 16, 896), (2, 2064, 640)])
+def test_dense_nvfp4_qa_equals_two_launches(dev, M, N, Kd):
+    """r9k_dense_nvfp4_qa (the activation quant inside the native NVFP4 GEMM launch, M <= 2) against quant_rows_fp8 +
+    the decode kernel over identity tables: bit for bit, every output written, and within the GEMM tolerance of the
+    oracle."""
+    print(f"dense nvfp4 qa M={M} N={N} K={Kd}", flush=True)
+    g = torch.Generator().manual_seed(20261201 + 4300 + M + N + Kd)
+    packed, s16, wg = make_nv(1, N, Kd, g)
+    W = K.prepare_nvfp4_weights(packed.to(dev), s16.to(dev), wg.to(dev))
+    x = torch.randn(M, Kd, generator=g).to(torch.bfloat16)
+    xd = x.to(dev)
+    one = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=dev)
+    assert K.dense_nvfp4_qa(xd, W, one), "shape not served"
+    q, s = K.quant_rows_fp8(xd)
+    two = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+    tabs = ops.IdentityTables.get(dev, M, K.MOE_BLOCK)
+    K.moe_gemm(q, s, W, two, *tabs, M, 1, None, num_experts=1, MT=1)
+    torch.cuda.synchronize()
+    assert torch.equal(one.view(torch.int16), two.view(torch.int16))
+    qo, so = O.quant_rows_fp8(x)
+    ref = O.nvfp4_gemm(qo, so, packed.numpy(), s16.view(torch.uint8).numpy(), wg.numpy(),
+                       np.zeros(M, dtype=np.int32), 1)
+    check(O.bf16_bits(one), ref)
+
+
+def test_dense_nvfp4_qa_refuses_unserved(dev):
+    """M > 2 or K not a multiple of 128: False, nothing launched (ops falls back to the two launches)."""
+    g = torch.Generator().manual_seed(7)
+    packed, s16, wg = make_nv(1, 64, 256, g)
+    W = K.prepare_nvfp4_weights(packed.to(dev), s16.to(dev), wg.to(dev))
+    assert not K.dense_nvfp4_qa(torch.zeros(3, 256, dtype=torch.bfloat16, device=dev), W,
+                                torch.empty(3, 64, dtype=torch.bfloat16, device=dev))
+    packed, s16, wg = make_nv(1, 64, 272, g)
+    W2 = K.prepare_nvfp4_weights(packed.to(dev), s16.to(dev), wg.to(dev))
+    assert not K.dense_nvfp4_qa(torch.zeros(1, 272, dtype=torch.bfloat16, device=dev), W2,
+                                torch.empty(1, 64, dtype=torch.bfloat16, device=dev))
+
+
 def test_nvfp4_linear_config4_prefill_sampled(dev):
     """BASELINE config 4's shape at M = 4096 on native NVFP4 weights (the 128 x 128 tile kernel), checked on 48
     sampled rows (rows are independent)."""
