@@ -28,6 +28,7 @@
 //   A partial last K-tile (K % 128 = 16 G) is stored whole, codes and scales zero past group G.
 //   Wg     : fp32 [N] (wg_estride floats per expert).
 #include "r9k_common.h"
+#include "r9k_dma.h"
 #include "r9k_rowquant.h"
 
 namespace {
@@ -288,18 +289,24 @@ void nv_launch(dim3 grid, hipStream_t st, long a, long as, long wq, long ws, lon
 // ------------------------------------------------------------------------------------------ prefill (tiles of 128)
 // Routed rows in blocks of 128 (a routing block of 128 or 256 rows covered by 1 or 2 workgroups along grid.y) x 128
 // output columns per workgroup; 4 waves in 2 x 2, each 64 rows x 64 columns = 4 x 4 tiles of the fp16 MFMA above.
-// K runs in 128-wide tiles through two LDS stages (activations 16 KB, codes 8 KB, scales 1 KB), the next tile's
-// global loads in flight while the current one is computed. Each wave widens its 4 column tiles' weights once per
-// K-tile (codes and scales straight from LDS, as in the decode kernel) and reuses them over its 4 row tiles; the
-// activation rows are widened per row tile. Activation row pieces are stored XOR-swizzled (16-byte piece p of row r
-// at p ^ (r & 7)) so the 16 rows a fragment read touches land in different banks.
+// K runs in 128-wide tiles through a ring of three LDS stages (activations 16 KB, codes 8 KB, scales 1 KB) filled by
+// direct global -> LDS DMA two K-tiles ahead of the MFMAs (every wave issues the same 7 DMA instructions a stage, so
+// the waits are fixed vmcnt counts; no compiler-tracked load sits in the loop). Each wave widens its 4 column tiles'
+// weights once per K-tile (codes and scales from LDS, as in the decode kernel) and reuses them over its 4 row tiles;
+// the activation rows are widened per row tile. Activation row pieces sit XOR-swizzled (16-byte piece p of row r at
+// position p ^ (r & 7)) so the 16 rows a fragment read touches land in different banks: the DMA lane that fills
+// position p of row r fetches piece p ^ (r & 7). Past K (a partial last K-tile) an activation piece is fetched from
+// the row's last valid piece; the weights' codes and scales there are zero, so those products are exact zeros.
 constexpr int PV_BM = 128, PV_BN = 128, PV_THREADS = 256;
+constexpr int PV_NS = 3;           // LDS stages
+constexpr int PV_DMA = 7;          // DMA instructions per wave and stage: 4 activation, 2 code, 1 scale
 
 struct PvStage {
   uint8_t a[PV_BM * NV_KT];        // fp8 activations, row-major, swizzled 16-byte pieces
   uint8_t b[8 * 1024];             // codes of the 8 column tiles, the global layout's K-tile
   uint8_t s[8 * 128];              // their scales
 };
+constexpr size_t PV_SMEM = PV_NS * sizeof(PvStage) + PV_BM * (sizeof(int) + 2 * sizeof(float));
 
 __global__ void __launch_bounds__(PV_THREADS, 2) nvfp4_prefill_kernel(
     const uint8_t* __restrict__ A, const float* __restrict__ As, const uint8_t* __restrict__ Wq,
@@ -307,8 +314,11 @@ __global__ void __launch_bounds__(PV_THREADS, 2) nvfp4_prefill_kernel(
     const int* __restrict__ sorted_ids, const int* __restrict__ expert_ids, const int* __restrict__ ntpp,
     const float* __restrict__ topk_w, long wq_estride, long ws_estride, long wg_estride, int numel, int a_row_div,
     int K, int N, int blk, int subs) {
-  __shared__ PvStage st[2];
-  __shared__ int s_fr[PV_BM];
+  extern __shared__ __align__(16) uint8_t pv_smem[];
+  PvStage* st = reinterpret_cast<PvStage*>(pv_smem);
+  int* s_fr = reinterpret_cast<int*>(pv_smem + PV_NS * sizeof(PvStage));
+  float* s_as = reinterpret_cast<float*>(s_fr + PV_BM);         // As of each tile row (read once, before the loop)
+  float* s_tw = s_as + PV_BM;                                  // topk_w of each tile row
   const int rb = blockIdx.y / subs, sub = blockIdx.y - rb * subs;
   const int row0 = rb * blk + sub * PV_BM;
   const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
@@ -320,62 +330,46 @@ __global__ void __launch_bounds__(PV_THREADS, 2) nvfp4_prefill_kernel(
   if (tid < PV_BM) {
     const int fr = sorted_ids[row0 + tid];
     s_fr[tid] = fr;
+    const bool live = fr >= 0 && fr < numel;
+    s_as[tid] = live ? As[fr / a_row_div] : 0.f;
+    s_tw[tid] = live && topk_w ? topk_w[fr] : 1.f;
   }
   __syncthreads();
   const int NT = N / 16, nkt = (K + NV_KT - 1) / NV_KT;
   const int nt0 = blockIdx.x * (PV_BN / 16);
-  const uint8_t* __restrict__ We = Wq + (size_t)e * wq_estride;
-  const uint8_t* __restrict__ Se = Ws + (size_t)e * ws_estride;
+  const uint8_t* We = uniform_ptr(Wq + (size_t)e * wq_estride);
+  const uint8_t* Se = uniform_ptr(Ws + (size_t)e * ws_estride);
   const float* __restrict__ Ge = Wg + (size_t)e * wg_estride;
 
-  // this thread's load slots: activation pieces q = tid + 256 i (row q >> 3, piece q & 7), code chunks
-  // q = tid + 256 i (column tile q >> 6, lane q & 63), scale chunks tid < 64 (column tile tid >> 3, part tid & 7).
-  // Rows are q >> 3 = (tid >> 3) + 32 i and pieces tid & 7 for every i.
-  const int prow = tid >> 3, ppiece = tid & 7;
-  const uint8_t* asrc0;
-  const uint8_t* asrc1;
-  const uint8_t* asrc2;
-  const uint8_t* asrc3;
-  {
-    int f0 = s_fr[prow], f1 = s_fr[prow + 32], f2 = s_fr[prow + 64], f3 = s_fr[prow + 96];
-    f0 = (f0 < 0 || f0 >= numel) ? first : f0;              // padding rows load a valid row, never stored
-    f1 = (f1 < 0 || f1 >= numel) ? first : f1;
-    f2 = (f2 < 0 || f2 >= numel) ? first : f2;
-    f3 = (f3 < 0 || f3 >= numel) ? first : f3;
-    asrc0 = A + (size_t)(f0 / a_row_div) * K + ppiece * 16;
-    asrc1 = A + (size_t)(f1 / a_row_div) * K + ppiece * 16;
-    asrc2 = A + (size_t)(f2 / a_row_div) * K + ppiece * 16;
-    asrc3 = A + (size_t)(f3 / a_row_div) * K + ppiece * 16;
+  // DMA sources (32-bit offsets from uniform bases; the host keeps A and one expert's codes below 4 GiB).
+  // Activations: instruction i of wave w fills LDS pieces q = (4 i + w) * 64 + lane, i.e. row r = 32 i + 8 w + lane / 8
+  // at position lane % 8, which holds the row's piece (lane % 8) ^ (r & 7) = (lane % 8) ^ (lane / 8).
+  const int gp16 = ((lane & 7) ^ (lane >> 3)) * 16;
+  uint32_t arow[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    int f = s_fr[32 * i + 8 * wave + (lane >> 3)];
+    f = (f < 0 || f >= numel) ? first : f;                     // padding rows load a valid row, never stored
+    arow[i] = (uint32_t)(f / a_row_div) * (uint32_t)K;
   }
-  const int aoff_l = ((ppiece ^ (prow & 7)) * 16);              // rows prow + 32 i share prow & 7
-  const uint8_t* bsrc0 = We + (size_t)min(nt0 + (tid >> 6), NT - 1) * nkt * 1024 + (size_t)(tid & 63) * 16;
-  const uint8_t* bsrc1 = We + (size_t)min(nt0 + 4 + (tid >> 6), NT - 1) * nkt * 1024 + (size_t)(tid & 63) * 16;
-  const uint8_t* ssrc = Se + (size_t)min(nt0 + (tid >> 3), NT - 1) * nkt * 128 + (size_t)(tid & 7) * 16;
-
-  uint4 ra0, ra1, ra2, ra3, rb0, rb1, rs = make_uint4(0u, 0u, 0u, 0u);
-#define PV_LOAD(kt)                                                                                               \
-  {                                                                                                               \
-    const int koff = (kt) * NV_KT + ppiece * 16;                                                                  \
-    const int kc = min(koff, K - 16) - ppiece * 16;              /* K tail: a clamped valid piece, zeroed below */ \
-    ra0 = *reinterpret_cast<const uint4*>(asrc0 + kc);                                                            \
-    ra1 = *reinterpret_cast<const uint4*>(asrc1 + kc);                                                            \
-    ra2 = *reinterpret_cast<const uint4*>(asrc2 + kc);                                                            \
-    ra3 = *reinterpret_cast<const uint4*>(asrc3 + kc);                                                            \
-    if (koff >= K) ra0 = ra1 = ra2 = ra3 = make_uint4(0u, 0u, 0u, 0u);                                            \
-    rb0 = *reinterpret_cast<const uint4*>(bsrc0 + (size_t)(kt) * 1024);                                          \
-    rb1 = *reinterpret_cast<const uint4*>(bsrc1 + (size_t)(kt) * 1024);                                          \
-    if (tid < 64) rs = *reinterpret_cast<const uint4*>(ssrc + (size_t)(kt) * 128);                                \
-  }
-#define PV_STORE(S)                                                                                               \
-  {                                                                                                               \
-    *reinterpret_cast<uint4*>((S).a + prow * NV_KT + aoff_l) = ra0;                                               \
-    *reinterpret_cast<uint4*>((S).a + (prow + 32) * NV_KT + aoff_l) = ra1;                                        \
-    *reinterpret_cast<uint4*>((S).a + (prow + 64) * NV_KT + aoff_l) = ra2;                                        \
-    *reinterpret_cast<uint4*>((S).a + (prow + 96) * NV_KT + aoff_l) = ra3;                                        \
-    *reinterpret_cast<uint4*>((S).b + tid * 16) = rb0;                                                            \
-    *reinterpret_cast<uint4*>((S).b + (tid + PV_THREADS) * 16) = rb1;                                             \
-    if (tid < 64) *reinterpret_cast<uint4*>((S).s + tid * 16) = rs;                                               \
-  }
+  // codes: instruction i of wave w fills column tile t = 4 i + w (1 KB); scales: wave w's dword lanes fill tiles
+  // 2 w and 2 w + 1 (128 bytes each)
+  uint32_t boff[2];
+#pragma unroll
+  for (int i = 0; i < 2; i++) boff[i] = (uint32_t)min(nt0 + 4 * i + wave, NT - 1) * (uint32_t)(nkt * 1024) + lane * 16;
+  const uint32_t soff = (uint32_t)min(nt0 + (tid >> 5), NT - 1) * (uint32_t)(nkt * 128) + (tid & 31) * 4;
+  const uint32_t la0 = lds_addr(&st[0].a[wave * 1024]);
+  const uint32_t lb0 = lds_addr(&st[0].b[wave * 1024]);
+  const uint32_t ls0 = lds_addr(&st[0].s[wave * 256]);
+  auto issue = [&](int kt, int sg) {
+    const uint32_t so = (uint32_t)(sg * (int)sizeof(PvStage));
+    const uint32_t ka = (uint32_t)min(kt * NV_KT + gp16, K - 16);
+#pragma unroll
+    for (int i = 0; i < 4; i++) dma16s(A, arow[i] + ka, la0 + so + i * 4096);
+#pragma unroll
+    for (int i = 0; i < 2; i++) dma16s(We, boff[i] + (uint32_t)kt * 1024u, lb0 + so + i * 4096);
+    dma4s(Se, soff + (uint32_t)kt * 128u, ls0 + so);
+  };
 
   v4f acc[4][4];
 #pragma unroll
@@ -383,12 +377,17 @@ __global__ void __launch_bounds__(PV_THREADS, 2) nvfp4_prefill_kernel(
 #pragma unroll
     for (int j = 0; j < 4; j++) acc[i][j] = (v4f){0.f, 0.f, 0.f, 0.f};
 
-  PV_LOAD(0)
-  PV_STORE(st[0])
-  __syncthreads();
+  issue(0, 0);
+  if (nkt > 1) issue(1, 1);
+  int sidx = 0;
   for (int kt = 0; kt < nkt; kt++) {
-    if (kt + 1 < nkt) PV_LOAD(kt + 1)
-    const PvStage& S = st[kt & 1];
+    // K-tile kt is in once only the next one's DMA (when issued) is outstanding
+    if (kt + 1 < nkt) asm volatile("s_waitcnt vmcnt(7)" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    // K-tile kt + 2 into the stage every wave finished reading in the previous iteration
+    if (kt + 2 < nkt) issue(kt + 2, sidx == 0 ? PV_NS - 1 : sidx - 1);
+    const PvStage& S = st[sidx];
     h8 b[4][4];
 #pragma unroll
     for (int j = 0; j < 4; j++) {
@@ -414,29 +413,37 @@ __global__ void __launch_bounds__(PV_THREADS, 2) nvfp4_prefill_kernel(
         acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a3, b[j][3], acc[i][j], 0, 0, 0);
       }
     }
-    if (kt + 1 < nkt) PV_STORE(st[(kt + 1) & 1])
-    __syncthreads();
+    sidx = sidx == PV_NS - 1 ? 0 : sidx + 1;
   }
-#undef PV_LOAD
-#undef PV_STORE
 
-  // epilogue: lane holds column c of each column tile, rows 4g .. 4g + 3 of each row tile
+  // epilogue: lane holds column c of each column tile, rows 4g .. 4g + 3 of each row tile; out = bf16(v * ((Wg[n] *
+  // As[row]) * topk_w[row])), the row factors from LDS and the lane's 4 column multipliers loaded together. Branch-free:
+  // every lane issues its 64 two-byte stores through a raw buffer of numel * N * 2 bytes (the host keeps it below
+  // 2 GiB), a padding row or a column past N going to offset `cbytes`, which the range check drops -- no store waits
+  // behind another.
+  float wgv[4];
 #pragma unroll
-  for (int j = 0; j < 4; j++) {
-    const int n = (nt0 + wn * 4 + j) * 16 + c;
-    if (n >= N) continue;
-    const float wg = Ge[n];
+  for (int j = 0; j < 4; j++) wgv[j] = Ge[min((nt0 + wn * 4 + j) * 16 + c, N - 1)];
+  const uint32_t cbytes = (uint32_t)numel * (uint32_t)N * 2u;
+  const auto crs = __builtin_amdgcn_make_buffer_rsrc(C, (short)0, (int)cbytes, 0x00020000);
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+  for (int i = 0; i < 4; i++)
 #pragma unroll
-      for (int q = 0; q < 4; q++) {
-        const int fr = s_fr[(wm * 4 + i) * 16 + 4 * g + q];
-        if (fr < 0 || fr >= numel) continue;
-        float sc = wg * As[fr / a_row_div];
-        if (topk_w) sc *= topk_w[fr];
-        C[(size_t)fr * N + n] = f2bf(acc[i][j][q] * sc);
+    for (int q = 0; q < 4; q++) {
+      const int row = (wm * 4 + i) * 16 + 4 * g + q;
+      const int fr = s_fr[row];
+      const bool live = fr >= 0 && fr < numel;
+      const float ras = s_as[row], rtw = s_tw[row];
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const int n = (nt0 + wn * 4 + j) * 16 + c;
+        float sc = wgv[j] * ras;
+        if (topk_w) sc *= rtw;
+        const uint16_t v = (uint16_t)(pack_bf16x2(acc[i][j][q] * sc, 0.f) & 0xffffu);
+        const uint32_t off = (live && n < N) ? ((uint32_t)fr * (uint32_t)N + (uint32_t)n) * 2u : cbytes;
+        __builtin_amdgcn_raw_buffer_store_b16(v, crs, (int)off, 0, 0);
       }
-  }
+    }
 }
 
 // ------------------------------------------------------------------- dense linear at decode widths, one launch
@@ -557,7 +564,13 @@ int r9k_nvfp4_prefill_launch(long a, long as, long wq, long ws, long wg, long c,
   if (ny > 0x7fffffffL) return -3;
   const dim3 grid((N + PV_BN - 1) / PV_BN, (unsigned)ny);
   const long wq_estride = (long)N * ((K + NV_KT - 1) / NV_KT) * 64;
-  hipLaunchKernelGGL(nvfp4_prefill_kernel, grid, dim3(PV_THREADS), 0, (hipStream_t)stream, (const uint8_t*)a,
+  // the DMA addresses activations and one expert's codes through 32-bit offsets
+  if ((long)((numel + a_row_div - 1) / a_row_div) * K >= (1L << 32) || wq_estride >= (1L << 32)) return -3;
+  if ((long)numel * N * 2 >= (1L << 31)) return -3;             // the epilogue's raw output buffer
+  static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(nvfp4_prefill_kernel),
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)PV_SMEM);
+  if (attr != hipSuccess) return -6;
+  hipLaunchKernelGGL(nvfp4_prefill_kernel, grid, dim3(PV_THREADS), PV_SMEM, (hipStream_t)stream, (const uint8_t*)a,
                      (const float*)as, (const uint8_t*)wq, (const uint8_t*)ws, (const float*)wg, (uint16_t*)c,
                      (const int*)sorted_ids, (const int*)expert_ids, (const int*)ntpp, (const float*)topk_w,
                      wq_estride, ws_estride, wg_estride, numel, a_row_div, K, N, blk, subs);
