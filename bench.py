@@ -489,6 +489,40 @@ def calib_copy(dev) -> None:
     torch.cuda.synchronize()
 
 
+def copy_rate_gbs(dev, nbytes: int = 512 << 20, reps: int = 10) -> float:
+    """Bytes moved per second (read + write) by a plain device-to-device copy of `nbytes`, over 4 rotating buffer
+    pairs (2 GiB in all, past the 256 MB Infinity Cache): the practical ceiling of a kernel whose traffic is half reads
+    and half writes, the mix of the prefill layer's intermediates."""
+    src = [torch.ones(nbytes // 4, dtype=torch.float32, device=dev) for _ in range(4)]
+    dst = [torch.empty_like(t) for t in src]
+    k = [0]
+
+    def one():
+        i = k[0] % 4
+        dst[i].copy_(src[i])
+        k[0] += 1
+    ms = events_ms(one, reps)
+    del src, dst
+    torch.cuda.empty_cache()
+    return 2 * nbytes / (ms * 1e-3) / 1e9
+
+
+def prefill_dataflow_bytes(T: int, topk: int, H: int, I: int, E: int) -> int:
+    """HBM bytes of the routed prefill layer's dataflow, each launch reading its inputs once and writing its outputs
+    once (gathered activation rows counted per routed row, as the GEMMs fetch them): routing + quant (logits, x in,
+    fp8 codes out), gate_up (weights of every expert, codes, bf16 out), SiLU + quant (bf16 in, codes out), down
+    (weights, codes, bf16 rows out) and the weighted top-k sum (rows in, bf16 out)."""
+    R = T * topk
+    w13 = E * (2 * I * H // 2 + 2 * I * H // 32)
+    w2 = E * (H * I // 2 + H * I // 32)
+    route = T * E * 2 + T * H * 2 + T * H
+    gate_up = w13 + R * H + R * 2 * I * 2
+    silu = R * 2 * I * 2 + R * I
+    down = w2 + R * I + R * H * 2
+    msum = R * H * 2 + T * H * 2
+    return route + gate_up + silu + down + msum
+
+
 def measured_traffic():
     """HBM bytes per gate_up launch at T=64 from the committed PMC summary (its line 'traffic_bytes_per_launch: N'),
     or None when there is none."""
@@ -593,10 +627,19 @@ def main():
         ms, n = graph_time(pl, 8, max(4, args.warmup // 4), windows=5)
         flops = 6 * 8192 * topk * layer.H * layer.I
         tf = flops / (ms * 1e-3) / 1e12
+        del pl
+        torch.cuda.empty_cache()
+        db = prefill_dataflow_bytes(8192, topk, layer.H, layer.I, layer.E)
+        cgbs = copy_rate_gbs(dev)
         prefill = {"workload": "cfg3 prefill T=8192", "ms_per_step": round(ms, 4), "tokens_per_s": round(8192 / (ms * 1e-3)),
                    "TFLOPS": round(tf, 1), "frac_fp4_peak": round(tf / FP4_PEAK_TFLOPS, 4),
-                   "frac_fp8_peak": round(tf / FP8_PEAK_TFLOPS, 4), "steps": n}
-        print(f"# prefill T=8192: {ms:.3f} ms/layer, {tf:.1f} TFLOPS", file=sys.stderr, flush=True)
+                   "frac_fp8_peak": round(tf / FP8_PEAK_TFLOPS, 4), "steps": n,
+                   "dataflow": {"what": "HBM bytes of the layer's launches (each input read once, each output written "
+                                        "once) / ms_per_step, against a measured device copy (read + write)",
+                                "bytes": db, "achieved_GBps": round(db / (ms * 1e-3) / 1e9, 1),
+                                "copy_GBps": round(cgbs, 1), "frac_copy": round(db / (ms * 1e-3) / 1e9 / cgbs, 4)}}
+        print(f"# prefill T=8192: {ms:.3f} ms/layer, {tf:.1f} TFLOPS; dataflow {db / 1e9:.3f} GB at "
+              f"{db / (ms * 1e-3) / 1e12:.2f} TB/s (device copy {cgbs / 1e3:.2f} TB/s)", file=sys.stderr, flush=True)
 
     router = None if args.no_router else router_times(dev)
     cfg4 = None if args.no_cfg4 else cfg4_lines(dev)
