@@ -367,6 +367,7 @@ def cache_lines(dev, steps: int) -> dict:
       hit:   T = 1 routed to 8 resident experts every step (the cold pass is provably empty, no inserts);
       wide:  T = 64 (~240 distinct experts > the 63-expert threshold): every non-resident expert is read through
              from host memory inside the GEMMs (PCIe);
+      wide staged: the wide step with R9K_STAGE_COLD=1 (the cold experts gathered into VRAM first, then read there);
       gather: r4d_lru_gather of 64 experts host -> slots alone (1.67 MB each)."""
     from r9700_vllm.kernels import moe as K
     from r9700_vllm.moe import cache as C
@@ -417,6 +418,21 @@ def cache_lines(dev, steps: int) -> dict:
         out[name] = row
         print(f"# cache {name}: {ms * 1e3:.1f} us/layer, {distinct} experts, {cold} read through from host, "
               f"{resident} of {ids.numel()} rows resident", file=sys.stderr, flush=True)
+    # the same wide step with cold staging (R9K_STAGE_COLD=1): the cold experts gathered into a VRAM staging area in
+    # one bulk copy, then the cold pass over that copy instead of reading host memory inside the GEMMs
+    os.environ["R9K_STAGE_COLD"] = "1"
+    try:
+        sc = C.LayerCache(0, cache.h_w13, cache.h_w2, W13.wsr, W2.wsr, 2 * I, H, H, I, S)
+    finally:
+        del os.environ["R9K_STAGE_COLD"]
+    exs = R9700Mxfp4Experts.standalone(sc.h_s13, sc.h_s2)
+    exs.r9k_cache = sc
+    fn = lambda: exs.apply(o, x, sc.h_w13, sc.h_w2, w, ids, "silu", E, None, None, None, None, None, None, False)
+    ms = timed(fn, max(4, steps // 10))
+    out["wide_T64_staged"] = {"T": 64, "ms_per_step": round(ms, 5), "staged": int(sc.stage_n.item())}
+    print(f"# cache wide_T64 staged: {ms * 1e3:.1f} us/layer, {out['wide_T64_staged']['staged']} experts staged "
+          f"into VRAM first", file=sys.stderr, flush=True)
+    del exs, sc
     miss = torch.stack([torch.arange(100, 164, dtype=torch.int32), torch.arange(0, 64, dtype=torch.int32)], 1)
     cache.miss[:64].copy_(miss.to(dev))
     cache.n_miss.fill_(64)

@@ -287,6 +287,15 @@ int r4d_lru_gather(long d0, long s0, long b0, long d1, long s1, long b1, long d2
  * (r4d_lru.hip:305-631, moe/cache.py:336-354). -1 mk < 0 / E <= 0, -3 null pointer, -6 launch error. */
 int r9k_lru_map_ids(long ids, int mk, int E, long table, long map_cold, long hot, long cold, long stream);
 
+/* Cold staging (the reference's opt-in R9K_STAGE_COLD, moe/cache.py:358-393, built there with torch ops; no
+ * counterpart as one entry): ids int32 [mk] (this step's routed experts), table int32 [E] (expert -> slot, -1 = host)
+ * after this step's manage -> stage_map int32 [E] (each routed non-resident expert's staging index, in ascending
+ * expert order; -1 otherwise), miss int32 [cap][2] ((expert, staging index) pairs for r4d_lru_gather), n_miss [1]
+ * (their count, at most cap; with every slot filled at most E - S experts are cold). One workgroup, deterministic.
+ * 0, -1 bad sizes (E > 8192), -3 null pointer, -6 launch error. */
+int r9k_lru_stage_map(long ids, int mk, int E, long table, int cap, long stage_map, long miss, long n_miss,
+                      long stream);
+
 /* Mapped pinned host memory for the expert store (the role of the reference's UVA tensors, utils/hostmem.py):
  * hipHostMalloc(Mapped | Portable), returned only when its device address equals its host address; 0 on failure or
  * bytes <= 0. r9k_host_free: 0 / -6. */

@@ -288,6 +288,57 @@ __global__ void __launch_bounds__(256) lru_map_ids_kernel(const int* __restrict_
   cold[i] = ok ? map_cold[e] : -1;
 }
 
+// Cold staging map (one workgroup): the experts routed this step that are not resident, numbered in ascending expert
+// order -- stage_map[e] = that number (-1 for every other expert), the miss list (e, number) the gather copies host ->
+// staging area, and their count. The numbering is a prefix sum of the cold flags, chunk by chunk over the experts
+// (a wave-inclusive scan, then the waves' totals), so it is deterministic.
+__global__ void __launch_bounds__(MT_THREADS) lru_stage_map_kernel(const int* __restrict__ ids, int mk, int E,
+                                                                   const int* __restrict__ table, int cap,
+                                                                   int* __restrict__ stage_map,
+                                                                   int* __restrict__ miss, int* __restrict__ n_miss) {
+  __shared__ uint8_t routed[MAX_E];
+  __shared__ int wsum[NWAVE];
+  const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
+  for (int e = tid; e < E; e += MT_THREADS) routed[e] = 0;
+  __syncthreads();
+  for (int i = tid; i < mk; i += MT_THREADS) {
+    const int e = ids[i];
+    if (e >= 0 && e < E) routed[e] = 1;                       // plain stores of the same value: no atomics needed
+  }
+  __syncthreads();
+  int base = 0;
+  for (int e0 = 0; e0 < E; e0 += MT_THREADS) {
+    const int e = e0 + tid;
+    const int cold = (e < E && routed[e] && table[e] < 0) ? 1 : 0;
+    int x = cold;
+#pragma unroll
+    for (int o = 1; o < WAVE; o <<= 1) {
+      const int y = __shfl_up(x, o, WAVE);
+      if (lane >= o) x += y;
+    }
+    if (lane == WAVE - 1) wsum[wave] = x;
+    __syncthreads();
+    int wb = 0, tot = 0;
+#pragma unroll
+    for (int w = 0; w < NWAVE; w++) {
+      wb += w < wave ? wsum[w] : 0;
+      tot += wsum[w];
+    }
+    if (e < E) {
+      const int idx = base + wb + x - cold;                   // exclusive rank among the cold experts
+      const bool staged = cold && idx < cap;
+      stage_map[e] = staged ? idx : -1;
+      if (staged) {
+        miss[2 * idx] = e;
+        miss[2 * idx + 1] = idx;
+      }
+    }
+    base += tot;
+    __syncthreads();
+  }
+  if (tid == 0) n_miss[0] = base < cap ? base : cap;
+}
+
 }  // namespace
 
 extern "C" int r9k_lru_manage_map(long ids, int mk, int E, int S, int max_distinct, int max_inserts, long table,
@@ -392,6 +443,21 @@ extern "C" int r9k_lru_map_ids(long ids, int mk, int E, long table, long map_col
   if (!ids || !table || !map_cold || !hot || !cold) return -3;
   hipLaunchKernelGGL(lru_map_ids_kernel, dim3((mk + 255) / 256), dim3(256), 0, (hipStream_t)stream,
                      (const int*)ids, mk, E, (const int*)table, (const int*)map_cold, (int*)hot, (int*)cold);
+  return hipGetLastError() == hipSuccess ? 0 : -6;
+}
+
+// No counterpart as one entry in the reference: its opt-in cold staging (R9K_STAGE_COLD=1, moe/cache.py:358-393)
+// builds the staging map with torch ops. ids int32 [mk] (this step's routed experts), table int32 [E] (expert ->
+// slot, -1 = host) after this step's manage -> stage_map int32 [E] (cold expert -> its staging index in ascending
+// expert order, else -1), miss int32 [cap][2] ((expert, staging index) pairs for r4d_lru_gather), n_miss int32 [1]
+// (their count, at most cap). A cold expert numbered cap or more is left unstaged (-1): with every slot of the arena
+// holding an expert, at most E - S are cold, so cap = E - S stages them all. 0, -1 bad sizes, -3 null, -6 launch.
+extern "C" int r9k_lru_stage_map(long ids, int mk, int E, long table, int cap, long stage_map, long miss,
+                                 long n_miss, long stream) {
+  if (E <= 0 || E > MAX_E || mk < 0 || cap < 0) return -1;
+  if ((mk && !ids) || !table || !stage_map || (cap && !miss) || !n_miss) return -3;
+  hipLaunchKernelGGL(lru_stage_map_kernel, dim3(1), dim3(MT_THREADS), 0, (hipStream_t)stream, (const int*)ids, mk,
+                     E, (const int*)table, cap, (int*)stage_map, (int*)miss, (int*)n_miss);
   return hipGetLastError() == hipSuccess ? 0 : -6;
 }
 

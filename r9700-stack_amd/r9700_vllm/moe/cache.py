@@ -59,6 +59,8 @@ def _L():
         L.r9k_lru_manage_tables.argtypes = [l, i, i, i, i, i] + [l] * 8 + [i] + [l] * 7 + [l]
         L.r4d_lru_fused.restype = i
         L.r4d_lru_fused.argtypes = [l, i, i, i, i, i] + [l] * 8 + [i, i, i] + [l] * 6 + [l]
+        L.r9k_lru_stage_map.restype = i
+        L.r9k_lru_stage_map.argtypes = [l, i, i, l, i, l, l, l, l]
         L.r9k_host_alloc.restype = l
         L.r9k_host_alloc.argtypes = [l]
         L.r9k_host_free.restype = i
@@ -136,7 +138,23 @@ def _num_moe_layers() -> int:
 
 
 def staging_enabled() -> bool:
-    return False
+    """R9K_STAGE_COLD=1 (opt-in, as in the reference): a step that needs the cold pass first copies every routed
+    expert that is not resident into a VRAM staging area with one bulk gather, and the cold pass reads it there
+    instead of reading host memory inside the GEMMs (once per routing block)."""
+    return os.environ.get("R9K_STAGE_COLD", "0") == "1"
+
+
+_STAGE_AREAS: dict = {}
+
+
+def _stage_area(dev: torch.device, cap: int, store) -> tuple:
+    """The staging slabs (w13, w2, s13, s2) for `cap` experts, shaped like the host store's, one set per device and
+    shape: layers run one after another on one stream, so every cached layer of a model shares it."""
+    key = (dev.index, cap) + tuple((tuple(h.shape[1:]), h.dtype) for h in store)
+    area = _STAGE_AREAS.get(key)
+    if area is None:
+        area = _STAGE_AREAS[key] = tuple(torch.empty((cap, *h.shape[1:]), dtype=h.dtype, device=dev) for h in store)
+    return area
 
 
 def stats_enabled() -> bool:
@@ -231,6 +249,14 @@ class LayerCache:
         self._init_lru_state(dev)
         self._init_policy()
         self._warm_start()
+        if staging_enabled() and self.E > self.S:
+            # every slot holds an expert after the warm start and keeps one, so at most E - S routed experts are cold
+            cap = self.E - self.S
+            self.stage = _stage_area(dev, cap, store)
+            self.stage_cap = cap
+            self.stage_map = torch.full((self.E,), -1, dtype=torch.int32, device=dev)
+            self.stage_miss = torch.full((cap, 2), -1, dtype=torch.int32, device=dev)
+            self.stage_n = torch.zeros((1,), dtype=torch.int32, device=dev)
         self.stats = None
         if stats_enabled():
             self.stats = torch.zeros((len(STAT_FIELDS),), dtype=torch.int64, device=dev)
@@ -290,12 +316,16 @@ class LayerCache:
         self.slot_stamp[:n] = torch.arange(n, 0, -1, dtype=torch.int64, device=dev) - n
         torch.cuda.synchronize()
 
-    def _gather(self):
+    def _gather(self, dst=None, miss=None, n_miss=None):
+        """The listed experts host -> their slots (default: the arena and the manager's miss list)."""
+        d13, d2, ds13, ds2 = dst if dst is not None else (self.a_w13, self.a_w2, self.a_s13, self.a_s2)
+        miss = self.miss if miss is None else miss
+        n_miss = self.n_miss if n_miss is None else n_miss
         b = self.bytes
         rc = _L().r4d_lru_gather(
-            self.a_w13.data_ptr(), self.h_w13.data_ptr(), b[0], self.a_w2.data_ptr(), self.h_w2.data_ptr(), b[1],
-            self.a_s13.data_ptr(), self.h_s13.data_ptr(), b[2], self.a_s2.data_ptr(), self.h_s2.data_ptr(), b[3],
-            0, 0, 0, 0, 0, 0, self.miss.data_ptr(), self.n_miss.data_ptr(), self.chunks, self.lanes, _stream())
+            d13.data_ptr(), self.h_w13.data_ptr(), b[0], d2.data_ptr(), self.h_w2.data_ptr(), b[1],
+            ds13.data_ptr(), self.h_s13.data_ptr(), b[2], ds2.data_ptr(), self.h_s2.data_ptr(), b[3],
+            0, 0, 0, 0, 0, 0, miss.data_ptr(), n_miss.data_ptr(), self.chunks, self.lanes, _stream())
         if rc:
             raise RuntimeError(f"r4d_lru_gather failed ({rc})")
 
@@ -394,7 +424,21 @@ class LayerCache:
         return (sh, eh, nh), (sc, ec, nc)
 
     def stage_cold(self, topk_ids: torch.Tensor):
-        raise RuntimeError("LayerCache.stage_cold: bulk staging of cold experts is not built for gfx950")
+        """After this step's manage: number the routed experts that are not resident (r9k_lru_stage_map, ascending
+        expert order), copy them host -> staging area with one gather, and return (w13, w2) experts over the staging
+        area plus stage_map [E] (expert -> staging index, -1 otherwise) for the cold pass's tables. Device work only
+        (no host sync), so a captured graph replays it."""
+        if self.stage is None:
+            raise RuntimeError("LayerCache.stage_cold: staging is off (R9K_STAGE_COLD=1 turns it on)")
+        ids = self._ids(topk_ids)
+        rc = _L().r9k_lru_stage_map(ids.data_ptr(), ids.numel(), self.E, self.table.data_ptr(), self.stage_cap,
+                                    self.stage_map.data_ptr(), self.stage_miss.data_ptr(), self.stage_n.data_ptr(),
+                                    _stream())
+        if rc:
+            raise RuntimeError(f"r9k_lru_stage_map failed ({rc}) E={self.E}")
+        self._gather(self.stage, self.stage_miss, self.stage_n)
+        w13, w2, s13, s2 = self.stage
+        return (*self._experts(w13, s13, w2, s2), self.stage_map)
 
     def _experts(self, w13, s13, w2, s2):
         return (K.Mxfp4Experts(w13, s13, self.N1, self.K1, self.fold[0]),

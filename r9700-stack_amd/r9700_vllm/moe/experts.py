@@ -202,14 +202,20 @@ class R9700Mxfp4Experts(_experts_base()):
                 raise RuntimeError("r9k expert cache: MXFP4 experts without an expert map only")
             (h1, h2), (c1, c2) = cache.hot(), cache.cold()
             need_cold = numel > cache.no_cold_limit
+            staged = need_cold and cache.stage is not None
             if cache.fused:
-                hot_al, cold_al = cache.update_fused(topk_ids, blk, need_cold)
+                # with staging the cold pass gets its tables from the stage map below, not from the host map
+                hot_al, cold_al = cache.update_fused(topk_ids, blk, need_cold and not staged)
                 if not need_cold:
                     slot_ids = cache.hot_ids.view(M, topk)   # every routed expert resident: each row's slot
             else:
                 cache.update(topk_ids)
                 hot_al = K.moe_align(topk_ids, blk, E, cache.table)
-                cold_al = K.moe_align(topk_ids, blk, E, cache.map_cold) if need_cold else None
+                cold_al = K.moe_align(topk_ids, blk, E, cache.map_cold) if need_cold and not staged else None
+            if staged:
+                # R9K_STAGE_COLD=1: the cold experts copied into VRAM in one gather, the cold pass over that copy
+                c1, c2, stage_map = cache.stage_cold(topk_ids)
+                cold_al = K.moe_align(topk_ids, blk, E, stage_map)
             passes = [(h1, h2, hot_al, (MT, pf_gate, pf_down))]
             if need_cold:
                 passes.append((c1, c2, cold_al, (MT, pf_gate, pf_down)))

@@ -8,6 +8,8 @@
   through both update paths, with the cache invariants and the oracle's state checked alongside.
 * A config 2 layer (E=288, hidden 2048, intermediate 512, top-8) through R9700Mxfp4Experts.apply with a 64-slot cache
   equals the same layer without one, bit for bit, at T = 1 (inserts) and T = 16 / 64 (read-through steps).
+* R9K_STAGE_COLD=1: the staging map against its contract, and the layer with its cold pass over the staged VRAM copy
+  equal to the resident layer, bit for bit.
 * update_fused captured in a HIP graph and replayed with new routing equals an eager twin on every replay
   (reference tests/test_cache_shapes.py part 2), and its buffers keep one address once the largest step was seen."""
 import numpy as np
@@ -318,6 +320,71 @@ def test_cached_layer_equals_resident_layer(dev, T):
         torch.cuda.synchronize()
         same = torch.equal(o0.view(torch.int16), o1.view(torch.int16))
         print(f"  step {step}: inserts {int(cache.n_miss.item())} bit-identical {same}", flush=True)
+        assert same
+
+
+def test_stage_map_numbers_routed_cold_experts(dev):
+    """r9k_lru_stage_map against a CPU restatement of its contract: the routed experts whose table entry is -1,
+    numbered in ascending expert order (stage_map, the (expert, index) miss list, the count), capped at cap."""
+    g = torch.Generator().manual_seed(61)
+    for E, mk, cap, seed in ((288, 512, 224, 1), (1500, 3000, 1400, 2), (64, 40, 5, 3), (16, 0, 8, 4)):
+        table = torch.full((E,), -1, dtype=torch.int32)
+        res = torch.randperm(E, generator=g)[: E // 3]
+        table[res] = torch.arange(res.numel(), dtype=torch.int32)
+        ids = torch.randint(-1, E, (mk,), generator=g, dtype=torch.int32)
+        sm = torch.full((E,), -7, dtype=torch.int32, device=dev)
+        miss = torch.full((max(cap, 1), 2), -7, dtype=torch.int32, device=dev)
+        n = torch.full((1,), -7, dtype=torch.int32, device=dev)
+        idd, td = ids.to(dev), table.to(dev)
+        rc = C._L().r9k_lru_stage_map(idd.data_ptr(), mk, E, td.data_ptr(), cap, sm.data_ptr(), miss.data_ptr(),
+                                      n.data_ptr(), torch.cuda.current_stream().cuda_stream)
+        assert rc == 0
+        torch.cuda.synchronize()
+        routed = np.zeros(E, dtype=bool)
+        for e in ids.tolist():
+            if 0 <= e < E:
+                routed[e] = True
+        cold = [e for e in range(E) if routed[e] and int(table[e]) < 0]
+        want = np.full(E, -1, dtype=np.int32)
+        for k, e in enumerate(cold[:cap]):
+            want[e] = k
+        print(f"stage map E={E} mk={mk} cap={cap}: {len(cold)} cold", flush=True)
+        assert np.array_equal(sm.cpu().numpy(), want)
+        assert int(n.item()) == min(len(cold), cap)
+        got = miss.cpu().numpy()[: min(len(cold), cap)]
+        assert np.array_equal(got[:, 0], np.array(cold[:cap], dtype=np.int32).reshape(-1)) if cold else True
+        assert np.array_equal(got[:, 1], np.arange(min(len(cold), cap), dtype=np.int32))
+
+
+@pytest.mark.parametrize("T", [16, 64])
+def test_staged_cold_pass_equals_resident_layer(dev, monkeypatch, T):
+    """R9K_STAGE_COLD=1: a config 2 layer whose wide steps stage the cold experts into VRAM (one gather) and run the
+    cold pass over that copy equals the same layer without a cache, bit for bit, over several steps."""
+    monkeypatch.setenv("R9K_STAGE_COLD", "1")
+    E, H, I, topk, S = 288, 2048, 512, 8, 64
+    print(f"staged cached layer T={T}", flush=True)
+    W13, W2 = make_w(dev, E, 2 * I, H, 71), make_w(dev, E, H, I, 72)
+    cache = C.LayerCache(0, C.to_host(W13.wq), C.to_host(W2.wq), W13.wsr, W2.wsr, 2 * I, H, H, I, S)
+    assert cache.stage is not None and cache.stage_cap == E - S
+    plain = R9700Mxfp4Experts.standalone(W13.wsr, W2.wsr)
+    cached = R9700Mxfp4Experts.standalone(cache.h_s13, cache.h_s2)
+    cached.r9k_cache = cache
+    g = torch.Generator().manual_seed(73 + T)
+    for step in range(3):
+        x = torch.randn(T, H, generator=g).to(torch.bfloat16).to(dev)
+        logits = torch.randn(T, E, generator=g).to(torch.bfloat16).to(dev)
+        w, ids = K.moe_topk(logits, topk, True)
+        o0 = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
+        o1 = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
+        plain.apply(o0, x, W13.wq, W2.wq, w, ids, "silu", E, None, None, None, None, None, None, False)
+        cached.apply(o1, x, cache.h_w13, cache.h_w2, w, ids, "silu", E, None, None, None, None, None, None, False)
+        torch.cuda.synchronize()
+        routed = set(ids.reshape(-1).tolist())
+        cold = sum(1 for e in routed if int(cache.table[e].item()) < 0)
+        same = torch.equal(o0.view(torch.int16), o1.view(torch.int16))
+        print(f"  step {step}: {cold} cold experts staged ({int(cache.stage_n.item())}), bit-identical {same}",
+              flush=True)
+        assert int(cache.stage_n.item()) == cold
         assert same
 
 
