@@ -59,6 +59,30 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// Wave-uniform unsigned max: DPP within 16-lane rows (quad swaps, row rotates by 4 and 8: every lane of a row then
+// holds the row's max), row_bcast:15 and row_bcast:31 carry the row maxima up to row 3, and lane 63's value is read
+// out. Lanes of the rows a broadcast does not write get 0, the identity of the unsigned max.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+#define R9K_DPP_MAX(ctrl, rows) v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, ctrl, rows, 0xF, false))
+  R9K_DPP_MAX(0xB1, 0xF);    // quad_perm [1,0,3,2]
+  R9K_DPP_MAX(0x4E, 0xF);    // quad_perm [2,3,0,1]
+  R9K_DPP_MAX(0x124, 0xF);   // row_ror:4
+  R9K_DPP_MAX(0x128, 0xF);   // row_ror:8
+  R9K_DPP_MAX(0x142, 0xA);   // row_bcast:15 -> rows 1, 3
+  R9K_DPP_MAX(0x143, 0xC);   // row_bcast:31 -> rows 2, 3
+#undef R9K_DPP_MAX
+  return __builtin_amdgcn_readlane(v, 63);
+}
+
+// Running max of the bf16 magnitudes of the two halves of w (sign bits cleared, compared as unsigned 16-bit
+// integers, two at a time). For bf16 magnitudes the integer order is the value order, and the inf / NaN patterns lie
+// above every finite one.
+typedef unsigned short r9k_u16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t max_mag_bf16x2(uint32_t acc, uint32_t w) {
+  const r9k_u16x2 a = __builtin_bit_cast(r9k_u16x2, acc), b = __builtin_bit_cast(r9k_u16x2, w & 0x7fff7fffu);
+  return __builtin_bit_cast(uint32_t, __builtin_elementwise_max(a, b));
+}
+
 __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) {
@@ -112,6 +136,20 @@ __device__ __forceinline__ uint2 pack8_bf16_e4m3(uint4 v, float inv) {
   return pack8_e4m3(f, inv);
 }
 
+// pack8_bf16_e4m3 for a chunk of a row whose largest magnitude amax is finite and inv = 448 / max(amax, 1e-12):
+// every product then has |x * inv| <= 448 (1 + 2^-23) < 464, the range where V_CVT_PK_FP8_F32 alone gives
+// f32_to_e4m3's bytes, so the out-of-range check is left out (same bytes as pack8_bf16_e4m3).
+__device__ __forceinline__ uint2 pack8_bf16_e4m3_finite(uint4 v, float inv) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+  uint32_t out[2];
+#pragma unroll
+  for (int h = 0; h < 2; h++) {
+    const int r = __builtin_amdgcn_cvt_pk_fp8_f32(lo16(w[2 * h]) * inv, hi16(w[2 * h]) * inv, 0, false);
+    out[h] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(lo16(w[2 * h + 1]) * inv, hi16(w[2 * h + 1]) * inv, r, true);
+  }
+  return make_uint2(out[0], out[1]);
+}
+
 // silu(g) * u with g, u the stored bf16 values, evaluated as (g / (1 + exp(-g))) * u in fp32 with the hardware
 // exponential (__expf, as the reference: kernels/r9k_moe_mxfp4a8.hip:526) and a reciprocal-multiply division
 // (V_RCP_F32, 1 ulp; within 2 ulp of the reference's IEEE division, whose sequence is 10 instructions an element in a
@@ -124,19 +162,43 @@ __device__ __forceinline__ float silu_mul(float gv, float uv) {
 // One wave quantises one row of K bf16 values (K % 8 == 0, K <= 512 * RMAX, the row 16-byte aligned, the code row
 // 8-byte aligned) to OCP e4m3 with a per-row scale:
 //   amax = max(max_k |x_k|, 1e-12);  inv = 448 / amax;  q_k = e4m3_rne(x_k * inv);  s = amax / 448.
-// Each lane keeps its 16-byte chunks (lane + 64 i) in registers, so the row is read once.
+// Each lane keeps its 16-byte chunks (lane + 64 i) in registers, so the row is read once. The row maximum is taken
+// on the bf16 magnitude bits (two values an instruction); a finite maximum is the float one exactly and lets every
+// code skip the range check. A row holding inf or NaN takes the float maximum, which passes over NaN, and the checked
+// conversion.
 template <int RMAX>
 __device__ __forceinline__ void quant_row_wave(const uint16_t* __restrict__ xrow, int K, uint8_t* __restrict__ qrow,
                                                float* __restrict__ s_out, int lane) {
   const uint4* xr = reinterpret_cast<const uint4*>(xrow);
   const int nvec = K / 8;
   uint4 v[RMAX];
-  float m = 0.f;
 #pragma unroll
   for (int i = 0; i < RMAX; i++) {
     const int c = lane + i * WAVE;
     v[i] = c < nvec ? xr[c] : make_uint4(0u, 0u, 0u, 0u);
   }
+  uint32_t mm = 0u;
+#pragma unroll
+  for (int i = 0; i < RMAX; i++) {
+    mm = max_mag_bf16x2(mm, v[i].x);
+    mm = max_mag_bf16x2(mm, v[i].y);
+    mm = max_mag_bf16x2(mm, v[i].z);
+    mm = max_mag_bf16x2(mm, v[i].w);
+  }
+  const uint32_t mb = wave_max_u32(max(mm & 0xffffu, mm >> 16));
+  uint2* qr = reinterpret_cast<uint2*>(qrow);
+  if (mb < 0x7f80u) {                                            // finite row (wave-uniform)
+    const float amax = fmaxf(__uint_as_float(mb << 16), 1e-12f);
+    const float inv = 448.f / amax;
+    if (lane == 0) *s_out = amax / 448.f;
+#pragma unroll
+    for (int i = 0; i < RMAX; i++) {
+      const int c = lane + i * WAVE;
+      if (c < nvec) qr[c] = pack8_bf16_e4m3_finite(v[i], inv);
+    }
+    return;
+  }
+  float m = 0.f;
 #pragma unroll
   for (int i = 0; i < RMAX; i++) {
     const uint32_t w[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
@@ -146,13 +208,10 @@ __device__ __forceinline__ void quant_row_wave(const uint16_t* __restrict__ xrow
   const float amax = fmaxf(wave_max(m), 1e-12f);
   const float inv = 448.f / amax;
   if (lane == 0) *s_out = amax / 448.f;
-  uint2* qr = reinterpret_cast<uint2*>(qrow);
 #pragma unroll
   for (int i = 0; i < RMAX; i++) {
     const int c = lane + i * WAVE;
-    if (c < nvec) {
-      qr[c] = pack8_bf16_e4m3(v[i], inv);
-    }
+    if (c < nvec) qr[c] = pack8_bf16_e4m3(v[i], inv);
   }
 }
 

@@ -54,30 +54,23 @@ constexpr int FW = FT / WAVE;
 
 #define R9K_DPP(v, ctrl) (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(v), ctrl, 0xF, 0xF, false)
 
-// Wave-uniform max of a 32-bit key: DPP within 16-lane rows (quad swaps, row rotates by 4 and 8), then the four row
-// results through v_readlane and a scalar max.
-__device__ __forceinline__ uint32_t wave_max_key(uint32_t v) {
-  v = max(v, R9K_DPP(v, 0xB1));    // quad_perm [1,0,3,2]
-  v = max(v, R9K_DPP(v, 0x4E));    // quad_perm [2,3,0,1]
-  v = max(v, R9K_DPP(v, 0x124));   // row_ror:4
-  v = max(v, R9K_DPP(v, 0x128));   // row_ror:8
-  const uint32_t a = __builtin_amdgcn_readlane(v, 0), b = __builtin_amdgcn_readlane(v, 16);
-  const uint32_t c = __builtin_amdgcn_readlane(v, 32), d = __builtin_amdgcn_readlane(v, 48);
-  return max(max(a, b), max(c, d));
-}
+// Wave-uniform max of a 32-bit key (wave_max_u32).
+__device__ __forceinline__ uint32_t wave_max_key(uint32_t v) { return wave_max_u32(v); }
 
-// Wave-uniform fmaxf / sum of a float, same DPP pattern (the sum in a fixed order: deterministic).
+// Wave-uniform fmaxf of a float, the same pattern (-inf for the lanes a broadcast does not write). The maximum does
+// not depend on the order of the steps.
 __device__ __forceinline__ float wave_max_dpp(float v) {
+  constexpr int NEG_INF = (int)0xff800000u;
   v = fmaxf(v, __uint_as_float(R9K_DPP(__float_as_uint(v), 0xB1)));
   v = fmaxf(v, __uint_as_float(R9K_DPP(__float_as_uint(v), 0x4E)));
   v = fmaxf(v, __uint_as_float(R9K_DPP(__float_as_uint(v), 0x124)));
   v = fmaxf(v, __uint_as_float(R9K_DPP(__float_as_uint(v), 0x128)));
-  const float a = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), 0));
-  const float b = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), 16));
-  const float c = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), 32));
-  const float d = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), 48));
-  return fmaxf(fmaxf(a, b), fmaxf(c, d));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(NEG_INF, __float_as_int(v), 0x142, 0xA, 0xF, false)));
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(NEG_INF, __float_as_int(v), 0x143, 0xC, 0xF, false)));
+  return __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), 63));
 }
+// Wave-uniform sum of a float in a fixed order (deterministic): the row sums through the same DPP steps, then the
+// four rows' lane-0 values as (row0 + row1) + (row2 + row3).
 __device__ __forceinline__ float wave_sum_dpp(float v) {
   v += __uint_as_float(R9K_DPP(__float_as_uint(v), 0xB1));
   v += __uint_as_float(R9K_DPP(__float_as_uint(v), 0x4E));
@@ -110,8 +103,19 @@ __device__ __forceinline__ void load_row(const uint16_t* __restrict__ row, int E
   }
 }
 
-// One wave routes one row from its preloaded logits. Lane k < topk ends holding selection k; writes w / ids
-// (global) and, when given, the ids to LDS.
+// The bf16 logit a live selection key holds (route_key's order-preserving bits inverted; -0 comes back as +0, which
+// gives the same softmax numerator).
+__device__ __forceinline__ uint16_t key_logit(uint32_t key) {
+  const uint32_t ord = (key >> 10) & 0xffffu;
+  return (uint16_t)((ord & 0x8000u) ? (ord & 0x7fffu) : (~ord & 0xffffu));
+}
+
+// One wave routes one row from its preloaded logits: softmax over the row (max, then exp(l - max) summed in the fixed
+// order of wave_sum_dpp), then topk rounds of a wave-wide key maximum, each taking the largest live logit left (ties
+// to the lower index) and clearing it. Lane k keeps round k's key; after the rounds it rebuilds the selection's
+// numerator from the key's logit bits (the same expression as the first pass, so the same value), divides by the sum
+// once, and the probabilities are added in round order for the renormalisation. Lane k < topk ends holding
+// selection k; writes w / ids (global) and, when given, the ids to LDS.
 template <int EPL>
 __device__ __forceinline__ void topk_core(const uint16_t* h, int E, int topk, bool renorm, float* __restrict__ w_out,
                                           int* __restrict__ id_out, short* lds_ids, int lane, bool agent = false) {
@@ -119,7 +123,6 @@ __device__ __forceinline__ void topk_core(const uint16_t* h, int E, int topk, bo
 #pragma unroll
   for (int i = 0; i < EPL; i++) mx = fmaxf(mx, bf2f(h[i]));
   mx = wave_max_dpp(mx);
-  float ex[EPL];
   uint32_t key[EPL];
   float s = 0.f;
 #pragma unroll
@@ -127,13 +130,11 @@ __device__ __forceinline__ void topk_core(const uint16_t* h, int E, int topk, bo
     const int e = lane + WAVE * i;
     const float d = bf2f(h[i]) - mx;
     const bool live = d >= -87.f;                        // false for NaN (NaN logit, or a +inf row)
-    ex[i] = (e < E && live) ? expf(d) : 0.f;
-    s += ex[i];
+    s += (e < E && live) ? expf(d) : 0.f;
     key[i] = e < E ? route_key(h[i], live, e) : 0u;
   }
   s = wave_sum_dpp(s);
-  float wsel = 0.f, tot = 0.f;
-  int isel = 0;
+  uint32_t won = 0u;                                     // lane k: the key taken in round k
   for (int k = 0; k < topk; k++) {
     uint32_t b = key[0];
 #pragma unroll
@@ -141,20 +142,20 @@ __device__ __forceinline__ void topk_core(const uint16_t* h, int E, int topk, bo
     b = wave_max_key(b);
     const int idx = 1023 - (int)(b & 1023u);
     const int owner = idx & (WAVE - 1), slot = idx / WAVE;
-    float eb = 0.f;
-#pragma unroll
-    for (int i = 0; i < EPL; i++)
-      if (i == slot) eb = ex[i];
-    eb = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(eb), owner));
 #pragma unroll
     for (int i = 0; i < EPL; i++)
       if (i == slot && lane == owner) key[i] = 0u;
-    const float p = s > 0.f ? eb / s : 0.f;
-    tot += p;
-    if (lane == k) { wsel = p; isel = idx; }
+    if (lane == k) won = b;
   }
-  float p = wsel;
-  if (renorm) p = tot > 0.f ? p / tot : 0.f;
+  float p = 0.f;
+  if (won & (1u << 26)) p = expf(bf2f(key_logit(won)) - mx);   // the first pass's numerator of this entry
+  p = s > 0.f ? p / s : 0.f;
+  if (renorm) {
+    float tot = 0.f;
+    for (int k = 0; k < topk; k++) tot += __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(p), k));
+    p = tot > 0.f ? p / tot : 0.f;
+  }
+  int isel = 1023 - (int)(won & 1023u);
   if (isel < 0 || isel >= E) isel = 0;               // unreachable (topk <= E); keeps every table write in range
   if (lane < topk) {
     w_out[lane] = p;
@@ -379,9 +380,7 @@ __device__ __forceinline__ void topk_rows(const uint16_t (&h)[NR][EPL], int E, i
 #pragma unroll
   for (int r = 0; r < NR; r++) {
     const uint32_t b = sel[r];
-    const uint32_t ord = (b >> 10) & 0xffffu;
-    const uint32_t hb = (ord & 0x8000u) ? (ord & 0x7fffu) : (~ord & 0xffffu);
-    const float eb = ((b >> 26) & 1u) ? expf(bf2f((uint16_t)hb) - mx[r]) : 0.f;
+    const float eb = ((b >> 26) & 1u) ? expf(bf2f(key_logit(b)) - mx[r]) : 0.f;
     float p = s[r] > 0.f ? eb / s[r] : 0.f;
     float tot = 0.f;
     for (int k = 0; k < topk; k++) tot += __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(p), k));

@@ -42,6 +42,38 @@ def test_quant_rows_fp8_strided_and_edge_rows(dev):
     assert np.array_equal(u8(q), qo) and np.array_equal(s.cpu().numpy(), so)
 
 
+@pytest.mark.parametrize("Kd", [64, 2048])
+def test_quant_rows_fp8_nonfinite_rows(dev, Kd):
+    """Rows holding NaN or +-inf take the checked conversion (the row maximum passes over NaN; an inf maximum gives
+    inv = 0, finite values -> +-0 and inf * 0 -> NaN -> sign | 0x7f); finite rows at the bf16 extremes (the largest
+    finite value, values under the 1e-12 floor, zeros) take the unchecked one. Codes and scale bits equal the
+    oracle's, standalone and in the fused top-k + quant launch."""
+    print(f"quant non-finite K={Kd}", flush=True)
+    g = torch.Generator().manual_seed(Kd)
+    x = torch.randn(12, Kd, generator=g)
+    x[0, 5] = float("nan")
+    x[1] = float("nan")
+    x[2, 9] = float("inf")
+    x[3, Kd - 1] = float("-inf")
+    x[4] = float("inf")
+    x[5, 3], x[5, 4] = float("inf"), float("nan")
+    x[6, 0] = 3.3895313892515355e38                     # the largest finite bf16
+    x[7] = 1e-30
+    x[8] = 0.0
+    x[9, ::3] = -0.0
+    x[10] = -3.0e38
+    xb = x.to(torch.bfloat16)
+    qo, so = O.quant_rows_fp8(xb)
+    q, s = K.quant_rows_fp8(xb.to(dev))
+    assert np.array_equal(u8(q), qo)
+    assert np.array_equal(s.cpu().numpy().view(np.uint32), so.view(np.uint32))
+    logits = torch.randn(12, 288, generator=g).to(torch.bfloat16).to(dev)
+    r = K.moe_topk_quant(logits, 8, True, xb.to(dev))
+    assert r is not None
+    assert np.array_equal(u8(r[2]), qo)
+    assert np.array_equal(r[3].cpu().numpy().view(np.uint32), so.view(np.uint32))
+
+
 def test_quant_rows_fp8_gate(dev):
     g = torch.Generator().manual_seed(11)
     x = torch.randn(37, 2048, generator=g).to(torch.bfloat16)
