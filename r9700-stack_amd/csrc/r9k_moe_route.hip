@@ -513,6 +513,132 @@ __global__ void __launch_bounds__(RW * WAVE) topk_quant_kernel(const uint16_t* _
   }
 }
 
+// Reductions over the 16 lanes of a DPP row, the result in every lane of the row. The sum pairs lanes by xor
+// butterflies (quad swaps, then half-row and row mirrors): each step adds two partial sums in either order, so all
+// 16 lanes hold the same bits.
+__device__ __forceinline__ uint32_t row16_max_u32(uint32_t v) {
+  v = max(v, R9K_DPP(v, 0xB1));
+  v = max(v, R9K_DPP(v, 0x4E));
+  v = max(v, R9K_DPP(v, 0x124));   // row_ror:4
+  v = max(v, R9K_DPP(v, 0x128));   // row_ror:8
+  return v;
+}
+__device__ __forceinline__ float row16_max_f(float v) {
+  v = fmaxf(v, __uint_as_float(R9K_DPP(__float_as_uint(v), 0xB1)));
+  v = fmaxf(v, __uint_as_float(R9K_DPP(__float_as_uint(v), 0x4E)));
+  v = fmaxf(v, __uint_as_float(R9K_DPP(__float_as_uint(v), 0x124)));
+  v = fmaxf(v, __uint_as_float(R9K_DPP(__float_as_uint(v), 0x128)));
+  return v;
+}
+__device__ __forceinline__ float row16_sum_f(float v) {
+  v += __uint_as_float(R9K_DPP(__float_as_uint(v), 0xB1));    // quad_perm [1,0,3,2]
+  v += __uint_as_float(R9K_DPP(__float_as_uint(v), 0x4E));    // quad_perm [2,3,0,1]
+  v += __uint_as_float(R9K_DPP(__float_as_uint(v), 0x141));   // row_half_mirror
+  v += __uint_as_float(R9K_DPP(__float_as_uint(v), 0x140));   // row_mirror
+  return v;
+}
+
+// Top-k of one row on the 16 lanes of a DPP row (four rows a wave), for the wide launches: NP dwords of logits a
+// lane (entries 2d and 2d + 1 of dword d = l16 + 16 i; E even), the same keys, selection rounds and numerator rebuild
+// as topk_core with row-wide reductions and no cross-row readlanes, about half of topk_core's VALU work a row. The
+// softmax sum is taken in this layout's order (lane sums, then the butterflies above). Lane l16 < topk of the row
+// stores selection l16 when `store`.
+template <int NP>
+__device__ __forceinline__ void topk_row16(const uint16_t* __restrict__ row, int E, int topk, bool renorm,
+                                           float* __restrict__ w_out, int* __restrict__ id_out, bool store,
+                                           int lane) {
+  const int l16 = lane & 15;
+  const uint32_t* rp = reinterpret_cast<const uint32_t*>(row);
+  uint32_t hv[NP];
+#pragma unroll
+  for (int i = 0; i < NP; i++) {
+    const int d = l16 + 16 * i;
+    hv[i] = 2 * d < E ? rp[d] : 0xff80ff80u;
+  }
+  float mx = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < NP; i++) mx = fmaxf(mx, fmaxf(lo16(hv[i]), hi16(hv[i])));
+  mx = row16_max_f(mx);
+  uint32_t key[2 * NP];
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < NP; i++) {
+#pragma unroll
+    for (int t = 0; t < 2; t++) {
+      const int e = 2 * (l16 + 16 * i) + t;
+      const uint16_t h = (uint16_t)(t ? hv[i] >> 16 : hv[i] & 0xffffu);
+      const float d = bf2f(h) - mx;
+      const bool live = d >= -87.f;
+      s += (e < E && live) ? expf(d) : 0.f;
+      key[2 * i + t] = e < E ? route_key(h, live, e) : 0u;
+    }
+  }
+  s = row16_sum_f(s);
+  uint32_t won = 0u;
+  for (int k = 0; k < topk; k++) {
+    uint32_t b = key[0];
+#pragma unroll
+    for (int j = 1; j < 2 * NP; j++) b = max(b, key[j]);
+    b = row16_max_u32(b);
+#pragma unroll
+    for (int j = 0; j < 2 * NP; j++) key[j] = key[j] == b ? 0u : key[j];   // keys are unique within a row
+    if (l16 == k) won = b;
+  }
+  float p = 0.f;
+  if (won & (1u << 26)) p = expf(bf2f(key_logit(won)) - mx);
+  p = s > 0.f ? p / s : 0.f;
+  if (renorm) {
+    float tot = 0.f;
+    for (int k = 0; k < topk; k++) tot += __shfl(p, (lane & ~15) + k, WAVE);
+    p = tot > 0.f ? p / tot : 0.f;
+  }
+  int isel = 1023 - (int)(won & 1023u);
+  if (isel < 0 || isel >= E) isel = 0;
+  if (store && l16 < topk) {
+    w_out[l16] = p;
+    id_out[l16] = isel;
+  }
+}
+
+constexpr int R16 = 4 * RW;        // rows a workgroup of the 16-lane top-k routes
+
+// The 16-lane top-k over the rows: R16 rows a workgroup, rows past M clamp their loads and store nothing.
+template <int NP>
+__global__ void __launch_bounds__(RW * WAVE) topk16_kernel(const uint16_t* __restrict__ logits, int ldl,
+                                                           float* __restrict__ weights, int* __restrict__ ids, int M,
+                                                           int E, int topk, int renorm) {
+  const int lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
+  const int r0 = (int)blockIdx.x * R16 + wave * 4;
+  if (r0 >= M) return;
+  const int r = r0 + (lane >> 4), rc = r < M ? r : M - 1;
+  topk_row16<NP>(logits + (size_t)rc * ldl, E, topk, renorm != 0, weights + (size_t)rc * topk,
+                 ids + (size_t)rc * topk, r < M, lane);
+}
+
+// topk16_kernel and the per-token fp8 quant in one launch: the first ceil(M / R16) workgroups route R16 rows each
+// (four rows a wave), the rest quantise eight rows each (one a wave, quant_row_wave). The long VALU-bound routing
+// workgroups are dispatched first, one or so a CU, and the HBM-bound quant workgroups fill the CUs around them.
+template <int NP, int R>
+__global__ void __launch_bounds__(RW * WAVE) topk16_quant_kernel(const uint16_t* __restrict__ logits, int ldl,
+                                                                 float* __restrict__ weights, int* __restrict__ ids,
+                                                                 int M, int E, int topk, int renorm,
+                                                                 const uint16_t* __restrict__ x, long ldx, int H,
+                                                                 uint8_t* __restrict__ xq, float* __restrict__ xs) {
+  const int lane = threadIdx.x % WAVE, wave = threadIdx.x / WAVE;
+  const int nroute = (M + R16 - 1) / R16;
+  if ((int)blockIdx.x < nroute) {
+    const int r0 = (int)blockIdx.x * R16 + wave * 4;
+    if (r0 >= M) return;
+    const int r = r0 + (lane >> 4), rc = r < M ? r : M - 1;
+    topk_row16<NP>(logits + (size_t)rc * ldl, E, topk, renorm != 0, weights + (size_t)rc * topk,
+                   ids + (size_t)rc * topk, r < M, lane);
+  } else {
+    const int r = ((int)blockIdx.x - nroute) * RW + wave;
+    if (r >= M) return;
+    quant_row_wave<R>(x + (size_t)r * ldx, H, xq + (size_t)r * H, xs + r, lane);
+  }
+}
+
 // Tables from ids in global memory, one workgroup, numel <= SMALL_MAX.
 __global__ void __launch_bounds__(AT) align_single_kernel(const int* __restrict__ ids, int numel, int E, int blk,
                                                           int* __restrict__ sorted_ids, int* __restrict__ expert_ids,
@@ -661,8 +787,32 @@ int epl_for(int E) {
   return -1;
 }
 
+// Dwords of logits a lane of the 16-lane top-k holds for E experts (E even, at most 512; 0 = not served: the
+// one-row-a-wave kernels run instead).
+int np16_for(const void* logits, int ldl, int E) {
+  if (E % 2 || E > 512 || (reinterpret_cast<uintptr_t>(logits) & 3) || (ldl & 1)) return 0;
+  const int need = (E + 31) / 32;
+  for (int v : {2, 4, 8, 9, 12, 16})
+    if (need <= v) return v;
+  return 0;
+}
+
 int launch_topk(const uint16_t* logits, int ldl, float* w, int* ids, int M, int E, int topk, int renorm,
                 hipStream_t st) {
+  if (const int np = np16_for(logits, ldl, E)) {
+    const dim3 grid16((M + R16 - 1) / R16), block16(RW * WAVE);
+#define TK16(NPV) hipLaunchKernelGGL(topk16_kernel<NPV>, grid16, block16, 0, st, logits, ldl, w, ids, M, E, topk, renorm)
+    switch (np) {
+      case 2: TK16(2); break;
+      case 4: TK16(4); break;
+      case 8: TK16(8); break;
+      case 9: TK16(9); break;
+      case 12: TK16(12); break;
+      default: TK16(16); break;
+    }
+#undef TK16
+    return 0;
+  }
   const dim3 grid((M + RW - 1) / RW), block(RW * WAVE);
 #define TK(EPLV) hipLaunchKernelGGL(topk_kernel<EPLV>, grid, block, 0, st, logits, ldl, w, ids, M, E, topk, renorm)
   switch (epl_for(E)) {
@@ -905,6 +1055,31 @@ extern "C" int r9k_moe_topk_quant(long logits, int ldl, long weights, long ids, 
   const int R = nv <= 1 ? 1 : nv <= 2 ? 2 : nv <= 4 ? 4 : 8;
   const dim3 grid(2 * ((M + RW - 1) / RW)), block(RW * WAVE);
   const hipStream_t st = (hipStream_t)stream;
+  if (const int np = np16_for((const void*)logits, ldl, E)) {
+    const dim3 grid16((M + R16 - 1) / R16 + (M + RW - 1) / RW);
+#define TQ16(NPV, RV)                                                                                              \
+  hipLaunchKernelGGL((topk16_quant_kernel<NPV, RV>), grid16, block, 0, st, (const uint16_t*)logits, ldl,          \
+                     (float*)weights, (int*)ids, M, E, topk, renorm, (const uint16_t*)x, ldx, H, (uint8_t*)xq,      \
+                     (float*)xs)
+#define TQ16R(NPV)                  \
+  switch (R) {                      \
+    case 1: TQ16(NPV, 1); break;    \
+    case 2: TQ16(NPV, 2); break;    \
+    case 4: TQ16(NPV, 4); break;    \
+    default: TQ16(NPV, 8); break;   \
+  }
+    switch (np) {
+      case 2: TQ16R(2); break;
+      case 4: TQ16R(4); break;
+      case 8: TQ16R(8); break;
+      case 9: TQ16R(9); break;
+      case 12: TQ16R(12); break;
+      default: TQ16R(16); break;
+    }
+#undef TQ16R
+#undef TQ16
+    return (int)hipGetLastError();
+  }
 #define TQ(EPLV, RV)                                                                                              \
   hipLaunchKernelGGL((topk_quant_kernel<EPLV, RV>), grid, block, 0, st, (const uint16_t*)logits, ldl,            \
                      (float*)weights, (int*)ids, M, E, topk, renorm, (const uint16_t*)x, ldx, H, (uint8_t*)xq,      \

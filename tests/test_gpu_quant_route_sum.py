@@ -274,6 +274,37 @@ def test_moe_route_degenerate_rows(dev):
         check_tables(s_[:cap].cpu().numpy(), e_[:cap // blk].cpu().numpy(), n_.cpu().numpy(), ido, blk, M * tk, Ed)
 
 
+@pytest.mark.parametrize("M,E,topk", [(37, 512, 16), (70, 288, 8), (33, 384, 8), (5, 100, 10), (64, 48, 6),
+                                      (40, 256, 8), (19, 160, 4), (9, 7, 2), (11, 1024, 8), (1, 2, 2)])
+def test_moe_topk_degenerate_rows(dev, M, E, topk):
+    """moe_topk (the wide launches' top-k: four rows a wave for even E <= 512, else one row a wave) and the fused
+    top-k + quant on NaN, +-inf, all-equal, zero and -3e38 rows and M not a multiple of the rows a workgroup
+    routes: ids equal the oracle's, weights within 2e-6, and the two launches agree bit for bit."""
+    print(f"topk degenerate M={M} E={E} topk={topk}", flush=True)
+    g = torch.Generator().manual_seed(M * 1000 + E)
+    x = torch.randn(M, E, generator=g) * 2
+    for r, fill in enumerate([float("nan"), None, float("inf"), float("-inf"), 0.0, 1.0, None, -3e38]):
+        if r >= M:
+            break
+        if r == 1:
+            x[1, : min(5, E)] = float("nan")
+        elif r == 6:
+            x[6, ::2] = float("inf")
+        else:
+            x[r] = fill
+    xb = x.to(torch.bfloat16)
+    w, ids = K.moe_topk(xb.to(dev), topk, True)
+    wo, ido = O.route(xb, topk, True)
+    assert np.array_equal(ids.cpu().numpy(), ido)
+    assert np.isfinite(w.cpu().numpy()).all() and np.abs(w.cpu().numpy() - wo).max() < 2e-6
+    xa = (torch.randn(M, 256, generator=g)).to(torch.bfloat16).to(dev)
+    r = K.moe_topk_quant(xb.to(dev), topk, True, xa)
+    assert r is not None
+    assert torch.equal(r[1], ids) and torch.equal(r[0], w)
+    q, s = K.quant_rows_fp8(xa)
+    assert torch.equal(r[2].view(torch.uint8), q.view(torch.uint8)) and torch.equal(r[3], s)
+
+
 def test_moe_route_large_m_path(dev):
     """numel above the one-workgroup limit: top-k kernel + single-workgroup table launch."""
     M, E, topk, blk = 1024, 288, 8, 64
