@@ -94,6 +94,14 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
   return v;
 }
 
+// Chunk c of a row of nvec 16-byte chunks (nvec >= 1), zero past the row. The load always goes out, to an in-range
+// chunk, and the zero is a select after it: a load under a branch is waited for inside that branch, which would
+// serialise a lane's chunk loads instead of keeping them in flight together.
+__device__ __forceinline__ uint4 load_chunk_or_zero(const uint4* __restrict__ row, int c, int nvec) {
+  const uint4 t = row[c < nvec ? c : nvec - 1];
+  return c < nvec ? t : make_uint4(0u, 0u, 0u, 0u);
+}
+
 // bf16 halves of a packed 32-bit word as fp32.
 __device__ __forceinline__ float lo16(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float hi16(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
@@ -175,7 +183,7 @@ __device__ __forceinline__ void quant_row_wave(const uint16_t* __restrict__ xrow
 #pragma unroll
   for (int i = 0; i < RMAX; i++) {
     const int c = lane + i * WAVE;
-    v[i] = c < nvec ? xr[c] : make_uint4(0u, 0u, 0u, 0u);
+    v[i] = load_chunk_or_zero(xr, c, nvec);
   }
   uint32_t mm = 0u;
 #pragma unroll
@@ -273,8 +281,8 @@ __device__ __forceinline__ void load_gate_up_row(const uint16_t* __restrict__ gr
 #pragma unroll
   for (int i = 0; i < R; i++) {
     const int c = lane + i * WAVE;
-    gv[i] = c < nvec ? gr[c] : make_uint4(0u, 0u, 0u, 0u);
-    uv[i] = c < nvec ? ur[c] : make_uint4(0u, 0u, 0u, 0u);
+    gv[i] = load_chunk_or_zero(gr, c, nvec);
+    uv[i] = load_chunk_or_zero(ur, c, nvec);
   }
 }
 

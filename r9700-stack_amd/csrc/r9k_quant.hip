@@ -45,7 +45,7 @@ __global__ void __launch_bounds__(WR * WAVE) quant_rows_wave_kernel(const uint16
 #pragma unroll
   for (int i = 0; i < R; i++) {
     const int c = lane + i * WAVE;
-    v[i] = c < nvec ? xr[c] : make_uint4(0u, 0u, 0u, 0u);
+    v[i] = load_chunk_or_zero(xr, c, nvec);
   }
 #pragma unroll
   for (int i = 0; i < R; i++) {
@@ -54,12 +54,11 @@ __global__ void __launch_bounds__(WR * WAVE) quant_rows_wave_kernel(const uint16
     for (int j = 0; j < 4; j++) m = fmaxf(m, fmaxf(fabsf(lo16(w[j])), fabsf(hi16(w[j]))));
     if constexpr (GATE) {
       const int c = lane + i * WAVE;
-      if (c < nvec) {
-        const uint4 gw = reinterpret_cast<const uint4*>(wg)[c];
-        const uint32_t u[4] = {gw.x, gw.y, gw.z, gw.w};
+      // chunks past the row are zero on both sides: their +0 terms leave the bf16 logit and its sigmoid as they are
+      const uint4 gw = load_chunk_or_zero(reinterpret_cast<const uint4*>(wg), c, nvec);
+      const uint32_t u[4] = {gw.x, gw.y, gw.z, gw.w};
 #pragma unroll
-        for (int j = 0; j < 4; j++) dot += lo16(w[j]) * lo16(u[j]) + hi16(w[j]) * hi16(u[j]);
-      }
+      for (int j = 0; j < 4; j++) dot += lo16(w[j]) * lo16(u[j]) + hi16(w[j]) * hi16(u[j]);
     }
   }
   const float amax = fmaxf(wave_max(m), 1e-12f);
@@ -95,17 +94,16 @@ __global__ void __launch_bounds__(QT) quant_rows_vec_kernel(const uint16_t* __re
 #pragma unroll
   for (int i = 0; i < QR; i++) {
     const int c = tid + i * QT;
-    v[i] = c < nvec ? xr[c] : make_uint4(0u, 0u, 0u, 0u);
+    v[i] = load_chunk_or_zero(xr, c, nvec);
     const uint32_t w[4] = {v[i].x, v[i].y, v[i].z, v[i].w};
 #pragma unroll
     for (int j = 0; j < 4; j++) m = fmaxf(m, fmaxf(fabsf(lo16(w[j])), fabsf(hi16(w[j]))));
     if constexpr (GATE) {
-      if (c < nvec) {
-        const uint4 gw = reinterpret_cast<const uint4*>(wg)[c];
-        const uint32_t u[4] = {gw.x, gw.y, gw.z, gw.w};
+      // chunks past the row are zero on both sides: their +0 terms leave the bf16 logit and its sigmoid as they are
+      const uint4 gw = load_chunk_or_zero(reinterpret_cast<const uint4*>(wg), c, nvec);
+      const uint32_t u[4] = {gw.x, gw.y, gw.z, gw.w};
 #pragma unroll
-        for (int j = 0; j < 4; j++) dot += lo16(w[j]) * lo16(u[j]) + hi16(w[j]) * hi16(u[j]);
-      }
+      for (int j = 0; j < 4; j++) dot += lo16(w[j]) * lo16(u[j]) + hi16(w[j]) * hi16(u[j]);
     }
   }
   const float rmax = block_max<QT>(m, sh);

@@ -19,12 +19,10 @@ __device__ __forceinline__ void load_row_group(const uint16_t* __restrict__ x, l
                                                int tid, uint4 (&v)[MG][XC]) {
 #pragma unroll
   for (int m = 0; m < MG; m++) {
-    const uint4* xr = reinterpret_cast<const uint4*>(x + (size_t)(m0 + m) * ldx);
+    const bool live = m0 + m < M;                    // rows past M read row M - 1 and keep zeros
+    const uint4* xr = reinterpret_cast<const uint4*>(x + (size_t)(live ? m0 + m : M - 1) * ldx);
 #pragma unroll
-    for (int i = 0; i < XC; i++) {
-      const int c = tid + i * T;
-      v[m][i] = (m0 + m < M && c < nvec) ? xr[c] : make_uint4(0u, 0u, 0u, 0u);
-    }
+    for (int i = 0; i < XC; i++) v[m][i] = load_chunk_or_zero(xr, live ? tid + i * T : nvec, nvec);
   }
 }
 

@@ -30,16 +30,27 @@ __device__ __forceinline__ void zero_counts(TabLds<NT>& sh, int E) {
   for (int i = threadIdx.x; i < TabLds<NT>::NW * TAB_MAX_E / 2; i += NT) p[i] = 0u;
 }
 
+// Block arithmetic of the table builders: rows rounded up to whole blocks and positions in blocks, by shifts and
+// masks for the powers of two every routing entry requires (P2), by integer division for the other block sizes the
+// expert cache's entries accept. The builders dispatch once on the block size (wave-uniform).
+template <bool P2>
+struct Blocks {
+  int blk, lb;
+  __device__ __forceinline__ explicit Blocks(int b) : blk(b), lb(P2 ? __builtin_ctz((unsigned)b) : 0) {}
+  __device__ __forceinline__ int up(int v) const { return P2 ? (v + blk - 1) & -blk : (v + blk - 1) / blk * blk; }
+  __device__ __forceinline__ int div(int v) const { return P2 ? v >> lb : v / blk; }
+};
+
 // Exclusive scan of the block-padded counts: offs[], returns the padded total. Thread t covers the experts
 // [t * ept, t * ept + ept), ept = ceil(E / NT) (one expert a thread while E <= NT), so offsets ascend with the expert.
-template <int NT>
-__device__ __forceinline__ int padded_scan(TabLds<NT>& sh, int E, int blk) {
+template <int NT, bool P2>
+__device__ __forceinline__ int padded_scan_impl(TabLds<NT>& sh, int E, const Blocks<P2> bk) {
   constexpr int NW = NT / WAVE;
   const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
   const int ept = (E + NT - 1) / NT;
   const int e0 = min(tid * ept, E), e1 = min(e0 + ept, E);
   int n = 0;
-  for (int e = e0; e < e1; e++) n += (sh.cnt[e] + blk - 1) / blk * blk;
+  for (int e = e0; e < e1; e++) n += bk.up(sh.cnt[e]);
   int x = n;
 #pragma unroll
   for (int o = 1; o < WAVE; o <<= 1) {
@@ -57,31 +68,45 @@ __device__ __forceinline__ int padded_scan(TabLds<NT>& sh, int E, int blk) {
   int o = wbase + x - n;
   for (int e = e0; e < e1; e++) {
     sh.offs[e] = o;
-    o += (sh.cnt[e] + blk - 1) / blk * blk;
+    o += bk.up(sh.cnt[e]);
   }
   lds_barrier();
   return total;
+}
+
+template <int NT>
+__device__ __forceinline__ int padded_scan(TabLds<NT>& sh, int E, int blk) {
+  if ((blk & (blk - 1)) == 0) return padded_scan_impl<NT, true>(sh, E, Blocks<true>(blk));
+  return padded_scan_impl<NT, false>(sh, E, Blocks<false>(blk));
 }
 
 // Expert blocks and padding entries of the experts e < E with e % nshare == share, every expert's cursor at its
 // first slot plus `pre` (the calling thread's expert's rows in earlier chunks), and this share's part of the
 // capacity tail: sorted_ids up to `cap` entries, expert_ids up to `cap_blocks` (cap < 0: this library's capacity,
 // ceil((numel + E (blk - 1)) / blk) * blk entries and cap / blk blocks). Ends with an LDS barrier.
-template <int NT>
-__device__ __forceinline__ void write_layout(TabLds<NT>& sh, int E, int blk, int numel, int total, int pre,
-                                             int share, int nshare, int* __restrict__ sorted_ids,
-                                             int* __restrict__ expert_ids, bool write_tail = true, long cap = -1,
-                                             long cap_blocks = -1) {
+template <int NT, bool P2>
+__device__ __forceinline__ void write_layout_impl(TabLds<NT>& sh, int E, const Blocks<P2> bk, int numel, int total,
+                                                  int pre, int share, int nshare, int* __restrict__ sorted_ids,
+                                                  int* __restrict__ expert_ids, bool write_tail, long cap,
+                                                  long cap_blocks) {
   constexpr int NW = NT / WAVE;
   const int tid = threadIdx.x, wave = tid / WAVE, lane = tid % WAVE;
   for (int e = tid; e < E; e += NT) sh.cursor[e] = sh.offs[e] + (e == tid ? pre : 0);   // pre: callers with E <= NT
-  // a wave per expert of the share: its block ids and its padding entries (up to blk - 1) written by the wave's lanes
-  for (int e = share + wave * nshare; e < E; e += NW * nshare) {
-    const int c = sh.cnt[e], o = sh.offs[e];
-    if (c > 0) {
-      const int n = ((c + blk - 1) / blk) * blk;
-      for (int b = o / blk + lane; b < (o + n) / blk; b += WAVE) expert_ids[b] = e;
-      for (int i = o + c + lane; i < o + n; i += WAVE) sorted_ids[i] = numel;
+  // a wave per expert of the share: its block ids and its padding entries (up to blk - 1) written by the wave's lanes.
+  // The wave's experts are e_j = share + (wave + NW j) nshare; lane j % 64 fetches e_j's count and offset for a pass
+  // of 64 of them, so the loop over the experts waits on no LDS read.
+  const int stride = NW * nshare;
+  for (int e0 = share + wave * nshare; e0 < E; e0 += WAVE * stride) {
+    const int el = e0 + lane * stride;
+    const int cl = el < E ? sh.cnt[el] : 0, ol = el < E ? sh.offs[el] : 0;
+    for (int j = 0; j < WAVE && e0 + j * stride < E; j++) {
+      const int e = e0 + j * stride;
+      const int c = __builtin_amdgcn_readlane(cl, j), o = __builtin_amdgcn_readlane(ol, j);
+      if (c > 0) {
+        const int n = bk.up(c);
+        for (int b = bk.div(o) + lane; b < bk.div(o + n); b += WAVE) expert_ids[b] = e;
+        for (int i = o + c + lane; i < o + n; i += WAVE) sorted_ids[i] = numel;
+      }
     }
   }
   if (!write_tail) {                            // live entries only: the capacity past ntpp is left as it was
@@ -89,16 +114,30 @@ __device__ __forceinline__ void write_layout(TabLds<NT>& sh, int E, int blk, int
     return;
   }
   if (cap < 0) {
-    cap = ((long)numel + (long)E * (blk - 1) + blk - 1) / blk * blk;
-    cap_blocks = cap / blk;
+    const long raw = (long)numel + (long)E * (bk.blk - 1) + bk.blk - 1;
+    cap = P2 ? raw & ~(long)(bk.blk - 1) : raw / bk.blk * bk.blk;
+    cap_blocks = P2 ? cap >> bk.lb : cap / bk.blk;
   }
-  const long tail = cap - total, per = (tail + nshare - 1) / nshare;
+  const long tail = cap - total, per = nshare == 1 ? tail : (tail + nshare - 1) / nshare;
   const long i1 = min(cap, total + (long)(share + 1) * per);
   for (long i = total + (long)share * per + tid; i < i1; i += NT) sorted_ids[i] = numel;
-  const long btail = cap_blocks - total / blk, bper = (btail + nshare - 1) / nshare;
-  const long b1 = min(cap_blocks, total / blk + (long)(share + 1) * bper);
-  for (long b = total / blk + (long)share * bper + tid; b < b1; b += NT) expert_ids[b] = -1;
+  const long b0 = bk.div(total), btail = cap_blocks - b0, bper = nshare == 1 ? btail : (btail + nshare - 1) / nshare;
+  const long b1 = min(cap_blocks, b0 + (long)(share + 1) * bper);
+  for (long b = b0 + (long)share * bper + tid; b < b1; b += NT) expert_ids[b] = -1;
   lds_barrier();
+}
+
+template <int NT>
+__device__ __forceinline__ void write_layout(TabLds<NT>& sh, int E, int blk, int numel, int total, int pre,
+                                             int share, int nshare, int* __restrict__ sorted_ids,
+                                             int* __restrict__ expert_ids, bool write_tail = true, long cap = -1,
+                                             long cap_blocks = -1) {
+  if ((blk & (blk - 1)) == 0)
+    write_layout_impl<NT, true>(sh, E, Blocks<true>(blk), numel, total, pre, share, nshare, sorted_ids, expert_ids,
+                                write_tail, cap, cap_blocks);
+  else
+    write_layout_impl<NT, false>(sh, E, Blocks<false>(blk), numel, total, pre, share, nshare, sorted_ids,
+                                 expert_ids, write_tail, cap, cap_blocks);
 }
 
 // The lanes of this wave whose id equals this lane's (ids in [0, 2^nbits), -1 = none): the valid lanes ANDed with,
@@ -134,8 +173,13 @@ __device__ __forceinline__ void stable_round(TabLds<NT>& sh, const short* ids, i
   if (e >= 0 && rank == cw - 1) sh.wcnt[wave][e] = (uint16_t)cw;     // the last of its expert in this wave
   lds_barrier();
   if (e >= 0) {
+    // the rows of earlier waves: every wave's count read at once (independent LDS reads), those below this wave added
     int pos = sh.cursor[e] + rank;
-    for (int w = 0; w < wave; w++) pos += sh.wcnt[w][e];
+    int c[NW];
+#pragma unroll
+    for (int w = 0; w < NW - 1; w++) c[w] = sh.wcnt[w][e];
+#pragma unroll
+    for (int w = 0; w < NW - 1; w++) pos += w < wave ? c[w] : 0;
     sorted_ids[pos] = row0 + t;
   }
   lds_barrier();
