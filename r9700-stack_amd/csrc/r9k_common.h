@@ -173,18 +173,18 @@ __device__ __forceinline__ float silu_mul(float gv, float uv) {
 // Each lane keeps its 16-byte chunks (lane + 64 i) in registers, so the row is read once. The row maximum is taken
 // on the bf16 magnitude bits (two values an instruction); a finite maximum is the float one exactly and lets every
 // code skip the range check. A row holding inf or NaN takes the float maximum, which passes over NaN, and the checked
-// conversion.
+// conversion. quant_row_load / quant_row_finish are the two halves, for callers that issue the row's loads early.
 template <int RMAX>
-__device__ __forceinline__ void quant_row_wave(const uint16_t* __restrict__ xrow, int K, uint8_t* __restrict__ qrow,
-                                               float* __restrict__ s_out, int lane) {
+__device__ __forceinline__ void quant_row_load(const uint16_t* __restrict__ xrow, int K, int lane, uint4 (&v)[RMAX]) {
   const uint4* xr = reinterpret_cast<const uint4*>(xrow);
-  const int nvec = K / 8;
-  uint4 v[RMAX];
 #pragma unroll
-  for (int i = 0; i < RMAX; i++) {
-    const int c = lane + i * WAVE;
-    v[i] = load_chunk_or_zero(xr, c, nvec);
-  }
+  for (int i = 0; i < RMAX; i++) v[i] = load_chunk_or_zero(xr, lane + i * WAVE, K / 8);
+}
+
+template <int RMAX>
+__device__ __forceinline__ void quant_row_finish(const uint4 (&v)[RMAX], int K, uint8_t* __restrict__ qrow,
+                                                 float* __restrict__ s_out, int lane) {
+  const int nvec = K / 8;
   uint32_t mm = 0u;
 #pragma unroll
   for (int i = 0; i < RMAX; i++) {
@@ -221,6 +221,15 @@ __device__ __forceinline__ void quant_row_wave(const uint16_t* __restrict__ xrow
     const int c = lane + i * WAVE;
     if (c < nvec) qr[c] = pack8_bf16_e4m3(v[i], inv);
   }
+}
+
+// quant_row_load then quant_row_finish: the row's chunks, all in flight together, then the quant.
+template <int RMAX>
+__device__ __forceinline__ void quant_row_wave(const uint16_t* __restrict__ xrow, int K, uint8_t* __restrict__ qrow,
+                                               float* __restrict__ s_out, int lane) {
+  uint4 v[RMAX];
+  quant_row_load<RMAX>(xrow, K, lane, v);
+  quant_row_finish<RMAX>(v, K, qrow, s_out, lane);
 }
 
 // The two halves of silu_quant_chunks, for callers that convert several rows at once and interleave their wave

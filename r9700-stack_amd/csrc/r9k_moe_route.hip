@@ -203,9 +203,16 @@ __global__ void __launch_bounds__(FT) route_fused_kernel(const uint16_t* __restr
   const int wave = threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
   const int numel = M * topk;
   const bool single = gridDim.x == 1;
-  auto quant_rows = [&]() {
+  // the input quant of this workgroup's rows; `pre`: the first row's chunks are already in xpre
+  uint4 xpre[R > 0 ? R : 1];
+  auto quant_rows = [&](bool pre) {
     if constexpr (R > 0) {
-      for (int r = blockIdx.x * FW + wave; r < M; r += gridDim.x * FW)
+      int r = blockIdx.x * FW + wave;
+      if (pre && r < M) {
+        quant_row_finish<R>(xpre, ex.H, ex.xq + (size_t)r * ex.H, ex.xs + r, lane);
+        r += gridDim.x * FW;
+      }
+      for (; r < M; r += gridDim.x * FW)
         quant_row_wave<R>(ex.x + (size_t)r * ex.ldx, ex.H, ex.xq + (size_t)r * ex.H, ex.xs + r, lane);
     }
   };
@@ -223,10 +230,13 @@ __global__ void __launch_bounds__(FT) route_fused_kernel(const uint16_t* __restr
       s_last = __hip_atomic_fetch_add(arrive, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (int)gridDim.x - 1;
     lds_barrier();
     if (!s_last) {
-      quant_rows();
+      quant_rows(false);
       return;
     }
     if (threadIdx.x == 0) __hip_atomic_store(arrive, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if constexpr (R > 0) {                                      // this workgroup's first rows: loads out before the build
+      if (blockIdx.x * FW + wave < M) quant_row_load<R>(ex.x + (size_t)(blockIdx.x * FW + wave) * ex.ldx, ex.H, lane, xpre);
+    }
     for (int t0 = 0; t0 < numel; t0 += 8 * FT) {                // other workgroups' ids, past this CU's caches
       int v[8];
 #pragma unroll
@@ -260,7 +270,7 @@ __global__ void __launch_bounds__(FT) route_fused_kernel(const uint16_t* __restr
   }
   if (big) build_from_counts(sh, lids, numel, E, ex.big_blk, ex.sorted_big, ex.expert_big, ex.ntpp_big, false);
   else build_from_counts(sh, lids, numel, E, blk, sorted_ids, expert_ids, ntpp);
-  quant_rows();
+  quant_rows(!single);
 }
 
 // ------------------------------------------------------------------ small batches: M <= 64 rows in one workgroup
