@@ -164,6 +164,39 @@ def test_manage_tables_one_launch_equals_composed(dev, E, S, thresh, max_ins, M,
             assert bool((ta[3] == -7).all()) and bool((ta[5] == -7).all()), step
 
 
+@pytest.mark.parametrize("blk", [24, 48])
+def test_manage_tables_block_not_power_of_two(dev, blk):
+    """The one-launch manage + tables at a block size that is not a power of two (the entry accepts any; the routing
+    entries require powers of two, so this is the table builders' division path): the resident pass's tables over the
+    whole capacity equal the oracle's align of the slot ids the launch wrote, bit for bit, over several steps."""
+    print(f"manage+tables blk={blk}", flush=True)
+    E, S, max_ins, M, k = 288, 64, 64, 16, 8
+    rng = np.random.default_rng(blk)
+    a = DevState(dev, E, S, max_ins)
+    L = C._L()
+    s_ = torch.cuda.current_stream().cuda_stream
+    i32 = dict(dtype=torch.int32, device=dev)
+    for step in range(6):
+        ids = torch.from_numpy(np.stack([rng.choice(E, size=k, replace=False) for _ in range(M)])
+                               .reshape(-1).astype(np.int32)).to(dev)
+        mk = ids.numel()
+        cap = K.capacity(mk, E, blk)
+        ta = [torch.full((cap,), -7, **i32), torch.full((cap // blk,), -7, **i32), torch.full((1,), -7, **i32)]
+        hot_out = torch.full((mk,), -7, **i32)
+        rc = L.r9k_lru_manage_tables(ids.data_ptr(), mk, E, S, S, max_ins, a.table.data_ptr(),
+                                     a.map_cold.data_ptr(), a.slot_expert.data_ptr(), a.slot_stamp.data_ptr(),
+                                     a.routed.data_ptr(), a.step.data_ptr(), a.miss.data_ptr(), a.n_miss.data_ptr(),
+                                     blk, ta[0].data_ptr(), ta[1].data_ptr(), ta[2].data_ptr(), 0, 0, 0,
+                                     hot_out.data_ptr(), s_)
+        assert rc == 0, rc
+        torch.cuda.synchronize()
+        so, eo, no = O.align(hot_out.cpu().numpy(), E, blk)
+        assert so.size == cap, (so.size, cap)
+        assert np.array_equal(ta[0].cpu().numpy(), so), step
+        assert np.array_equal(ta[1].cpu().numpy(), eo), step
+        assert int(ta[2].item()) == int(no[0]), step
+
+
 def test_r4d_lru_fused_reference_sizing(dev):
     """The reference's entry with vLLM's table lengths (L = min(mk * bs, mk + E (bs - 1)) while mk < E): the tables
     equal this library's over their first L / NB entries and nothing past L / NB is written; E > 1024 is not served
