@@ -37,7 +37,10 @@ constexpr int APAD = 16;          // bytes of padding per LDS code row (row stri
 
 // LDS: codes [M][K + APAD] (fp8), row scales [MAXM] fp32, partial tiles [SK][NPW][256] fp32 (sized by M, so small M
 // leaves room for several workgroups a CU).
-template <int NPW, int SK, int U, int MG>
+// DB: a wave's K range is exactly two batches of U K-tiles, and the second batch is issued right after the row
+// quant (into a second register set) instead of after the first batch is consumed, so the wave's whole weight range
+// is requested within the prologue, as a plain streaming read would request it. The MFMAs run in the same order.
+template <int NPW, int SK, int U, int MG, bool DB = false>
 __global__ void __launch_bounds__(WAVE * SK) dense_mxfp4_qa_kernel(
     const uint16_t* __restrict__ x, long ldx, const uint8_t* __restrict__ Wq, const uint8_t* __restrict__ Ws,
     uint16_t* __restrict__ out, long ldo, int M, int N, int K) {
@@ -60,37 +63,37 @@ __global__ void __launch_bounds__(WAVE * SK) dense_mxfp4_qa_kernel(
   }
   const int kt0 = wave * nkt / SK, kt1 = (wave + 1) * nkt / SK;
 
-  u32x4 bf[U][NPW];
-  uint32_t sb[U][NPW];
-  auto issue = [&](int kb) {
+  u32x4 bf[U][NPW], bf2[DB ? U : 1][NPW];
+  uint32_t sb[U][NPW], sb2[DB ? U : 1][NPW];
+  auto issue = [&](int kb, auto& bq, auto& sq) {
 #pragma unroll
     for (int u = 0; u < U; u++) {
       const int k = min(kb + u, kt1 - 1);
 #pragma unroll
       for (int j = 0; j < NPW; j++) {
-        bf[u][j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wtile[j] + (size_t)k * 1024));
-        sb[u][j] = __builtin_nontemporal_load(stile[j] + k * 64);
+        bq[u][j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wtile[j] + (size_t)k * 1024));
+        sq[u][j] = __builtin_nontemporal_load(stile[j] + k * 64);
       }
     }
   };
   // the activation rows' reads (M <= MG), then the first batch of weight loads, then the rows' quant (whose latency
-  // the weight loads overlap)
+  // the weight loads overlap); with DB the second batch follows the quant
   {
     constexpr int T = WAVE * SK, XC = row_chunks<T>();
     const int nvec = K / 8;
     uint4 xv[MG][XC];
     load_row_group<T, MG, XC>(x, ldx, 0, M, nvec, tid, xv);
-    issue(kt0);
+    issue(kt0, bf, sb);
     quant_row_group<T, MG, XC>(xv, 0, M, nvec, A, lda, s_row, red, tid);
   }
+  if constexpr (DB) issue(kt0 + U, bf2, sb2);
 
   v4f acc[NPW];
 #pragma unroll
   for (int j = 0; j < NPW; j++) acc[j] = (v4f){0.f, 0.f, 0.f, 0.f};
   const bool arow = r < M;
   const uint8_t* ar = A + (size_t)(arow ? r : 0) * lda + 16 * g;
-  for (int kb = kt0; kb < kt1; kb += U) {
-    if (kb != kt0) issue(kb);
+  auto consume = [&](int kb, const auto& bq, const auto& sq) {
 #pragma unroll
     for (int u = 0; u < U; u++) {
       const int k = kb + u;
@@ -101,10 +104,19 @@ __global__ void __launch_bounds__(WAVE * SK) dense_mxfp4_qa_kernel(
         const v8i a = (v8i){(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
 #pragma unroll
         for (int j = 0; j < NPW; j++) {
-          const v8i b = (v8i){(int)bf[u][j].x, (int)bf[u][j].y, (int)bf[u][j].z, (int)bf[u][j].w, 0, 0, 0, 0};
-          acc[j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, acc[j], 0, 4, 0, E8M0_ONE, 0, (int)sb[u][j]);
+          const v8i b = (v8i){(int)bq[u][j].x, (int)bq[u][j].y, (int)bq[u][j].z, (int)bq[u][j].w, 0, 0, 0, 0};
+          acc[j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, acc[j], 0, 4, 0, E8M0_ONE, 0, (int)sq[u][j]);
         }
       }
+    }
+  };
+  if constexpr (DB) {
+    consume(kt0, bf, sb);
+    consume(kt0 + U, bf2, sb2);
+  } else {
+    for (int kb = kt0; kb < kt1; kb += U) {
+      if (kb != kt0) issue(kb, bf, sb);
+      consume(kb, bf, sb);
     }
   }
 
@@ -247,9 +259,24 @@ extern "C" int r9k_dense_mxfp4_qa(long x, long ldx, long wq, long ws, long out, 
   // measured 20.2 us against 14.2 us in two batches of 5)
   const int U = env_int("R9K_DENSE_U", per <= 4 ? 4 : (per <= 5 ? 5 : (per <= 8 ? 4 : (per <= 10 ? 5 : 8))));
   const int MG = M == 1 ? 1 : (M == 2 ? 2 : 4);
+  // both batches of a two-batch K range issued in the prologue (R9K_DENSE_DB=0: one batch after the other)
+  static const bool db_on = env_int("R9K_DENSE_DB", 1) != 0;
+  const bool DB = db_on && per == 2 * U && SK == 4 && U == 5 && ((NPW == 1 && MG == 1) || (NPW == 2 && MG == 2));
   const size_t smem = (size_t)M * (K + APAD) + MAXM * sizeof(float) + (size_t)SK * NPW * 256 * sizeof(float);
   const dim3 grid((NT + NPW - 1) / NPW), block(WAVE * SK);
   const hipStream_t st = (hipStream_t)stream;
+#define DQB(NPWv, MGv)                                                                                             \
+  if (DB && NPW == NPWv && MG == MGv) {                                                                            \
+    static const hipError_t a = hipFuncSetAttribute(                                                               \
+        reinterpret_cast<const void*>(dense_mxfp4_qa_kernel<NPWv, 4, 5, MGv, true>),                               \
+        hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);                                                    \
+    if (a != hipSuccess) return -6;                                                                                \
+    hipLaunchKernelGGL((dense_mxfp4_qa_kernel<NPWv, 4, 5, MGv, true>), grid, block, smem, st, (const uint16_t*)x,  \
+                       ldx, (const uint8_t*)wq, (const uint8_t*)ws, (uint16_t*)out, ldo, M, N, K);                 \
+    return hipGetLastError() == hipSuccess ? 0 : -6;                                                               \
+  }
+  DQB(1, 1) DQB(2, 2)
+#undef DQB
 #define DQ(NPWv, SKv, Uv, MGv)                                                                                     \
   if (NPW == NPWv && SK == SKv && U == Uv && MG == MGv) {                                                          \
     static const hipError_t a = hipFuncSetAttribute(                                                               \
