@@ -148,8 +148,8 @@ int r9k_moe_route_dual(long logits, int ldl, long weights, long ids, long sorted
 
 /* Align tables only, from ids int32 [numel] (the role of vLLM's moe_align_block_size, called at
  * r9700_vllm/moe/experts.py:172 of the reference). ids outside [0, E) are left out. scratch: at least
- * r9k_moe_align_scratch_ints(numel, E) int32, zeroed once by the caller: an arrival counter (left zero by every
- * call) and the per-chunk histograms (rewritten by every call); calls sharing one scratch must not overlap. */
+ * r9k_moe_align_scratch_ints(numel, E) int32: the per-chunk histograms of the multi-workgroup path (rewritten by
+ * every call, so its contents at entry do not matter); calls sharing one scratch must not overlap. */
 int r9k_moe_align(long ids, int numel, int E, int blk, long sorted_ids, long expert_ids, long ntpp, long scratch,
                   long scratch_ints, long stream);
 long r9k_moe_align_scratch_ints(int numel, int E);
@@ -164,7 +164,7 @@ int r9k_moe_align_live(long ids, int numel, int E, int blk, long sorted_ids, lon
 /* No counterpart in the reference. r9k_moe_align for callers that cannot allocate (code under HIP graph capture,
  * tight serving loops, harnesses that forbid hipMalloc): no scratch argument, nothing allocated; the multi-workgroup
  * path uses the library's own file-scope device array (r9k_moe_align_noalloc_max_ints() int32 = 1 MiB per GPU, held
- * until the process ends; its arrival counter starts zero and every call leaves it zero). Every call on one GPU
+ * until the process ends; every call rewrites the histograms it reads). Every call on one GPU
  * shares that array: calls that overlap on one GPU race. Tables bit-identical to r9k_moe_align's. 0; 1 bad arguments
  * or HIP error; -9 the step needs more than r9k_moe_align_noalloc_max_ints() scratch ints (see
  * r9k_moe_align_scratch_ints); -6 the array's device address could not be obtained. */

@@ -697,22 +697,17 @@ __global__ void __launch_bounds__(AT) align_big_single_kernel(const int* __restr
   }
 }
 
-// Scratch of the multi-block align (int32): [0] the arrival counter (zero at entry, left zero), from ALIGN_HIST on
-// (nch + 2) rows of E: rows c < nch the chunks' histograms, then their bases; row nch each expert's first slot, row
-// nch + 1 its row count; then the padded total.
+// Scratch of the multi-block align (int32): from ALIGN_HIST on, nch rows of E: each chunk's per-expert histogram
+// (the first ALIGN_HIST ints are not used and stay as the caller left them, zero).
 constexpr int ALIGN_HIST = 16;
 
-// Multi-block align, pass 1 (one workgroup per chunk of CH routed rows): the chunk's per-expert histogram, stored
-// with agent-scope stores (coherent across the XCDs' L2s); after they complete each workgroup counts itself in the
-// arrival counter, and the last to arrive reads every histogram back with agent-scope loads and turns them into the
-// placement bases in place: row c = an expert's rows in chunks before c, row nch = its first slot (the padded
-// exclusive scan), row nch + 1 = its count, then the padded total, also written to ntpp.
-__global__ void __launch_bounds__(AT) align_count_kernel(const int* __restrict__ ids, int numel, int E, int blk,
-                                                         int* __restrict__ scratch, int* __restrict__ ntpp) {
+// Multi-block align, pass 1 (one workgroup per chunk of CH routed rows): the chunk's per-expert histogram, stored as
+// row c of the scratch. The next launch reads every row (a launch boundary orders them).
+__global__ void __launch_bounds__(AT) align_count_kernel(const int* __restrict__ ids, int numel, int E,
+                                                         int* __restrict__ scratch) {
   __shared__ TabLds<AT> sh;
-  __shared__ int s_last;
   int* __restrict__ hist = scratch + ALIGN_HIST;
-  const int tid = threadIdx.x, c = blockIdx.x, nch = gridDim.x;
+  const int tid = threadIdx.x, c = blockIdx.x;
   for (int e = tid; e < E; e += AT) sh.cnt[e] = 0;
   const int t0 = c * CH, t1 = min(numel, t0 + CH);
   int v[CH / AT];
@@ -723,51 +718,18 @@ __global__ void __launch_bounds__(AT) align_count_kernel(const int* __restrict__
   for (int u = 0; u < CH / AT; u++)
     if (v[u] >= 0 && v[u] < E) atomicAdd(&sh.cnt[v[u]], 1);
   lds_barrier();
-  for (int e = tid; e < E; e += AT)
-    __hip_atomic_store(hist + (size_t)c * E + e, sh.cnt[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");             // this thread's histogram stores have completed
-  lds_barrier();
-  if (tid == 0) s_last = __hip_atomic_fetch_add(scratch, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == nch - 1;
-  lds_barrier();
-  if (!s_last) return;
-  if (tid == 0) __hip_atomic_store(scratch, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  int tot = 0;
-  if (tid < E) {                                               // E <= AT: one expert a thread, 16 loads in flight
-    for (int c0 = 0; c0 < nch; c0 += 16) {
-      int h[16];
-#pragma unroll
-      for (int u = 0; u < 16; u++)
-        h[u] = c0 + u < nch
-                   ? __hip_atomic_load(hist + (size_t)(c0 + u) * E + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                   : 0;
-#pragma unroll
-      for (int u = 0; u < 16; u++)
-        if (c0 + u < nch) {
-          hist[(size_t)(c0 + u) * E + tid] = tot;
-          tot += h[u];
-        }
-    }
-    sh.cnt[tid] = tot;
-  }
-  lds_barrier();
-  const int total = padded_scan(sh, E, blk);
-  if (tid < E) {
-    hist[(size_t)nch * E + tid] = sh.offs[tid];
-    hist[(size_t)(nch + 1) * E + tid] = tot;
-  }
-  if (tid == 0) {
-    hist[(size_t)(nch + 2) * E] = total;
-    ntpp[0] = total;
-  }
+  for (int e = tid; e < E; e += AT) hist[(size_t)c * E + e] = sh.cnt[e];
 }
 
-// Multi-block align, pass 2 (one workgroup per chunk): this chunk's bases, each expert's first slot and count and
-// the padded total from pass 1 (the previous launch's writes are visible), this chunk's share of the layout writes
-// (expert blocks of experts e = c, c + nch, ...; the capacity tail split by chunk), then the stable placement of its
-// rows.
+// Multi-block align, pass 2 (one workgroup per chunk): every chunk's histogram (16 loads in flight a thread, one
+// expert a thread) gives this chunk's base within each expert (the rows of earlier chunks), each expert's count, and
+// by the padded scan each expert's first slot and the padded total (workgroup 0 writes ntpp). Then this chunk's share
+// of the layout writes (expert blocks of experts e = c, c + nch, ...; the capacity tail split by chunk) and the
+// stable placement of its rows.
 __global__ void __launch_bounds__(AT) align_scatter_kernel(const int* __restrict__ ids, int numel, int E, int blk,
                                                            int* __restrict__ sorted_ids, int* __restrict__ expert_ids,
-                                                           const int* __restrict__ scratch, int tail) {
+                                                           int* __restrict__ ntpp, const int* __restrict__ scratch,
+                                                           int tail) {
   __shared__ TabLds<AT> sh;
   __shared__ short lids[CH];
   const int* __restrict__ hist = scratch + ALIGN_HIST;
@@ -778,14 +740,25 @@ __global__ void __launch_bounds__(AT) align_scatter_kernel(const int* __restrict
     const int e = ids[t0 + t];
     lids[t] = (short)(e >= 0 && e < E ? e : -1);
   }
-  int pre = 0;
-  if (tid < E) {
-    pre = hist[(size_t)c * E + tid];
-    sh.offs[tid] = hist[(size_t)nch * E + tid];
-    sh.cnt[tid] = hist[(size_t)(nch + 1) * E + tid];
+  int pre = 0, tot = 0;
+  if (tid < E) {                                               // E <= AT: one expert a thread
+    for (int c0 = 0; c0 < nch; c0 += 16) {
+      int h[16];
+#pragma unroll
+      for (int u = 0; u < 16; u++) h[u] = hist[(size_t)min(c0 + u, nch - 1) * E + tid];
+#pragma unroll
+      for (int u = 0; u < 16; u++)
+        if (c0 + u < nch) {
+          pre += c0 + u < c ? h[u] : 0;
+          tot += h[u];
+        }
+    }
   }
-  const int total = hist[(size_t)(nch + 2) * E];
+  lds_barrier();                                               // zero_counts is done before the counts go in
+  if (tid < E) sh.cnt[tid] = tot;
   lds_barrier();
+  const int total = padded_scan(sh, E, blk);
+  if (c == 0 && tid == 0) ntpp[0] = total;
   write_layout(sh, E, blk, numel, total, pre, c, nch, sorted_ids, expert_ids, tail != 0);
   for (int base = 0; base < n; base += AT) stable_round(sh, lids, base, n, t0, E, sorted_ids);
 }
@@ -839,8 +812,8 @@ int launch_topk(const uint16_t* logits, int ldl, float* w, int* ids, int M, int 
 }
 
 // Tables for numel routed rows from ids in global memory (any numel): one workgroup up to SMALL_MAX, else the
-// histogram + placement launches over CH-row chunks (scratch: align_scratch_ints(numel, E) int32, zeroed once by
-// the caller; the launches leave its arrival counter zero).
+// histogram + placement launches over CH-row chunks (scratch: align_scratch_ints(numel, E) int32 for the chunk
+// histograms, which the count launch overwrites).
 long align_scratch_ints(int numel, int E) {
   return numel <= SMALL_MAX ? 1 : ALIGN_HIST + (long)((numel + CH - 1) / CH + 2) * E + 1;
 }
@@ -854,9 +827,9 @@ int launch_align(const int* ids, int numel, int E, int blk, int* sorted_ids, int
   }
   if (!scratch) return 1;
   const int nch = (numel + CH - 1) / CH;
-  hipLaunchKernelGGL(align_count_kernel, dim3(nch), dim3(AT), 0, st, ids, numel, E, blk, scratch, ntpp);
+  hipLaunchKernelGGL(align_count_kernel, dim3(nch), dim3(AT), 0, st, ids, numel, E, scratch);
   hipLaunchKernelGGL(align_scatter_kernel, dim3(nch), dim3(AT), 0, st, ids, numel, E, blk, sorted_ids, expert_ids,
-                     (const int*)scratch, tail);
+                     ntpp, (const int*)scratch, tail);
   return 0;
 }
 
@@ -1125,13 +1098,13 @@ extern "C" int r9k_moe_topk(long logits, int ldl, long weights, long ids, int M,
   return (int)hipGetLastError();
 }
 
-// int32 count of the scratch r9k_moe_align needs for `numel` routed rows over E experts (an arrival counter and the
-// per-chunk histograms / bases; zeroed once by the caller, the counter left zero by every call).
+// int32 count of the scratch r9k_moe_align needs for `numel` routed rows over E experts (the per-chunk histograms
+// of the multi-workgroup path, rewritten by every call).
 extern "C" long r9k_moe_align_scratch_ints(int numel, int E) { return align_scratch_ints(numel, E); }
 
 // Tables only, from ids int32 [numel] (the stock moe_align_block_size role; ids outside [0, E) are skipped).
-// scratch: r9k_moe_align_scratch_ints(numel, E) int32, zeroed once by the caller (its first int is the arrival
-// counter of the histogram launch, left zero; calls sharing one scratch must not overlap). 0 / 1 bad args / HIP
+// scratch: r9k_moe_align_scratch_ints(numel, E) int32 (the chunk histograms of the two-launch path, overwritten by
+// every call; calls sharing one scratch must not overlap). 0 / 1 bad args / HIP
 // error.
 extern "C" int r9k_moe_align(long ids, int numel, int E, int blk, long sorted_ids, long expert_ids, long ntpp,
                              long scratch, long scratch_ints, long stream) {
@@ -1144,12 +1117,10 @@ extern "C" int r9k_moe_align(long ids, int numel, int E, int blk, long sorted_id
 }
 
 // ---------------------------------------------------------------------------------- align without allocation
-// r9k_moe_align's multi-workgroup path needs scratch (the histograms' arrival counter and the per-chunk histograms /
-// bases). Callers that cannot allocate (code under HIP graph capture, tight serving loops, harnesses that forbid
+// r9k_moe_align's multi-workgroup path needs scratch (the per-chunk histograms). Callers that cannot allocate (code under HIP graph capture, tight serving loops, harnesses that forbid
 // hipMalloc) use r9k_moe_align_noalloc, whose scratch is this file-scope device array: 1 MiB per GPU, held by every
-// GPU the library runs on until the process ends. Its first int is the arrival counter: zero when the code object is
-// loaded (device globals start zeroed) and left zero by every call (the last-arriving histogram workgroup resets
-// it), so it is zero at the start of each call; the rest is fully written before it is read within a call. All
+// GPU the library runs on until the process ends. The histograms are fully written before they are read within a
+// call. All
 // calls on one GPU share the array and keep the last call's contents: calls that overlap on one GPU (other streams,
 // concurrent graph replays) race on it.
 namespace {
