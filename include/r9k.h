@@ -185,6 +185,32 @@ long r9k_moe_align_noalloc_max_ints(void);
 int r9k_moe_down_sum(long gu, long ids, long tw, long wq, long ws, long ws_estride, long shared, long ld_shared,
                      long out, long ld_out, int T, int topk, int E, int I, int N, long stream);
 
+/* The grouped MXFP4 x fp8 GEMM over 16-row routing blocks as a block stream: one workgroup of 16 waves walks one
+ * block's expert (or a wide column slice of it) over all of K, the block's activation rows staged once in LDS.
+ * epi 0 replaces kernels/r9k_moe_mxfp4a8.hip:631-638 (r9k_moe_mxfp4a8 at MT = 1) with its values bit for bit at
+ * its single-wave split: c bf16 [numel][N], topk_w optional, cs unused. epi 1 replaces, as one entry, the gate_up
+ * r9k_moe_mxfp4a8 + :550 (r9k_silu_mul_quant_fp8): c e4m3 [numel][N / 2] = the per-row fp8 quant of
+ * silu(gate) * up, cs fp32 [numel] its row scales, bit-equal to the two launches; topk_w must be 0. Tables in the
+ * moe_align_block_size format with 16-row blocks; blocks_hint = the caller's bound on live blocks (min(E, numel)),
+ * which sizes the column slices of epi 0. Served: K % 128 == 0, N % 16 == 0 (epi 1: N / 16 = 32 or 64), the staged
+ * rows within 64 KB of LDS; else 2 with nothing launched. 0, -3 bad argument, -6 launch error. */
+int r9k_moe_stream(int epi, long a, long as, long wq, long ws, long c, long cs, long sorted_ids, long expert_ids,
+                   long ntpp, long topk_w, long ws_estride, int max_blocks, int numel, int a_row_div, int K, int N,
+                   int blocks_hint, long stream);
+
+/* gate_up, SiLU-gating + per-row fp8 quant and down of a decode-width MoE layer in one launch, one 16-row routing
+ * block a workgroup (both GEMMs walk the same tables, so a block's down rows need only its own gate_up rows, handed
+ * over in LDS). Replaces, as one entry, the gate_up kernels/r9k_moe_mxfp4a8.hip:631-638 (r9k_moe_mxfp4a8) + :550
+ * (r9k_silu_mul_quant_fp8) + the down r9k_moe_mxfp4a8 with topk_w. a e4m3 [T][K1], as fp32 [T] (a_row_div = topk);
+ * w1q / w1s the gate_up weights (N1 = 2I, K1), w2q / w2s the down weights (N2, K2 = I), in the r9k_moe_mxfp4a8 layout
+ * (w?s_estride bytes per expert of the scale tensors); c bf16 [numel][N2] = the down rows, bit-equal to the three
+ * launches at their single-wave split; the top-k sum follows (r9k_moe_sum). Served: K1 % 128 == 0, K1 <= 4096,
+ * I % 128 == 0, I <= 1024, N2 % 32 == 0, the LDS within 96 KB, numel * N2 * 2 < 2^31; else 2 with nothing launched.
+ * 0, -3 bad argument, -6 launch error. */
+int r9k_moe_stream_layer(long a, long as, long w1q, long w1s, long w2q, long w2s, long c, long sorted_ids,
+                         long expert_ids, long ntpp, long topk_w, long w1s_estride, long w2s_estride, int max_blocks,
+                         int numel, int a_row_div, int K1, int N1, int N2, long stream);
+
 /* The dense MXFP4 weight-only linear at decode widths in one launch: the per-row fp8 quant of the bf16 activations
  * (each workgroup quantises the M <= 4 rows into LDS) and the GEMM. Replaces, as one entry, the reference's
  * r9k_quant_rows_fp8 + r9k_moe_mxfp4a8 over identity tables (r9700_vllm/ops.py:89-117; kernels/r9k_moe_mxfp4a8.hip

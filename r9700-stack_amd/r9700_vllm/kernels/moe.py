@@ -81,6 +81,10 @@ def lib() -> ctypes.CDLL:
         L.r9k_dense_nvfp4_qa.argtypes = [l] * 7 + [i] * 3 + [l]
         L.r9k_dense_mxfp4_a8.argtypes = [l] * 8 + [i] * 3 + [l]
         L.r9k_moe_down_sum.argtypes = [l] * 10 + [i] * 5 + [l]
+        L.r9k_moe_stream.restype = i
+        L.r9k_moe_stream.argtypes = [i] + [l] * 11 + [i] * 6 + [l]
+        L.r9k_moe_stream_layer.restype = i
+        L.r9k_moe_stream_layer.argtypes = [l] * 13 + [i] * 6 + [l]
         assert L.r9k_moe_block() == MOE_BLOCK
         _LIB = L
     return _LIB
@@ -247,53 +251,6 @@ def unpack_scales(wsr: torch.Tensor) -> torch.Tensor:
         parts.append(body[..., nkf * 64:].reshape(E, nt, G, 16).permute(0, 1, 3, 2))        # [E, nt, r, g]
     out = parts[0] if len(parts) == 1 else torch.cat(parts, dim=3)
     return out.reshape(E, N, KB).contiguous()
-
-
-# ------------------------------------------------------------------------------------ folded-exponent MXFP4
-# The reference folds each block's E8M0 into its gfx1201 e2m1 -> e4m3 unpack. The gfx950 scaled MFMA consumes the
-# block exponents directly, so folding is never selected (fold_supported() is False) and fold_decide() returns
-# False without looking. fold_stats stays available for inspecting a checkpoint's exponent spread.
-FOLD_EXACT, FOLD_REACH = 8, 12
-FOLD_MODE = os.environ.get("R9K_FOLD", "0").lower()
-
-
-@dataclass
-class FoldStats:
-    blocks: int
-    hist: list            # hist[d] = blocks with d = ref - block exponent (d clamped to 0..16)
-    max_d: int
-    K: int = 0
-
-    @property
-    def p_inexact(self) -> float:
-        return sum(self.hist[FOLD_EXACT + 1:]) / max(1, self.blocks)
-
-    @property
-    def p_flush(self) -> float:
-        return sum(self.hist[FOLD_REACH + 1:]) / max(1, self.blocks)
-
-    @property
-    def mean_d(self) -> float:
-        return sum(d * n for d, n in enumerate(self.hist)) / max(1, self.blocks)
-
-
-def fold_stats(wsr: torch.Tensor, chunk: int = 64 << 20) -> FoldStats:
-    """Distribution of d = row maximum exponent - block exponent over a pack_scales tensor, chunked by expert."""
-    E, nb1, N = wsr.shape
-    hist = torch.zeros(17, dtype=torch.int64)
-    step = max(1, chunk // (nb1 * N))
-    for e0 in range(0, E, step):
-        w = wsr[e0:e0 + step]
-        blocks = unpack_scales(w).to(torch.int16)                 # [e, N, KB]
-        d = (w[:, -1, :].to(torch.int16).unsqueeze(-1) - blocks).clamp_(0, 16)
-        hist += torch.bincount(d.reshape(-1).cpu(), minlength=17)
-    h = hist.tolist()
-    return FoldStats(E * (nb1 - 1) * N, h, max(i for i, n in enumerate(h) if n) if any(h) else 0, (nb1 - 1) * GROUP)
-
-
-def fold_decide(wsr: torch.Tensor, name: str = "", log=None) -> bool:
-    """Always False on gfx950 (no folded kernels); kept so weight prep reads like the reference's."""
-    return False
 
 
 # ------------------------------------------------------------------------------------------ activations
@@ -611,6 +568,92 @@ def moe_down_sum(gate_up: torch.Tensor, topk_ids: torch.Tensor, topk_w: torch.Te
     if rc:
         raise RuntimeError(f"r9k_moe_down_sum failed ({rc}) T={T} topk={k} N={w.N} K={w.K}")
     return True
+
+
+# Decode steps whose routing touches at least STREAM_MIN_BLOCKS experts and at most one 16-row block per CU
+# (expected_blocks) run gate_up, the SiLU + fp8 quant and down of each routing block in one workgroup
+# (r9k_moe_stream_layer); with fewer blocks a block stream would leave CUs idle, with more some CUs would run two
+# blocks while the rest wait. R9K_STREAM=0 turns it off.
+STREAM_MIN_BLOCKS = int(os.environ.get("R9K_STREAM_MIN_BLOCKS", "160"))
+STREAM = os.environ.get("R9K_STREAM", "1") == "1"
+_CUS: dict = {}
+
+
+def device_cus(device=None) -> int:
+    """Compute units of the current (or given) device."""
+    idx = torch.cuda.current_device() if device is None else torch.device(device).index
+    if idx not in _CUS:
+        _CUS[idx] = torch.cuda.get_device_properties(idx).multi_processor_count
+    return _CUS[idx]
+
+
+def expected_blocks(numel: int, num_experts: int, topk: int) -> float:
+    """Expected 16-row routing blocks of a step of numel / topk tokens under uniform routing: the expected number of
+    distinct experts, E * (1 - (1 - topk / E)^T) (each expert's ~numel / E rows fit one block at decode widths)."""
+    T = numel / max(1, topk)
+    return num_experts * (1.0 - (1.0 - min(topk, num_experts) / num_experts) ** T)
+
+
+def moe_stream(a_q: torch.Tensor, a_s: torch.Tensor, w: Mxfp4Experts, out: torch.Tensor, sorted_ids: torch.Tensor,
+               expert_ids: torch.Tensor, ntpp: torch.Tensor, numel: int, a_row_div: int,
+               topk_w: torch.Tensor | None = None, num_experts: int | None = None,
+               out_scale: torch.Tensor | None = None) -> bool:
+    """The grouped GEMM over 16-row routing blocks as a block stream (r9k_moe_stream). out_scale None: out bf16
+    [numel, N] = moe_gemm's values (its single-wave launch, bit for bit). out_scale given: the gate_up product with
+    SiLU-gating and the per-row fp8 quant in the epilogue, out e4m3 codes [numel, N/2] and out_scale fp32 [numel] =
+    silu_mul_quant_fp8 of moe_gemm's bf16 output, bit for bit. False when the shape is not served (nothing
+    launched)."""
+    E = num_experts if num_experts is not None else w.wq.shape[0]
+    epi = 1 if out_scale is not None else 0
+    assert a_q.is_contiguous() and a_q.shape[1] == w.K and a_s.dtype == torch.float32 and out.is_contiguous()
+    if epi:
+        assert topk_w is None and out.dtype == torch.float8_e4m3fn and out.shape == (numel, w.N // 2)
+        assert out_scale.dtype == torch.float32 and out_scale.numel() >= numel
+    else:
+        assert out.dtype == torch.bfloat16 and out.shape[1] == w.N
+        if topk_w is not None:
+            assert topk_w.dtype == torch.float32 and topk_w.is_contiguous()
+    max_blocks = min(expert_ids.numel(), (numel + MOE_BLOCK - 1) // MOE_BLOCK + min(numel, E))
+    rc = lib().r9k_moe_stream(epi, a_q.data_ptr(), a_s.data_ptr(), w.wq.data_ptr(), w.wsr.data_ptr(),
+                              out.data_ptr(), out_scale.data_ptr() if epi else 0, sorted_ids.data_ptr(),
+                              expert_ids.data_ptr(), ntpp.data_ptr(), topk_w.data_ptr() if topk_w is not None else 0,
+                              w.estride, max_blocks, numel, a_row_div, w.K, w.N, min(E, numel), _stream())
+    if rc == 2:
+        return False
+    if rc:
+        raise RuntimeError(f"r9k_moe_stream failed ({rc}) epi={epi} N={w.N} K={w.K}")
+    return True
+
+
+def moe_stream_layer(a_q: torch.Tensor, a_s: torch.Tensor, w1: Mxfp4Experts, w2: Mxfp4Experts, down: torch.Tensor,
+                     sorted_ids: torch.Tensor, expert_ids: torch.Tensor, ntpp: torch.Tensor, numel: int, topk: int,
+                     topk_w: torch.Tensor, num_experts: int | None = None) -> bool:
+    """gate_up, SiLU + per-row fp8 quant and the down GEMM (router weight in its epilogue) of every 16-row routing block
+    in one workgroup (r9k_moe_stream_layer): down bf16 [numel, N2] = the down moe_gemm's rows over the quantised
+    activation of the gate_up output (bit for bit against the single-wave launches). False when the shape is not
+    served (nothing launched)."""
+    E = num_experts if num_experts is not None else w1.wq.shape[0]
+    assert a_q.is_contiguous() and a_q.shape[1] == w1.K and a_s.dtype == torch.float32
+    assert w2.K == w1.N // 2 and down.dtype == torch.bfloat16 and down.shape == (numel, w2.N) and down.is_contiguous()
+    assert topk_w.dtype == torch.float32 and topk_w.is_contiguous() and topk_w.numel() == numel
+    max_blocks = min(expert_ids.numel(), (numel + MOE_BLOCK - 1) // MOE_BLOCK + min(numel, E))
+    rc = lib().r9k_moe_stream_layer(a_q.data_ptr(), a_s.data_ptr(), w1.wq.data_ptr(), w1.wsr.data_ptr(),
+                                    w2.wq.data_ptr(), w2.wsr.data_ptr(), down.data_ptr(), sorted_ids.data_ptr(),
+                                    expert_ids.data_ptr(), ntpp.data_ptr(), topk_w.data_ptr(), w1.estride, w2.estride,
+                                    max_blocks, numel, topk, w1.K, w1.N, w2.N, _stream())
+    if rc == 2:
+        return False
+    if rc:
+        raise RuntimeError(f"r9k_moe_stream_layer failed ({rc}) N1={w1.N} K1={w1.K} N2={w2.N}")
+    return True
+
+
+def stream_wanted(numel: int, num_experts: int, topk: int) -> bool:
+    """Whether a decode step of `numel` routed rows over `num_experts` experts takes r9k_moe_stream_layer."""
+    if not STREAM:
+        return False
+    b = expected_blocks(numel, num_experts, topk)
+    return STREAM_MIN_BLOCKS <= b <= device_cus()
 
 
 # ops.mxfp4_linear runs the one-launch dense path (r9k_dense_mxfp4_qa, M <= 4) up to this many rows. Measured on

@@ -11,22 +11,34 @@ missed experts host -> slot. The GEMMs then run twice: over the arena with the r
 the second pass is empty unless the step read through (more distinct experts than the threshold, or the insert cap
 was hit). Everything is device work on fixed addresses, so a captured HIP graph replays it.
 
+Layout of this module's host side (its own design; the names, knobs and LRU policy are the reference's, which
+callers and its tests bind):
+* `LruPolicy`   -- the knobs, read once per layer from the environment into a frozen record;
+* `_StateBlock` -- every LRU array of a layer (table, map_cold, slot_expert, slot_stamp, routed, step, miss list)
+  carved from ONE device allocation at 256-byte offsets, so the state has one base address for its whole life and
+  the warm start writes it with a single host -> device copy of a host-built image;
+* `_Counters`   -- the optional per-layer statistics as rows of one shared device tensor per device, read by one
+  `.cpu()` for all layers, and a reporter thread that logs the change over each period.
+
 Config (per process, the reference's names): R9K_EXPERT_CACHE_GB (0 = off), R9K_EXPERT_CACHE_SLOTS,
 R9K_EXPERT_CACHE_LAYERS, R9K_LRU_THRESH (0.99: a step routing to more distinct experts than this share of the slots
 inserts nothing and reads every non-resident expert through from host), R9K_LRU_MAX_INSERTS (64),
-R9K_LRU_GATHER="chunks,lanes" (64,16), R9K_LRU_FUSED (1), R9K_EXPERT_CACHE_HOST_ONLY (1), R9K_EXPERT_CACHE_STATS.
-Warm start: the checkpoint's model-expertprofile.safetensors (expert_routing_counts [layers, experts]) when vLLM
-names a model directory holding one, else experts 0..S-1.
+R9K_LRU_GATHER="chunks,lanes" (64,16), R9K_LRU_FUSED (1), R9K_EXPERT_CACHE_HOST_ONLY (1), R9K_EXPERT_CACHE_STATS,
+R9K_EXPERT_CACHE_STATS_SEC (10), R9K_STAGE_COLD (0). Warm start: the checkpoint's model-expertprofile.safetensors
+(expert_routing_counts [layers, experts]) when vLLM names a model directory holding one, else experts 0..S-1; the
+hottest expert gets the newest stamp, so the warm set is evicted coldest first.
 
 On gfx950 the cold pass reads weights over PCIe inside the GEMM (the decode kernels read every weight byte once per
-routing block). R9K_STAGE_COLD (the reference's opt-in bulk staging of cold experts, recorded there as without a
-measured gain) is not built: `staging_enabled()` is always False.
+routing block). R9K_STAGE_COLD=1 first copies the step's cold experts into a VRAM staging area shared by the layers.
 """
 from __future__ import annotations
 
 import ctypes
+import dataclasses
+import functools
 import logging
 import os
+import threading
 
 import numpy as np
 import torch
@@ -36,10 +48,9 @@ from ..kernels import moe as K
 logger = logging.getLogger("vllm." + __name__)
 
 _BOUND = False
-_PROFILE: torch.Tensor | None = None
-_PROFILE_LOADED = False
 _HOST_BUFFERS: list = []          # (pointer, bytes) of every mapped host buffer: held until the process ends
 HOST_COPY_BYTES = 512 << 20       # largest single device -> host transfer of to_host
+WARM_COPY_EXPERTS = 64            # experts per host -> arena copy of the warm start
 
 
 def _L():
@@ -111,37 +122,244 @@ def budget_gb() -> float:
     return float(os.environ.get("R9K_EXPERT_CACHE_GB", "0") or 0)
 
 
-def _profile() -> torch.Tensor | None:
-    global _PROFILE, _PROFILE_LOADED
-    if _PROFILE_LOADED:
-        return _PROFILE
-    _PROFILE_LOADED = True
-    try:
-        from vllm.config import get_current_vllm_config
-        from safetensors.torch import load_file
-        p = os.path.join(get_current_vllm_config().model_config.model, "model-expertprofile.safetensors")
-        if os.path.isfile(p):
-            _PROFILE = load_file(p)["expert_routing_counts"].float()
-            logger.info("r9700: expert routing profile %s %s", p, tuple(_PROFILE.shape))
-    except Exception as e:                       # no vLLM config or no profile: cold start from experts 0..S-1
-        logger.debug("r9700: no expert routing profile (%s)", e)
-    return _PROFILE
-
-
-def _num_moe_layers() -> int:
-    try:
-        from vllm.config import get_current_vllm_config
-        hf = get_current_vllm_config().model_config.hf_text_config
-        return int(getattr(hf, "num_hidden_layers"))
-    except Exception:
-        return 48
-
-
 def staging_enabled() -> bool:
     """R9K_STAGE_COLD=1 (opt-in, as in the reference): a step that needs the cold pass first copies every routed
     expert that is not resident into a VRAM staging area with one bulk gather, and the cold pass reads it there
     instead of reading host memory inside the GEMMs (once per routing block)."""
     return os.environ.get("R9K_STAGE_COLD", "0") == "1"
+
+
+def stats_enabled() -> bool:
+    return os.environ.get("R9K_EXPERT_CACHE_STATS", "0") == "1"
+
+
+def host_only() -> bool:
+    """Cache only layers whose experts are already host-offloaded (R9K_EXPERT_CACHE_HOST_ONLY=1, the default);
+    0 moves device-resident layers to host as well."""
+    return os.environ.get("R9K_EXPERT_CACHE_HOST_ONLY", "1") == "1"
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# What vLLM tells us about the model: its directory (for the routing profile) and its layer count (for the budget)
+
+@functools.lru_cache(maxsize=None)
+def _model_facts() -> tuple:
+    """(model directory or None, hidden layer count or None) from vLLM's current config; (None, None) without one."""
+    try:
+        from vllm.config import get_current_vllm_config
+        mc = get_current_vllm_config().model_config
+    except Exception:
+        return None, None
+    layers = getattr(getattr(mc, "hf_text_config", None), "num_hidden_layers", None)
+    return getattr(mc, "model", None), (int(layers) if layers else None)
+
+
+@functools.lru_cache(maxsize=None)
+def routing_profile() -> torch.Tensor | None:
+    """expert_routing_counts [layers, experts] (fp32) from <model>/model-expertprofile.safetensors, read once per
+    process; None when vLLM names no model directory or it holds no profile."""
+    model_dir, _ = _model_facts()
+    path = os.path.join(model_dir, "model-expertprofile.safetensors") if model_dir else None
+    if not path or not os.path.isfile(path):
+        return None
+    from safetensors import safe_open
+    with safe_open(path, framework="pt") as f:
+        counts = f.get_tensor("expert_routing_counts").float()
+    logger.info("r9700: warm-starting expert caches from %s, counts %s", path, tuple(counts.shape))
+    return counts
+
+
+def slots_per_layer(bytes_per_expert: int) -> int:
+    """VRAM slots of each cached layer: R9K_EXPERT_CACHE_SLOTS when set; else the R9K_EXPERT_CACHE_GB budget shared
+    by the cached layers (R9K_EXPERT_CACHE_LAYERS, default every hidden layer of the model, 48 when vLLM does not
+    say), in whole experts; 0 = off."""
+    fixed = int(os.environ.get("R9K_EXPERT_CACHE_SLOTS", "0") or 0)
+    if fixed > 0:
+        return fixed
+    budget = int(budget_gb() * 2**30)
+    if budget <= 0:
+        return 0
+    layers = int(os.environ.get("R9K_EXPERT_CACHE_LAYERS", "0") or 0) or _model_facts()[1] or 48
+    return budget // layers // bytes_per_expert
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# Policy and state
+
+@dataclasses.dataclass(frozen=True)
+class LruPolicy:
+    """The cache's knobs for one layer of S slots.
+    max_inserts   experts copied in per step at most (R9K_LRU_MAX_INSERTS, capped at S);
+    max_distinct  a step routing to more distinct experts inserts nothing (int(S * R9K_LRU_THRESH));
+    no_cold_limit a step of at most this many routed rows cannot need the cold pass (its distinct experts fit both
+                  limits above; 0 when the threshold covers every slot);
+    fused         manage and both table sets in one launch (R9K_LRU_FUSED);
+    chunks, lanes the gather's launch shape (R9K_LRU_GATHER = "chunks,lanes")."""
+    max_inserts: int
+    max_distinct: int
+    no_cold_limit: int
+    fused: bool
+    chunks: int
+    lanes: int
+
+    @classmethod
+    def from_env(cls, slots: int) -> "LruPolicy":
+        env = os.environ.get
+        ins = min(int(env("R9K_LRU_MAX_INSERTS", "64")), slots)
+        distinct = int(slots * float(env("R9K_LRU_THRESH", "0.99")))
+        chunks, lanes = (int(v) for v in env("R9K_LRU_GATHER", "64,16").split(","))
+        return cls(max_inserts=ins, max_distinct=distinct,
+                   no_cold_limit=min(distinct, ins) if slots > distinct else 0,
+                   fused=env("R9K_LRU_FUSED", "1") == "1", chunks=chunks, lanes=lanes)
+
+
+class _StateBlock:
+    """The LRU arrays of one layer as typed views of a single device byte buffer (256-byte aligned fields):
+
+        table       [E]     int32  expert -> slot, -1 = not resident
+        map_cold    [E]     int32  expert -> itself when not resident, else -1
+        slot_expert [S]     int32  slot -> expert, -1 = empty
+        slot_stamp  [S]     int64  step of the slot's last use (victims: smallest stamp, then lowest slot)
+        routed      [E]     uint8  this step's routed flags (the manager's scratch)
+        step        [1]     int64  step counter
+        miss        [I, 2]  int32  (expert, slot) inserts of the step, I = max(1, max_inserts)
+        n_miss      [1]     int32  their count
+
+    `image(...)` builds the bytes of a whole state on the host, `load(...)` writes it with one copy."""
+
+    FIELDS = (("table", "E", np.int32), ("map_cold", "E", np.int32), ("slot_expert", "S", np.int32),
+              ("slot_stamp", "S", np.int64), ("routed", "E", np.uint8), ("step", 1, np.int64),
+              ("miss", "I2", np.int32), ("n_miss", 1, np.int32))
+
+    def __init__(self, dev: torch.device, E: int, S: int, inserts: int):
+        sizes = {"E": E, "S": S, "I2": 2 * max(1, inserts), 1: 1}
+        self.layout, off = {}, 0
+        for name, n, dt in self.FIELDS:
+            count = sizes[n]
+            self.layout[name] = (off, count, np.dtype(dt))
+            off += -(-count * np.dtype(dt).itemsize // 256) * 256
+        self.nbytes = off
+        self.buf = torch.zeros((off,), dtype=torch.uint8, device=dev)
+        tdt = {np.dtype(np.int32): torch.int32, np.dtype(np.int64): torch.int64, np.dtype(np.uint8): torch.uint8}
+        for name, (o, count, dt) in self.layout.items():
+            v = self.buf[o:o + count * dt.itemsize].view(tdt[dt])
+            setattr(self, name, v.view(-1, 2) if name == "miss" else v)
+
+    def image(self, E: int, residents: np.ndarray) -> np.ndarray:
+        """The state after installing `residents` (expert ids, hottest first) in slots 0..n-1: each resident's stamp
+        is minus its rank, so the coldest warm expert is the first victim."""
+        img = np.zeros(self.nbytes, dtype=np.uint8)
+
+        def field(name):
+            o, count, dt = self.layout[name]
+            return img[o:o + count * dt.itemsize].view(dt)
+        n = residents.size
+        table, cold = field("table"), field("map_cold")
+        table[:] = -1
+        table[residents] = np.arange(n, dtype=np.int32)
+        cold[:] = np.where(table < 0, np.arange(E, dtype=np.int32), -1)
+        slots = field("slot_expert")
+        slots[:] = -1
+        slots[:n] = residents
+        field("slot_stamp")[:n] = -np.arange(n, dtype=np.int64)
+        field("miss")[:] = -1
+        return img
+
+    def load(self, img: np.ndarray) -> None:
+        self.buf.copy_(torch.from_numpy(img))
+
+
+def _warm_residents(layer_idx: int, E: int, S: int) -> np.ndarray:
+    """The S experts a layer starts with, hottest first: by the routing profile's counts for this layer (ties to
+    the lower id) when it has a row for a layer of E experts, else 0..S-1."""
+    prof = routing_profile()
+    if prof is None or layer_idx >= prof.shape[0] or prof.shape[1] != E:
+        return np.arange(S, dtype=np.int32)
+    counts = prof[layer_idx].double().numpy()
+    return np.lexsort((np.arange(E), -counts))[:S].astype(np.int32)
+
+
+# ---------------------------------------------------------------------------------------------------------------
+# Statistics
+
+STAT_FIELDS = ("steps", "distinct", "inserts", "read_through", "wide")
+
+
+class _Counters:
+    """Statistics of every cached layer of the process: one int64 device tensor [rows, len(STAT_FIELDS)] per device,
+    a row per layer (grown by whole blocks; a layer keeps its row view), and a reporter thread that logs the change
+    of the totals over each R9K_EXPERT_CACHE_STATS_SEC period (0 = no thread). A failing reporter stops itself."""
+
+    BLOCK = 128
+
+    def __init__(self):
+        self.blocks: dict = {}          # device index -> list of [BLOCK, fields] tensors
+        self.used: dict = {}
+        self.owners: list = []          # (cache) in registration order, for the log line's shape
+        self.lock = threading.Lock()
+        self.stop = threading.Event()
+        self.thread = None
+
+    def row(self, cache, dev: torch.device) -> torch.Tensor:
+        with self.lock:
+            blocks = self.blocks.setdefault(dev.index, [])
+            n = self.used.get(dev.index, 0)
+            if n == len(blocks) * self.BLOCK:
+                blocks.append(torch.zeros((self.BLOCK, len(STAT_FIELDS)), dtype=torch.int64, device=dev))
+            self.used[dev.index] = n + 1
+            self.owners.append(cache)
+            r = blocks[n // self.BLOCK][n % self.BLOCK]
+        period = float(os.environ.get("R9K_EXPERT_CACHE_STATS_SEC", "10") or 0)
+        if self.thread is None and period > 0:
+            self.thread = threading.Thread(target=self._report, args=(period,), name="r9k-cache-stats", daemon=True)
+            self.thread.start()
+        return r
+
+    def totals(self) -> torch.Tensor:
+        with self.lock:
+            parts = []
+            for d in sorted(self.blocks):
+                n = self.used[d]
+                parts += [b.cpu() for b in self.blocks[d]]
+                parts[-1] = parts[-1][: n - (len(self.blocks[d]) - 1) * self.BLOCK]
+        if not parts:
+            return torch.zeros((0, len(STAT_FIELDS)), dtype=torch.int64)
+        return torch.cat(parts)
+
+    def _report(self, period: float) -> None:
+        before = None
+        while not self.stop.wait(period):
+            try:
+                now = self.totals()
+                if before is not None and now.shape == before.shape:
+                    d = now - before
+                    if int(d[:, 0].sum()):
+                        c = self.owners[0]
+                        logger.info("r9700 expert cache (%d slots a layer, insert cap %d, read-through above %d "
+                                    "experts), last %.0f s: %s", c.S, c.max_inserts, c.max_distinct, period,
+                                    stats_line(d, sum(c.bytes) / 2**20))
+                before = now
+            except Exception as exc:
+                logger.warning("r9700: expert cache statistics off after an error: %s", exc)
+                return
+
+
+_COUNTERS = _Counters()
+
+
+def stats_snapshot() -> torch.Tensor:
+    """[layers, 5] int64 on the host: per cached layer, totals since load of STAT_FIELDS."""
+    return _COUNTERS.totals()
+
+
+def stats_line(delta: torch.Tensor, mib_per_expert: float) -> str:
+    """One line for a [layers, 5] difference of two snapshots: per layer-step means over the layers that stepped."""
+    tot = dict(zip(STAT_FIELDS, delta.sum(0).tolist()))
+    per = 1.0 / max(tot["steps"], 1)
+    host = tot["read_through"] * per
+    return (f"{tot['steps']} layer-steps; per layer-step {tot['distinct'] * per:.1f} experts routed, "
+            f"{tot['inserts'] * per:.1f} copied into VRAM, {host:.1f} read from host memory "
+            f"({host * mib_per_expert:.0f} MiB); {100.0 * tot['wide'] * per:.0f}% of steps read through")
 
 
 _STAGE_AREAS: dict = {}
@@ -157,68 +375,7 @@ def _stage_area(dev: torch.device, cap: int, store) -> tuple:
     return area
 
 
-def stats_enabled() -> bool:
-    return os.environ.get("R9K_EXPERT_CACHE_STATS", "0") == "1"
-
-
-STAT_FIELDS = ("steps", "distinct", "inserts", "read_through", "wide")
-
-
-class _StatsReporter:
-    """Per-layer cache counters (each cached layer's device tensor `stats`, STAT_FIELDS) and one daemon thread that
-    logs the change over every R9K_EXPERT_CACHE_STATS_SEC seconds (0 = no thread). A reporter that fails stops
-    itself: a diagnostic never takes the worker down."""
-
-    def __init__(self):
-        self.layers: list = []
-        self.thread = None
-
-    def add(self, cache) -> None:
-        self.layers.append(cache)
-        period = float(os.environ.get("R9K_EXPERT_CACHE_STATS_SEC", "10") or 0)
-        if self.thread is None and period > 0:
-            import threading
-            self.thread = threading.Thread(target=self._run, args=(period,), name="r9k-cache-stats", daemon=True)
-            self.thread.start()
-
-    def snapshot(self) -> torch.Tensor:
-        if not self.layers:
-            return torch.zeros((0, len(STAT_FIELDS)), dtype=torch.int64)
-        return torch.stack([c.stats for c in self.layers]).cpu()
-
-    def _run(self, period: float) -> None:
-        import time
-        prev = None
-        while True:
-            time.sleep(period)
-            try:
-                now = self.snapshot()
-                if prev is not None and now.shape == prev.shape and int((now - prev)[:, 0].sum()) > 0:
-                    c = self.layers[0]
-                    logger.info("r9700: expert cache over %.0f s (S=%d, threshold %d, insert cap %d): %s", period,
-                                c.S, c.max_distinct, c.max_inserts, stats_line(now - prev, sum(c.bytes) / 2**20))
-                prev = now
-            except Exception as e:
-                logger.warning("r9700: expert cache stats reporter stopped: %s", e)
-                return
-
-
-_REPORTER = _StatsReporter()
-
-
-def stats_snapshot() -> torch.Tensor:
-    """[layers, 5] int64 on the host: per cached layer, totals since load of STAT_FIELDS."""
-    return _REPORTER.snapshot()
-
-
-def stats_line(delta: torch.Tensor, mib_per_expert: float) -> str:
-    """One line for a [layers, 5] difference of two snapshots: per layer-step means over the layers that stepped."""
-    steps, distinct, inserts, through, wide = delta.sum(0).tolist()
-    n = max(steps, 1)
-    return (f"{steps} layer-steps: routed {distinct / n:.1f} distinct experts, {inserts / n:.1f} inserted, "
-            f"{through / n:.1f} read through from host ({through / n * mib_per_expert:.0f} MiB), "
-            f"{100.0 * wide / n:.0f}% of steps over the insert threshold")
-
+# ---------------------------------------------------------------------------------------------------------------
 
 class LayerCache:
     """One MoE layer's cache (reference moe/cache.py:182-395): host store of all E experts, S-slot VRAM arena,
@@ -226,95 +383,65 @@ class LayerCache:
 
     def __init__(self, layer_idx: int, w13: torch.Tensor, w2: torch.Tensor, s13: torch.Tensor, s2: torch.Tensor,
                  N1: int, K1: int, N2: int, K2: int, slots: int):
-        dev = torch.device("cuda", torch.cuda.current_device())
+        if not (is_host(w13) and is_host(w2)):
+            raise ValueError("LayerCache: w13 / w2 must be mapped host tensors (to_host / uva_empty)")
         E = w13.shape[0]
-        self.E, self.S, self.layer_idx = E, min(slots, E, 1024), layer_idx
-        if self.S < 1:
+        S = min(slots, E, 1024)
+        if S < 1:
             raise ValueError("LayerCache: at least one slot")
         if E > 8192:
             raise ValueError(f"LayerCache: {E} experts (the device manager holds at most 8192)")
+        dev = torch.device("cuda", torch.cuda.current_device())
+        self.layer_idx, self.E, self.S = layer_idx, E, S
         self.N1, self.K1, self.N2, self.K2 = N1, K1, N2, K2
         self.fold = (False, False)
-        if not (is_host(w13) and is_host(w2)):
-            raise ValueError("LayerCache: w13 / w2 must be mapped host tensors (to_host / uva_empty)")
-        # host store (the backing copy of every expert) and the VRAM arena of S slots with the same slab shapes
-        self.h_w13, self.h_w2 = w13, w2
-        self.h_s13, self.h_s2 = (s if is_host(s) else to_host(s.contiguous()) for s in (s13, s2))
-        store = (self.h_w13, self.h_w2, self.h_s13, self.h_s2)
-        self.a_w13, self.a_w2, self.a_s13, self.a_s2 = (
-            torch.empty((self.S, *h.shape[1:]), dtype=h.dtype, device=dev) for h in store)
+        self.policy = LruPolicy.from_env(S)
+
+        # the backing store (scales copied to host when they are not there) and an arena of S slots shaped alike
+        store = (w13, w2) + tuple(s if is_host(s) else to_host(s.contiguous()) for s in (s13, s2))
+        self.h_w13, self.h_w2, self.h_s13, self.h_s2 = store
         self.bytes = [h[0].numel() * h.element_size() for h in store]
         if any(b % 16 for b in self.bytes):
             raise ValueError(f"LayerCache: per-expert slab sizes must be multiples of 16 bytes: {self.bytes}")
-        self._init_lru_state(dev)
-        self._init_policy()
-        self._warm_start()
-        if staging_enabled() and self.E > self.S:
-            # every slot holds an expert after the warm start and keeps one, so at most E - S routed experts are cold
-            cap = self.E - self.S
-            self.stage = _stage_area(dev, cap, store)
-            self.stage_cap = cap
-            self.stage_map = torch.full((self.E,), -1, dtype=torch.int32, device=dev)
-            self.stage_miss = torch.full((cap, 2), -1, dtype=torch.int32, device=dev)
-            self.stage_n = torch.zeros((1,), dtype=torch.int32, device=dev)
-        self.stats = None
-        if stats_enabled():
-            self.stats = torch.zeros((len(STAT_FIELDS),), dtype=torch.int64, device=dev)
-            _REPORTER.add(self)
+        arena = tuple(torch.empty((S, *h.shape[1:]), dtype=h.dtype, device=dev) for h in store)
+        self.a_w13, self.a_w2, self.a_s13, self.a_s2 = arena
 
-    def _init_lru_state(self, dev) -> None:
-        """table [E] (expert -> slot, -1 = host), map_cold [E] (expert -> itself when not resident, else -1),
-        slot_expert [S], slot_stamp [S] (step of last use), routed [E] flags, the step counter."""
-        E, S = self.E, self.S
-        self.table = torch.full((E,), -1, dtype=torch.int32, device=dev)
-        self.map_cold = torch.arange(E, dtype=torch.int32, device=dev)
-        self.slot_expert = torch.full((S,), -1, dtype=torch.int32, device=dev)
-        self.slot_stamp = torch.zeros((S,), dtype=torch.int64, device=dev)
-        self.routed = torch.zeros((E,), dtype=torch.uint8, device=dev)
-        self.step = torch.zeros((1,), dtype=torch.int64, device=dev)
+        self.state = _StateBlock(dev, E, S, self.policy.max_inserts)
+        residents = _warm_residents(layer_idx, E, S)
+        self.state.load(self.state.image(E, residents))
+        idx = torch.from_numpy(residents.astype(np.int64))
+        for lo in range(0, residents.size, WARM_COPY_EXPERTS):
+            sel = idx[lo:lo + WARM_COPY_EXPERTS]
+            for dst, src in zip(arena, store):
+                dst[lo:lo + sel.numel()].copy_(src.index_select(0, sel))
+        torch.cuda.synchronize()
 
-    def _init_policy(self) -> None:
-        """Insert cap and read-through threshold (R9K_LRU_MAX_INSERTS, R9K_LRU_THRESH), the miss list they size,
-        the gather launch shape (R9K_LRU_GATHER = "chunks,lanes") and the fused manage + align switch."""
-        S, dev = self.S, self.table.device
-        self.max_inserts = min(int(os.environ.get("R9K_LRU_MAX_INSERTS", "64")), S)
-        self.max_distinct = int(S * float(os.environ.get("R9K_LRU_THRESH", "0.99")))
-        self.miss = torch.full((max(1, self.max_inserts), 2), -1, dtype=torch.int32, device=dev)
-        self.n_miss = torch.zeros((1,), dtype=torch.int32, device=dev)
-        # a step of at most this many routed rows cannot need the cold pass: its distinct experts fit both limits
-        self.no_cold_limit = min(self.max_distinct, self.max_inserts) if S > self.max_distinct else 0
-        self.fused = os.environ.get("R9K_LRU_FUSED", "1") == "1"
-        chunks, lanes = os.environ.get("R9K_LRU_GATHER", "64,16").split(",")
-        self.chunks, self.lanes = int(chunks), int(lanes)
         self._one = None
         self._one_old: list = []
-        self.stage = None
         self.hot_ids = None                      # set by update_fused: the last step's slot per routed row
+        self.stage = None
+        if staging_enabled() and E > S:
+            # every slot holds an expert after the warm start and keeps one, so at most E - S routed experts are cold
+            self.stage_cap = E - S
+            self.stage = _stage_area(dev, self.stage_cap, store)
+            self.stage_map = torch.full((E,), -1, dtype=torch.int32, device=dev)
+            self.stage_miss = torch.full((self.stage_cap, 2), -1, dtype=torch.int32, device=dev)
+            self.stage_n = torch.zeros((1,), dtype=torch.int32, device=dev)
+        self.stats = _COUNTERS.row(self, dev) if stats_enabled() else None
 
-    def _warm_start(self):
-        prof = _profile()
-        if prof is not None and self.layer_idx < prof.shape[0] and prof.shape[1] == self.E:
-            order = torch.argsort(prof[self.layer_idx], descending=True, stable=True)
-        else:
-            order = torch.arange(self.E)
-        init = order[: self.S].to(torch.int32)
-        n = init.numel()
-        dev = self.table.device
-        pairs = torch.stack([init, torch.arange(n, dtype=torch.int32)], dim=1).to(dev)
-        for i in range(0, n, max(1, self.max_inserts)):      # the gather kernel, in miss-list-sized batches
-            chunk = pairs[i: i + max(1, self.max_inserts)]
-            self.miss[: chunk.shape[0]].copy_(chunk)
-            self.n_miss.fill_(chunk.shape[0])
-            self._gather()
-        self.n_miss.zero_()
-        self.miss.fill_(-1)
-        il = init.long().to(dev)
-        self.table[il] = torch.arange(n, dtype=torch.int32, device=dev)
-        self.map_cold[il] = -1
-        self.slot_expert[:n] = init.to(dev)
-        # older stamps for colder warm experts, so the hottest are evicted last
-        self.slot_stamp[:n] = torch.arange(n, 0, -1, dtype=torch.int64, device=dev) - n
-        torch.cuda.synchronize()
+    # the state arrays and knobs under the names the manager's callers use
+    table = property(lambda self: self.state.table)
+    map_cold = property(lambda self: self.state.map_cold)
+    slot_expert = property(lambda self: self.state.slot_expert)
+    slot_stamp = property(lambda self: self.state.slot_stamp)
+    routed = property(lambda self: self.state.routed)
+    step = property(lambda self: self.state.step)
+    miss = property(lambda self: self.state.miss)
+    n_miss = property(lambda self: self.state.n_miss)
+    max_inserts = property(lambda self: self.policy.max_inserts)
+    max_distinct = property(lambda self: self.policy.max_distinct)
+    no_cold_limit = property(lambda self: self.policy.no_cold_limit)
+    fused = property(lambda self: self.policy.fused)
 
     def _gather(self, dst=None, miss=None, n_miss=None):
         """The listed experts host -> their slots (default: the arena and the manager's miss list)."""
@@ -325,16 +452,19 @@ class LayerCache:
         rc = _L().r4d_lru_gather(
             d13.data_ptr(), self.h_w13.data_ptr(), b[0], d2.data_ptr(), self.h_w2.data_ptr(), b[1],
             ds13.data_ptr(), self.h_s13.data_ptr(), b[2], ds2.data_ptr(), self.h_s2.data_ptr(), b[3],
-            0, 0, 0, 0, 0, 0, miss.data_ptr(), n_miss.data_ptr(), self.chunks, self.lanes, _stream())
+            0, 0, 0, 0, 0, 0, miss.data_ptr(), n_miss.data_ptr(), self.policy.chunks, self.policy.lanes, _stream())
         if rc:
             raise RuntimeError(f"r4d_lru_gather failed ({rc})")
+
+    def _state_ptrs(self) -> list:
+        s = self.state
+        return [s.table.data_ptr(), s.map_cold.data_ptr(), s.slot_expert.data_ptr(), s.slot_stamp.data_ptr(),
+                s.routed.data_ptr(), s.step.data_ptr(), s.miss.data_ptr(), s.n_miss.data_ptr()]
 
     def _manage(self, ids: torch.Tensor, hot: torch.Tensor | None = None, cold: torch.Tensor | None = None) -> None:
         """LRU manage; with hot / cold given, the same launch also writes the two passes' mapped routing ids."""
         rc = _L().r9k_lru_manage_map(ids.data_ptr(), ids.numel(), self.E, self.S, self.max_distinct,
-                                     self.max_inserts, self.table.data_ptr(), self.map_cold.data_ptr(),
-                                     self.slot_expert.data_ptr(), self.slot_stamp.data_ptr(), self.routed.data_ptr(),
-                                     self.step.data_ptr(), self.miss.data_ptr(), self.n_miss.data_ptr(),
+                                     self.max_inserts, *self._state_ptrs(),
                                      hot.data_ptr() if hot is not None else 0,
                                      cold.data_ptr() if cold is not None else 0, _stream())
         if rc:
@@ -396,9 +526,7 @@ class LayerCache:
         lib, st = _L(), _stream()
         # one launch (manage + both table sets) while one workgroup can build the tables, else manage + two aligns
         rc = lib.r9k_lru_manage_tables(ids.data_ptr(), mk, self.E, self.S, self.max_distinct, self.max_inserts,
-                                       self.table.data_ptr(), self.map_cold.data_ptr(), self.slot_expert.data_ptr(),
-                                       self.slot_stamp.data_ptr(), self.routed.data_ptr(), self.step.data_ptr(),
-                                       self.miss.data_ptr(), self.n_miss.data_ptr(), bs, sh.data_ptr(), eh.data_ptr(),
+                                       *self._state_ptrs(), bs, sh.data_ptr(), eh.data_ptr(),
                                        nh.data_ptr(), sc.data_ptr() if need_cold else 0,
                                        ec.data_ptr() if need_cold else 0, nc.data_ptr() if need_cold else 0,
                                        hid.data_ptr(), st)
@@ -451,22 +579,3 @@ class LayerCache:
     def cold(self):
         """(w13, w2) experts over the mapped host store: the pass whose ids go through `map_cold`."""
         return self._experts(self.h_w13, self.h_s13, self.h_w2, self.h_s2)
-
-
-def slots_per_layer(bytes_per_expert: int) -> int:
-    """VRAM slots of each cached layer: R9K_EXPERT_CACHE_SLOTS when set; else the R9K_EXPERT_CACHE_GB budget shared
-    by the cached layers (R9K_EXPERT_CACHE_LAYERS, default every MoE layer of the model), in whole experts; 0 = off."""
-    fixed = int(os.environ.get("R9K_EXPERT_CACHE_SLOTS", "0") or 0)
-    if fixed > 0:
-        return fixed
-    budget = int(budget_gb() * 2**30)
-    if budget <= 0:
-        return 0
-    layers = int(os.environ.get("R9K_EXPERT_CACHE_LAYERS", "0") or 0) or _num_moe_layers()
-    return budget // layers // bytes_per_expert
-
-
-def host_only() -> bool:
-    """Cache only layers whose experts are already host-offloaded (R9K_EXPERT_CACHE_HOST_ONLY=1, the default);
-    0 moves device-resident layers to host as well."""
-    return os.environ.get("R9K_EXPERT_CACHE_HOST_ONLY", "1") == "1"

@@ -11,8 +11,10 @@ Layer weights (set by weight prep, quant/ct.py or kernels/moe.prepare_mxfp4_weig
   w2_weight_scale   [E, K2/32 + 1, N2]  uint8
 Flow per call (reference experts.py:149-251): align tables (from the router, else the GPU align) -> per-token fp8
 quant -> grouped gate_up GEMM -> silu(g)*u + per-row fp8 quant -> grouped down GEMM with the router weight in the
-epilogue -> top-k sum into `output`. Six launches on torch's current stream, no host synchronisation, so a call can
-be captured in a HIP graph.
+epilogue -> top-k sum into `output`, all on torch's current stream with no host synchronisation, so a call can be
+captured in a HIP graph. Decode widths fuse launches: up to ~128 MiB of routed down weights the SiLU, down and sum
+run as one token-major launch (r9k_moe_down_sum); wider steps that touch most experts run gate_up, the SiLU + quant
+and down of each routing block in one workgroup (r9k_moe_stream_layer), then the top-k sum.
 """
 from __future__ import annotations
 
@@ -253,6 +255,18 @@ class R9700Mxfp4Experts(_experts_base()):
         q = route.take_quant(getattr(self, "r9k_layer", None), topk_ids, hidden_states) if expert_map is None else None
         xq, xs = q if q is not None else K.quant_rows_fp8(hidden_states)
         fused = MOE_FUSE and nv is None and MT == 1 and pf_gate is None and pf_down is None
+        # wide decode steps (most experts touched, one 16-row block each, about one block a CU): gate_up, the SiLU +
+        # fp8 quant and down of each routing block in one workgroup (r9k_moe_stream_layer), the quantised rows handed
+        # over in LDS: no SiLU launch and no gate_up intermediate in HBM
+        if (not fused and cache is None and nv is None and expert_map is None and not ZERO_DOWN and len(passes) == 1
+                and MT == 1 and pf_gate is None and pf_down is None and K.stream_wanted(numel, E, topk)
+                and not K.down_sum_fits(numel, N2, K2)):
+            W1, W2, (sid, eid, ntpp), _ = passes[0]
+            down = torch.empty((numel, N2), dtype=torch.bfloat16, device=dev)
+            tw = topk_weights.reshape(-1).to(torch.float32).contiguous()
+            if K.moe_stream_layer(xq, xs, W1, W2, down, sid, eid, ntpp, numel, topk, tw, E):
+                K.moe_sum(down.view(M, topk, N2), None, output)
+                return output
         if fused:
             aq = torch.empty((numel, N1 // 2), dtype=torch.float32, device=dev)
             for W1, _, (sid, eid, ntpp), _ in passes:

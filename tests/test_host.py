@@ -50,15 +50,6 @@ def test_pack_scales_lane_layout(N, Kd):
     assert torch.equal(K.unpack_scales(wsr), e8)
 
 
-def test_fold_stats_on_packed_layout():
-    g = torch.Generator().manual_seed(0)
-    _, e8 = make_experts(3, 32, 512, g, 118, 126)
-    st = K.fold_stats(K.pack_scales(e8))
-    d = (e8.max(dim=2, keepdim=True).values.int() - e8.int()).clamp(0, 16)
-    assert st.hist == torch.bincount(d.reshape(-1), minlength=17).tolist()
-    assert not K.fold_decide(K.pack_scales(e8))
-
-
 def test_capacity_and_pick_mt():
     assert K.capacity(512, 288, 16) == (512 + 288 * 15 + 15) // 16 * 16
     assert K.pick_mt(8, 288) == 1 and K.pick_mt(65536, 288) == 4 and K.pick_mt(288 * 20, 288) == 2
@@ -149,3 +140,17 @@ def test_align_block_size_ref_matches_oracle_align():
         assert N == int(rt[0])
         assert np.array_equal(s[:N].numpy(), rs[:N]) and np.array_equal(e[: N // blk].numpy(), re_[: N // blk])
         assert bool((s[N:] == n).all()) and bool((e[N // blk:] == -1).all())
+
+
+def test_expected_blocks_closed_form():
+    """expected_blocks is E (1 - (1 - k/E)^T): checked against a brute-force count of distinct experts over random
+    top-k draws (uniform routing), and its limits (one token -> k experts; many tokens -> E)."""
+    import numpy as np
+    from r9700_vllm.kernels import moe as K
+    assert abs(K.expected_blocks(8, 288, 8) - 8.0) < 1e-9
+    assert abs(K.expected_blocks(8 * 100000, 288, 8) - 288.0) < 1e-6
+    rng = np.random.default_rng(5)
+    for T in (16, 64, 100):
+        d = np.mean([len(np.unique(np.concatenate([rng.choice(288, 8, replace=False) for _ in range(T)])))
+                     for _ in range(200)])
+        assert abs(K.expected_blocks(T * 8, 288, 8) - d) < 0.03 * d, (T, d)
