@@ -50,26 +50,40 @@ constexpr int HCH = 2;             // 8-value activation chunks a thread at most
 constexpr long MAX_WG = 16384;     // workgroups of one launch at most; more blocks are walked grid-stride
 constexpr int LDS_MAX = 96 * 1024;
 
-// The block's 16 rows of activation codes (K bytes each) into LDS at `dst` (row stride K + APAD). Padding rows read
-// the block's first row. Every load of a thread is in flight before the first store; chunks past the rows clamp to
-// the last chunk, whose own bytes those threads store again, so no load or store sits under a branch (a load under
-// a branch is waited for inside it).
-__device__ __forceinline__ void stage_rows(uint8_t* dst, const uint8_t* __restrict__ A, int fr_l, int first, int numel,
-                                           int a_row_div, int K, int tid) {
-  const int cpr = K / 16, astride = K + APAD;
+// The block's 16 rows of activation codes (K bytes each) into LDS at `dst` (row stride K + APAD), in two halves so
+// the caller can put other loads between them: stage_load issues every load of a thread (padding rows read the
+// block's first row), stage_store writes them. Chunks past the rows clamp to the last chunk, whose own bytes those
+// threads store again, so no load or store sits under a branch (a load under a branch is waited for inside it).
+struct Staged {
   uint4 av[ACH];
   int at[ACH];
+};
+__device__ __forceinline__ void stage_load(Staged& sg, const uint8_t* __restrict__ A, int fr_l, int first, int numel,
+                                           int a_row_div, int K, int tid) {
+  const int cpr = K / 16, astride = K + APAD;
 #pragma unroll
   for (int it = 0; it < ACH; it++) {
     const int c = min(tid + it * NW * WAVE, BLK * cpr - 1);
     const int i = c / cpr, q = c - i * cpr;
     int fr = __shfl(fr_l, i, WAVE);
     if (fr < 0 || fr >= numel) fr = first;
-    av[it] = reinterpret_cast<const uint4*>(A + (size_t)(fr / a_row_div) * K)[q];
-    at[it] = i * astride + q * 16;
+    sg.av[it] = reinterpret_cast<const uint4*>(A + (size_t)(fr / a_row_div) * K)[q];
+    sg.at[it] = i * astride + q * 16;
   }
+}
+__device__ __forceinline__ void stage_store(const Staged& sg, uint8_t* dst) {
 #pragma unroll
-  for (int it = 0; it < ACH; it++) *reinterpret_cast<uint4*>(dst + at[it]) = av[it];
+  for (int it = 0; it < ACH; it++) *reinterpret_cast<uint4*>(dst + sg.at[it]) = sg.av[it];
+}
+
+// Per-row factors of the block for the lanes r < 16 of every wave (loaded unconditionally, from the block's first
+// row for padding rows): the token's activation scale and, with topk_w, the router weight.
+__device__ __forceinline__ void row_factors(const float* __restrict__ As, const float* __restrict__ topk_w, int fr_l,
+                                            int first, int numel, int a_row_div, float& as, float& tw) {
+  const bool live = fr_l >= 0 && fr_l < numel;
+  const int fr = live ? fr_l : first;
+  as = As[fr / a_row_div];
+  tw = topk_w ? topk_w[fr] : 1.f;
 }
 
 // Unit claim: lane 0 takes the next unit index from the workgroup's counter; the value is wave-uniform.
@@ -127,15 +141,26 @@ __device__ __forceinline__ void load_batch(Batches<TG, U>& bs, int un, int b, in
     }
 }
 
-// One wave's part of a block's units. Set 0 already holds the loads of batch 0 of unit `un` (load_batch), which the
-// wave owns before any claim (units 0 .. NW-1 go to waves 0 .. NW-1; the counter starts at NW); further units are
-// claimed from the counter. Unit `un` covers column tiles tile0 + un * TG .. + TG - 1 over nkt K-tiles (nkt % U == 0)
-// in batches of U; A fragments from the LDS rows at `arow` (lane r's row, 16 g bytes in). The two sets alternate, so
-// while one batch's MFMAs run the next batch's loads are in flight (the same unit's next K-tiles, or the first of the
-// next claimed unit). done(un, acc) runs after a unit's last batch.
+// One wave's part of a block's units. Units 0 .. NW-1 go to waves 0 .. NW-1 before any claim, and with nb == 1
+// batch a unit also units NW .. 2 NW - 1 (first_units); further units are claimed from the counter, which the caller
+// set to first_units(...). On entry the wave's first two batches are in flight (issue_first: set 0 = batch 0 of unit
+// `wave`, set 1 = its successor), so a barrier the caller puts between issue_first and this call does not empty the
+// wave's queue. Unit `un` covers column tiles tile0 + un * TG .. + TG - 1 over nkt K-tiles (nkt % U == 0) in batches
+// of U; A fragments from the LDS rows at `arow` (lane r's row, 16 g bytes in). The two sets alternate, so while one
+// batch's MFMAs run the next batch's loads are in flight. done(un, acc) runs after a unit's last batch.
+__device__ __forceinline__ int first_units(int nkt, int U) { return nkt / U == 1 ? 2 * NW : NW; }
+
+template <int TG, int U>
+__device__ __forceinline__ void issue_first(Batches<TG, U>& bs, int wave, int units, int tile0, int nkt,
+                                            const ExpertRsrc& x, uint32_t kbytes, uint32_t sbytes, int lane) {
+  load_batch<0>(bs, wave, 0, units, tile0, x, kbytes, sbytes, lane);
+  if (nkt / U > 1) load_batch<1>(bs, wave, 1, units, tile0, x, kbytes, sbytes, lane);
+  else load_batch<1>(bs, wave + NW, 0, units, tile0, x, kbytes, sbytes, lane);
+}
+
 template <int TG, int U, class Done>
-__device__ __forceinline__ void stream_units(Batches<TG, U>& bs, int un, int* counter, int units, int tile0, int nkt,
-                                             const ExpertRsrc& x, uint32_t kbytes, uint32_t sbytes,
+__device__ __forceinline__ void stream_units(Batches<TG, U>& bs, int wave, int* counter, int units, int tile0,
+                                             int nkt, const ExpertRsrc& x, uint32_t kbytes, uint32_t sbytes,
                                              const uint8_t* arow, int lane, Done&& done) {
   const int nb = nkt / U;
   v4f acc[TG];
@@ -160,9 +185,9 @@ __device__ __forceinline__ void stream_units(Batches<TG, U>& bs, int un, int* co
 #pragma unroll
     for (int j = 0; j < TG; j++) acc[j] = (v4f){0.f, 0.f, 0.f, 0.f};
   };
-  if (un >= units) return;
-  int b = 0;
-  int un2 = un, b2 = 0;
+  // (un, b): the batch in the set about to be computed; (un2, b2): the one after it
+  int un = wave, b = 0;
+  int un2 = nb > 1 ? wave : wave + NW, b2 = nb > 1 ? 1 : 0;
   auto advance = [&]() {
     if (b2 + 1 < nb) {
       b2++;
@@ -171,10 +196,10 @@ __device__ __forceinline__ void stream_units(Batches<TG, U>& bs, int un, int* co
       b2 = 0;
     }
   };
-  advance();
+  if (un >= units) return;
   reset();
+  // set 0 holds (un, b), set 1 holds (un2, b2)
   for (;;) {
-    load_batch<1>(bs, un2, b2, units, tile0, x, kbytes, sbytes, lane);
     compute(std::integral_constant<int, 0>{}, b);
     if (b == nb - 1) {
       done(un, acc);
@@ -194,6 +219,7 @@ __device__ __forceinline__ void stream_units(Batches<TG, U>& bs, int un, int* co
     un = un2;
     b = b2;
     advance();
+    load_batch<1>(bs, un2, b2, units, tile0, x, kbytes, sbytes, lane);
   }
 }
 
@@ -279,7 +305,7 @@ __global__ void __launch_bounds__(NW * WAVE) moe_stream_kernel(
   const auto crs = __builtin_amdgcn_make_buffer_rsrc(Cout, (short)0, (int)cbytes, 0x00020000);
 
   const int wave = __builtin_amdgcn_readfirstlane(tid / WAVE);
-  if (tid == 0) s_next = NW;                                // units 0 .. NW-1 belong to waves 0 .. NW-1
+  if (tid == 0) s_next = first_units(K / KT, U);            // the units each wave owns before any claim
   Batches<TG, U> bs;
 
   for (int rb = blockIdx.y; rb < ny; rb += gridDim.y) {
@@ -288,16 +314,17 @@ __global__ void __launch_bounds__(NW * WAVE) moe_stream_kernel(
     if (hd == 0) break;
     if (hd == 1) continue;
     const ExpertRsrc x = expert_rsrc(Wq, Ws, wq_estride, ws_estride, e);
-    // this wave's first unit goes out before the rows are staged: its bytes arrive during the staging round trip
-    load_batch<0>(bs, wave, 0, units, tile0, x, 8u * K, K / 2, lane);
-    stage_rows(lds, A, fr_l, first, numel, a_row_div, K, tid);
+    // the rows' loads first, then this wave's first unit: the staging waits only for its own loads (vmcnt counts in
+    // issue order) while the weight bytes arrive behind them
+    Staged sg;
+    stage_load(sg, A, fr_l, first, numel, a_row_div, K, tid);
+    float ras, rtw;
+    row_factors(As, EPI == 0 ? topk_w : nullptr, fr_l, first, numel, a_row_div, ras, rtw);
+    issue_first(bs, wave, units, tile0, K / KT, x, 8u * K, K / 2, lane);
+    stage_store(sg, lds);
     if (tid < BLK) {
-      const bool live = fr_l >= 0 && fr_l < numel;
-      const int fr = live ? fr_l : first;
-      float sc = As[fr / a_row_div];
-      if (EPI == 0 && topk_w) sc *= topk_w[fr];
-      s_fr[tid] = live ? fr : -1;
-      s_sc[tid] = sc;
+      s_fr[tid] = fr_l >= 0 && fr_l < numel ? fr_l : -1;
+      s_sc[tid] = ras * rtw;
       s_max[tid] = 0u;
     }
     __syncthreads();
@@ -331,7 +358,7 @@ __global__ void __launch_bounds__(NW * WAVE) moe_stream_kernel(
                        [&](int i, float s) { Cs[s_fr[i]] = s; });
     }
     __syncthreads();                                        // every claim and LDS read of this block done
-    if (tid == 0) s_next = NW;                              // for the next block (its staging barrier follows)
+    if (tid == 0) s_next = first_units(K / KT, U);          // for the next block (its staging barrier follows)
   }
 }
 
@@ -363,7 +390,8 @@ __global__ void __launch_bounds__(NW * WAVE) moe_stream_layer_kernel(
   const auto crs = __builtin_amdgcn_make_buffer_rsrc(C, (short)0, (int)cbytes, 0x00020000);
 
   const int wave = __builtin_amdgcn_readfirstlane(tid / WAVE);
-  if (tid < 2) s_next[tid] = NW;                            // units 0 .. NW-1 of each GEMM belong to waves 0 .. NW-1
+  // the units each wave owns before any claim, per GEMM
+  if (tid < 2) s_next[tid] = tid == 0 ? first_units(K1 / KT, U1) : first_units(N1 / 2 / KT, U2);
   Batches<1, U1> b1;
   Batches<TG2, U2> b2;
   const int units1 = N1 / 16, units2 = N2 / (16 * TG2);
@@ -375,15 +403,18 @@ __global__ void __launch_bounds__(NW * WAVE) moe_stream_layer_kernel(
     if (hd == 1) continue;
     const ExpertRsrc x1 = expert_rsrc(W1q, W1s, w1q_estride, w1s_estride, e);
     const ExpertRsrc x2 = expert_rsrc(W2q, W2s, w2q_estride, w2s_estride, e);
-    // this wave's first gate_up unit goes out before the rows are staged
-    load_batch<0>(b1, wave, 0, units1, 0, x1, 8u * K1, K1 / 2, lane);
-    stage_rows(lds, A, fr_l, first, numel, a_row_div, K1, tid);
+    // the rows' loads first, then this wave's first gate_up unit: the staging waits only for its own loads (vmcnt
+    // counts in issue order) while the weight bytes arrive behind them
+    Staged sg;
+    stage_load(sg, A, fr_l, first, numel, a_row_div, K1, tid);
+    float ras, rtw;
+    row_factors(As, topk_w, fr_l, first, numel, a_row_div, ras, rtw);
+    issue_first(b1, wave, units1, 0, K1 / KT, x1, 8u * K1, K1 / 2, lane);
+    stage_store(sg, lds);
     if (tid < BLK) {
-      const bool live = fr_l >= 0 && fr_l < numel;
-      const int fr = live ? fr_l : first;
-      s_sc[tid] = As[fr / a_row_div];
-      s_tw[tid] = topk_w ? topk_w[fr] : 1.f;
-      s_fr[tid] = live ? fr : -1;
+      s_sc[tid] = ras;
+      s_tw[tid] = rtw;
+      s_fr[tid] = fr_l >= 0 && fr_l < numel ? fr_l : -1;
       s_max[tid] = 0u;
     }
     __syncthreads();
@@ -394,8 +425,8 @@ __global__ void __launch_bounds__(NW * WAVE) moe_stream_layer_kernel(
 #pragma unroll
       for (int q = 0; q < 4; q++) gu[(4 * g + q) * N1 + un * 16 + r] = f2bf(acc[0][q] * s_sc[4 * g + q]);
     });
-    // this wave's first down unit goes out before the SiLU: its bytes arrive during the barriers and the activation
-    load_batch<0>(b2, wave, 0, units2, 0, x2, 8u * I, I / 2, lane);
+    // this wave's first down batches go out before the SiLU: their bytes arrive during the barriers and the activation
+    issue_first(b2, wave, units2, 0, I / KT, x2, 8u * I, I / 2, lane);
     __syncthreads();
 
     // SiLU + quant into LDS; padding rows' codes are never read for a stored output
@@ -420,7 +451,7 @@ __global__ void __launch_bounds__(NW * WAVE) moe_stream_layer_kernel(
       }
     });
     __syncthreads();                                        // every claim and LDS read of this block done
-    if (tid < 2) s_next[tid] = NW;                          // for the next block (its staging barrier follows)
+    if (tid < 2) s_next[tid] = tid == 0 ? first_units(K1 / KT, U1) : first_units(I / KT, U2);   // for the next block
   }
 }
 
@@ -537,7 +568,7 @@ extern "C" int r9k_moe_stream_layer(long a, long as, long w1q, long w1s, long w2
   const size_t smem = (size_t)BLK * (K1 + APAD) + (size_t)BLK * N1 * 2 + (size_t)BLK * (I + APAD);
   if (smem > (size_t)LDS_MAX) return 2;
   const int U1 = env_int("R9K_STREAM_U", batch_of(K1 / KT, 4));
-  const int TG2 = env_int("R9K_STREAM_TG", 1), U2 = env_int("R9K_STREAM_U2", batch_of(I / KT, 4));
+  const int TG2 = env_int("R9K_STREAM_TG", 1), U2 = env_int("R9K_STREAM_U2", batch_of(I / KT, 2));
   if ((K1 / KT) % U1 || (I / KT) % U2 || (N2 / 16) % TG2) return 2;
   const long ny = max_blocks < MAX_WG ? max_blocks : MAX_WG;
   const hipStream_t st = (hipStream_t)stream;
@@ -552,8 +583,7 @@ extern "C" int r9k_moe_stream_layer(long a, long as, long w1q, long w1s, long w2
                        w1s_estride, (long)N2 * I / 2, w2s_estride, numel, a_row_div, K1, N1, N2, (int)ny);       \
     return hipGetLastError() == hipSuccess ? 0 : -6;                                                               \
   }
-  L(4, 2, 2) L(4, 2, 1) L(4, 1, 4) L(4, 1, 2) L(4, 1, 1) L(2, 2, 2) L(2, 2, 1) L(2, 1, 4) L(1, 2, 2) L(1, 2, 1)
-  L(1, 1, 4)
+  L(4, 1, 2) L(4, 1, 1) L(4, 2, 1) L(2, 1, 2) L(2, 1, 1) L(2, 2, 1) L(1, 1, 2) L(1, 1, 1) L(1, 2, 1)
 #undef L
   return 2;
 }
