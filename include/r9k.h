@@ -148,8 +148,9 @@ int r9k_moe_route_dual(long logits, int ldl, long weights, long ids, long sorted
 
 /* Align tables only, from ids int32 [numel] (the role of vLLM's moe_align_block_size, called at
  * r9700_vllm/moe/experts.py:172 of the reference). ids outside [0, E) are left out. scratch: at least
- * r9k_moe_align_scratch_ints(numel, E) int32: the per-chunk histograms of the multi-workgroup path (rewritten by
- * every call, so its contents at entry do not matter); calls sharing one scratch must not overlap. */
+ * r9k_moe_align_scratch_ints(numel, E) int32 (1 up to 4096 routed rows, else 16 + ceil(numel / 2048) * E): the
+ * per-chunk histograms of the multi-workgroup path (rewritten by every call, so its contents at entry do not matter);
+ * calls sharing one scratch must not overlap. */
 int r9k_moe_align(long ids, int numel, int E, int blk, long sorted_ids, long expert_ids, long ntpp, long scratch,
                   long scratch_ints, long stream);
 long r9k_moe_align_scratch_ints(int numel, int E);

@@ -815,7 +815,7 @@ int launch_topk(const uint16_t* logits, int ldl, float* w, int* ids, int M, int 
 // histogram + placement launches over CH-row chunks (scratch: align_scratch_ints(numel, E) int32 for the chunk
 // histograms, which the count launch overwrites).
 long align_scratch_ints(int numel, int E) {
-  return numel <= SMALL_MAX ? 1 : ALIGN_HIST + (long)((numel + CH - 1) / CH + 2) * E + 1;
+  return numel <= SMALL_MAX ? 1 : ALIGN_HIST + (long)((numel + CH - 1) / CH) * E;
 }
 
 int launch_align(const int* ids, int numel, int E, int blk, int* sorted_ids, int* expert_ids, int* ntpp,

@@ -62,42 +62,67 @@ def mxfp4_gemm_q(q: torch.Tensor, s: torch.Tensor, W, out: torch.Tensor, M: int,
     KM.moe_gemm(q, s, W, out, *tabs, M, 1, topk_w, *cfg[:3], num_experts=1, MT=MT)
 
 
+# The prefill GEMMs address their activation rows and their output through 32-bit buffer ranges, so one launch may
+# touch at most this many bytes of either; a longer dense linear runs as row ranges (row_ranges), each a launch of its
+# own over its own identity tables.
+BUF_LIMIT = (1 << 31) - 1
+
+
+def row_ranges(M: int, N: int, K: int, limit: int = BUF_LIMIT) -> list:
+    """[(r0, r1), ...] covering rows 0..M, as few and as even as possible, each range's output [r1 - r0, N] bf16 and
+    fp8 activation codes [r1 - r0, K] within `limit` bytes."""
+    per_row = max(2 * N, K, 1)
+    n = -(-M // max(1, limit // per_row)) if M else 0
+    bounds = [M * i // n for i in range(n + 1)] if n else [0]
+    return list(zip(bounds[:-1], bounds[1:]))
+
+
+def _mxfp4_linear_rows(x: torch.Tensor, W, out: torch.Tensor, fold: bool) -> None:
+    from .kernels import moe as KM
+    M = x.shape[0]
+    if M <= KM.DENSE_QA_MAX_M and not fold and KM.dense_mxfp4_qa(x, W, out):   # decode widths: quant in the launch
+        return
+    q, s = KM.quant_rows_fp8(x)
+    mxfp4_gemm_q(q, s, W, out, M, KM.pick_cfg(W.N, W.K, M=M, kind="mxfp4", fold=fold))
+
+
 def _mxfp4_linear(x: torch.Tensor, wq: torch.Tensor, wsr: torch.Tensor, N: int, K: int, fold: bool = False
                   ) -> torch.Tensor:
     from .kernels import moe as KM
     M = x.shape[0]
     out = torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
-    if M == 0:
-        return out
     W = KM.Mxfp4Experts(wq, wsr, N, K, fold)
-    if M <= KM.DENSE_QA_MAX_M and KM.dense_mxfp4_qa(x, W, out):   # decode widths: the quant inside the GEMM launch
-        return out
-    q, s = KM.quant_rows_fp8(x)
-    mxfp4_gemm_q(q, s, W, out, M, KM.pick_cfg(N, K, M=M, kind="mxfp4", fold=fold))
+    for r0, r1 in row_ranges(M, N, K):
+        _mxfp4_linear_rows(x[r0:r1], W, out[r0:r1], fold)
     return out
 
 
-def _nvfp4_linear(x: torch.Tensor, wq: torch.Tensor, ws: torch.Tensor, wg: torch.Tensor, N: int, K: int
-                  ) -> torch.Tensor:
-    """Native NVFP4 weights (prepare_nvfp4_weights of one expert) with per-row fp8 activations: one launch with the
-    quant inside up to DENSE_NV_QA_MAX_M rows, the decode-family kernel below NV_PREFILL_MIN_M rows, the 128 x 128-tile
-    prefill kernel (r9k_moe_4bit_prefill nv = 1) from there."""
+def _nvfp4_linear_rows(x: torch.Tensor, W, out: torch.Tensor) -> None:
     from .kernels import moe as KM
     M = x.shape[0]
-    out = torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
-    if M == 0:
-        return out
-    W = KM.Nvfp4Experts(wq, ws, wg, N, K)
     if M <= KM.DENSE_NV_QA_MAX_M and KM.dense_nvfp4_qa(x, W, out):   # decode widths: the quant inside the GEMM launch
-        return out
+        return
     q, s = KM.quant_rows_fp8(x)
-    if M >= KM.NV_PREFILL_MIN_M and K % 32 == 0:
+    if M >= KM.NV_PREFILL_MIN_M and W.K % 32 == 0:
         tabs = IdentityTables.get(x.device, M, KM.prefill_block(KM.NV_PREFILL_CFG))
         KM.moe_gemm(q, s, W, out, *tabs, M, 1, None, num_experts=1, prefill=KM.NV_PREFILL_CFG)
     else:
         MT = _decode_mt(M)
         tabs = IdentityTables.get(x.device, M, KM.MOE_BLOCK * MT)
         KM.moe_gemm(q, s, W, out, *tabs, M, 1, None, num_experts=1, MT=MT)
+
+
+def _nvfp4_linear(x: torch.Tensor, wq: torch.Tensor, ws: torch.Tensor, wg: torch.Tensor, N: int, K: int
+                  ) -> torch.Tensor:
+    """Native NVFP4 weights (prepare_nvfp4_weights of one expert) with per-row fp8 activations: one launch with the
+    quant inside up to DENSE_NV_QA_MAX_M rows, the decode-family kernel below NV_PREFILL_MIN_M rows, the 128 x 128-tile
+    prefill kernel (r9k_moe_4bit_prefill nv = 1) from there; row ranges past the 2 GiB buffer range (row_ranges)."""
+    from .kernels import moe as KM
+    M = x.shape[0]
+    out = torch.empty((M, N), dtype=torch.bfloat16, device=x.device)
+    W = KM.Nvfp4Experts(wq, ws, wg, N, K)
+    for r0, r1 in row_ranges(M, N, K):
+        _nvfp4_linear_rows(x[r0:r1], W, out[r0:r1])
     return out
 
 

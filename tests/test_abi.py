@@ -57,7 +57,7 @@ def test_shape_errors_before_launch():
     assert L.r9k_moe_topk(1, 64, 1, 1, 1, 64, 65, 1, z) == 1
     assert L.r9k_moe_align(1, 100000, 64, 64, 1, 1, 1, 1, 1, z) == 1          # scratch too small
     assert L.r9k_moe_align_scratch_ints(4096, 64) == 1
-    assert L.r9k_moe_align_scratch_ints(65536, 288) == 16 + (32 + 2) * 288 + 1   # counter, 32 chunk rows, 2 more, total
+    assert L.r9k_moe_align_scratch_ints(65536, 288) == 16 + 32 * 288          # 16 unused ints, 32 chunk histograms
     # sum: N % 8
     assert L.r9k_moe_sum(16, 0, 16, 1, 8, 12, 0, 12, z) == 1
     # quant: nothing to do for M == 0; tiled gate refused

@@ -157,6 +157,43 @@ def test_dense_mxfp4_linear_config4_prefill_sampled(dev):
     assert r < 2e-3 and cosine(bf16_bits_to_f64(got), bf16_bits_to_f64(ref)) > 0.99999
 
 
+@pytest.mark.parametrize("kind", ["mxfp4", "nvfp4"])
+def test_dense_linear_output_past_2gib(dev, kind):
+    """A dense linear whose bf16 output just crosses 2 GiB (config 4's N = 17408, M = 61682 rows, K = 1024): ops runs
+    it as two row ranges, each inside the kernels' 32-bit buffer range. Checked on the first and last rows of each
+    range and 24 random rows against the oracle."""
+    M, N, Kd = 61682, 17408, 1024
+    assert M * N * 2 > ops.BUF_LIMIT
+    ranges = ops.row_ranges(M, N, Kd)
+    assert len(ranges) == 2
+    print(f"dense {kind} past 2 GiB: M={M} N={N} K={Kd} ranges={ranges}", flush=True)
+    g = torch.Generator().manual_seed(61682 + (kind == "nvfp4"))
+    x = torch.randn(M, Kd, generator=g).to(torch.bfloat16)
+    edge = [r for r0, r1 in ranges for r in (r0, r0 + 1, r1 - 2, r1 - 1)]
+    rows = np.unique(np.concatenate([edge, np.random.default_rng(1).choice(M, 24, replace=False)]))
+    qo, so = O.quant_rows_fp8(x[torch.from_numpy(rows)])
+    zero = np.zeros(rows.size, dtype=np.int32)
+    if kind == "mxfp4":
+        packed, e8 = make_experts(1, N, Kd, g)
+        W = K.prepare_mxfp4_weights(packed.to(dev), e8.to(dev))
+        out = ops.mxfp4_linear(x.to(dev), W.wq, W.wsr, N, Kd)
+        ref = O.grouped_gemm(qo, so, {0: O.mxfp4_dequant(packed[0], e8[0], torch.float32)}, zero, 1,
+                             acc_dtype=torch.float32)
+    else:
+        packed = torch.randint(0, 256, (1, N, Kd // 2), generator=g, dtype=torch.int32).to(torch.uint8)
+        s16 = (torch.randn(1, N, Kd // 16, generator=g).abs() * 0.05).to(torch.float8_e4m3fn)
+        wg = torch.rand(1, N, generator=g) * 1.5 + 0.5
+        W = K.prepare_nvfp4_weights(packed.to(dev), s16.to(dev), wg.to(dev))
+        out = ops.nvfp4_linear(x.to(dev), W.wq, W.ws, W.wg, N, Kd)
+        ref = O.nvfp4_gemm(qo, so, packed.numpy(), s16.view(torch.uint8).numpy(), wg.numpy(), zero, 1)
+    got = O.bf16_bits(out[torch.from_numpy(rows).to(dev)])
+    del out
+    a, b = bf16_bits_to_f64(got), bf16_bits_to_f64(ref)
+    r, c = rel_err(a, b), cosine(a, b)
+    print(f"  rel {r:.2e} cos {c:.7f}", flush=True)
+    assert not np.isnan(a.numpy()).any() and r < 2e-3 and c > 0.99999
+
+
 def test_nvfp4_to_mxfp4_config4_bit_exact(dev):
     """BASELINE config 4 full shape: [17408, 5120] NVFP4 (uniform codes, s16 = e4m3(|N(0,1)| * 0.05), global 1)."""
     g = torch.Generator().manual_seed(20261201 + 4000)
@@ -596,7 +633,7 @@ def decode_gemm(q, s, W, out, M, topk_w=None):
 
 @pytest.mark.parametrize("M,N,Kd", [(1, 17408, 5120), (2, 17408, 5120), (4, 17408, 5120), (3, 1024, 2048),
                                     (4, 1024, 2048), (3, 48, 1024), (2, 272, 384), (1, 64, 8192), (4, 64, 8192),
-                                    (1, 32, 256), (4, 16, 896)])
+                                    (1, 32, 256), (4, 16, 896), (1, 17408, 4992), (2, 2064, 4864)])
 def test_dense_qa_equals_two_launches(dev, M, N, Kd):
     """r9k_dense_mxfp4_qa (the activation quant inside the dense GEMM launch, M <= 4) against quant_rows_fp8 + the
     decode GEMM over identity tables: bit for bit (same K split over waves), and within the GEMM tolerance of the

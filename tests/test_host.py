@@ -154,3 +154,22 @@ def test_expected_blocks_closed_form():
         d = np.mean([len(np.unique(np.concatenate([rng.choice(288, 8, replace=False) for _ in range(T)])))
                      for _ in range(200)])
         assert abs(K.expected_blocks(T * 8, 288, 8) - d) < 0.03 * d, (T, d)
+
+
+def test_dense_row_ranges_stay_in_the_buffer_range():
+    """ops.row_ranges: ranges cover 0..M in order without gaps, each range's output (2N bytes a row) and activation
+    codes (K bytes a row) within the 2 GiB limit, as few ranges as that allows, balanced to one row."""
+    from r9700_vllm import ops
+    for M, N, K in ((0, 17408, 5120), (1, 17408, 5120), (61680, 17408, 5120), (61681, 17408, 5120),
+                    (200000, 17408, 5120), (10, 8, 1 << 30), (7, 3, 5)):
+        rr = ops.row_ranges(M, N, K)
+        if M == 0:
+            assert rr == []
+            continue
+        assert rr[0][0] == 0 and rr[-1][1] == M and all(a[1] == b[0] for a, b in zip(rr, rr[1:]))
+        per = max(2 * N, K)
+        assert all((r1 - r0) * per <= ops.BUF_LIMIT for r0, r1 in rr)
+        assert len(rr) == -(-M // (ops.BUF_LIMIT // per))
+        sizes = [r1 - r0 for r0, r1 in rr]
+        assert max(sizes) - min(sizes) <= 1
+    assert len(ops.row_ranges(61680, 17408, 5120)) == 1 and len(ops.row_ranges(61681, 17408, 5120)) == 2

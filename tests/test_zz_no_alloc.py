@@ -40,10 +40,16 @@ def test_align_noalloc_equals_align(dev, E, topk, blk, Ts):
 
 
 def test_align_noalloc_refuses_oversize(dev):
+    """The array holds 16 + 255 chunk histograms of E = 1024: 255 * 2048 routed rows are served (tables as
+    r9k_moe_align's), one more row needs a 256th chunk and is refused before any launch."""
     L = K.lib()
-    E, numel = 1024, 600000                          # (ceil(600000 / 2048) + 2) * 1024 + 17 ints > 2^18
-    assert L.r9k_moe_align_scratch_ints(numel, E) > L.r9k_moe_align_noalloc_max_ints()
-    ids = torch.zeros(numel, dtype=torch.int32, device=dev)
+    E, numel = 1024, 255 * 2048
+    assert L.r9k_moe_align_scratch_ints(numel, E) == 16 + 255 * 1024 <= L.r9k_moe_align_noalloc_max_ints()
+    assert L.r9k_moe_align_scratch_ints(numel + 1, E) == 16 + 256 * 1024 > L.r9k_moe_align_noalloc_max_ints()
+    ids = torch.randint(0, E, (numel + 1,), generator=torch.Generator().manual_seed(7), dtype=torch.int32).to(dev)
+    a = _tables(K.moe_align, ids[:numel], 256, E)
+    b = _tables(K.moe_align_noalloc, ids[:numel], 256, E)
+    assert a[2] == b[2] and np.array_equal(a[0], b[0]) and np.array_equal(a[1], b[1])
     with pytest.raises(RuntimeError, match="scratch ints"):
         K.moe_align_noalloc(ids, 256, E)
-    assert L.r9k_moe_align_noalloc(ids.data_ptr(), numel, E, 256, 0, 0, 0, 0) == -9   # refused before any launch
+    assert L.r9k_moe_align_noalloc(ids.data_ptr(), numel + 1, E, 256, 0, 0, 0, 0) == -9   # refused before any launch
