@@ -49,3 +49,21 @@ def check_tables(sorted_ids, expert_ids, ntpp, ids, blk: int, numel: int, E: int
                 assert flat[x] == e[b], f"row {x} (expert {flat[x]}) in a block of expert {e[b]}"
     cnt = np.bincount(np.asarray(flat, dtype=np.int64), minlength=E)
     assert n == int(sum((c + blk - 1) // blk * blk for c in cnt)), "ntpp != sum of padded counts"
+
+
+def block_edge_tokens(ids, E: int, blk: int, topk: int) -> np.ndarray:
+    """Sorted tokens that hold the first or the last live routed row of some blk-row block of the canonical align
+    tables over ids [T, topk] (every block of every expert, the hot expert's included): a check on these tokens
+    reads every block's edges."""
+    from oracle import oracle as O
+    flat = np.asarray(ids).reshape(-1)
+    numel = flat.size
+    s, _, n = O.align(flat, E, blk)
+    s = s[: int(n[0])].reshape(-1, blk)
+    live = s < numel
+    nl = live.sum(1)
+    keep = nl > 0
+    first = s[keep, 0]                                      # live rows lead each block, padding follows
+    last = s[keep, nl[keep] - 1]
+    assert (live[keep, 0]).all() and (s[keep][np.arange(keep.sum()), nl[keep] - 1] < numel).all()
+    return np.unique(np.concatenate([first, last]) // topk)

@@ -7,7 +7,7 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import bf16_bits_to_f64, cosine, make_experts, rel_err
+from helpers import bf16_bits_to_f64, block_edge_tokens, cosine, make_experts, rel_err
 from oracle import oracle as O
 from r9700_vllm import ops
 from r9700_vllm.kernels import moe as K
@@ -74,6 +74,13 @@ def test_grouped_gemm_prefill_256(dev, E, M, topk, N, Kd, down):
     a column block past N, one and several 256-row blocks per expert, blocks of ~25 live rows whose other 64-row
     pieces are never loaded)."""
     gemm_case(dev, E, M, topk, N, Kd, seed=E + M + N + Kd, prefill=12, down=down)
+
+
+@pytest.mark.parametrize("down", [False, True])
+def test_grouped_gemm_prefill_256_config5_widths(dev, down):
+    """The whole output of the 256-row prefill GEMM at config 5's widths (gate_up N = K = 4096, down N = 4096 with
+    K = 2048) over 4 experts, against the fp64 oracle."""
+    gemm_case(dev, 4, 700, 2, 4096, 2048 if down else 4096, seed=4096 + down, prefill=12, down=down)
 
 
 @pytest.mark.parametrize("E,M,topk,N,gate_up,zipf", [
@@ -245,7 +252,9 @@ def make_layer(dev, E, H, I, seed, lo=118, hi=126):
     return (p13, e13), (p2, e2), W13, W2
 
 
-def run_layer(dev, E, H, I, T, topk, seed, tokens=None, zipf=False, lo=118, hi=126):
+def run_layer(dev, E, H, I, T, topk, seed, tokens=None, zipf=False, lo=118, hi=126, edges=None, extra=0):
+    """The layer through apply() against the oracle on `tokens` (default all), or, with `edges`, on the tokens
+    holding the first and last live row of every `edges`-row block plus `extra` random tokens."""
     (p13, e13), (p2, e2), W13, W2 = make_layer(dev, E, H, I, seed, lo, hi)
     g = torch.Generator().manual_seed(seed + 1)
     x = torch.randn(T, H, generator=g).to(torch.bfloat16)
@@ -261,6 +270,9 @@ def run_layer(dev, E, H, I, T, topk, seed, tokens=None, zipf=False, lo=118, hi=1
     torch.cuda.synchronize()
     ro = O.route(logits, topk, True)
     assert np.array_equal(ids.cpu().numpy(), ro[1]), "routing ids"
+    if edges:
+        rnd = np.random.default_rng(seed).choice(T, extra, replace=False)
+        tokens = np.union1d(block_edge_tokens(ro[1], E, edges, topk), rnd)
     need = np.unique(ro[1][tokens] if tokens is not None else ro[1])
     sub = lambda p: {int(e): p[int(e)].cpu() for e in need}                         # only touched experts
     c13 = (_Lazy(sub(p13)), _Lazy(sub(e13)))
@@ -290,8 +302,8 @@ def test_layer_config2_decode(dev, T):
 
 
 def test_layer_config3_prefill_sampled(dev):
-    tokens = np.random.default_rng(3).choice(8192, 96, replace=False)
-    run_layer(dev, 288, 2048, 512, 8192, 8, seed=20261201 + 3000 + 8192, tokens=np.sort(tokens))
+    """Config 3 on the tokens holding every 256-row block's first and last live row, plus 32 random tokens."""
+    run_layer(dev, 288, 2048, 512, 8192, 8, seed=20261201 + 3000 + 8192, edges=256, extra=32)
 
 
 @pytest.mark.parametrize("T", [1, 32])
@@ -300,8 +312,10 @@ def test_layer_config5_skewed(dev, T):
 
 
 def test_layer_config5_skewed_4096_sampled(dev):
-    tokens = np.sort(np.random.default_rng(5).choice(4096, 32, replace=False))
-    run_layer(dev, 384, 4096, 2048, 4096, 8, seed=20261201 + 5000 + 4096, tokens=tokens, zipf=True, lo=116, hi=126)
+    """Config 5 at T = 4096 (Zipf routing: the hot expert spans many 256-row blocks) on the tokens holding every
+    256-row block's first and last live row, plus 16 random tokens."""
+    run_layer(dev, 384, 4096, 2048, 4096, 8, seed=20261201 + 5000 + 4096, zipf=True, lo=116, hi=126, edges=256,
+              extra=16)
 
 
 @pytest.mark.parametrize("E,T,H,I,topk", [(288, 1, 2048, 512, 8), (288, 8, 2048, 512, 8), (288, 64, 2048, 512, 8),
@@ -474,7 +488,7 @@ def test_layer_config5_T256_router_handoff(dev, monkeypatch):
     print(f"cfg5 T=256 hand-off: touched {int((counts > 0).sum())}, 256-row blocks {nbig}, kept "
           f"{'256-row' if want_big else '16-row'} layout, bit-equal to it alone: {same}", flush=True)
     assert same
-    tokens = np.sort(np.random.default_rng(256).choice(T, 32, replace=False))
+    tokens = np.arange(T)                                      # every token: the whole output
     ro = O.route(logits, topk, True)
     assert np.array_equal(ids.cpu().numpy(), ro[1]), "routing ids"
     need = np.unique(ro[1][tokens])
