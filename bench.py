@@ -121,14 +121,15 @@ class Step:
 
     def __call__(self, c: int):
         K, route, L = self.K, self.route, self.layer
-        bb = route.dual_wanted(self.routed, self.numel, L.E) if self.fused else 0
+        fused = self.fused and not route.split_planned(self.routed, self.numel, L.E)
+        bb = route.dual_wanted(self.routed, self.numel, L.E) if fused else 0
         if bb == 256:
             # as R9kTopKRouter for a wide decode step of a layer that runs the device-picked pair: both layouts
             w, ids, xq, xs = route.moe_route_dual(self.logits, self.topk, True, self.blk, self.sid, self.eid,
                                                   self.ntpp, self.scratch, self.x, bb, *self.big, K.DEVICE_MIN_ROWS)
             self.routed._r9k_tables = route.Tables(ids, self.sid, self.eid, self.ntpp, self.blk, self.numel,
                                                    self.x, self.x._version, xq, xs, big=(*self.big, bb))
-        elif self.fused:
+        elif fused:
             w, ids, xq, xs = route.moe_route_quant(self.logits, self.topk, True, self.blk, self.sid, self.eid,
                                                    self.ntpp, self.scratch, self.x)
             self.routed._r9k_tables = route.Tables(ids, self.sid, self.eid, self.ntpp, self.blk, self.numel,

@@ -162,6 +162,16 @@ long r9k_moe_align_scratch_ints(int numel, int E);
 int r9k_moe_align_live(long ids, int numel, int E, int blk, long sorted_ids, long expert_ids, long ntpp,
                        long scratch, long scratch_ints, long stream);
 
+/* No counterpart in the reference (it sends every expert through one block size picked on the host): the tables of
+ * one routed step split by expert size on the device, for prefill steps whose routing leaves many experts with a
+ * handful of rows. Experts with more than thr rows get blk_big-row blocks in (sorted_big, expert_big, ntpp_big), the
+ * others blk_small-row blocks in the small tables; each table holds only its experts' rows (ascending within each
+ * expert, as r9k_moe_align) and is written up to its ntpp only (as r9k_moe_align_live). Capacities and scratch as
+ * r9k_moe_align's for each block size. 0 / 1 bad arguments or HIP error. */
+int r9k_moe_align_split(long ids, int numel, int E, int thr, int blk_big, long sorted_big, long expert_big,
+                        long ntpp_big, int blk_small, long sorted_small, long expert_small, long ntpp_small,
+                        long scratch, long scratch_ints, long stream);
+
 /* No counterpart in the reference. r9k_moe_align for callers that cannot allocate (code under HIP graph capture,
  * tight serving loops, harnesses that forbid hipMalloc): no scratch argument, nothing allocated; the multi-workgroup
  * path uses the library's own file-scope device array (r9k_moe_align_noalloc_max_ints() int32 = 1 MiB per GPU, held

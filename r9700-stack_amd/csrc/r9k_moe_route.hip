@@ -664,6 +664,42 @@ __global__ void __launch_bounds__(AT) align_single_kernel(const int* __restrict_
   build_tables(sh, lids, numel, E, blk, sorted_ids, expert_ids, ntpp, tail != 0);
 }
 
+// The split tables of launch_align_split in one workgroup (numel <= SMALL_MAX): one count of every id, then the big
+// experts' table (their rows only) and the small experts' table (the ids read again, the other rows left out).
+__global__ void __launch_bounds__(AT) align_split_single_kernel(
+    const int* __restrict__ ids, int numel, int E, int thr, int blk_big, int* __restrict__ sorted_big,
+    int* __restrict__ expert_big, int* __restrict__ ntpp_big, int blk_small, int* __restrict__ sorted_small,
+    int* __restrict__ expert_small, int* __restrict__ ntpp_small) {
+  __shared__ TabLds<AT> sh;
+  __shared__ short lids[SMALL_MAX];
+  __shared__ int full[TAB_MAX_E];
+  zero_counts(sh, E);
+  for (int t = threadIdx.x; t < numel; t += AT) {
+    const int e = ids[t];
+    lids[t] = (short)(e >= 0 && e < E ? e : -1);
+  }
+  lds_barrier();
+  count_ids(sh, lids, numel);
+  for (int e = threadIdx.x; e < E; e += AT) {
+    const int c = sh.cnt[e];
+    full[e] = c;
+    sh.cnt[e] = c > thr ? c : 0;
+  }
+  lds_barrier();
+  for (int t = threadIdx.x; t < numel; t += AT) {
+    const int e = lids[t];
+    if (e >= 0 && sh.cnt[e] == 0) lids[t] = -1;
+  }
+  build_from_counts(sh, lids, numel, E, blk_big, sorted_big, expert_big, ntpp_big, false);
+  for (int e = threadIdx.x; e < E; e += AT) sh.cnt[e] = full[e] <= thr ? full[e] : 0;
+  lds_barrier();
+  for (int t = threadIdx.x; t < numel; t += AT) {
+    const int e = ids[t];
+    lids[t] = (short)(e >= 0 && e < E && sh.cnt[e] > 0 ? e : -1);
+  }
+  build_from_counts(sh, lids, numel, E, blk_small, sorted_small, expert_small, ntpp_small, false);
+}
+
 // Tables from ids in global memory for any numel in one workgroup without scratch (the reference route entry's
 // large-M path): count every id, scan, layout, then place chunk by chunk with each expert's cursor in a register.
 __global__ void __launch_bounds__(AT) align_big_single_kernel(const int* __restrict__ ids, int numel, int E, int blk,
@@ -726,10 +762,12 @@ __global__ void __launch_bounds__(AT) align_count_kernel(const int* __restrict__
 // by the padded scan each expert's first slot and the padded total (workgroup 0 writes ntpp). Then this chunk's share
 // of the layout writes (expert blocks of experts e = c, c + nch, ...; the capacity tail split by chunk) and the
 // stable placement of its rows.
+// cls selects the experts this table holds by their total row count: 0 every expert, 1 those with more than thr rows,
+// 2 those with 1..thr rows (the rows of the others are left out, as ids outside [0, E)).
 __global__ void __launch_bounds__(AT) align_scatter_kernel(const int* __restrict__ ids, int numel, int E, int blk,
                                                            int* __restrict__ sorted_ids, int* __restrict__ expert_ids,
                                                            int* __restrict__ ntpp, const int* __restrict__ scratch,
-                                                           int tail) {
+                                                           int tail, int cls, int thr) {
   __shared__ TabLds<AT> sh;
   __shared__ short lids[CH];
   const int* __restrict__ hist = scratch + ALIGN_HIST;
@@ -755,9 +793,18 @@ __global__ void __launch_bounds__(AT) align_scatter_kernel(const int* __restrict
     }
   }
   lds_barrier();                                               // zero_counts is done before the counts go in
-  if (tid < E) sh.cnt[tid] = tot;
+  if (tid < E) {
+    const bool keep = cls == 0 || (cls == 1 ? tot > thr : tot <= thr);
+    sh.cnt[tid] = keep ? tot : 0;
+    pre = keep ? pre : 0;
+  }
   lds_barrier();
-  const int total = padded_scan(sh, E, blk);
+  if (cls != 0)                                                // rows of experts of the other class are not placed
+    for (int t = tid; t < n; t += AT) {
+      const int e = lids[t];
+      if (e >= 0 && sh.cnt[e] == 0) lids[t] = -1;
+    }
+  const int total = padded_scan(sh, E, blk);                   // (write_layout's closing barrier orders lids)
   if (c == 0 && tid == 0) ntpp[0] = total;
   write_layout(sh, E, blk, numel, total, pre, c, nch, sorted_ids, expert_ids, tail != 0);
   for (int base = 0; base < n; base += AT) stable_round(sh, lids, base, n, t0, E, sorted_ids);
@@ -829,7 +876,28 @@ int launch_align(const int* ids, int numel, int E, int blk, int* sorted_ids, int
   const int nch = (numel + CH - 1) / CH;
   hipLaunchKernelGGL(align_count_kernel, dim3(nch), dim3(AT), 0, st, ids, numel, E, scratch);
   hipLaunchKernelGGL(align_scatter_kernel, dim3(nch), dim3(AT), 0, st, ids, numel, E, blk, sorted_ids, expert_ids,
-                     ntpp, (const int*)scratch, tail);
+                     ntpp, (const int*)scratch, tail, 0, 0);
+  return 0;
+}
+
+// Two live-only tables of one routed step split by expert size: experts with more than thr rows in blk_big-row
+// blocks, the others in blk_small-row blocks. One workgroup (two builds from one count) up to SMALL_MAX rows, else
+// the count launch and one scatter launch per table.
+int launch_align_split(const int* ids, int numel, int E, int thr, int blk_big, int* sorted_big, int* expert_big,
+                       int* ntpp_big, int blk_small, int* sorted_small, int* expert_small, int* ntpp_small,
+                       int* scratch, hipStream_t st) {
+  if (numel <= SMALL_MAX) {
+    hipLaunchKernelGGL(align_split_single_kernel, dim3(1), dim3(AT), 0, st, ids, numel, E, thr, blk_big, sorted_big,
+                       expert_big, ntpp_big, blk_small, sorted_small, expert_small, ntpp_small);
+    return 0;
+  }
+  if (!scratch) return 1;
+  const int nch = (numel + CH - 1) / CH;
+  hipLaunchKernelGGL(align_count_kernel, dim3(nch), dim3(AT), 0, st, ids, numel, E, scratch);
+  hipLaunchKernelGGL(align_scatter_kernel, dim3(nch), dim3(AT), 0, st, ids, numel, E, blk_big, sorted_big,
+                     expert_big, ntpp_big, (const int*)scratch, 0, 1, thr);
+  hipLaunchKernelGGL(align_scatter_kernel, dim3(nch), dim3(AT), 0, st, ids, numel, E, blk_small, sorted_small,
+                     expert_small, ntpp_small, (const int*)scratch, 0, 2, thr);
   return 0;
 }
 
@@ -1179,6 +1247,27 @@ extern "C" int r9k_moe_align_noalloc(long ids, int numel, int E, int blk, long s
   if (numel > SMALL_MAX && !(sp = noalloc_scratch())) return -6;
   if (launch_align((const int*)ids, numel, E, blk, (int*)sorted_ids, (int*)expert_ids, (int*)ntpp, sp,
                    (hipStream_t)stream))
+    return 1;
+  return (int)hipGetLastError();
+}
+
+// No counterpart in the reference (it routes every expert through one block size picked on the host): the tables of
+// one routed step split by expert size on the device. Experts with more than thr rows get blk_big-row blocks in
+// (sorted_big, expert_big, ntpp_big), the others blk_small-row blocks in the small tables; each table holds only its
+// experts' rows (ascending within each expert, as r9k_moe_align) and is written up to its ntpp only (live, as
+// r9k_moe_align_live). Capacities as r9k_moe_align's for each block size; scratch as r9k_moe_align's. 0 / 1 bad
+// arguments or HIP error.
+extern "C" int r9k_moe_align_split(long ids, int numel, int E, int thr, int blk_big, long sorted_big, long expert_big,
+                                   long ntpp_big, int blk_small, long sorted_small, long expert_small,
+                                   long ntpp_small, long scratch, long scratch_ints, long stream) {
+  if (numel < 1 || E < 1 || E > MAX_E || thr < 0) return 1;
+  for (int b : {blk_big, blk_small})
+    if (b < 1 || (b & (b - 1))) return 1;
+  if (!sorted_big || !expert_big || !ntpp_big || !sorted_small || !expert_small || !ntpp_small) return 1;
+  if (numel > SMALL_MAX && (!scratch || scratch_ints < r9k_moe_align_scratch_ints(numel, E))) return 1;
+  if (launch_align_split((const int*)ids, numel, E, thr, blk_big, (int*)sorted_big, (int*)expert_big,
+                         (int*)ntpp_big, blk_small, (int*)sorted_small, (int*)expert_small, (int*)ntpp_small,
+                         (int*)scratch, (hipStream_t)stream))
     return 1;
   return (int)hipGetLastError();
 }

@@ -60,6 +60,8 @@ def lib() -> ctypes.CDLL:
         L.r9k_moe_align.argtypes = [l, i, i, i, l, l, l, l, l, l]
         L.r9k_moe_align_live.restype = i
         L.r9k_moe_align_live.argtypes = [l, i, i, i, l, l, l, l, l, l]
+        L.r9k_moe_align_split.restype = i
+        L.r9k_moe_align_split.argtypes = [l, i, i, i, i, l, l, l, i, l, l, l, l, l, l]
         L.r9k_moe_align_scratch_ints.restype = l
         L.r9k_moe_align_noalloc.restype = i
         L.r9k_moe_align_noalloc.argtypes = [l, i, i, i, l, l, l, l]
@@ -597,11 +599,12 @@ def expected_blocks(numel: int, num_experts: int, topk: int) -> float:
 def moe_stream(a_q: torch.Tensor, a_s: torch.Tensor, w: Mxfp4Experts, out: torch.Tensor, sorted_ids: torch.Tensor,
                expert_ids: torch.Tensor, ntpp: torch.Tensor, numel: int, a_row_div: int,
                topk_w: torch.Tensor | None = None, num_experts: int | None = None,
-               out_scale: torch.Tensor | None = None) -> bool:
+               out_scale: torch.Tensor | None = None, blocks_hint: int | None = None) -> bool:
     """The grouped GEMM over 16-row routing blocks as a block stream (r9k_moe_stream). out_scale None: out bf16
     [numel, N] = moe_gemm's values (its single-wave launch, bit for bit). out_scale given: the gate_up product with
     SiLU-gating and the per-row fp8 quant in the epilogue, out e4m3 codes [numel, N/2] and out_scale fp32 [numel] =
-    silu_mul_quant_fp8 of moe_gemm's bf16 output, bit for bit. False when the shape is not served (nothing
+    silu_mul_quant_fp8 of moe_gemm's bf16 output, bit for bit. blocks_hint: the live blocks expected (sets how many
+    workgroups split a block's columns; default min(E, numel)). False when the shape is not served (nothing
     launched)."""
     E = num_experts if num_experts is not None else w.wq.shape[0]
     epi = 1 if out_scale is not None else 0
@@ -617,7 +620,8 @@ def moe_stream(a_q: torch.Tensor, a_s: torch.Tensor, w: Mxfp4Experts, out: torch
     rc = lib().r9k_moe_stream(epi, a_q.data_ptr(), a_s.data_ptr(), w.wq.data_ptr(), w.wsr.data_ptr(),
                               out.data_ptr(), out_scale.data_ptr() if epi else 0, sorted_ids.data_ptr(),
                               expert_ids.data_ptr(), ntpp.data_ptr(), topk_w.data_ptr() if topk_w is not None else 0,
-                              w.estride, max_blocks, numel, a_row_div, w.K, w.N, min(E, numel), _stream())
+                              w.estride, max_blocks, numel, a_row_div, w.K, w.N,
+                              blocks_hint if blocks_hint else min(E, numel), _stream())
     if rc == 2:
         return False
     if rc:
@@ -654,6 +658,42 @@ def stream_wanted(numel: int, num_experts: int, topk: int) -> bool:
         return False
     b = expected_blocks(numel, num_experts, topk)
     return STREAM_MIN_BLOCKS <= b <= device_cus()
+
+
+# Steps whose routing may leave many experts with a handful of rows (config 5's Zipf skew: at T = 4096, 104 of 169
+# touched experts hold at most 16 rows) split their tables on the device (moe_align_split): experts with more than
+# split_thr(numel) rows go to 256-row blocks on the prefill kernel, the others to 16-row blocks on the block stream,
+# which reads their weights at the streaming rate instead of paying a 256-row tile's DMA for a few rows. Measured on
+# MI355X at config 5, each GEMM alone at T = 4096 (169 touched experts): gate_up 840 us in one 256-row layout, 537
+# (65 experts over 16 rows, 256-row kernel) + 144 us (104 experts, block stream) split; down 439 against 315 + 76 us.
+# The layer: T = 4096 1312 -> 1181 us (threshold 16; 32 / 64 / 128: 1298 / 1287 / 1382 us), T = 256 363 us on the
+# device-picked layout pair -> 318 us split at threshold 32 (16 / 64 / 128: 358 / 350 / 378 us: at 2048 routed rows
+# the 256-row kernel has too few tiles to fill the CUs, so more experts stay on the stream). Taken from
+# SPLIT_MIN_NUMEL routed rows while the mean rows per expert is at most SPLIT_MEAN_MAX (a uniform config 3 step, 227
+# rows an expert, never has experts that small). Up to the router's table-building width (4096 routed rows) only
+# for experts of at least SPLIT_DECODE_MIN_BYTES of gate_up codes: config 2's 1 MB experts run T = 128 / 256 faster
+# on the router's tables and decode blocks (110 / 127 us against 135 / 142 us split; T = 512: 193 against 170 us).
+# The stream's column split is sized for SPLIT_HINT live blocks. R9K_SPLIT=0 turns it off.
+SPLIT = os.environ.get("R9K_SPLIT", "1") == "1"
+SPLIT_MIN_NUMEL = int(os.environ.get("R9K_SPLIT_MIN_NUMEL", "1024"))
+SPLIT_MEAN_MAX = int(os.environ.get("R9K_SPLIT_MEAN_MAX", "128"))
+SPLIT_DECODE_MIN_BYTES = int(os.environ.get("R9K_SPLIT_DECODE_MIN_BYTES", str(4 << 20)))
+SPLIT_HINT = int(os.environ.get("R9K_SPLIT_HINT", "128"))
+_SPLIT_THR = os.environ.get("R9K_SPLIT_THR")
+
+
+def split_wanted(numel: int, num_experts: int, K1: int, K2: int) -> bool:
+    """Whether a step of `numel` routed rows over `num_experts` experts (gate_up K1 x 2 K2, down K2) splits its
+    tables by expert size: the block stream and the 256-row kernel serve K % 128 == 0, the stream up to 4096."""
+    if not (SPLIT and SPLIT_MIN_NUMEL <= numel <= SPLIT_MEAN_MAX * num_experts
+            and all(k % 128 == 0 and 0 < k <= 4096 for k in (K1, K2)) and big_block_cfg(K1, K2) is not None):
+        return False
+    return numel > 4096 or K1 * K2 >= SPLIT_DECODE_MIN_BYTES          # gate_up codes: K1 * 2 K2 / 2 bytes
+
+
+def split_thr(numel: int) -> int:
+    """Rows up to which an expert of a split step goes to the block stream."""
+    return int(_SPLIT_THR) if _SPLIT_THR else (32 if numel <= 4096 else 16)
 
 
 # ops.mxfp4_linear runs the one-launch dense path (r9k_dense_mxfp4_qa, M <= 4) up to this many rows. Measured on
@@ -754,7 +794,7 @@ def _align_scratch(device: torch.device, n: int) -> torch.Tensor:
     key = (device.type, device.index)
     t = _ALIGN_SCRATCH.get(key)
     if t is None or t.numel() < n:
-        # arrival counter + per-chunk histograms: zeroed once here, the counter left zero by every call
+        # the multi-workgroup align's per-chunk histograms (every call rewrites what it reads)
         t = torch.zeros(max(n, 1 << 16), dtype=torch.int32, device=device)
         _ALIGN_SCRATCH[key] = t
     return t
@@ -785,6 +825,30 @@ def moe_align(topk_ids: torch.Tensor, block: int, num_experts: int, expert_map: 
     if rc:
         raise RuntimeError(f"r9k_moe_align failed ({rc}) numel={numel} E={num_experts} block={block}")
     return sorted_ids, expert_ids, ntpp
+
+
+def moe_align_split(topk_ids: torch.Tensor, num_experts: int, thr: int, big_block: int, small_block: int):
+    """Tables of one routed step split by expert size on the device (r9k_moe_align_split): (big, small), each
+    (sorted_ids, expert_ids, ntpp) int32 written up to its ntpp. big holds the experts with more than thr rows in
+    big_block-row blocks, small the others in small_block-row blocks. small's expert_ids is cut to the most blocks
+    its experts can fill (at most min(E, numel) experts of at most thr rows), so a kernel gridded on its length
+    launches no more workgroups than that."""
+    ids = topk_ids.reshape(-1).to(torch.int32).contiguous()
+    numel, E, dev = ids.numel(), num_experts, ids.device
+    i32 = dict(dtype=torch.int32, device=dev)
+    capb = capacity(numel, E, big_block)
+    nbs = min(E, numel) * -(-max(thr, 1) // small_block)
+    big = (torch.empty(capb, **i32), torch.empty(capb // big_block, **i32), torch.empty(1, **i32))
+    small = (torch.empty(max(capacity(numel, E, small_block), nbs * small_block), **i32),
+             torch.empty(capacity(numel, E, small_block) // small_block, **i32), torch.empty(1, **i32))
+    L = lib()
+    n = L.r9k_moe_align_scratch_ints(numel, E)
+    scratch = _align_scratch(dev, n)
+    rc = L.r9k_moe_align_split(ids.data_ptr(), numel, E, thr, big_block, *(t.data_ptr() for t in big), small_block,
+                               *(t.data_ptr() for t in small), scratch.data_ptr(), scratch.numel(), _stream())
+    if rc:
+        raise RuntimeError(f"r9k_moe_align_split failed ({rc}) numel={numel} E={E} thr={thr}")
+    return big, (small[0], small[1][:nbs], small[2])
 
 
 def moe_align_noalloc(topk_ids: torch.Tensor, block: int, num_experts: int, out=None):

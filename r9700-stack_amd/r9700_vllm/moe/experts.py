@@ -51,6 +51,17 @@ def chunk_tokens(M: int, topk: int, N1: int, K1: int, N2: int, K2: int, limit: i
     return list(zip(bounds[:-1], bounds[1:]))
 
 
+# A pass whose GEMMs run on the block stream (r9k_moe_stream over 16-row blocks): the small-expert table of a split
+# prefill step (kernels.moe.split_wanted).
+STREAM_PASS = 0
+
+
+def _stream_pass(a, a_s, W, out, sid, eid, ntpp, numel: int, a_row_div: int, tw, E: int) -> None:
+    if not K.moe_stream(a, a_s, W, out, sid, eid, ntpp, numel, a_row_div, tw, num_experts=E,
+                        blocks_hint=K.SPLIT_HINT):
+        raise RuntimeError(f"r9k MoE: the block stream does not serve N={W.N} K={W.K} (split tables need it)")
+
+
 def r9k_available() -> bool:
     """ROCm torch with a gfx950 device and the kernel library loadable."""
     try:
@@ -224,14 +235,24 @@ class R9700Mxfp4Experts(_experts_base()):
         else:
             layer = getattr(self, "r9k_layer", None)
             bc = K.big_block_cfg(K1, K2)
-            dual_ok = (nv is None and expert_map is None and not MOE_FUSE and bc is not None
-                       and K.DEVICE_BLOCKS_MIN > 0)
+            plain = nv is None and expert_map is None and not MOE_FUSE
+            dual_ok = plain and bc is not None and K.DEVICE_BLOCKS_MIN > 0
             if layer is not None:
-                # tells the router (route.dual_wanted) to build both layouts for this layer's wide decode steps
+                # tells the router which of this layer's steps need no tables from it (route.split_planned: the
+                # experts split theirs) and for which it should build both layouts (route.dual_wanted)
+                layer._r9k_split_k = (K1, K2) if plain else None
                 layer._r9k_dual_blk = bc[1] if dual_ok else 0
-            tabs = route.take(layer, topk_ids, blk, numel) if expert_map is None else None
+            split = plain and K.split_wanted(numel, E, K1, K2)
+            tabs = route.take(layer, topk_ids, blk, numel) if expert_map is None and not split else None
             tabs_big = route.take_big(layer, topk_ids, blk, numel) if tabs is not None else None
-            if tabs is None:
+            tabs_small = None
+            if split:
+                # experts with a handful of rows on the block stream, the rest in the 256-row layout (split on the
+                # device: the host cannot see the counts)
+                MT, (pf_gate, blk) = 1, bc
+                pf_down = pf_gate
+                tabs, tabs_small = K.moe_align_split(topk_ids, E, K.split_thr(numel), blk, K.MOE_BLOCK)
+            elif tabs is None:
                 tabs = K.moe_align(topk_ids, blk, E, expert_map)
             if nv is not None:
                 W1 = K.Nvfp4Experts(w1, self.w1_scale, nv[0], N1, K1)
@@ -240,12 +261,14 @@ class R9700Mxfp4Experts(_experts_base()):
                 W1 = K.Mxfp4Experts(w1, self.w1_scale, N1, K1)
                 W2 = K.Mxfp4Experts(w2, self.w2_scale, N2, K2)
             passes = [(W1, W2, tabs, (MT, pf_gate, pf_down))]
+            if tabs_small is not None:
+                passes.append((W1, W2, tabs_small, (STREAM_PASS, None, None)))
             if tabs_big is not None:
                 # the router built both layouts and the device kept one: both passes run (the other's GEMMs exit)
                 if big is not None or not dual_ok or tabs_big[3] != bc[1]:
                     raise RuntimeError("r9k MoE: the router's second table layout does not fit this layer's pass")
                 passes.append((W1, W2, tabs_big[:3], (1, bc[0], bc[0])))
-            elif big is None and dual_ok and numel >= K.DEVICE_BLOCKS_MIN:
+            elif big is None and dual_ok and not split and numel >= K.DEVICE_BLOCKS_MIN:
                 # skew the host cannot see: the 256-row layout too, the device keeps one (the other's GEMMs exit)
                 tabs_big = K.moe_align(topk_ids, bc[1], E, live_only=True)
                 K.pick_blocks(tabs[2], tabs_big[2], numel, bc[1])
@@ -275,8 +298,11 @@ class R9700Mxfp4Experts(_experts_base()):
         else:
             gate_up = torch.empty((numel, N1), dtype=torch.bfloat16, device=dev)
             for W1, _, (sid, eid, ntpp), (mt, pfg, _) in passes:
-                K.moe_gemm(xq, xs, W1, gate_up, sid, eid, ntpp, numel, topk, None, num_experts=E, MT=mt,
-                           prefill=pfg)
+                if mt == STREAM_PASS:
+                    _stream_pass(xq, xs, W1, gate_up, sid, eid, ntpp, numel, topk, None, E)
+                else:
+                    K.moe_gemm(xq, xs, W1, gate_up, sid, eid, ntpp, numel, topk, None, num_experts=E, MT=mt,
+                               prefill=pfg)
             # the token-major tail's expert ids: the routing ids, or each row's slot when every routed expert is
             # resident (the cache's one-launch manage wrote them; the host pass is provably empty)
             ds_ids = topk_ids.to(torch.int32).contiguous() if cache is None else slot_ids
@@ -294,7 +320,10 @@ class R9700Mxfp4Experts(_experts_base()):
             down = torch.empty((numel, N2), dtype=torch.bfloat16, device=dev)
         tw = topk_weights.reshape(-1).to(torch.float32).contiguous()
         for _, W2, (sid, eid, ntpp), (mt, _, pfd) in passes:
-            K.moe_gemm(aq, as_, W2, down, sid, eid, ntpp, numel, 1, tw, num_experts=E, MT=mt, prefill=pfd,
-                       fuse=2 if fused else 0)
+            if mt == STREAM_PASS:
+                _stream_pass(aq, as_, W2, down, sid, eid, ntpp, numel, 1, tw, E)
+            else:
+                K.moe_gemm(aq, as_, W2, down, sid, eid, ntpp, numel, 1, tw, num_experts=E, MT=mt, prefill=pfd,
+                           fuse=2 if fused else 0)
         K.moe_sum(down.view(M, topk, N2), None, output)
         return output

@@ -6,7 +6,8 @@ object router and experts share. The role and names of the reference's r9700_vll
 How a call is routed (`plan_route`, then `route_step`, both vLLM-free):
   * "decode"  1..MAX_ROWS rows: r9k_moe_route (or r9k_moe_route_quant, which also quantises the layer input) on the
               router's persistent table buffers (`RouteBuffers`), so the experts skip their align;
-  * "wide"    more rows: r9k_moe_topk_quant (top-k and the input quant in one launch); the experts build the tables;
+  * "wide"    more rows, or any step whose experts split their tables by expert size themselves (`split_planned`):
+              r9k_moe_topk_quant (top-k and the input quant in one launch); the experts build the tables;
   * "stock"   anything the kernels do not take (other index dtypes, too many experts or top-k): vLLM's router.
 The hand-off is a `Tables` record on the layer, keyed by the ids tensor the router returned, so apply() uses it
 only for the very call it was made for (`take`, `take_quant`).
@@ -239,11 +240,21 @@ def take_big(layer, topk_ids: torch.Tensor, blk: int, numel: int):
     return t.big if t is not None and t.big is not None and t.matches(topk_ids, blk, numel) else None
 
 
+def split_planned(layer, numel: int, E: int) -> bool:
+    """Whether the experts of `layer` split the tables of a call of `numel` routed rows by expert size themselves
+    (kernels.moe.split_wanted with the widths they signalled in `_r9k_split_k`): the router then builds no tables
+    and takes the wide path (top-k and the input quant in one launch)."""
+    ks = getattr(layer, "_r9k_split_k", None) if layer is not None else None
+    return ks is not None and KM.split_wanted(numel, E, *ks)
+
+
 def dual_wanted(layer, numel: int, E: int) -> int:
     """The big block size when the router should build both layouts for a call of `numel` routed rows: the experts
-    of `layer` signalled they run the device-picked pair (their `_r9k_dual_blk`), the step has at least
-    DEVICE_BLOCKS_MIN rows and the host would keep small blocks (touched experts average below PREFILL_MOE_ROWS);
-    else 0."""
+    of `layer` signalled they run the device-picked pair (their `_r9k_dual_blk`) and do not split the step's tables
+    (split_planned), the step has at least DEVICE_BLOCKS_MIN rows and the host would keep small blocks (touched
+    experts average below PREFILL_MOE_ROWS); else 0."""
+    if split_planned(layer, numel, E):
+        return 0
     bb = getattr(layer, "_r9k_dual_blk", 0) if layer is not None else 0
     if not bb or KM.DEVICE_BLOCKS_MIN <= 0 or numel < KM.DEVICE_BLOCKS_MIN or numel > QUANT_MAX_NUMEL:
         return 0
@@ -302,14 +313,16 @@ def _quantisable(x, M: int, topk: int) -> bool:
 
 
 def route_step(logits: torch.Tensor, x, topk: int, renorm: bool, E: int, bufs: RouteBuffers | None,
-               indices_type=None, use_ops: bool = True, dual_blk: int = 0):
+               indices_type=None, use_ops: bool = True, dual_blk: int = 0, wide: bool = False):
     """Route one call: (weights, ids, Tables) on the decode / wide paths, or None when the stock router must run.
     At decode widths `bufs` holds the tables; use_ops routes the launch through the torch.ops.r9700 custom ops
     (the compiled-graph path), else the plain functions. dual_blk (dual_wanted): also the big-block layout, of which
-    the device keeps one (moe_route_dual)."""
+    the device keeps one (moe_route_dual). wide (split_planned): the wide path at any width (no tables)."""
     path = plan_route(logits, topk, E, x, indices_type)
     if path == "stock":
         return None
+    if wide:
+        path = "wide"
     M = logits.shape[0]
     numel = M * topk
     if path == "wide":
@@ -366,9 +379,11 @@ def make_router(stock, routed_experts):
 
         def _compute_routing(self, hidden_states, router_logits, indices_type, *, input_ids=None):
             numel = router_logits.shape[0] * self.top_k
-            r = route_step(router_logits, hidden_states, self.top_k, self.renormalize, self.global_num_experts,
+            E = self.global_num_experts
+            r = route_step(router_logits, hidden_states, self.top_k, self.renormalize, E,
                            self._bufs_for(router_logits.device), indices_type,
-                           dual_blk=dual_wanted(self.routed_experts, numel, self.global_num_experts))
+                           dual_blk=dual_wanted(self.routed_experts, numel, E),
+                           wide=split_planned(self.routed_experts, numel, E))
             if r is None:
                 self.routed_experts._r9k_tables = None
                 return super()._compute_routing(hidden_states, router_logits, indices_type, input_ids=input_ids)

@@ -318,6 +318,16 @@ def test_layer_config5_skewed_4096_sampled(dev):
               extra=16)
 
 
+@pytest.mark.parametrize("E,H,I,T,topk", [(64, 512, 256, 600, 4), (384, 1024, 512, 512, 8)])
+def test_layer_split_tables(dev, monkeypatch, E, H, I, T, topk):
+    """A prefill step on split tables (K.moe_align_split: experts with at most SPLIT_THR rows on the block stream,
+    the others on the 256-row kernel) under Zipf routing, against the oracle on every token."""
+    monkeypatch.setattr(K, "SPLIT_MEAN_MAX", 1 << 20)
+    monkeypatch.setattr(K, "SPLIT_DECODE_MIN_BYTES", 0)
+    assert K.split_wanted(T * topk, E, H, I)
+    run_layer(dev, E, H, I, T, topk, seed=20261201 + 18000 + E + T, zipf=True)
+
+
 @pytest.mark.parametrize("E,T,H,I,topk", [(288, 1, 2048, 512, 8), (288, 8, 2048, 512, 8), (288, 64, 2048, 512, 8),
                                           (16, 5, 512, 256, 4), (8, 3, 320, 160, 2), (4, 2, 64, 32, 2)])
 def test_fused_decode_gemms_equal_unfused(dev, E, T, H, I, topk):
@@ -368,6 +378,7 @@ def test_device_block_choice(dev, monkeypatch, zipf):
     256-row layout's block count (skewed routing), else the decode blocks. The output equals, bit for bit, the same layer run on that
     layout alone (forced from the host)."""
     E, H, I, T, topk = 128, 512, 256, 256, 8
+    monkeypatch.setattr(K, "SPLIT", False)                    # the device-picked layout pair, not split tables
     print(f"device block choice zipf={zipf}", flush=True)
     (_, _), (_, _), W13, W2 = make_layer(dev, E, H, I, 20261201 + 8000 + zipf)
     g = torch.Generator().manual_seed(8001 + zipf)
@@ -443,6 +454,7 @@ def test_layer_config5_T256_router_handoff(dev, monkeypatch):
     256-row layout built beside them, r9k_moe_pick_blocks keeping one). Checked against the oracle on 32 sampled
     tokens, and bit for bit against the layout the host-side counts say must be kept, run alone."""
     from r9700_vllm.moe import route
+    monkeypatch.setattr(K, "SPLIT", False)                    # the device-picked layout pair, not split tables
     E, H, I, T, topk = 384, 4096, 2048, 256, 8
     seed = 20261201 + 5000 + T
     (p13, e13), (p2, e2), W13, W2 = make_layer(dev, E, H, I, seed, 116, 126)
@@ -501,14 +513,59 @@ def test_layer_config5_T256_router_handoff(dev, monkeypatch):
     assert r < 1e-2 and c >= 0.9999
 
 
+def test_layer_config5_T256_split_handoff(dev):
+    """BASELINE config 5 at T = 256 on split tables as a serving step runs it: apply() signals the router
+    (route.split_planned), the router takes the wide path (top-k + input quant, no tables; route.route_step), apply()
+    splits the tables on the device (experts with at most split_thr rows on the block stream, the rest in 256-row
+    blocks) and uses the router's quant. Every token against the oracle."""
+    from r9700_vllm.moe import route
+    E, H, I, T, topk = 384, 4096, 2048, 256, 8
+    seed = 20261201 + 5000 + T + 1
+    (p13, e13), (p2, e2), W13, W2 = make_layer(dev, E, H, I, seed, 116, 126)
+    g = torch.Generator().manual_seed(seed + 1)
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    rank = torch.randperm(E, generator=g).float() + 1
+    logits = (torch.randn(T, E, generator=g) - 1.1 * torch.log(rank)[None, :]).to(torch.bfloat16)
+    xd, ld = x.to(dev), logits.to(dev)
+    numel = T * topk
+
+    class Routed:
+        _r9k_tables = None
+
+    ex = R9700Mxfp4Experts.standalone(W13.wsr, W2.wsr)
+    ex.r9k_layer = Routed()
+    out = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
+    bufs = route.RouteBuffers(dev, E, topk)
+    for step in range(2):                                      # the first call signals the router
+        wide = route.split_planned(ex.r9k_layer, numel, E)
+        assert wide == (step == 1)
+        w, ids, ex.r9k_layer._r9k_tables = route.route_step(ld, xd, topk, True, E, bufs, use_ops=False, wide=wide,
+                                                            dual_blk=route.dual_wanted(ex.r9k_layer, numel, E))
+        ex.apply(out, xd, W13.wq, W2.wq, w, ids, "silu", E, None, None, None, None, None, None, False)
+    torch.cuda.synchronize()
+    assert K.split_wanted(numel, E, H, I)
+    ro = O.route(logits, topk, True)
+    assert np.array_equal(ids.cpu().numpy(), ro[1]), "routing ids"
+    need = np.unique(ro[1])
+    sub = lambda p: {int(e): p[int(e)].cpu() for e in need}
+    ref = O.moe_layer(x, logits, (_Lazy(sub(p13)), _Lazy(sub(e13))), (_Lazy(sub(p2)), _Lazy(sub(e2))), topk, True,
+                      route_out=ro)
+    a, b = bf16_bits_to_f64(O.bf16_bits(out)), bf16_bits_to_f64(ref["out"])
+    r, c = rel_err(a, b), cosine(a, b)
+    print(f"cfg5 T=256 split hand-off: rel {r:.2e} cos {c:.7f}", flush=True)
+    assert r < 1e-2 and c >= 0.9999
+
+
 @pytest.mark.parametrize("E,H,I,T,zipf", [(384, 4096, 2048, 256, True), (384, 4096, 2048, 256, False),
                                         (288, 2048, 512, 128, False), (288, 2048, 512, 256, True)])
-def test_layer_router_dual_layout(dev, E, H, I, T, zipf):
+def test_layer_router_dual_layout(dev, monkeypatch, E, H, I, T, zipf):
     """The router's one-launch dual layout (route.route_step with dual_blk: routing, input quant, both table
     layouts and the device's pick in r9k_moe_route_dual) through apply(): bit for bit the output of the same call
     whose experts build the second layout themselves (moe_align + r9k_moe_pick_blocks), whichever layout the
-    device keeps; apply() signals the router through the layer object (route.dual_wanted)."""
+    device keeps; apply() signals the router through the layer object (route.dual_wanted). Split tables off (they
+    take these steps by default)."""
     from r9700_vllm.moe import route
+    monkeypatch.setattr(K, "SPLIT", False)
     topk = 8
     seed = 20261201 + 7000 + E + T + int(zipf)
     (_, _), (_, _), W13, W2 = make_layer(dev, E, H, I, seed, 116, 126)

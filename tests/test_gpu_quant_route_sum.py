@@ -426,3 +426,36 @@ def test_align_live_only(dev, T, E, topk, blk):
     assert int(n1.item()) == n
     assert torch.equal(s1[:n], s0[:n]) and torch.equal(e1[: n // blk], e0[: n // blk])
     assert bool((s1[n:] == -777).all()) and bool((e1[n // blk:] == -777).all())
+
+
+@pytest.mark.parametrize("E,T,topk,thr,zipf", [(384, 4096, 8, 16, True), (384, 256, 8, 16, True),
+                                               (64, 300, 4, 8, False), (288, 1024, 8, 0, False),
+                                               (128, 1000, 4, 10000, True), (16, 3, 2, 1, False),
+                                               (1024, 600, 16, 3, True)])
+def test_align_split_tables(dev, E, T, topk, thr, zipf):
+    """r9k_moe_align_split: the big table (experts with more than thr rows, 256-row blocks) and the small table
+    (the others, 16-row blocks) each equal the oracle's canonical align over the ids of its own experts (the other
+    ids left out) up to ntpp, bit for bit; together they place every routed row once. One workgroup up to 4096
+    routed rows, the count + two scatter launches above."""
+    g = torch.Generator().manual_seed(20261201 + 17000 + E + T + thr)
+    logits = torch.randn(T, E, generator=g)
+    if zipf:
+        logits = logits - 1.1 * torch.log(torch.randperm(E, generator=g).float() + 1)[None, :]
+    ids = K.moe_topk(logits.to(torch.bfloat16).to(dev), topk, True)[1]
+    numel = T * topk
+    big, small = K.moe_align_split(ids, E, thr, 256, 16)
+    torch.cuda.synchronize()
+    flat = ids.reshape(-1).cpu().numpy()
+    cnt = np.bincount(flat, minlength=E)
+    placed = []
+    for (s, e, n), blk, keep in ((big, 256, cnt > thr), (small, 16, (cnt > 0) & (cnt <= thr))):
+        want = np.where(keep[flat], flat, -1).astype(np.int32)
+        so, eo, no = O.align(want, E, blk)
+        m = int(n.item())
+        assert m == int(no[0]), (blk, m, int(no[0]))
+        assert np.array_equal(s[:m].cpu().numpy(), so[:m]) and np.array_equal(e[: m // blk].cpu().numpy(), eo[: m // blk])
+        sm = s[:m].cpu().numpy()
+        placed.append(sm[sm < numel])
+    print(f"align split E={E} T={T} k={topk} thr={thr}: big ntpp {int(big[2].item())}, small ntpp "
+          f"{int(small[2].item())} ({int(((cnt > 0) & (cnt <= thr)).sum())} small experts)", flush=True)
+    assert np.array_equal(np.sort(np.concatenate(placed)), np.arange(numel))

@@ -173,3 +173,27 @@ def test_dense_row_ranges_stay_in_the_buffer_range():
         sizes = [r1 - r0 for r0, r1 in rr]
         assert max(sizes) - min(sizes) <= 1
     assert len(ops.row_ranges(61680, 17408, 5120)) == 1 and len(ops.row_ranges(61681, 17408, 5120)) == 2
+
+
+def test_split_plan():
+    """Which steps split their tables by expert size, the threshold, and the router's side of the hand-off."""
+    from r9700_vllm.kernels import moe as K
+    from r9700_vllm.moe import route
+    assert K.split_wanted(32768, 384, 4096, 2048)            # config 5 T = 4096
+    assert K.split_wanted(2048, 384, 4096, 2048)             # config 5 T = 256
+    assert not K.split_wanted(65536, 288, 2048, 512)         # config 3: 227 rows an expert
+    assert not K.split_wanted(512, 288, 2048, 512)           # config 2 T = 64: below SPLIT_MIN_NUMEL
+    assert not K.split_wanted(2048, 288, 2048, 512)          # config 2 T = 256: 1 MB experts at decode widths
+    assert K.split_wanted(8192, 288, 2048, 512)              # config 2 T = 1024: past the router's table width
+    assert not K.split_wanted(32768, 384, 5120, 2048)        # K past the block stream's 4096
+    assert not K.split_wanted(32768, 384, 4096, 2000)        # K not a multiple of 128
+    assert K.split_thr(2048) == 32 and K.split_thr(32768) == 16
+
+    class Layer:
+        _r9k_split_k = (4096, 2048)
+        _r9k_dual_blk = 256
+
+    assert route.split_planned(Layer, 2048, 384) and route.dual_wanted(Layer, 2048, 384) == 0
+    assert not route.split_planned(Layer, 512, 384)
+    Layer._r9k_split_k = None
+    assert not route.split_planned(Layer, 2048, 384) and not route.split_planned(None, 2048, 384)
