@@ -5,7 +5,9 @@ MXFP4 TFLOPS at prefill).
 
 A step is one MoE layer forward over one batch of synthetic tokens: routing (softmax top-8 + align tables, and at
 T <= 64 the per-token fp8 quant of x in the same launch) -> grouped gate_up GEMM -> SiLU*up + fp8 quant -> grouped
-down GEMM (router weight folded) -> top-k sum, five launches on one stream (six above T = 64). The headline `value`
+down GEMM (router weight folded) -> top-k sum. At the headline point the middle three run as one launch
+(r9k_moe_stream_layer: each 16-row routing block's gate_up, SiLU + quant and down in one workgroup), so the T=64
+step is three launches: routing, the layer, the sum. The headline `value`
 is BASELINE config 2 (E=288 experts, hidden 2048, expert intermediate 512, top-8) at T=64 tokens, the
 bandwidth-bound decode point; T = 1, 8, 16, the config 3 prefill (T=8192) and the router gate GEMM that produces
 the layer's logits (r9k_router_gemm against stock's F.linear) are reported beside it, with config 4 (NVFP4 -> MXFP4
@@ -14,9 +16,11 @@ Zipf-skewed routing, T = 1, 32, 256, 4096).
 
 Method: weights and inputs are resident in HBM before timing. Steps run as HIP-graph replays that cycle through
 COPIES independent weight copies (> 2x the 256 MB Infinity Cache per cycle), so weight bytes come from HBM, not from
-a cache warmed by the previous step. The dominant kernel (the gate_up GEMM) is also launched on its own, bracketed by
-HIP events on the stream it runs on, for the roofline figure. The CPU baseline is the oracle's dequant-then-matmul
-layer (oracle/, the reference's torch CPU path restated) timed on this host on a bounded sample.
+a cache warmed by the previous step. The dominant kernel (r9k_moe_stream_layer at T=64) is also launched on its own,
+bracketed by HIP events on the stream it runs on, for the roofline figure. The CPU baselines are the oracle's
+dequant-then-matmul layer and converter (oracle/, the reference's torch CPU path restated) timed on this host on
+bounded samples: config 2 T=64 (`cpu_baseline`), config 1, the config 3 prefill, the config 4 conversion and GEMM,
+config 5 T=4096.
 """
 from __future__ import annotations
 
@@ -196,24 +200,25 @@ def graph_time(step: Step, steps: int, warmup: int, windows: int = 1, min_warm_m
     return float(np.median(times)), reps * copies
 
 
-def gate_up_kernel_time(step: Step, reps: int = 40):
-    """Average duration (ms) of the gate_up GEMM launch alone, HIP events on its stream, rotating weight copies.
-    Returns (ms, algorithmic bytes per launch, flops per launch, experts touched)."""
+def layer_kernel_time(step: Step, reps: int = 40):
+    """Average duration (ms) of the T=64 step's dominant launch alone: r9k_moe_stream_layer (gate_up, SiLU + quant
+    and down of each 16-row routing block in one workgroup), HIP events on its stream, rotating weight copies. Returns
+    (ms, algorithmic bytes per launch, flops per launch, experts touched): bytes = the touched experts' gate_up and
+    down codes + e8m0 exponents, the fp8 input rows and their scales, the router weights and the bf16 down rows."""
     K, L = step.K, step.layer
     step(0)
     torch.cuda.synchronize()
     ids = step.ids
     E = L.E
-    tabs = K.moe_align(ids, step.blk, E)
+    tabs = K.moe_align(ids, K.MOE_BLOCK, E)
     xq, xs = K.quant_rows_fp8(step.x)
-    N1, K1 = 2 * L.I, L.H
-    out = torch.empty(step.numel, N1, dtype=torch.bfloat16, device=step.dev)
-    MT = step.blk // K.MOE_BLOCK
-    pf = K.pick_moe_prefill(MT, K1, gate_up=True)
+    tw = step.w.reshape(-1).to(torch.float32).contiguous()
+    down = torch.empty(step.numel, L.H, dtype=torch.bfloat16, device=step.dev)
     copies = len(L.W13)
 
     def launch(c):
-        K.moe_gemm(xq, xs, L.W13[c], out, *tabs, step.numel, step.topk, None, num_experts=E, MT=MT, prefill=pf)
+        if not K.moe_stream_layer(xq, xs, L.W13[c], L.W2[c], down, *tabs, step.numel, step.topk, tw, E):
+            raise RuntimeError("r9k_moe_stream_layer does not serve the T=64 step")
 
     for i in range(8):
         launch(i % copies)
@@ -234,8 +239,9 @@ def gate_up_kernel_time(step: Step, reps: int = 40):
     torch.cuda.synchronize()
     ms = a.elapsed_time(b) / reps
     touched = int(torch.unique(ids).numel())
-    nbytes = touched * (N1 * K1 // 2 + N1 * K1 // 32) + step.T * K1 + step.T * 4 + step.numel * N1 * 2
-    flops = 2 * step.numel * N1 * K1
+    H, I = L.H, L.I
+    nbytes = touched * L.bytes_per_expert() + step.T * H + step.T * 4 + step.numel * 4 + step.numel * H * 2
+    flops = 2 * step.numel * (2 * I * H + H * I)
     return ms, nbytes, flops, touched
 
 
@@ -253,7 +259,7 @@ def events_ms(fn, reps: int) -> float:
     return a.elapsed_time(b) / reps
 
 
-def cfg4_lines(dev) -> dict:
+def cfg4_lines(dev, cpu: bool = False) -> dict:
     """the load-time NVFP4 -> MXFP4 conversion of a [17408, 5120] dense weight (uniform codes,
     s16 = e4m3(|N(0,1)| * 0.05), global 1), one launch over all rows, then the fp8-act x MXFP4 GEMM on the converted
     weight at M = 1, 4, 16, 4096 (ops.mxfp4_linear: per-row quant + GEMM), and the native NVFP4 GEMM
@@ -276,6 +282,8 @@ def cfg4_lines(dev) -> dict:
     print(f"# cfg4 convert [17408, 5120]: {ms * 1e3:.1f} us, {res['convert']['GBps']} GB/s", file=sys.stderr,
           flush=True)
     mp, me = conv()
+    if cpu:
+        res["cpu"] = cpu_cfg4(packed, s16, mp, me, g, dev)
     W0 = K.prepare_mxfp4_weights(mp.unsqueeze(0), me.unsqueeze(0))
     del packed, s16, mp, me
     Ws = [W0] + [K.Mxfp4Experts(W0.wq.clone(), W0.wsr.clone(), N, Kd) for _ in range(11)]
@@ -336,7 +344,7 @@ def cfg4_lines(dev) -> dict:
     return {"workload": "cfg4 dense [17408, 5120]: NVFP4 -> MXFP4 conversion, then fp8-act x MXFP4 GEMM", **res}
 
 
-def cfg5_lines(dev, steps: int, warmup: int) -> dict:
+def cfg5_lines(dev, steps: int, warmup: int, cpu: bool = False) -> dict:
     """hidden 4096, intermediate 2048, 384 experts (e8m0 in [116, 126]), top-8 over Zipf(1.1)-biased
     logits, T = 1, 32, 256, 4096; the same Step and graph timing as config 2 (4 weight copies, 19 GB)."""
     layer = Layer(384, 4096, 2048, dev, lo=116, hi=126, seed=SEED + 5000)
@@ -354,6 +362,8 @@ def cfg5_lines(dev, steps: int, warmup: int) -> dict:
                        "top_expert_share": round(float(counts.max() / counts.sum()), 4)}
         print(f"# cfg5 T={T}: {ms * 1e3:.1f} us/layer, {out[str(T)]['layer_GBps']} GB/s, "
               f"{out[str(T)]['TFLOPS']} TFLOPS over {touched} experts", file=sys.stderr, flush=True)
+        if cpu and T == 4096:
+            out[str(T)]["cpu"] = cpu_layer_sample(st, 64)
         del st
     del layer
     torch.cuda.empty_cache()
@@ -493,7 +503,7 @@ def router_times(dev, reps_bytes: int = 512 << 20):
 
 
 CALIB_BYTES = 256 << 20
-TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "moe_gate_up_t64_pmc_traffic.md")
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "moe_decode_t64_pmc_traffic.md")
 
 
 def calib_copy(dev) -> None:
@@ -541,8 +551,8 @@ def prefill_dataflow_bytes(T: int, topk: int, H: int, I: int, E: int) -> int:
 
 
 def measured_traffic():
-    """HBM bytes per gate_up launch at T=64 from the committed PMC summary (its line 'traffic_bytes_per_launch: N'),
-    or None when there is none."""
+    """HBM bytes per r9k_moe_stream_layer launch at T=64 from the committed PMC summary (its line
+    'traffic_bytes_per_launch: N'), or None when there is none."""
     try:
         with open(TRAFFIC_PROFILE) as f:
             for line in f:
@@ -600,6 +610,93 @@ def cpu_baseline(step: Step, budget_s: float = 10.0) -> dict:
                       f" oracle dequant-then-matmul in fp32 on {threads} host threads, {el:.1f} s"}
 
 
+def _budget_loop(fn, budget_s: float, max_n: int = 30):
+    """Calls fn() until budget_s seconds have passed (at least once); (calls, seconds)."""
+    n, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        n += 1
+        el = time.perf_counter() - t0
+        if el > budget_s or n >= max_n:
+            return n, el
+
+
+def cpu_layer_sample(step: Step, ntok: int, budget_s: float = 6.0) -> dict:
+    """The oracle's CPU layer on the first `ntok` tokens of a step's workload (the reference's CPU path: per-token
+    quant, per-expert dequant + fp32 matmul, SiLU quant, down, sum); tokens/s of that batch."""
+    from oracle import oracle as O
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    L = step.layer
+    x, logits = step.x_cpu[:ntok], step.logits_cpu[:ntok]
+    ids = O.route(logits, step.topk, True)[1]
+    need = np.unique(ids)
+    w = [{int(e): t[int(e)].cpu() for e in need} for t in (L.p13, L.e13, L.p2, L.e2)]
+    n, el = _budget_loop(lambda: O.moe_layer(x, logits, (w[0], w[1]), (w[2], w[3]), step.topk, True), budget_s)
+    return {"value": round(n * ntok / el, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"the first {ntok} of the step's {step.T} tokens as one batch ({len(need)} experts touched), "
+                      f"{n} forward(s) in {el:.1f} s, oracle dequant-then-matmul in fp32"}
+
+
+def cpu_cfg1(dev, budget_s: float = 3.0) -> dict:
+    """BASELINE config 1 on the GPU (ops.mxfp4_linear, [16, 2048] x [1024, 2048]) and on the reference's CPU torch
+    path (the oracle's per-token fp8 quant, MXFP4 dequant, fp32 matmul)."""
+    from oracle import oracle as O
+    from r9700_vllm import ops
+    from r9700_vllm.kernels import moe as K
+    M, N, Kd = 16, 1024, 2048
+    g = torch.Generator().manual_seed(SEED + 1000)
+    packed = torch.randint(0, 256, (N, Kd // 2), generator=g, dtype=torch.int32).to(torch.uint8)
+    e8 = torch.randint(118, 127, (N, Kd // 32), generator=g, dtype=torch.int32).to(torch.uint8)
+    x = torch.randn(M, Kd, generator=g).to(torch.bfloat16)
+    W = K.prepare_mxfp4_weights(packed.unsqueeze(0).to(dev), e8.unsqueeze(0).to(dev))
+    xd = x.to(dev)
+    gpu_ms = events_ms(lambda: ops.mxfp4_linear(xd, W.wq, W.wsr, N, Kd), 50)
+    threads = os.cpu_count() or 1
+
+    def cpu_call():
+        q, sc = O.quant_rows_fp8(x)
+        O.grouped_gemm(q, sc, {0: O.mxfp4_dequant(packed, e8, torch.float32)}, np.zeros(M, dtype=np.int32), 1,
+                       acc_dtype=torch.float32)
+    n, el = _budget_loop(cpu_call, budget_s)
+    return {"workload": "cfg1 dense MXFP4 linear [16, 2048] x [1024, 2048]", "gpu_us": round(gpu_ms * 1e3, 2),
+            "cpu": {"value": round(el / n * 1e6, 1), "unit": "us per call", "cores": threads, "kind": "port",
+                    "sample": f"{n} whole calls (quant, dequant, fp32 matmul) in {el:.1f} s"}}
+
+
+def cpu_cfg4(packed, s16, mp, me, g, dev, budget_s: float = 4.0) -> dict:
+    """BASELINE config 4 on the reference's CPU path: the NVFP4 -> MXFP4 conversion (oracle restatement of the
+    reference's torch converter) on a 512-row sample, scaled to the [17408, 5120] matrix; the GEMM as the CPU path
+    runs it per call (quant, dequant of the whole weight, fp32 matmul) at M = 1, 4, 16 and, on 256 of its rows, 4096."""
+    from oracle import oracle as O
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    N, Kd = packed.shape[0], packed.shape[1] * 2
+    rows = 512
+    p_s, s_s = packed[:rows].cpu().numpy(), s16[:rows].view(torch.uint8).cpu().numpy()
+    div = np.ones(rows, dtype=np.float32)
+    n, el = _budget_loop(lambda: O.nvfp4_to_mxfp4(p_s, s_s, div), budget_s)
+    conv_ms = el / n * 1e3 * N / rows
+    wp, we = mp.cpu(), me.cpu()
+    t0 = time.perf_counter()
+    Wd = O.mxfp4_dequant(wp, we, torch.float32)
+    deq_ms = (time.perf_counter() - t0) * 1e3
+    gemm = {}
+    for M in (1, 4, 16, 4096):
+        m = min(M, 256)
+        x = torch.randn(m, Kd, generator=torch.Generator().manual_seed(M)).to(torch.bfloat16)
+
+        def mm():
+            q, sc = O.quant_rows_fp8(x)
+            return (O.e4m3_dequant(q, torch.float32) @ Wd.T) * torch.from_numpy(sc)[:, None]
+        n, el = _budget_loop(mm, budget_s / 4)
+        gemm[str(M)] = round(deq_ms + el / n * 1e3 * M / m, 1)
+    return {"convert_ms": round(conv_ms, 1), "gemm_ms_per_call": gemm, "dequant_ms": round(deq_ms, 1),
+            "cores": threads, "kind": "port",
+            "sample": f"conversion on {rows} of {N} rows scaled by {N / rows:.1f}; GEMM = one whole-weight dequant "
+                      f"({deq_ms:.0f} ms) + quant and fp32 matmul, M = 4096 timed on 256 rows and scaled by 16"}
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -634,9 +731,9 @@ def main():
             main_step, main_ms, main_n = st, ms, n
 
     calib_copy(dev)
-    k_ms, k_bytes, k_flops, k_touched = gate_up_kernel_time(main_step)
+    k_ms, k_bytes, k_flops, k_touched = layer_kernel_time(main_step)
     k_gbs = k_bytes / (k_ms * 1e-3) / 1e9
-    print(f"# gate_up GEMM alone: {k_ms * 1e3:.1f} us, {k_gbs:.0f} GB/s", file=sys.stderr, flush=True)
+    print(f"# stream layer launch alone: {k_ms * 1e3:.1f} us, {k_gbs:.0f} GB/s", file=sys.stderr, flush=True)
 
     prefill = None
     if not args.no_prefill:
@@ -644,6 +741,7 @@ def main():
         ms, n = graph_time(pl, 8, max(4, args.warmup // 4), windows=5)
         flops = 6 * 8192 * topk * layer.H * layer.I
         tf = flops / (ms * 1e-3) / 1e12
+        pl_cpu = None if args.no_cpu else cpu_layer_sample(pl, 256)
         del pl
         torch.cuda.empty_cache()
         db = prefill_dataflow_bytes(8192, topk, layer.H, layer.I, layer.E)
@@ -654,13 +752,15 @@ def main():
                    "dataflow": {"what": "HBM bytes of the layer's launches (each input read once, each output written "
                                         "once) / ms_per_step, against a measured device copy (read + write)",
                                 "bytes": db, "achieved_GBps": round(db / (ms * 1e-3) / 1e9, 1),
-                                "copy_GBps": round(cgbs, 1), "frac_copy": round(db / (ms * 1e-3) / 1e9 / cgbs, 4)}}
+                                "copy_GBps": round(cgbs, 1), "frac_copy": round(db / (ms * 1e-3) / 1e9 / cgbs, 4)},
+                   "cpu": pl_cpu}
         print(f"# prefill T=8192: {ms:.3f} ms/layer, {tf:.1f} TFLOPS; dataflow {db / 1e9:.3f} GB at "
               f"{db / (ms * 1e-3) / 1e12:.2f} TB/s (device copy {cgbs / 1e3:.2f} TB/s)", file=sys.stderr, flush=True)
 
     router = None if args.no_router else router_times(dev)
-    cfg4 = None if args.no_cfg4 else cfg4_lines(dev)
-    cfg5 = None if args.no_cfg5 else cfg5_lines(dev, args.steps, args.warmup)
+    cfg4 = None if args.no_cfg4 else cfg4_lines(dev, cpu=not args.no_cpu)
+    cfg5 = None if args.no_cfg5 else cfg5_lines(dev, args.steps, args.warmup, cpu=not args.no_cpu)
+    cfg1 = None if args.no_cpu else cpu_cfg1(dev)
     cache = None if args.no_cache else cache_lines(dev, args.steps)
     cpu = None if args.no_cpu else cpu_baseline(main_step)
     line = {
@@ -679,16 +779,18 @@ def main():
         "config": {"workload": "cfg2 decode MoE layer: E=288, hidden 2048, intermediate 512, top-8, T=64 tokens",
                    "tokens": 64, "experts": 288, "hidden": 2048, "intermediate": 512, "topk": 8,
                    "weight_copies_rotated": COPIES},
-        "roofline": {"bound": "hbm", "kernel": "r9k_moe_mxfp4a8 gate_up (T=64)", "achieved": round(k_gbs, 1),
+        "roofline": {"bound": "hbm", "kernel": "r9k_moe_stream_layer (gate_up + SiLU + quant + down, T=64)",
+                     "achieved": round(k_gbs, 1),
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(k_gbs / HBM_PEAK_GBS, 4),
                      "traffic": measured_traffic(),
                      "traffic_source": "not measured in this run: the committed PMC summary "
-                                       "profiles/moe_gate_up_t64_pmc_traffic.md (rocprofv3 --pmc FETCH_SIZE, then "
+                                       "profiles/moe_decode_t64_pmc_traffic.md (rocprofv3 --pmc FETCH_SIZE, then "
                                        "WRITE_SIZE, scaled by this script's 256 MiB calibration copy)",
                      "kernel_us": round(k_ms * 1e3, 2), "bytes_per_launch": k_bytes,
                      "layer": {"what": "whole T=64 layer (all launches), algorithmic bytes / ms_per_step",
                                "achieved": sweep["64"]["layer_GBps"], "frac": sweep["64"]["hbm_frac"]}},
         "cpu_baseline": cpu,
+        "cfg1": cfg1,
         "decode_sweep": sweep,
         "prefill": prefill,
         "router": router,

@@ -377,6 +377,19 @@ __global__ void __launch_bounds__(NTH) moe_prefill_persistent_kernel(
   // (the group's blocks of one column block run side by side, so a hot expert's weight tile is fetched into the
   // XCD's L2 once for up to `grp` of its blocks)
   const int nblk = ntpp[0] / BM;
+  if (grp <= 0) {                                              // chosen here: 4 when experts average 2+ blocks
+    __shared__ int s_grp;
+    if (wave == 0) {
+      int starts = 0;                                          // blocks that begin an expert's run
+      for (int b0 = 0; b0 < nblk; b0 += WAVE) {
+        const int b = b0 + lane;
+        starts += __popcll(__ballot(b < nblk && (b == 0 || expert_ids[b] != expert_ids[b - 1])));
+      }
+      if (lane == 0) s_grp = nblk >= 2 * starts ? 4 : 1;
+    }
+    __syncthreads();
+    grp = __builtin_amdgcn_readfirstlane(s_grp);
+  }
   auto tile_rb = [&](int m) {
     const int L = start + jj + m * S, g = L / (grp * nnb), r = L - g * grp * nnb;
     const int gb = min(grp, nblk - g * grp);
@@ -934,11 +947,13 @@ int r9k_prefill_launch(long a, long as, long wq, long ws, long c, long sorted_id
     if (hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
       return -6;
-    // routing blocks per tile group (column-major within a group): 4 measured on MI355X at config 5 T = 4096 (the
-    // hot experts' blocks sharing each weight tile through L2): down 312 -> 292 us, gate_up 531 -> 526 us, config 3
-    // gate_up unchanged (one block an expert)
+    // routing blocks per tile group (column-major within a group), chosen in the kernel from the table (0): 4 when
+    // the experts average two or more blocks, else 1. Measured on MI355X: config 5 T = 4096's 256-row pass (65
+    // experts, 169 blocks, the hot experts' blocks sharing each weight tile through L2) down 312 -> 292 us, gate_up
+    // 531 -> 526 us with 4; config 3's gate_up (300 blocks, 288 experts) reads 460 MB with 1 and 495 MB with 4
+    // (four experts' activation blocks live in L2 at once), 148 -> 152 us. R9K_PREFILL_GROUP forces a size.
     const char* pv = getenv("R9K_PREFILL_GROUP");
-    const int grp = pv && atoi(pv) > 0 ? atoi(pv) : 4;
+    const int grp = pv && atoi(pv) > 0 ? atoi(pv) : 0;
     const long tiles = (long)max_blocks * nnb;
     const int grid = (int)(tiles < cus ? tiles : cus);
     hipLaunchKernelGGL(moe_prefill_persistent_kernel, dim3(grid), dim3(NTH), SMEM_P, (hipStream_t)stream,
