@@ -26,7 +26,10 @@ extern "C" {
  * out[r, n] = bf16((sum_k A[r / a_row_div, k] * W_e[n, k]) * (As[r / a_row_div] * topk_w[r])) for every routed
  * flat row r of the align tables (sorted_ids / expert_ids / ntpp, blocks of 16 * (MT & 7) rows).
  * a e4m3 [Ma][K]; as fp32 [Ma]; wq / ws as above (ws_estride = bytes per expert of ws); c bf16 [numel][N];
- * topk_w fp32 [numel] or 0. Errors: -1 N % 16, -2 K % 32, -3 bad argument, -5/-7 bad MT, -6 launch error. */
+ * topk_w fp32 [numel] or 0. (WV, SK, NPW): the gfx950 launch shape -- K-tiles per load batch, waves splitting K,
+ * 16-column tiles per wave, each 1, 2 or 4 (kernels/tuned.json via pick_cfg) -- or all three 0 for the kernel's own
+ * choice; the reference passes its gfx1201 knobs here. Errors: -1 N % 16, -2 K % 32, -3 bad argument, -5 launch
+ * shape not built (or only some of WV / SK / NPW given), -7 bad MT, -6 launch error. */
 int r9k_moe_mxfp4a8(long a, long as, long wq, long ws, long wref, long c, long sorted_ids, long expert_ids,
                     long ntpp, long topk_w, long ws_estride, long wref_estride, int max_blocks, int numel,
                     int a_row_div, int K, int N, int WV, int SK, int NPW, int MT, long stream);

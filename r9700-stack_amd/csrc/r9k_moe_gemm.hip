@@ -356,8 +356,9 @@ int env_int(const char* name, int dflt) {
 // grid is small, 2 once it holds >= 12K waves' worth of tiles, in 4-tile load batches below 4K tiles (config 2 at
 // T <= 8: one memory round trip a wave) and 2-tile batches above; short K stays in one wave (no LDS reduction), with
 // 4-tile load batches while the grid is small. Measured on MI355X over config-2 decode widths (T = 1..64).
-// R9K_GEMM_SK / R9K_GEMM_NPW / R9K_GEMM_U override (tuning sweeps).
-Pick pick(int MT, int N, int K, int max_blocks) {
+// A caller's shape (req: U, SK, NPW all > 0, from the tuned table) replaces this choice. R9K_GEMM_SK / R9K_GEMM_NPW /
+// R9K_GEMM_U override both (tuning sweeps).
+Pick pick(int MT, int N, int K, int max_blocks, const Pick* req = nullptr) {
   const int nkt = (K + KT - 1) / KT;
   const int NT = N / 16;
   int NPW = NT >= 2 ? 2 : 1;
@@ -371,6 +372,11 @@ Pick pick(int MT, int N, int K, int max_blocks) {
     U = tiles >= 8192 ? 1 : 4;
   }
   if (MT >= 4) U = U > 2 ? 2 : U;
+  if (req) {
+    U = req->U;
+    SK = req->SK;
+    NPW = req->NPW;
+  }
   SK = env_int("R9K_GEMM_SK", SK);
   NPW = env_int("R9K_GEMM_NPW", NPW);
   U = env_int("R9K_GEMM_U", U);
@@ -394,7 +400,7 @@ int launch_one(dim3 grid, hipStream_t st, long a, long as, long wq, long ws, lon
 // ws_estride: bytes per expert of the packed scale tensor; the code stride is N * K / 2 bytes.
 int moe_dispatch(long a, long as, long wq, long ws, long c, long sorted_ids, long expert_ids, long ntpp, long topk_w,
                  long ws_estride, int max_blocks, int numel, int a_row_div, int K, int N, int MT, int blk,
-                 long stream, int fuse = 0) {
+                 long stream, int fuse = 0, const Pick* req = nullptr) {
   if (N % 16 || N <= 0) return -1;
   if (K % GROUP || K <= 0) return -2;
   if (MT != 1 && MT != 2 && MT != 4) return -7;
@@ -405,7 +411,7 @@ int moe_dispatch(long a, long as, long wq, long ws, long c, long sorted_ids, lon
   if (fuse == 1 && N % 32) return -1;                       // gate and up halves of whole 16-column tiles
   if (max_blocks <= 0 || numel <= 0) return 0;
   if (!a || (!as && fuse != 2) || !wq || !ws || !c || !sorted_ids || !expert_ids || !ntpp) return -3;
-  Pick p = pick(MT, N, K, max_blocks);
+  Pick p = pick(MT, N, K, max_blocks, req);
   if (fuse == 1) p.NPW = 2;
   const int subs = blk / (16 * MT);
   const long ny = (long)max_blocks * subs;
@@ -462,16 +468,22 @@ int r9k_nvfp4_prefill_launch(long a, long as, long wq, long ws, long wg, long c,
                              long ntpp, long topk_w, long ws_estride, long wg_estride, int max_blocks, int numel,
                              int a_row_div, int K, int N, int blk, long stream);
 
-// Reference: kernels/r9k_moe_mxfp4a8.hip:625-638 (r9k_moe_mxfp4a8). `wref`, WV, SK, NPW and the MT bits 3 (LDS-A)
-// and 4 (fold) are gfx1201 tuning / layout knobs with no meaning here and are ignored; MT & 7 in {1, 2, 4} sets the
-// routing block (16 * MT rows). ws_estride: bytes per expert of the scale tensor. 0 / negative error code.
+// Reference: kernels/r9k_moe_mxfp4a8.hip:625-638 (r9k_moe_mxfp4a8). (WV, SK, NPW) is the launch shape with gfx950
+// meanings: WV = K-tiles per load batch, SK = waves splitting K, NPW = 16-column tiles per wave, each 1, 2 or 4 (the
+// built shapes; another value returns -5); all three 0 lets the kernel pick from the shape (a shape changes only the
+// fp32 summation order of SK > 1). `wref` and the MT bits 3 (LDS-A) and 4 (fold) are gfx1201 layout knobs with no
+// meaning here and are ignored; MT & 7 in {1, 2, 4} sets the routing block (16 * MT rows). ws_estride: bytes per
+// expert of the scale tensor. 0 / negative error code.
 extern "C" int r9k_moe_mxfp4a8(long a, long as, long wq, long ws, long wref, long c, long sorted_ids, long expert_ids,
                                long ntpp, long topk_w, long ws_estride, long wref_estride, int max_blocks, int numel,
                                int a_row_div, int K, int N, int WV, int SK, int NPW, int MT, long stream) {
-  (void)wref; (void)wref_estride; (void)WV; (void)SK; (void)NPW;
+  (void)wref; (void)wref_estride;
   const int mt = MT & 7;
+  const Pick req{mt, NPW, SK, WV};
+  const bool given = WV > 0 && SK > 0 && NPW > 0;
+  if (!given && (WV > 0 || SK > 0 || NPW > 0)) return -5;
   const int rc = moe_dispatch(a, as, wq, ws, c, sorted_ids, expert_ids, ntpp, topk_w, ws_estride, max_blocks, numel,
-                              a_row_div, K, N, mt, 16 * mt, stream);
+                              a_row_div, K, N, mt, 16 * mt, stream, 0, given ? &req : nullptr);
   if (rc) return rc;
   return hipGetLastError() == hipSuccess ? 0 : -6;
 }

@@ -349,13 +349,14 @@ def pick_atiled(N: int, K: int, M: int, fold: bool = True):
 
 def moe_gemm(a_q: torch.Tensor, a_s: torch.Tensor, w: Mxfp4Experts, out: torch.Tensor,
              sorted_ids: torch.Tensor, expert_ids: torch.Tensor, ntpp: torch.Tensor, numel: int,
-             a_row_div: int, topk_w: torch.Tensor | None = None, WV: int = 2, SK: int = 4, NPW: int = 2,
+             a_row_div: int, topk_w: torch.Tensor | None = None, WV: int = 0, SK: int = 0, NPW: int = 0,
              num_experts: int | None = None, MT: int = 1, ldsa: bool = False, prefill: int | None = None,
              a_tiled: bool = False, fuse: int = 0):
     """out[r, :] = dequant(a_q[r // a_row_div]) @ W[expert(r)]^T (* topk_w[r]) for every routed flat row r.
 
-    sorted_ids/expert_ids must come from an align with block_size 16*MT (or prefill_block(prefill)). WV/SK/NPW/ldsa
-    are the reference's gfx1201 launch knobs and are accepted but not used: the gfx950 kernel picks its own split.
+    sorted_ids/expert_ids must come from an align with block_size 16*MT (or prefill_block(prefill)). WV/SK/NPW: the
+    decode kernel's gfx950 launch shape (K-tiles per load batch, waves splitting K, column tiles per wave: pick_cfg's
+    tuned values), all 0 for the kernel's own choice; ldsa is a gfx1201 knob, accepted and not used.
     The grid covers at most ceil(numel/BLK) + min(numel, E) blocks -- the most an align can fill with numel routed
     rows over E experts -- so the launch stays graph-capturable."""
     E = num_experts if num_experts is not None else w.wq.shape[0]
@@ -444,24 +445,40 @@ def moe_gemm(a_q: torch.Tensor, a_s: torch.Tensor, w: Mxfp4Experts, out: torch.T
 
 def pick_cfg(N: int, K: int, group: int = GROUP, M: int | None = None, kind: str | None = None,
              fold: bool = False) -> tuple:
-    """A (WV, SK, NPW) tuple for the decode kernel, or ("P", cfg) for the prefill entry at M >= PREFILL_MIN_M.
-    The tuple's values are the reference's gfx1201 knobs (ignored by the gfx950 kernel, which sizes its own split);
-    they are still returned legal for the shape so callers written against the reference keep working."""
+    """("P", cfg) for the prefill entry at M >= PREFILL_MIN_M, else the decode kernel's (WV, SK, NPW) launch shape on
+    this device for a dense [M, K] x [N, K]^T product: the gfx950 table's entry (kernels/tuned.json, written by
+    kernels/tune.py's sweep; WV = K-tiles per load batch, SK = waves splitting K, NPW = column tiles per wave) for the
+    nearest measured M, or (0, 0, 0) -- the kernel's own choice -- for a shape the table does not hold.
+    R9K_TUNED=0 ignores the table."""
     if kind and M:
         if M >= PREFILL_MIN_M and K % prefill_bk(PREFILL_DEFAULT) == 0:
             return ("P", PREFILL_DEFAULT if M >= 512 else PREFILL_DEFAULT_SMALL)
-    for WV, SK, NPW in ((2, 4, 2), (4, 2, 1), (2, 5, 2), (4, 1, 1)):
-        if K % (SK * group) == 0 and (K >= 1024 or SK <= 2):
-            return WV, SK, NPW
-    return 4, 1, 1
+    from . import tuned
+    cfg = tuned.lookup(kind or "mxfp4", N, K, M or 1)
+    return legal_cfg(cfg, N, K, group, decode_mt(M or 1)) if cfg else (0, 0, 0)
 
 
-def legal_cfg(cfg: tuple, N: int, K: int, group: int = GROUP) -> tuple:
-    """cfg's (WV, SK, NPW) if legal for this shape (K % (SK*group) == 0), else pick_cfg's."""
-    WV, SK, NPW = cfg[:3]
-    if K % (SK * group) == 0 and WV * SK * 32 <= 1024:
+def decode_mt(M: int) -> int:
+    """M tiles per routing block of a dense decode GEMM over identity tables (ops.mxfp4_gemm_q): 16-row blocks up to
+    31 rows, 32 up to 63, then 64."""
+    return 4 if M >= 64 else (2 if M >= 32 else 1)
+
+
+# Launch shapes the decode kernel is built for (r9k_moe_gemm.hip): each of WV (K-tiles per load batch), SK (waves
+# splitting K) and NPW (column tiles per wave) in {1, 2, 4}.
+BUILT_KNOBS = (1, 2, 4)
+
+
+def legal_cfg(cfg: tuple, N: int, K: int, group: int = GROUP, MT: int = 1) -> tuple:
+    """cfg's (WV, SK, NPW) when the decode kernel is built for it at MT M-tiles a block (NPW 4 only below MT 4) and
+    the shape can use it (SK waves each hold at least one of the K / 128 K-tiles, NPW column tiles fit in N / 16),
+    else (0, 0, 0): the kernel's own choice."""
+    WV, SK, NPW = (int(v) for v in cfg[:3])
+    nkt, nt = -(-K // 128), N // 16
+    if (all(v in BUILT_KNOBS for v in (WV, SK, NPW)) and SK <= nkt and NPW <= max(1, nt) and K % group == 0
+            and not (MT >= 4 and NPW > 2)):
         return WV, SK, NPW
-    return pick_cfg(N, K, group)[:3]
+    return 0, 0, 0
 
 
 MOE_MT = int(os.environ.get("R9K_MOE_MT", "0"))

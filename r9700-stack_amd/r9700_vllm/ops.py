@@ -41,8 +41,9 @@ class IdentityTables:
 
 
 def _decode_mt(M: int) -> int:
-    """M-tiles per routing block of a dense decode GEMM: 16-row blocks up to 31 rows, 32 up to 63, then 64."""
-    return 4 if M >= 64 else (2 if M >= 32 else 1)
+    """M-tiles per routing block of a dense decode GEMM (kernels.moe.decode_mt)."""
+    from .kernels import moe as KM
+    return KM.decode_mt(M)
 
 
 def mxfp4_gemm_q(q: torch.Tensor, s: torch.Tensor, W, out: torch.Tensor, M: int, cfg, topk_w=None) -> None:

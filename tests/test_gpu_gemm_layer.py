@@ -790,3 +790,50 @@ def test_dense_qa_refuses_unserved(dev):
     for M in (5, 17):
         assert not K.dense_mxfp4_qa(torch.zeros(M, 256, dtype=torch.bfloat16, device=dev), W2,
                                     torch.empty(M, 64, dtype=torch.bfloat16, device=dev))
+
+
+@pytest.mark.parametrize("MT", [1, 2, 4])
+def test_decode_gemm_every_launch_shape(dev, MT):
+    """r9k_moe_mxfp4a8 at every built launch shape (WV K-tiles a load batch, SK waves splitting K, NPW column tiles a
+    wave, as the launch table passes them) over MoE routing tables, against the oracle; a shape not built raises."""
+    import itertools
+    E, M, topk, N, Kd = 8, 100, 2, 320, 1024
+    g = torch.Generator().manual_seed(20261201 + 21000 + MT)
+    packed, e8 = make_experts(E, N, Kd, g)
+    W = K.prepare_mxfp4_weights(packed.to(dev), e8.to(dev))
+    x = (torch.randn(M, Kd, generator=g) * 0.5).to(torch.bfloat16)
+    ids = torch.stack([torch.randperm(E, generator=g)[:topk] for _ in range(M)]).to(torch.int32)
+    sid, eid, ntpp = (t.to(dev) for t in K.align_block_size_ref(ids, E, 16 * MT))
+    xq, xs = K.quant_rows_fp8(x.to(dev))
+    qo, so = O.quant_rows_fp8(x)
+    ref = O.grouped_gemm(qo, so, {e: O.mxfp4_dequant(packed[e], e8[e]) for e in range(E)}, ids.reshape(-1).numpy(),
+                         topk)
+    shapes = [c for c in itertools.product(K.BUILT_KNOBS, repeat=3) if K.legal_cfg(c, N, Kd, MT=MT) == c]
+    assert len(shapes) >= 18
+    for cfg in shapes:
+        out = torch.full((M * topk, N), float("nan"), dtype=torch.bfloat16, device=dev)
+        K.moe_gemm(xq, xs, W, out, sid, eid, ntpp, M * topk, topk, None, *cfg, num_experts=E, MT=MT)
+        a, b = bf16_bits_to_f64(O.bf16_bits(out)), bf16_bits_to_f64(ref)
+        assert not np.isnan(a.numpy()).any(), cfg
+        assert rel_err(a, b) < 2e-3 and cosine(a, b) > 0.99999, cfg
+    with pytest.raises(RuntimeError):
+        K.moe_gemm(xq, xs, W, torch.empty(M * topk, N, dtype=torch.bfloat16, device=dev), sid, eid, ntpp, M * topk,
+                   topk, None, 3, 1, 1, num_experts=E, MT=MT)
+
+
+@pytest.mark.parametrize("M,N,Kd", [(17, 1024, 2048), (40, 1024, 2048), (100, 1024, 2048), (48, 17408, 5120)])
+def test_dense_linear_tuned_shapes(dev, M, N, Kd):
+    """ops.mxfp4_linear between the dense weight stream's 16 rows and the prefill kernel's 128: the decode kernel at
+    the launch table's shape (kernels/tuned.json), against the oracle on 24 sampled rows."""
+    g = torch.Generator().manual_seed(20261201 + 22000 + M + N)
+    packed, e8 = make_experts(1, N, Kd, g)
+    W = K.prepare_mxfp4_weights(packed.to(dev), e8.to(dev))
+    x = torch.randn(M, Kd, generator=g).to(torch.bfloat16)
+    print(f"dense tuned M={M} N={N} K={Kd}: cfg {K.pick_cfg(N, Kd, M=M, kind='mxfp4')}", flush=True)
+    out = ops.mxfp4_linear(x.to(dev), W.wq, W.wsr, N, Kd)
+    rows = np.sort(np.random.default_rng(M).choice(M, min(M, 24), replace=False))
+    qo, so = O.quant_rows_fp8(x[torch.from_numpy(rows)])
+    ref = O.grouped_gemm(qo, so, {0: O.mxfp4_dequant(packed[0], e8[0], torch.float32)}, np.zeros(rows.size, np.int32),
+                         1, acc_dtype=torch.float32)
+    a, b = bf16_bits_to_f64(O.bf16_bits(out)[rows]), bf16_bits_to_f64(ref)
+    assert rel_err(a, b) < 2e-3 and cosine(a, b) > 0.99999

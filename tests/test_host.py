@@ -197,3 +197,33 @@ def test_split_plan():
     assert not route.split_planned(Layer, 512, 384)
     Layer._r9k_split_k = None
     assert not route.split_planned(Layer, 2048, 384) and not route.split_planned(None, 2048, 384)
+
+
+def test_tuned_table_lookup(tmp_path, monkeypatch):
+    """The gfx950 launch table: nearest measured M at or below, else the smallest; legal_cfg drops shapes the decode
+    kernel is not built for; pick_cfg answers (0, 0, 0) for shapes the table does not hold."""
+    import json
+    from r9700_vllm.kernels import moe as K, tuned
+    doc = {"entries": [{"kind": "mxfp4", "N": 1024, "K": 2048, "M": 17, "cfg": [4, 2, 2]},
+                       {"kind": "mxfp4", "N": 1024, "K": 2048, "M": 64, "cfg": [2, 1, 2]},
+                       {"kind": "mxfp4", "N": 512, "K": 256, "M": 17, "cfg": [4, 4, 4]}]}
+    path = tmp_path / "t.json"
+    path.write_text(json.dumps(doc))
+    monkeypatch.setenv("R9K_TUNED", str(path))
+    monkeypatch.setattr(tuned, "_TABLE", None)
+    assert tuned.lookup("mxfp4", 1024, 2048, 17) == (4, 2, 2)
+    assert tuned.lookup("mxfp4", 1024, 2048, 63) == (4, 2, 2)
+    assert tuned.lookup("mxfp4", 1024, 2048, 100) == (2, 1, 2)
+    assert tuned.lookup("mxfp4", 1024, 2048, 5) == (4, 2, 2)
+    assert tuned.lookup("mxfp4", 999, 2048, 17) is None
+    assert K.pick_cfg(1024, 2048, M=40, kind="mxfp4") == (4, 2, 2)
+    assert K.pick_cfg(1024, 2048, M=200, kind="mxfp4")[0] == "P"
+    assert K.pick_cfg(999, 2048, M=40, kind="mxfp4") == (0, 0, 0)
+    assert K.pick_cfg(512, 256, M=17, kind="mxfp4") == (0, 0, 0)   # SK 4 > the 2 K-tiles of K = 256
+    assert K.legal_cfg((2, 2, 4), 1024, 2048, MT=4) == (0, 0, 0)   # NPW 4 is not built at MT 4
+    assert K.legal_cfg((2, 2, 4), 1024, 2048, MT=2) == (2, 2, 4)
+    assert K.legal_cfg((3, 1, 1), 1024, 2048) == (0, 0, 0)
+    monkeypatch.setenv("R9K_TUNED", "0")
+    monkeypatch.setattr(tuned, "_TABLE", None)
+    assert K.pick_cfg(1024, 2048, M=40, kind="mxfp4") == (0, 0, 0)
+    monkeypatch.setattr(tuned, "_TABLE", None)
