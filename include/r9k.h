@@ -11,9 +11,10 @@
  *   wq  [E][N*K/2 bytes]: per 16-row column tile, 1 KB per 128-K tile = one 16x16x128 scaled-MFMA B operand
  *       (permute_fragments). Same size as the checkpoint codes, so weight prep stays in place.
  *   ws  [E][(K/32 + 1) * N bytes]: e8m0 exponents in the kernel's fragment order + the per-row max (pack_scales).
- * Knobs that only meant something on gfx1201 (WV, SK, NPW, the LDS-A and fold bits of MT, wref) are accepted and
- * ignored; the routing-block contract is honoured: blk = 16 * (MT & 7) rows at decode, r9k_moe_prefill_bm(cfg)
- * rows in the prefill entry.
+ * Knobs that only meant something on gfx1201 (WV, SK, NPW as the reference passes them, the LDS-A and fold bits of
+ * MT, wref) are accepted and ignored; the routing-block contract is honoured: blk = 16 * (MT & 7) rows at decode,
+ * r9k_moe_prefill_bm(cfg) rows in the prefill entry. r9k_moe_mxfp4a8 alone reads (WV, SK, NPW) as its gfx950 launch
+ * shape, and only when the caller sets MT bit 5 (R9K_MT_SHAPE), which the reference never does.
  */
 #ifndef R9K_H
 #define R9K_H
@@ -26,10 +27,11 @@ extern "C" {
  * out[r, n] = bf16((sum_k A[r / a_row_div, k] * W_e[n, k]) * (As[r / a_row_div] * topk_w[r])) for every routed
  * flat row r of the align tables (sorted_ids / expert_ids / ntpp, blocks of 16 * (MT & 7) rows).
  * a e4m3 [Ma][K]; as fp32 [Ma]; wq / ws as above (ws_estride = bytes per expert of ws); c bf16 [numel][N];
- * topk_w fp32 [numel] or 0. (WV, SK, NPW): the gfx950 launch shape -- K-tiles per load batch, waves splitting K,
- * 16-column tiles per wave, each 1, 2 or 4 (kernels/tuned.json via pick_cfg) -- or all three 0 for the kernel's own
- * choice; the reference passes its gfx1201 knobs here. Errors: -1 N % 16, -2 K % 32, -3 bad argument, -5 launch
- * shape not built (or only some of WV / SK / NPW given), -7 bad MT, -6 launch error. */
+ * topk_w fp32 [numel] or 0. With MT & R9K_MT_SHAPE, (WV, SK, NPW) is the gfx950 launch shape -- K-tiles per load
+ * batch, waves splitting K, 16-column tiles per wave, each 1, 2 or 4 (kernels/tuned.json via pick_cfg); without it
+ * the kernel picks the shape and ignores them (the reference passes its gfx1201 knobs there). Errors: -1 N % 16,
+ * -2 K % 32, -3 bad argument, -5 launch shape not built (R9K_MT_SHAPE set), -7 bad MT, -6 launch error. */
+#define R9K_MT_SHAPE 32
 int r9k_moe_mxfp4a8(long a, long as, long wq, long ws, long wref, long c, long sorted_ids, long expert_ids,
                     long ntpp, long topk_w, long ws_estride, long wref_estride, int max_blocks, int numel,
                     int a_row_div, int K, int N, int WV, int SK, int NPW, int MT, long stream);

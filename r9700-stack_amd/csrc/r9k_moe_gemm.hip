@@ -468,20 +468,24 @@ int r9k_nvfp4_prefill_launch(long a, long as, long wq, long ws, long wg, long c,
                              long ntpp, long topk_w, long ws_estride, long wg_estride, int max_blocks, int numel,
                              int a_row_div, int K, int N, int blk, long stream);
 
-// Reference: kernels/r9k_moe_mxfp4a8.hip:625-638 (r9k_moe_mxfp4a8). (WV, SK, NPW) is the launch shape with gfx950
-// meanings: WV = K-tiles per load batch, SK = waves splitting K, NPW = 16-column tiles per wave, each 1, 2 or 4 (the
-// built shapes; another value returns -5); all three 0 lets the kernel pick from the shape (a shape changes only the
-// fp32 summation order of SK > 1). `wref` and the MT bits 3 (LDS-A) and 4 (fold) are gfx1201 layout knobs with no
-// meaning here and are ignored; MT & 7 in {1, 2, 4} sets the routing block (16 * MT rows). ws_estride: bytes per
-// expert of the scale tensor. 0 / negative error code.
+// MT bit 5: (WV, SK, NPW) carry this library's launch shape. The reference never sets it and passes its gfx1201 tile
+// knobs in those arguments, which then mean nothing here.
+constexpr int MT_SHAPE = 32;
+
+// Reference: kernels/r9k_moe_mxfp4a8.hip:625-638 (r9k_moe_mxfp4a8). With MT & MT_SHAPE, (WV, SK, NPW) is the launch
+// shape with gfx950 meanings: WV = K-tiles per load batch, SK = waves splitting K, NPW = 16-column tiles per wave,
+// each 1, 2 or 4 (the built shapes; another value returns -5; a shape changes only the fp32 summation order of
+// SK > 1). Without it the kernel picks the shape and (WV, SK, NPW) are ignored, as are `wref` and the MT bits 3
+// (LDS-A) and 4 (fold): the reference's gfx1201 knobs. MT & 7 in {1, 2, 4} sets the routing block (16 * MT rows).
+// ws_estride: bytes per expert of the scale tensor. 0 / negative error code.
 extern "C" int r9k_moe_mxfp4a8(long a, long as, long wq, long ws, long wref, long c, long sorted_ids, long expert_ids,
                                long ntpp, long topk_w, long ws_estride, long wref_estride, int max_blocks, int numel,
                                int a_row_div, int K, int N, int WV, int SK, int NPW, int MT, long stream) {
   (void)wref; (void)wref_estride;
   const int mt = MT & 7;
   const Pick req{mt, NPW, SK, WV};
-  const bool given = WV > 0 && SK > 0 && NPW > 0;
-  if (!given && (WV > 0 || SK > 0 || NPW > 0)) return -5;
+  const bool given = (MT & MT_SHAPE) != 0;
+  if (given && !(WV > 0 && SK > 0 && NPW > 0)) return -5;
   const int rc = moe_dispatch(a, as, wq, ws, c, sorted_ids, expert_ids, ntpp, topk_w, ws_estride, max_blocks, numel,
                               a_row_div, K, N, mt, 16 * mt, stream, 0, given ? &req : nullptr);
   if (rc) return rc;

@@ -356,7 +356,8 @@ def moe_gemm(a_q: torch.Tensor, a_s: torch.Tensor, w: Mxfp4Experts, out: torch.T
 
     sorted_ids/expert_ids must come from an align with block_size 16*MT (or prefill_block(prefill)). WV/SK/NPW: the
     decode kernel's gfx950 launch shape (K-tiles per load batch, waves splitting K, column tiles per wave: pick_cfg's
-    tuned values), all 0 for the kernel's own choice; ldsa is a gfx1201 knob, accepted and not used.
+    tuned values, passed with MT_SHAPE set), all 0 for the kernel's own choice; ldsa is a gfx1201 knob, accepted and
+    not used.
     The grid covers at most ceil(numel/BLK) + min(numel, E) blocks -- the most an align can fill with numel routed
     rows over E experts -- so the launch stays graph-capturable."""
     E = num_experts if num_experts is not None else w.wq.shape[0]
@@ -437,7 +438,7 @@ def moe_gemm(a_q: torch.Tensor, a_s: torch.Tensor, w: Mxfp4Experts, out: torch.T
         a_q.data_ptr(), a_s.data_ptr(), w.wq.data_ptr(), wsr.data_ptr(), wsr.data_ptr() + (w.K // GROUP) * w.N,
         out.data_ptr(), sorted_ids.data_ptr(), expert_ids.data_ptr(), ntpp.data_ptr(), tw,
         w.estride, w.estride, max_blocks, numel, a_row_div, w.K, w.N, WV, SK, NPW,
-        MT | (8 if ldsa and MT > 1 else 0), _stream())
+        MT | (8 if ldsa and MT > 1 else 0) | (MT_SHAPE if (WV or SK or NPW) else 0), _stream())
     if rc:
         raise RuntimeError(f"r9k_moe_mxfp4a8 failed ({rc}) N={w.N} K={w.K} MT={MT}")
     return out
@@ -463,6 +464,10 @@ def decode_mt(M: int) -> int:
     31 rows, 32 up to 63, then 64."""
     return 4 if M >= 64 else (2 if M >= 32 else 1)
 
+
+# r9k_moe_mxfp4a8's MT bit that marks (WV, SK, NPW) as this library's launch shape; without it the kernel picks the
+# shape and the three are ignored, as the reference's gfx1201 knobs are.
+MT_SHAPE = 32
 
 # Launch shapes the decode kernel is built for (r9k_moe_gemm.hip): each of WV (K-tiles per load batch), SK (waves
 # splitting K) and NPW (column tiles per wave) in {1, 2, 4}.

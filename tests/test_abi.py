@@ -38,6 +38,11 @@ def test_shape_errors_before_launch():
     assert L.r9k_moe_mxfp4a8(1, 1, 1, 1, 1, 1, 1, 1, 1, z, 0, 0, 4, 16, 1, 64, 17, 2, 4, 2, 1, z) == -1
     assert L.r9k_moe_mxfp4a8(1, 1, 1, 1, 1, 1, 1, 1, 1, z, 0, 0, 4, 16, 1, 48, 16, 2, 4, 2, 1, z) == -2
     assert L.r9k_moe_mxfp4a8(1, 1, 1, 1, 1, 1, 1, 1, 1, z, 0, 0, 4, 16, 1, 64, 16, 2, 4, 2, 3, z) == -7
+    # the launch shape is read only with MT bit 5 set: a partial or unbuilt shape is -5 (SK = 5 is one of the
+    # reference's gfx1201 knob sets, which without the bit are ignored)
+    assert K.MT_SHAPE == 32
+    assert L.r9k_moe_mxfp4a8(1, 1, 1, 1, 1, 1, 1, 1, 1, z, 0, 0, 4, 16, 1, 64, 16, 0, 4, 2, 1 | 32, z) == -5
+    assert L.r9k_moe_mxfp4a8(1, 1, 1, 1, 1, 1, 1, 1, 1, z, 0, 0, 4, 16, 1, 640, 16, 2, 5, 2, 1 | 32, z) == -5
     assert L.r9k_moe_4bit_prefill(0, 1, 1, 1, 1, 1, 1, 1, 1, 1, z, 0, 0, 4, 16, 1, 64, 16, 99, z) == -7
     assert L.r9k_moe_4bit_prefill(3, 1, 1, 1, 1, 1, 1, 1, 1, 1, z, 0, 0, 4, 16, 1, 64, 16, 17, z) == -8
     # native NVFP4 prefill: 64-row cfg 17 is refused (-7); nothing to do for numel == 0 (no launch)

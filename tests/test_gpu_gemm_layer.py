@@ -821,6 +821,36 @@ def test_decode_gemm_every_launch_shape(dev, MT):
                    topk, None, 3, 1, 1, num_experts=E, MT=MT)
 
 
+@pytest.mark.parametrize("MT", [1, 2])
+def test_decode_gemm_reference_knobs_ignored(dev, MT):
+    """The reference's ctypes wrapper passes its gfx1201 (WV, SK, NPW) sets to r9k_moe_mxfp4a8 without the launch
+    shape bit (MT bit 5): every such call returns 0 and gives the bits of the kernel's own choice (all three 0)."""
+    E, M, topk, N, Kd = 8, 64, 2, 320, 2560
+    g = torch.Generator().manual_seed(20261201 + 23000 + MT)
+    packed, e8 = make_experts(E, N, Kd, g)
+    W = K.prepare_mxfp4_weights(packed.to(dev), e8.to(dev))
+    x = (torch.randn(M, Kd, generator=g) * 0.5).to(torch.bfloat16)
+    ids = torch.stack([torch.randperm(E, generator=g)[:topk] for _ in range(M)]).to(torch.int32)
+    sid, eid, ntpp = (t.to(dev) for t in K.align_block_size_ref(ids, E, 16 * MT))
+    xq, xs = K.quant_rows_fp8(x.to(dev))
+    numel = M * topk
+    max_blocks = min(eid.numel(), (numel + 16 * MT - 1) // (16 * MT) + min(numel, E))
+
+    def run(WV, SK, NPW):
+        out = torch.full((numel, N), float("nan"), dtype=torch.bfloat16, device=dev)
+        rc = K.lib().r9k_moe_mxfp4a8(
+            xq.data_ptr(), xs.data_ptr(), W.wq.data_ptr(), W.wsr.data_ptr(), W.wsr.data_ptr() + (Kd // 32) * N,
+            out.data_ptr(), sid.data_ptr(), eid.data_ptr(), ntpp.data_ptr(), 0, W.estride, W.estride, max_blocks,
+            numel, topk, Kd, N, WV, SK, NPW, MT, torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        assert rc == 0, (WV, SK, NPW, rc)
+        return O.bf16_bits(out)
+
+    auto = run(0, 0, 0)
+    for knobs in ((2, 4, 2), (4, 2, 1), (2, 5, 2), (4, 1, 1), (8, 10, 3)):
+        assert np.array_equal(run(*knobs), auto), knobs
+
+
 @pytest.mark.parametrize("M,N,Kd", [(17, 1024, 2048), (40, 1024, 2048), (100, 1024, 2048), (48, 17408, 5120)])
 def test_dense_linear_tuned_shapes(dev, M, N, Kd):
     """ops.mxfp4_linear between the dense weight stream's 16 rows and the prefill kernel's 128: the decode kernel at
