@@ -695,11 +695,12 @@ def test_down_sum_refuses_unserved_shapes(dev):
 
 
 def decode_gemm(q, s, W, out, M, topk_w=None):
-    """The decode-family GEMM (r9k_moe_mxfp4a8) over identity tables, 16-row blocks: the two-launch dense path's GEMM
-    as the reference runs it (ops.mxfp4_gemm_q itself takes the dense kernel up to 16 rows)."""
+    """The decode-family GEMM (r9k_moe_mxfp4a8) over identity tables, 16-row blocks, at the kernel's own launch shape:
+    the two-launch dense path's GEMM as the reference runs it (ops.mxfp4_gemm_q itself takes the dense kernel up to 16
+    rows). The one-launch dense kernels split K over waves as that shape does; a launch-table shape with another SK
+    sums in another order."""
     tabs = ops.IdentityTables.get(q.device, M, K.MOE_BLOCK)
-    cfg = K.pick_cfg(W.N, W.K, M=M, kind="mxfp4")
-    K.moe_gemm(q, s, W, out, *tabs, M, 1, topk_w, *cfg[:3], num_experts=1, MT=1)
+    K.moe_gemm(q, s, W, out, *tabs, M, 1, topk_w, num_experts=1, MT=1)
 
 
 @pytest.mark.parametrize("M,N,Kd", [(1, 17408, 5120), (2, 17408, 5120), (4, 17408, 5120), (3, 1024, 2048),
