@@ -307,13 +307,16 @@ int r4d_lru_fused(long ids, int mk, int E, int S, int max_distinct, int max_inse
 /* r4d_lru_fused with this library's table capacity (sorted capacity(mk, E, blk) = ceil((mk + E (blk - 1)) / blk)
  * * blk entries, expert ids capacity / blk, as r9k_moe_align writes them); sorted_c = 0 skips the host pass's tables
  * (steps whose host pass is provably empty); hot_ids (int32 [mk], 0 = not wanted) receives each routed row's slot
- * (-1 = not resident), for the token-major decode tail over the slots. No counterpart of its own in the reference
- * (the same step as r4d_lru_fused, bound by moe/cache.py LayerCache.update_fused). 2 when not served (E > 1024 or
- * mk > 4096). */
+ * (-1 = not resident), for the token-major decode tail over the slots. x != 0: the same launch writes the experts'
+ * input quant, xq e4m3 [T][H] + xs fp32 [T] = r9k_quant_rows_fp8 of the T <= 64 bf16 rows of x (row stride ldx,
+ * 16-byte aligned; H % 8 == 0, H <= 4096). No counterpart of its own in the reference (the same step as
+ * r4d_lru_fused plus the quant the reference launches after it, moe/experts.py:167-199; bound by moe/cache.py
+ * LayerCache.update_fused). 2 when not served (E > 1024 or mk > 4096: nothing launched, x not quantised); -7 quant
+ * arguments out of range. */
 int r9k_lru_manage_tables(long ids, int mk, int E, int S, int max_distinct, int max_inserts, long table, long map_cold,
                           long slot_expert, long slot_stamp, long routed, long step, long miss, long n_miss, int blk,
                           long sorted_h, long eids_h, long ntpp_h, long sorted_c, long eids_c, long ntpp_c,
-                          long hot_ids, long stream);
+                          long hot_ids, long x, long ldx, int H, int T, long xq, long xs, long stream);
 
 /* Copy each listed expert's six per-expert slabs host -> slot (replaces r4d_lru.hip:276-303, bound at
  * moe/cache.py:42-44): slab i of expert e at s_i + e * b_i goes to d_i + slot * b_i for the first n_miss[0]

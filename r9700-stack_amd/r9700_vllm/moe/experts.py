@@ -206,7 +206,7 @@ class R9700Mxfp4Experts(_experts_base()):
             pf_down = None if nv is not None else K.pick_moe_prefill(MT, K2)
             pf_gate = None if nv is not None else K.pick_moe_prefill(MT, K1, gate_up=True)
         cache = getattr(self, "r9k_cache", None)
-        slot_ids = None
+        slot_ids = cache_q = None
         if cache is not None:
             # host-offloaded experts (moe/cache.py): LRU manage + gather, then a pass over the VRAM slots (ids
             # through table) and, unless provably empty, one over the host store (ids through map_cold); every
@@ -217,8 +217,12 @@ class R9700Mxfp4Experts(_experts_base()):
             need_cold = numel > cache.no_cold_limit
             staged = need_cold and cache.stage is not None
             if cache.fused:
-                # with staging the cold pass gets its tables from the stage map below, not from the host map
-                hot_al, cold_al = cache.update_fused(topk_ids, blk, need_cold and not staged)
+                # with staging the cold pass gets its tables from the stage map below, not from the host map; the
+                # same launch quantises the input unless the router already did
+                rq = route.take_quant(getattr(self, "r9k_layer", None), topk_ids, hidden_states)
+                hot_al, cold_al = cache.update_fused(topk_ids, blk, need_cold and not staged,
+                                                     x=hidden_states if rq is None else None)
+                cache_q = cache.x_quant
                 if not need_cold:
                     slot_ids = cache.hot_ids.view(M, topk)   # every routed expert resident: each row's slot
             else:
@@ -276,6 +280,8 @@ class R9700Mxfp4Experts(_experts_base()):
 
         # the router's fp8 quant of this input, when it made one (with its tables at decode, alone at prefill)
         q = route.take_quant(getattr(self, "r9k_layer", None), topk_ids, hidden_states) if expert_map is None else None
+        if q is None:
+            q = cache_q                                      # the expert cache's manage launch made it
         xq, xs = q if q is not None else K.quant_rows_fp8(hidden_states)
         fused = MOE_FUSE and nv is None and MT == 1 and pf_gate is None and pf_down is None
         # wide decode steps (most experts touched, one 16-row block each, about one block a CU): gate_up, the SiLU +

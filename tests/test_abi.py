@@ -103,6 +103,15 @@ def test_shape_errors_before_launch():
     assert Lc.r4d_lru_gather(*([0, 16, 16] + [16, 16, 16] * 5), 16, 16, 64, 16, z) == -3
     assert Lc.r9k_lru_manage_map(8, 4, 64, 16, 1, 4, *p8, 8, 0, z) == -3          # hot without cold
     assert Lc.r9k_lru_manage_map(8, 4, 64, 16, 1, 17, *p8, 8, 8, z) == -2
+    # manage + tables with the folded input quant: rows past 64, a hidden size off the 8-value grid or past 4096, a row
+    # stride below H, a row base off 16 bytes (-7); E past one workgroup's tables is not served (2)
+    mt = (8, 4, 64, 16, 16, 4, *p8, 16, 8, 8, 8, 0, 0, 0, 8)
+    assert Lc.r9k_lru_manage_tables(*mt, 16, 2048, 2048, 65, 16, 16, z) == -7
+    assert Lc.r9k_lru_manage_tables(*mt, 16, 2048, 2044, 4, 16, 16, z) == -7
+    assert Lc.r9k_lru_manage_tables(*mt, 16, 8192, 8192, 4, 16, 16, z) == -7
+    assert Lc.r9k_lru_manage_tables(*mt, 16, 1024, 2048, 4, 16, 16, z) == -7
+    assert Lc.r9k_lru_manage_tables(*mt, 8, 2048, 2048, 4, 16, 16, z) == -7
+    assert Lc.r9k_lru_manage_tables(8, 4, 2048, 16, 16, 4, *p8, 16, 8, 8, 8, 0, 0, 0, 8, 0, 0, 0, 0, 0, 0, z) == 2
     assert Lc.r9k_lru_map_ids(16, 0, 64, 16, 16, 16, 16, z) == 0
     assert Lc.r9k_lru_map_ids(16, -1, 64, 16, 16, 16, 16, z) == -1
     assert Lc.r9k_lru_map_ids(0, 4, 64, 16, 16, 16, 16, z) == -3

@@ -109,11 +109,17 @@ def _tables_state(d: DevState):
 
 @pytest.mark.parametrize("E,S,thresh,max_ins,M,k,blk,seed", [
     (64, 48, 0.5, 48, 4, 6, 16, 11), (288, 64, 0.99, 64, 8, 8, 16, 12), (384, 256, 0.99, 64, 32, 8, 32, 13),
-    (1024, 512, 0.99, 256, 500, 8, 16, 14), (16, 16, 1.0, 16, 3, 4, 64, 15)])
+    (1024, 512, 0.99, 256, 500, 8, 16, 14), (16, 16, 1.0, 16, 3, 4, 64, 15), (96, 64, 0.99, 64, 5, 8, 32, 16),
+    (64, 48, 0.1, 48, 4, 6, 16, 17)])
 def test_manage_tables_one_launch_equals_composed(dev, E, S, thresh, max_ins, M, k, blk, seed):
     """r9k_lru_manage_tables (manage + both passes' tables in one launch) against r9k_lru_manage_map + two
     r9k_moe_align launches on a twin state: every state array and both table sets (the whole capacity) bit for bit
-    after every step, with the host tables skipped on some steps; the state also against the oracle's manager."""
+    after every step, with the host tables skipped on some steps; the state also against the oracle's manager. On
+    every other step (M <= 64 rows) the launch also quantises M activation rows: xq / xs bit for bit against
+    quant_rows_fp8 (rows of 16 + more waves than rows, a hidden size that leaves lanes idle, a padded row stride).
+    Steps of at most 64 routed rows whose experts are all resident take the launch's ballot path (no installs); the
+    cases include a 32-row block there and a distinct-expert threshold that sends all-resident steps to the
+    read-through branch."""
     print(f"manage+tables E={E} S={S} M={M} k={k} blk={blk}", flush=True)
     rng = np.random.default_rng(seed)
     a, b = DevState(dev, E, S, max_ins), DevState(dev, E, S, max_ins)
@@ -139,12 +145,24 @@ def test_manage_tables_one_launch_equals_composed(dev, E, S, thresh, max_ins, M,
               torch.full((cap,), -7, **i32), torch.full((cap // blk,), -7, **i32), torch.full((1,), -7, **i32)]
         cold_ptrs = [t.data_ptr() for t in ta[3:]] if need_cold else [0, 0, 0]
         hot_out = torch.full((mk,), -7, **i32)
+        quant = step % 2 == 0 and M <= C.QUANT_MAX_ROWS
+        qa = ()
+        if quant:
+            H = (2048, 136, 4096)[step % 3]
+            xp = (torch.randn(M, H + 8, generator=torch.Generator().manual_seed(seed * 100 + step)) * 3)
+            x = xp.to(torch.bfloat16).to(dev)[:, :H]
+            xq = torch.full((M, H), 7, dtype=torch.uint8, device=dev)
+            xs = torch.full((M,), -1.0, device=dev)
+            qa = (x.data_ptr(), x.stride(0), H, M, xq.data_ptr(), xs.data_ptr())
         rc = L.r9k_lru_manage_tables(ids.data_ptr(), mk, E, S, max_distinct, max_ins, a.table.data_ptr(),
                                      a.map_cold.data_ptr(), a.slot_expert.data_ptr(), a.slot_stamp.data_ptr(),
                                      a.routed.data_ptr(), a.step.data_ptr(), a.miss.data_ptr(), a.n_miss.data_ptr(),
                                      blk, ta[0].data_ptr(), ta[1].data_ptr(), ta[2].data_ptr(), *cold_ptrs,
-                                     hot_out.data_ptr(), s_)
+                                     hot_out.data_ptr(), *(qa or (0, 0, 0, 0, 0, 0)), s_)
         assert rc == 0, rc
+        if quant:
+            rq, rs = K.quant_rows_fp8(x)
+            assert torch.equal(xq, rq.view(torch.uint8)) and torch.equal(xs, rs), (step, H)
         hid, cid = b.manage(ids, max_distinct, max_ins, mapped=True)
         hb = K.moe_align(hid, blk, E)
         cb = K.moe_align(cid, blk, E) if need_cold else None
@@ -164,20 +182,23 @@ def test_manage_tables_one_launch_equals_composed(dev, E, S, thresh, max_ins, M,
             assert bool((ta[3] == -7).all()) and bool((ta[5] == -7).all()), step
 
 
-@pytest.mark.parametrize("blk", [24, 48])
-def test_manage_tables_block_not_power_of_two(dev, blk):
+@pytest.mark.parametrize("blk,M", [(24, 16), (48, 16), (24, 5), (48, 3)])
+def test_manage_tables_block_not_power_of_two(dev, blk, M):
     """The one-launch manage + tables at a block size that is not a power of two (the entry accepts any; the routing
     entries require powers of two, so this is the table builders' division path): the resident pass's tables over the
-    whole capacity equal the oracle's align of the slot ids the launch wrote, bit for bit, over several steps."""
-    print(f"manage+tables blk={blk}", flush=True)
-    E, S, max_ins, M, k = 288, 64, 64, 16, 8
-    rng = np.random.default_rng(blk)
+    whole capacity equal the oracle's align of the slot ids the launch wrote, bit for bit, over several steps. With
+    M = 5 / 3 rows (40 / 24 routed) the steps after the first route to resident experts only, the launch's ballot
+    path."""
+    print(f"manage+tables blk={blk} M={M}", flush=True)
+    E, S, max_ins, k = 288, 64, 64, 8
+    rng = np.random.default_rng(blk + M)
     a = DevState(dev, E, S, max_ins)
     L = C._L()
     s_ = torch.cuda.current_stream().cuda_stream
     i32 = dict(dtype=torch.int32, device=dev)
+    pool = rng.permutation(E)[: S // 2] if M * k <= 64 else np.arange(E)
     for step in range(6):
-        ids = torch.from_numpy(np.stack([rng.choice(E, size=k, replace=False) for _ in range(M)])
+        ids = torch.from_numpy(np.stack([rng.choice(pool, size=k, replace=False) for _ in range(M)])
                                .reshape(-1).astype(np.int32)).to(dev)
         mk = ids.numel()
         cap = K.capacity(mk, E, blk)
@@ -187,7 +208,7 @@ def test_manage_tables_block_not_power_of_two(dev, blk):
                                      a.map_cold.data_ptr(), a.slot_expert.data_ptr(), a.slot_stamp.data_ptr(),
                                      a.routed.data_ptr(), a.step.data_ptr(), a.miss.data_ptr(), a.n_miss.data_ptr(),
                                      blk, ta[0].data_ptr(), ta[1].data_ptr(), ta[2].data_ptr(), 0, 0, 0,
-                                     hot_out.data_ptr(), s_)
+                                     hot_out.data_ptr(), 0, 0, 0, 0, 0, 0, s_)
         assert rc == 0, rc
         torch.cuda.synchronize()
         so, eo, no = O.align(hot_out.cpu().numpy(), E, blk)
