@@ -218,9 +218,11 @@ void or_moe_sum(const uint16_t* down, const uint16_t* shared, uint16_t* out, int
 static const double E2M1[16] = {0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0, -0.0, -0.5, -1.0, -1.5, -2.0, -3.0, -4.0, -6.0};
 
 /* nearest E2M1 magnitude of |v| with ties to the smaller magnitude (torch.bucketize right=False on the midpoints
- * 0.25 .. 5.0), found by distance (exact in fp64); sign bit for v < 0 (not for -0.0). */
+ * 0.25 .. 5.0), found by distance (exact in fp64); sign bit for v < 0 (not for -0.0). An infinite |v| lies past
+ * every midpoint, so bucketize gives the last bucket: 6. */
 uint8_t or_e2m1_encode(float v) {
   double a = fabs((double)v);
+  if (isinf(a)) return (uint8_t)(7 | (v < 0.f ? 8 : 0));
   int best = 0;
   for (int c = 1; c < 8; c++) {
     double dc = fabs(a - E2M1[c]), db = fabs(a - E2M1[best]);

@@ -48,20 +48,6 @@ __device__ __forceinline__ void dequant_group(const uint32_t w0, const uint32_t 
   }
 }
 
-// Nearest E2M1 code of v with ties to the smaller magnitude (the reference's bucketize on 0.25 .. 5.0, > 5
-// saturating to 6), sign bit for v < 0. V_CVT_SCALEF32_PK_FP4_F32 (scale 1) rounds to nearest even and saturates
-// (measured on gfx950 against this rule over 1M values): it differs exactly at the ties whose lower neighbour is odd
-// (|v| = 0.75, 1.75, 3.5, where it takes the even code above) and at -0.0 / NaN (sign or code kept; the rule gives 0).
-__device__ __forceinline__ uint32_t e2m1_encode(float v) {
-  const uint32_t hw = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(0u, v, 0.f, 1.0f, 0) & 0xfu;
-  const uint32_t b = __float_as_uint(v), t = b & 0x7fffffffu;
-  // |v| in {0.75, 1.75, 3.5}: low 21 bits zero and t >> 21 = 0x1fa + {0, 5, 9} (bits 0, 5, 9 of 0x221), branch-free
-  const uint32_t k = (t >> 21) - 0x1fau;
-  const uint32_t tie = (uint32_t)((t & 0x1fffffu) == 0u) & (uint32_t)(k < 10u) & ((0x221u >> (k & 15u)) & 1u);
-  const uint32_t zero = (uint32_t)(b == 0x80000000u) | (uint32_t)(t > 0x7f800000u);
-  return zero ? 0u : hw - tie;
-}
-
 // The 8 E2M1 codes of one dword (low nibble first) as fp32 values, exact.
 __device__ __forceinline__ void e2m1_decode8(uint32_t w, float (&v)[8]) {
   typedef float f2 __attribute__((ext_vector_type(2)));
@@ -72,14 +58,80 @@ __device__ __forceinline__ void e2m1_decode8(uint32_t w, float (&v)[8]) {
   v[0] = a[0]; v[1] = a[1]; v[2] = b[0]; v[3] = b[1]; v[4] = c[0]; v[5] = c[1]; v[6] = d[0]; v[7] = d[1];
 }
 
-// smallest integer e with a <= 6 * 2^e, for a normal positive fp32 a
+// smallest integer e with a <= 6 * 2^e, for a normal positive fp32 a; past the clamp (128) for +inf, as the
+// reference's ceil(log2(inf / 6)) is
 __device__ __forceinline__ int exp_no_clip(float a) {
+  if (a > 0x1.fffffep127f) return 128;
   int p;
   const float m = frexpf(a, &p);          // a = m * 2^p, m in [0.5, 1)
   return p - 3 + (m > 0.75f ? 1 : 0);     // 6 * 2^e = 0.75 * 2^(e + 3)
 }
 
-// MSE-searched MXFP4 encode of one 32-element fp32 block: packed codes (4 dwords) and the e8m0 byte.
+// The 8 codes of x[0..8) / 2^e, packed low nibble first: for each v = x / 2^e the nearest E2M1 code with ties to the
+// smaller magnitude (the reference's bucketize on 0.25 .. 5.0, > 5 saturating to 6), sign bit for v < 0.
+// V_CVT_SCALEF32_PK_FP4_F32 (scale 1) converts two values into a byte (four conversions chain the dword); it rounds to
+// nearest even and saturates (measured on gfx950 against this rule over 1M values), so it differs exactly at the ties
+// whose lower neighbour is odd (|v| = 0.75, 1.75, 3.5, where it takes the even code above) and at -0.0 / NaN (sign or
+// code kept; the rule gives 0). One mask subtracts 1 from every tied nibble (its magnitude is >= 2: no borrow), another
+// clears every -0.0 / NaN nibble.
+__device__ __forceinline__ uint32_t e2m1_encode8(const float* x, int e) {
+  float v[8];
+#pragma unroll
+  for (int j = 0; j < 8; j++) v[j] = ldexpf(x[j], -e);
+  uint32_t w = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(0u, v[0], v[1], 1.0f, 0);
+  w = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(w, v[2], v[3], 1.0f, 1);
+  w = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(w, v[4], v[5], 1.0f, 2);
+  w = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(w, v[6], v[7], 1.0f, 3);
+  uint32_t tie = 0u, zero = 0u;
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    const uint32_t b = __float_as_uint(v[j]), t = b & 0x7fffffffu;
+    const uint32_t tb = (uint32_t)(t == 0x3f400000u) | (uint32_t)(t == 0x3fe00000u) | (uint32_t)(t == 0x40600000u);
+    const uint32_t zb = (uint32_t)(b == 0x80000000u) | (uint32_t)(t > 0x7f800000u);
+    tie |= tb << (4 * j);
+    zero |= (zb * 0xfu) << (4 * j);
+  }
+  return (w - tie) & ~zero;
+}
+
+// fp32 sum of the squared errors of codes cw at exponent e against the block, each term an fma in ascending order.
+// It is within 34 * 2^-24 (relative) of the exact sum whenever it is finite and no term underflows past 2^-100.
+__device__ __forceinline__ float block_err32(const float (&x)[32], const uint32_t (&cw)[4], int e) {
+  float err = 0.f;
+#pragma unroll
+  for (int q = 0; q < 4; q++) {
+    float v[8];
+    e2m1_decode8(cw[q], v);
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      const float dv = ldexpf(v[j], e) - x[8 * q + j];
+      err = fmaf(dv, dv, err);
+    }
+  }
+  return err;
+}
+
+// The reference's comparison sum: fp64 terms added in ascending i (each term's difference exact in fp64).
+__device__ __forceinline__ double block_err64(const float (&x)[32], const uint32_t (&cw)[4], int e) {
+  double err = 0.0;
+#pragma unroll
+  for (int q = 0; q < 4; q++) {
+    float v[8];
+    e2m1_decode8(cw[q], v);                              // the codes' values (exact), back at the block scale
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      const double dv = (double)ldexpf(v[j], e) - (double)x[8 * q + j];
+      err += dv * dv;
+    }
+  }
+  return err;
+}
+
+// MSE-searched MXFP4 encode of one 32-element fp32 block: packed codes (4 dwords) and the e8m0 byte. The e0 - 1
+// candidate wins when its fp64 error sum (block_err64) is strictly lower. The fp32 sums decide first: each is within
+// DELTA (relative) of the exact error and the fp64 sums within ~2^-47, so when the fp32 sums are apart by more than
+// that margin the fp64 comparison agrees with them; ties, near-ties and sums outside fp32's safe range fall back to
+// the fp64 sums, so the byte and the codes are the same as from the fp64 comparison alone.
 __device__ __forceinline__ uint32_t search_block(const float (&x)[32], uint32_t (&best_w)[4]) {
   float amax = 0.f;
 #pragma unroll
@@ -87,37 +139,25 @@ __device__ __forceinline__ uint32_t search_block(const float (&x)[32], uint32_t 
   amax = fmaxf(amax, 0x1p-126f);
   int e0 = exp_no_clip(amax);
   e0 = e0 < -126 ? -126 : (e0 > 127 ? 127 : e0);
-  int best_e = 0;
-  double best_err = 0.0;
-  double xd[32];
+  const int e1 = e0 - 1;                                  // >= -127: no clamp needed
+  uint32_t c0[4], c1[4];
 #pragma unroll
-  for (int i = 0; i < 32; i++) xd[i] = (double)x[i];
-#pragma unroll
-  for (int d = 0; d >= -1; d--) {
-    int e = e0 + d;
-    e = e < -127 ? -127 : (e > 127 ? 127 : e);
-    uint32_t cw[4] = {0u, 0u, 0u, 0u};
-#pragma unroll
-    for (int i = 0; i < 32; i++) cw[i >> 3] |= e2m1_encode(ldexpf(x[i], -e)) << (4 * (i & 7));
-    double err = 0.0;
-#pragma unroll
-    for (int q = 0; q < 4; q++) {
-      float v[8];
-      e2m1_decode8(cw[q], v);                              // the codes' values (exact), back at the block scale
-#pragma unroll
-      for (int j = 0; j < 8; j++) {
-        const double dv = (double)ldexpf(v[j], e) - xd[8 * q + j];
-        err += dv * dv;
-      }
-    }
-    if (d == 0 || err < best_err) {
-      best_err = err;
-      best_e = e;
-#pragma unroll
-      for (int q = 0; q < 4; q++) best_w[q] = cw[q];
-    }
+  for (int q = 0; q < 4; q++) {
+    c0[q] = e2m1_encode8(x + 8 * q, e0);
+    c1[q] = e2m1_encode8(x + 8 * q, e1);
   }
-  return (uint32_t)(best_e + 127);
+  const float a = block_err32(x, c0, e0), b = block_err32(x, c1, e1);
+  constexpr float DELTA = 1e-5f;                          // > 34 * 2^-24 plus the rounding of these products
+  bool take1;
+  if (a >= 0x1p-100f && b >= 0x1p-100f && a <= 0x1p120f && b <= 0x1p120f &&
+      (b * (1.f + DELTA) < a * (1.f - DELTA) || b * (1.f - DELTA) > a * (1.f + DELTA))) {
+    take1 = b < a;
+  } else {
+    take1 = block_err64(x, c1, e1) < block_err64(x, c0, e0);
+  }
+#pragma unroll
+  for (int q = 0; q < 4; q++) best_w[q] = take1 ? c1[q] : c0[q];
+  return (uint32_t)((take1 ? e1 : e0) + 127);
 }
 
 __global__ void __launch_bounds__(256) nvfp4_to_mxfp4_kernel(const uint8_t* __restrict__ packed,

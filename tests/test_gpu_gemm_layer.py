@@ -239,6 +239,44 @@ def test_quantize_mxfp4_search_bit_exact(dev):
     assert np.array_equal(pm.cpu().numpy(), po) and np.array_equal(em.cpu().numpy(), eo)
 
 
+def test_quantize_mxfp4_search_decision_edges(dev):
+    """The search's fp32 error sums decide only when they are apart by more than their error bound; the rest fall back
+    to the fp64 sums. Blocks that reach each branch, bit for bit against the oracle: exact candidate ties (one value
+    at 3.5 * 2^k, whose two candidates both err by (2^(k-1))^2: the e0 candidate wins), near ties just inside and just
+    outside the margin, denormal-only and mixed blocks (sums under 2^-100), blocks near the fp32 maximum (sums past
+    2^120), NaN, +-inf and -0.0 entries, across exponents from -130 to 127."""
+    rows = []
+    for k in (-120, -20, -1, 0, 7, 30, 100):
+        for rel in (0.0, 2.0 ** -22, -(2.0 ** -22), 2.0 ** -18, -(2.0 ** -18), 2.0 ** -10):
+            blk = np.zeros(32, np.float32)
+            blk[3] = np.float32(3.5 * 2.0 ** k * (1 + rel))
+            blk[17] = np.float32(-1.25 * 2.0 ** k) if rel < 0 else 0.0
+            rows.append(blk)
+    rng = np.random.default_rng(31)
+    for scale in (1e-44, 1e-40, 1e-38, 3e-36, 2.0 ** 59, 2.0 ** 61, 1e37, 5e37):
+        blk = (rng.standard_normal(32) * scale).astype(np.float32)
+        rows.append(blk)
+    mixed = (rng.standard_normal(32) * 1e-39).astype(np.float32)
+    mixed[0] = 1e-30
+    rows.append(mixed)
+    withnan = rng.standard_normal(32).astype(np.float32)
+    withnan[5] = np.nan
+    rows.append(withnan)
+    negz = np.full(32, -0.0, np.float32)
+    negz[9] = 0.75
+    rows.append(negz)
+    withinf = rng.standard_normal(32).astype(np.float32)
+    withinf[2], withinf[30] = np.inf, -np.inf
+    rows.append(withinf)
+    if len(rows) % 2:
+        rows.append(np.zeros(32, np.float32))
+    w = np.concatenate(rows).reshape(-1, 64)
+    pm, em = NV.quantize_mxfp4_search(torch.from_numpy(w).to(dev))
+    po, eo = O.quantize_mxfp4_search(w)
+    assert np.array_equal(em.cpu().numpy(), eo), np.argwhere(em.cpu().numpy() != eo)[:8]
+    assert np.array_equal(pm.cpu().numpy(), po)
+
+
 # --------------------------------------------------------------------------------------------------- layer
 def make_layer(dev, E, H, I, seed, lo=118, hi=126):
     """MXFP4 layer weights drawn on the GPU (seeded), plus their checkpoint-layout copies for the oracle."""

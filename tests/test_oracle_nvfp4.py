@@ -64,6 +64,7 @@ def test_e2m1_encode_matches_bucketize():
         grid += [m32, np.nextafter(m32, np.float32(0)), np.nextafter(m32, np.float32(10))]
     rng = np.random.default_rng(0)
     v = np.concatenate([np.array(grid, dtype=np.float32), rng.uniform(0, 8, 5000).astype(np.float32)])
+    v = np.concatenate([v, np.array([np.inf], dtype=np.float32)])
     v = np.concatenate([v, -v, np.array([-0.0, -1e-30], dtype=np.float32)])
     lib = O.lib()
     got = np.array([lib.or_e2m1_encode(float(x)) for x in v], dtype=np.uint8)
@@ -172,7 +173,8 @@ def test_search_matches_torch_restatement_on_arbitrary_fp32():
       * block maxima 1..8 ulp above 6 * 2^k for k in [-100, 98], where fp32 ceil(log2(amax / 6)) can land one
         below the exact exponent -- the result still agrees, because both candidate pairs contain e = k and the
         coarser exponent never wins for a block whose maximum sits on 6 * 2^k;
-      * the 2048 blocks (of 200K) whose two candidate errors are closest, exact ties included (ties keep e0 in both).
+      * the 2048 blocks (of 200K) whose two candidate errors are closest, exact ties included (ties keep e0 in both);
+      * blocks holding +-inf next to finite values (bucketize puts inf past the last midpoint: code 6).
     The mismatch count is 0 on every set."""
     g = torch.Generator().manual_seed(11)
     wide = torch.randn(256, 2048, generator=g) * torch.exp(torch.randn(256, 1, generator=g) * 2)
@@ -194,7 +196,10 @@ def test_search_matches_torch_restatement_on_arbitrary_fp32():
         errs.append(((v - x.double()) ** 2).sum(-1))
     near = x[torch.argsort(((errs[0] - errs[1]).abs() / errs[0]))[:2048]].reshape(-1, 256).contiguous()
     assert float(((errs[0] - errs[1]).abs() / errs[0]).min()) == 0.0      # the set really holds exact ties
-    for name, w in (("wide-range", wide), ("log2 edge", edge), ("near-tie", near)):
+    inf = torch.randn(8, 256, generator=g)
+    inf[0, 3], inf[1, 40], inf[2, 7], inf[2, 9], inf[3, :32] = float("inf"), -float("inf"), float("inf"), -1e30, 0.0
+    inf[3, 31] = -float("inf")
+    for name, w in (("wide-range", wide), ("log2 edge", edge), ("near-tie", near), ("infinite", inf)):
         bad, n = _mismatches(w)
         print(f"{name}: {bad} of {n} blocks differ from the fp32 torch restatement", flush=True)
         assert bad == 0, name
