@@ -42,6 +42,7 @@ HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
 FP8_PEAK_TFLOPS = 5000.0       # dense fp8 MFMA
 FP4_PEAK_TFLOPS = 10100.0      # dense fp4 / fp6 MFMA
 COPIES = 4
+HIT_LAYERS = COPIES           # cached layers in the expert cache's all-hit graph
 SEED = 20261201
 
 
@@ -375,7 +376,10 @@ def cache_lines(dev, steps: int) -> dict:
     """Host-offloaded experts (moe/cache.py) on config 2's layer (E=288, hidden 2048, intermediate 512, top-8) with a
     64-slot VRAM cache over the mapped host store, each from a HIP graph of the whole apply (LRU manage, gather,
     align tables, GEMMs over the slots and, when needed, over host memory):
-      hit:   T = 1 routed to 8 resident experts every step (the cold pass is provably empty, no inserts);
+      hit:   T = 1 routed to 8 resident experts every step (the cold pass is provably empty, no inserts), four
+             layers in one graph, each with its own cache over one shared host store (as the resident decode lines
+             replay four steps a graph: one apply a replay measures the host's graph launch rate, ~22 us, not the
+             GPU);
       wide:  T = 64 (~240 distinct experts > the 63-expert threshold): every non-resident expert is read through
              from host memory inside the GEMMs (PCIe);
       wide staged: the wide step with R9K_STAGE_COLD=1 (the cold experts gathered into VRAM first, then read there);
@@ -392,13 +396,16 @@ def cache_lines(dev, steps: int) -> dict:
     g = torch.Generator(device=dev).manual_seed(SEED + 9001)
     out = {"slots": S, "bytes_per_expert": layer.bytes_per_expert()}
 
-    def timed(fn, n):
+    def timed(fns, n):
+        """ms per apply over a graph of the applies in `fns`, replayed n times."""
         for _ in range(2):
-            fn()
+            for fn in fns:
+                fn()
         torch.cuda.synchronize()
         gr = torch.cuda.CUDAGraph()
         with torch.cuda.graph(gr):
-            fn()
+            for fn in fns:
+                fn()
         gr.replay()
         torch.cuda.synchronize()
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -407,7 +414,15 @@ def cache_lines(dev, steps: int) -> dict:
             gr.replay()
         b.record()
         torch.cuda.synchronize()
-        return a.elapsed_time(b) / n
+        return a.elapsed_time(b) / (n * len(fns))
+
+    # the hit step's other three layers: caches of their own (arena, LRU state) over the same host store
+    hit_layers = [(ex, cache)]
+    for i in range(1, HIT_LAYERS):
+        c = C.LayerCache(i, cache.h_w13, cache.h_w2, W13.wsr, W2.wsr, 2 * I, H, H, I, S)
+        e = R9700Mxfp4Experts.standalone(c.h_s13, c.h_s2)
+        e.r9k_cache = c
+        hit_layers.append((e, c))
 
     for name, T, ids_fn in (("hit_T1", 1, lambda: torch.arange(8, dtype=torch.int32, device=dev).view(1, 8)),
                             ("wide_T64", 64, None)):
@@ -417,13 +432,16 @@ def cache_lines(dev, steps: int) -> dict:
         if ids_fn is not None:
             ids = ids_fn()
         o = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
-        fn = lambda: ex.apply(o, x, cache.h_w13, cache.h_w2, w, ids, "silu", E, None, None, None, None, None, None,
-                              False)
-        ms = timed(fn, steps if T == 1 else max(4, steps // 10))
+
+        def apply(e, c):
+            return lambda: e.apply(o, x, c.h_w13, c.h_w2, w, ids, "silu", E, None, None, None, None, None, None, False)
+        fns = [apply(e, c) for e, c in hit_layers] if T == 1 else [apply(ex, cache)]
+        ms = timed(fns, steps if T == 1 else max(4, steps // 10))
         distinct = int(torch.unique(ids).numel())
         resident = int((cache.table[ids.reshape(-1).long()] >= 0).sum())
         cold = distinct - int((cache.table[torch.unique(ids).long()] >= 0).sum())
-        row = {"T": T, "ms_per_step": round(ms, 5), "distinct": distinct, "read_through": cold}
+        row = {"T": T, "ms_per_step": round(ms, 5), "distinct": distinct, "read_through": cold,
+               "layers_a_graph": len(fns)}
         if cold:
             row["host_GBps"] = round(cold * layer.bytes_per_expert() / (ms * 1e-3) / 1e9, 1)
         out[name] = row
@@ -438,8 +456,8 @@ def cache_lines(dev, steps: int) -> dict:
         del os.environ["R9K_STAGE_COLD"]
     exs = R9700Mxfp4Experts.standalone(sc.h_s13, sc.h_s2)
     exs.r9k_cache = sc
-    fn = lambda: exs.apply(o, x, sc.h_w13, sc.h_w2, w, ids, "silu", E, None, None, None, None, None, None, False)
-    ms = timed(fn, max(4, steps // 10))
+    ms = timed([lambda: exs.apply(o, x, sc.h_w13, sc.h_w2, w, ids, "silu", E, None, None, None, None, None, None,
+                                  False)], max(4, steps // 10))
     out["wide_T64_staged"] = {"T": 64, "ms_per_step": round(ms, 5), "staged": int(sc.stage_n.item())}
     print(f"# cache wide_T64 staged: {ms * 1e3:.1f} us/layer, {out['wide_T64_staged']['staged']} experts staged "
           f"into VRAM first", file=sys.stderr, flush=True)
@@ -447,13 +465,13 @@ def cache_lines(dev, steps: int) -> dict:
     miss = torch.stack([torch.arange(100, 164, dtype=torch.int32), torch.arange(0, 64, dtype=torch.int32)], 1)
     cache.miss[:64].copy_(miss.to(dev))
     cache.n_miss.fill_(64)
-    ms = timed(cache._gather, 10)
+    ms = timed([cache._gather], 10)
     cache.n_miss.zero_()
     nbytes = 64 * sum(cache.bytes)
     out["gather_64"] = {"ms": round(ms, 4), "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1), "bytes": nbytes}
     print(f"# cache gather of 64 experts: {ms * 1e3:.0f} us, {out['gather_64']['GBps']} GB/s host -> HBM",
           file=sys.stderr, flush=True)
-    del ex, cache, layer
+    del ex, cache, layer, hit_layers
     torch.cuda.empty_cache()
     return out
 
