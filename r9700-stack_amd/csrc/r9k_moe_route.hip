@@ -403,8 +403,8 @@ __device__ __forceinline__ void topk_rows(const uint16_t (&h)[NR][EPL], int E, i
 
 // Routing + tables + (optionally) the per-token fp8 quant of the activations for M <= 64 rows, one launch.
 // Routing workgroups g < nrt = ceil(M / rpw) take rows g * rpw + wave (wave < rpw, one row a wave; waves without a
-// row skip the top-k, which is VALU-bound at 4 cycles an instruction). With one routing workgroup (rpw = 16,
-// M <= 16) the ids stay on chip; with several (rpw = 4: one row per SIMD) each stores its ids as agent-scope
+// row skip the top-k, which is VALU-bound at 4 cycles an instruction). With one routing workgroup (rpw = 8,
+// M <= 8) the ids stay on chip; with several (rpw = 4: one row per SIMD) each stores its ids as agent-scope
 // atomics, waits for them to complete (vmcnt) and then counts itself in `arrive`; the last to arrive reads every id
 // back with agent-scope atomic loads and builds the tables, resetting `arrive` to zero. (Agent-scope atomic
 // accesses are coherent across the XCDs' L2s on their own, so no whole-L2 writeback / invalidate fence is needed.)
@@ -922,8 +922,10 @@ hipError_t launch_small_inst(dim3 grid, size_t lds, hipStream_t st, const uint16
 }
 
 // Routing rows per workgroup of route_small_kernel: all M in one workgroup up to this many rows (no cross-workgroup
-// hand-off), else SMALL_RPW rows each (one row per SIMD) and the last workgroup to arrive builds the tables.
-constexpr int SMALL_ONE_WG = 16;
+// hand-off), else SMALL_RPW rows each (one row per SIMD) and the last workgroup to arrive builds the tables. Up to 8
+// rows the one workgroup holds at most two rows a SIMD; at 9-16 rows (three or four a SIMD, the top-k VALU-bound)
+// the hand-off is faster: config 2 T = 16 41.0 against 41.9 us a layer on MI355X, T <= 12 unchanged.
+constexpr int SMALL_ONE_WG = 8;
 constexpr int SMALL_RPW = 4;
 int small_rpw(int M) { return M <= SMALL_ONE_WG ? SMALL_ONE_WG : SMALL_RPW; }
 
