@@ -619,15 +619,16 @@ __global__ void __launch_bounds__(NTH) moe_prefill_persistent_kernel(
 // a global -> LDS DMA with an explicit wait, none a compiler-tracked load, so no compiler-inserted vmcnt wait drains
 // the ring (vmcnt completes in order, and a load issued after the output stores would wait for them). Per column
 // step and wave: 8 K-steps x 4 column tiles of the 32x32x64 scaled MFMA (weights as the fp4 A operand with their
-// block exponent, activations as the fp8 B operand), then the persistent kernel's epilogue (bf16(acc * As *
-// topk_w), permlane32 pairs, 16-byte buffer stores, padding rows and columns past N sent to the dropped offset).
-// Every step issues the same DMA count per wave, column steps 8 stores and activation steps none, so the vmcnt
-// waits are exact counts.
+// block exponent, activations as the fp8 B operand), then bf16(acc * As * topk_w) staged through 2 KB of LDS a
+// wave, so each 16-byte-a-lane buffer store writes 64 contiguous bytes of 16 rows (padding rows and columns past N
+// sent to the dropped offset). Every step issues the same DMA count per wave, column steps 8 stores and activation
+// steps none, so the vmcnt waits are exact counts.
 constexpr int RR_K = 512;
 constexpr int RR_KS = RR_K / 64;                 // K-steps of one MFMA
 constexpr int RR_NTS = 8;                        // 16-column weight tiles per step (128 columns)
 constexpr int RR_NS = 4;                         // weight stages
-constexpr int RR_MAXB = 8;                       // routing blocks a workgroup's item range may touch
+constexpr int RR_MAXB = 7;                       // routing blocks a workgroup's item range may touch (the LDS
+                                                 // beside the ring holds their tables and the output staging)
 constexpr int RR_TB = RR_K * 8;                  // code bytes of one 16-column tile over K (4 KB)
 constexpr int RR_SB = 16 * (RR_K / 32);          // exponent bytes of one 16-column tile over K (256 B)
 
@@ -640,7 +641,8 @@ struct __align__(16) RRMeta {
   int eid[RR_MAXB];
   int nlive[RR_MAXB];                            // live rows (a prefix of the block); 0 for a block with no expert
 };
-constexpr size_t SMEM_RR = sizeof(RRStage) * RR_NS + sizeof(RRMeta);
+constexpr int RR_OST = 2048;                     // LDS bytes a wave stages its output through (2 x 16 rows x 64 B)
+constexpr size_t SMEM_RR = sizeof(RRStage) * RR_NS + sizeof(RRMeta) + (size_t)(NTH / WAVE) * RR_OST;
 static_assert(SMEM_RR <= 160 * 1024, "LDS");
 
 constexpr int RR_DMA_OPS = 5;                    // weight DMA instructions per wave and step
@@ -670,6 +672,7 @@ __global__ void __launch_bounds__(NTH) moe_prefill_rowres_kernel(
   extern __shared__ __align__(16) uint8_t smem[];
   RRStage* st = reinterpret_cast<RRStage*>(smem);
   RRMeta& mt = *reinterpret_cast<RRMeta*>(smem + RR_NS * sizeof(RRStage));
+  uint8_t* ost = smem + RR_NS * sizeof(RRStage) + sizeof(RRMeta) + (threadIdx.x / WAVE) * RR_OST;
 
   const int G = gridDim.x, wg = blockIdx.x, x = wg % NXCD, jj = wg / NXCD;
   const int S = (G - x + NXCD - 1) / NXCD;                     // workgroups on XCD x
@@ -787,8 +790,8 @@ __global__ void __launch_bounds__(NTH) moe_prefill_rowres_kernel(
 
   u32x4 alo[RR_KS], ahi[RR_KS];
   float sc = 0.f;
-  uint32_t rowoff = 0;
-  bool rlive = false, wlive = false;
+  uint32_t trow[2] = {0u, 0u};                                 // output rows of this lane's stores (x N)
+  bool tlive[2] = {false, false}, wlive = false;
   int sidx = 0;
   for (int s = 0; s < nst; s++) {
     // DMA of step s: younger are the stores of steps s - 3 .. s - 1 and the DMA of steps s + 1 and s + 2
@@ -805,9 +808,15 @@ __global__ void __launch_bounds__(NTH) moe_prefill_rowres_kernel(
       if ((wave >> 1) == cc.off) {
         // this wave's 32 rows of the block: activation fragments for all of K, scale, output row
         const int b = cc.b, nl = mt.nlive[b];
-        const int r = (wave & 1) * 32 + c32, row = cc.off * 64 + r;
-        rlive = row < nl;
+        const int r = (wave & 1) * 32 + c32;
         wlive = wave * 32 < nl;
+        // the epilogue stores rows 16 hs + lane / 4 of the wave's 32
+#pragma unroll
+        for (int hs = 0; hs < 2; hs++) {
+          const int orow = cc.off * 64 + (wave & 1) * 32 + 16 * hs + (lane >> 2);
+          tlive[hs] = orow < nl;
+          trow[hs] = tlive[hs] ? (uint32_t)mt.rows[b][orow] * (uint32_t)N : 0u;
+        }
         const uint8_t* ab = &Sg.b[r * RR_K];
 #pragma unroll
         for (int t = 0; t < RR_KS; t++) {
@@ -817,7 +826,6 @@ __global__ void __launch_bounds__(NTH) moe_prefill_rowres_kernel(
         const float* sf = reinterpret_cast<const float*>(Sg.s);
         sc = sf[r];
         if (topk_w) sc *= sf[WAVE + r];
-        rowoff = rlive ? (uint32_t)mt.rows[b][row] * (uint32_t)N : 0u;
       }
     } else {
       const int cs = first_cs(cc.b) + cc.off - RR_ACH;
@@ -863,10 +871,16 @@ __global__ void __launch_bounds__(NTH) moe_prefill_rowres_kernel(
         issue(ci, snext);
         advance(ci);
       }
-      // epilogue: as the persistent kernel's (lanes l and l + 32 hold row c32; permlane32 pairs make 16-byte runs),
-      // RR_STORES stores a wave (padding rows and columns past N to the dropped offset)
-#pragma unroll
-      for (int j = 0; j < 4; j++) {
+      // epilogue: bf16(acc * sc). Lanes l and l + 32 hold row c32; after the permlane32 pairs of the persistent
+      // kernel's epilogue, lane (c32, g) holds 16-byte piece 2 h + g of each 32-column tile j. The wave stages the
+      // rows through its 1 KB of LDS so that every store writes 64 contiguous bytes of 16 rows instead of 32 bytes of
+      // 32 rows. For tile j, half hs (its own 1 KB): the 32 lanes of rows 16 hs .. 16 hs + 15 write their two pieces
+      // (piece q of row r at position q ^ (r & 3)) and every lane reads piece lane & 3 of row lane / 4. A wave's LDS
+      // operations execute in issue order, so the reads see the writes with no wait between them; tile j + 1 is
+      // packed while the reads are in flight, then tile j's two stores go out. RR_STORES = 8 stores a wave and
+      // column step, the count the vmcnt waits assume; rows past the live ones and columns past N go to the dropped
+      // offset.
+      auto pack_tile = [&](int j, v4i (&v)[2]) {
         uint32_t pk[4][2];
 #pragma unroll
         for (int qb = 0; qb < 4; qb++) {
@@ -881,11 +895,30 @@ __global__ void __launch_bounds__(NTH) moe_prefill_rowres_kernel(
             const auto pr = __builtin_amdgcn_permlane32_swap(pk[2 * h][kk], pk[2 * h + 1][kk], false, false);
             got[kk] = g == 0 ? pr[1] : pr[0];
           }
-          const v4i v = g == 0 ? (v4i){(int)pk[2 * h][0], (int)pk[2 * h][1], (int)got[0], (int)got[1]}
-                               : (v4i){(int)got[0], (int)got[1], (int)pk[2 * h + 1][0], (int)pk[2 * h + 1][1]};
-          const int col = cs * RR_NTS * 16 + j * 32 + 16 * h + 8 * g;
-          const uint32_t off = (rlive && col < N) ? (rowoff + (uint32_t)col) * 2u : cbytes;
-          __builtin_amdgcn_raw_buffer_store_b128(v, crs, (int)off, 0, 0);
+          v[h] = g == 0 ? (v4i){(int)pk[2 * h][0], (int)pk[2 * h][1], (int)got[0], (int)got[1]}
+                        : (v4i){(int)got[0], (int)got[1], (int)pk[2 * h + 1][0], (int)pk[2 * h + 1][1]};
+        }
+      };
+      const int rr = lane >> 2, qq = lane & 3, rl = c32 & 15;
+      v4i vb[2][2];
+      pack_tile(0, vb[0]);
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        {
+          uint8_t* ow = ost + (c32 >> 4) * 1024 + rl * 64;
+#pragma unroll
+          for (int h = 0; h < 2; h++) *reinterpret_cast<v4i*>(ow + (((2 * h + g) ^ (rl & 3)) * 16)) = vb[j & 1][h];
+        }
+        v4i w[2];
+#pragma unroll
+        for (int hs = 0; hs < 2; hs++)
+          w[hs] = *reinterpret_cast<const v4i*>(ost + hs * 1024 + rr * 64 + ((qq ^ (rr & 3)) * 16));
+        if (j + 1 < 4) pack_tile(j + 1, vb[(j + 1) & 1]);
+        const int col = cs * RR_NTS * 16 + j * 32 + qq * 8;
+#pragma unroll
+        for (int hs = 0; hs < 2; hs++) {
+          const uint32_t off = (tlive[hs] && col < N) ? (trow[hs] + (uint32_t)col) * 2u : cbytes;
+          __builtin_amdgcn_raw_buffer_store_b128(w[hs], crs, (int)off, 0, 0);
         }
       }
       nstores = RR_STORES;

@@ -90,7 +90,7 @@ def test_grouped_gemm_prefill_256_config5_widths(dev, down):
     (4, 300, 1, 272, False, False),       # three column steps, the last one mostly past N
     (8, 700, 2, 512, True, False),        # activation rows shared by the top-k rows of a token (row divisor 2)
     (3, 20, 1, 128, False, False),        # fewer work items than XCDs
-    (64, 6000, 8, 128, False, False),     # more blocks per workgroup than the row-resident kernel preloads
+    (64, 6000, 8, 128, False, False),     # one column step a block: a workgroup's items span two blocks
     (2, 3, 1, 16, False, False),          # one 16-column tile: every step's other tiles past N
     (5, 700, 2, 2064, False, False),      # 17 column steps, the last one 16 columns wide
 ])
