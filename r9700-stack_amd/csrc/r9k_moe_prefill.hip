@@ -348,10 +348,15 @@ __device__ __forceinline__ void mfma_load_kfrag(v16f (&acc)[2][4], const KFrag& 
 // load under the current chunk's second-half MFMAs. Group j (chunk j + 3 plus 2 metadata dwords) is issued after
 // barrier j, into the stage chunk j was read from. A tile's sorted_ids and expert id arrive 6 chunks before its
 // first chunk, its per-row scales (As, topk_w) with its first chunk's DMA; its output is stored after its last
-// chunk. Every wave issues exactly 9 loads a group (7 chunk pieces and 2 metadata or dummy dwords), so the waits
-// are fixed counts: at barrier i chunk i + 1's loads are complete once at most 2 + 9 younger loads are outstanding.
-// Needs K / 128 >= 3 (a metadata slot -- 4 tiles of sorted_ids, 2 of scales -- is refilled at least one barrier
-// after its tile's last reader).
+// chunk, staged through the activation region of that chunk's stage so each store writes 64 contiguous bytes of 16
+// rows. That region is also where the group issued after the tile's last barrier puts its activation parts, so
+// those 4 parts go out after the epilogue (each wave stages in the slots its own parts fill) while the group's
+// weight, exponent and metadata parts go out under the MFMAs as usual. Every wave issues exactly 9 loads a group (7
+// chunk pieces and 2 metadata or dummy dwords) and 16 stores a tile, so the waits are fixed counts: at barrier i
+// chunk i + 1's loads are complete once at most 2 + 9 younger loads are outstanding, 2 + 9 + 16 at a tile's first
+// chunk, and 9 at its second (the deferred parts came after the stores). Needs K / 128 >= 4: a metadata slot -- 4
+// tiles of sorted_ids, 2 of scales -- is refilled at least one barrier after its tile's last reader, and the
+// deferred group's chunk is the next tile's third, so its part 0 sets up no tile.
 __global__ void __launch_bounds__(NTH) moe_prefill_persistent_kernel(
     const uint8_t* __restrict__ A, const float* __restrict__ As, const uint8_t* __restrict__ Wq,
     const uint8_t* __restrict__ Ws, uint16_t* __restrict__ C, const int* __restrict__ sorted_ids,
@@ -542,64 +547,113 @@ __global__ void __launch_bounds__(NTH) moe_prefill_persistent_kernel(
       if (i + 1 < iters) {
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");    // this wave's reads of chunk i are done
         // chunk i + 1 (group i - 2) is complete once no more than its 2 metadata dwords, group i - 1 (when issued)
-        // and the previous tile's 16 output stores (when they came after group i - 2: c = 0 or 1) are outstanding
-        const bool epi = m > 0 && c < 2;
-        if (i + 2 < iters) {
-          if (epi) asm volatile("s_waitcnt vmcnt(27)" ::: "memory");
-          else asm volatile("s_waitcnt vmcnt(11)" ::: "memory");
+        // and the previous tile's 16 output stores (when they came after group i - 2: c = 0 or 1) are outstanding.
+        // Every tile but the last defers its last group's activation parts until after its epilogue's stores, so at
+        // c = 1 of the next tile only group i - 1 is younger than chunk i + 1's last part.
+        if (c == 1 && m > 0) {
+          if (i + 2 < iters) asm volatile("s_waitcnt vmcnt(9)" ::: "memory");
+          else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         } else {
-          if (epi) asm volatile("s_waitcnt vmcnt(18)" ::: "memory");
-          else asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
+          const bool epi = m > 0 && c == 0;
+          if (i + 2 < iters) {
+            if (epi) asm volatile("s_waitcnt vmcnt(27)" ::: "memory");
+            else asm volatile("s_waitcnt vmcnt(11)" ::: "memory");
+          } else {
+            if (epi) asm volatile("s_waitcnt vmcnt(18)" ::: "memory");
+            else asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
+          }
         }
         asm volatile("s_barrier" ::: "memory");
       }
       __builtin_amdgcn_sched_barrier(0);
       // second-half MFMAs, each followed by a part of the next DMA group (into chunk i's stage, released by the
       // barrier) and reads of chunk i + 1's first half (after the last chunk they read a stale stage, unused)
+      const bool defer = c == nchunk - 1 && m + 1 < ntiles;      // uniform; then i + 3 < iters (nchunk >= 4)
       mfma_load_kfrag(acc, F1, st[nidx], fo, 0, F0, live, [&](int k) {
-        if (i + 3 < iters) issue_part(k);
+        if (i + 3 < iters && !(defer && k < 4)) issue_part(k);
       });
       __builtin_amdgcn_sched_barrier(0);
       sidx = nidx;
     }
-    // tile m's output (rows and scales from its metadata slots, valid until a barrier after this). Lane l (g = 0)
-    // and lane l + 32 (g = 1) hold the same row: runs of 4 columns at 8 qb + 4 g. One v_permlane32_swap per packed
-    // dword trades runs so that g = 0 holds columns 0-7 and 16-23 of each 32-column tile and g = 1 holds 8-15 and
-    // 24-31: two 16-byte stores per tile and lane, each instruction writing 32 contiguous bytes of 32 rows (half the
-    // store instructions of 8-byte runs, and the epilogue is bound by the rows each store touches). Every lane takes
-    // part in the swaps; padding rows only skip the stores.
-    const int nl = nlm, nb = tile_nb(m);
+    {
+      // tile m's output through 2 KB of LDS a wave in the activation region of its last chunk's stage (free since
+      // that chunk's barrier): the 1 KB slots this wave's own activation parts 0 and 1 fill, so only its own deferred
+      // DMA, issued after its reads, writes there. For M tile ii and 32-column tile j the wave's 32 rows x 64 B go in
+      // (lane (c32, g) writes its 16-byte pieces 2 h + g of row c32, piece q of row r at position q ^ (r & 3) in half
+      // r / 16), each lane reads piece lane & 3 of row lane / 4 of both halves,
+      // and each store writes 64 contiguous bytes of 16 rows -- a row's pieces in neighbouring lanes, which the write
+      // path merges. A wave's LDS operations execute in issue order; the next tile is packed while the reads return.
+      // 16 stores a wave, as EPI_STORES; padding rows and columns past N go to the dropped offset.
+      const int nl = nlm, nb = tile_nb(m);
+      const int fidx = sidx == 0 ? NSTAGE - 1 : sidx - 1;      // the last chunk's stage
+      uint8_t* ob = &st[fidx].a[wave * 1024];                 // half hs at + hs * 8192 (part hs's slot)
+      const int rr = lane >> 2, qq = lane & 3, rl = c32 & 15;
+      uint32_t trow[2][2];
+      bool tlv[2][2];
+      float scv[2];
 #pragma unroll
-    for (int ii = 0; ii < 2; ii++) {
-      const int row = wm * 64 + ii * 32 + c32;
-      const bool live = row < nl;
-      const int fr = ax.rows[m & 3][row];
-      float sc = ax.as[m & 1][row];
-      if (topk_w) sc *= ax.tw[m & 1][row];
-      const uint32_t rowoff = (uint32_t)(live ? fr : 0) * (uint32_t)N;
+      for (int ii = 0; ii < 2; ii++) {
+        const int orow = wm * 64 + ii * 32 + c32;
+        float sc = ax.as[m & 1][orow];
+        if (topk_w) sc *= ax.tw[m & 1][orow];
+        scv[ii] = sc;
 #pragma unroll
-      for (int j = 0; j < 4; j++) {
+        for (int hs = 0; hs < 2; hs++) {
+          const int r = wm * 64 + ii * 32 + hs * 16 + rr;
+          tlv[ii][hs] = r < nl;
+          trow[ii][hs] = tlv[ii][hs] ? (uint32_t)ax.rows[m & 3][r] * (uint32_t)N : 0u;
+        }
+      }
+      auto pack_tile = [&](int t, v4i (&v)[2]) {
+        const int ii = t >> 2, j = t & 3;
         uint32_t p[4][2];
 #pragma unroll
         for (int qb = 0; qb < 4; qb++) {
-          p[qb][0] = pack_bf16x2(acc[ii][j][4 * qb] * sc, acc[ii][j][4 * qb + 1] * sc);
-          p[qb][1] = pack_bf16x2(acc[ii][j][4 * qb + 2] * sc, acc[ii][j][4 * qb + 3] * sc);
+          p[qb][0] = pack_bf16x2(acc[ii][j][4 * qb] * scv[ii], acc[ii][j][4 * qb + 1] * scv[ii]);
+          p[qb][1] = pack_bf16x2(acc[ii][j][4 * qb + 2] * scv[ii], acc[ii][j][4 * qb + 3] * scv[ii]);
         }
 #pragma unroll
-        for (int h = 0; h < 2; h++) {                  // column runs 16 h .. 16 h + 15 of the 32-column tile
+        for (int h = 0; h < 2; h++) {
           uint32_t got[2];
 #pragma unroll
           for (int k = 0; k < 2; k++) {
-            // swap(old = A, src = B): a low lane receives its partner's A, a high lane its partner's B
             const auto r = __builtin_amdgcn_permlane32_swap(p[2 * h][k], p[2 * h + 1][k], false, false);
             got[k] = g == 0 ? r[1] : r[0];
           }
-          const v4i v = g == 0 ? (v4i){(int)p[2 * h][0], (int)p[2 * h][1], (int)got[0], (int)got[1]}
-                               : (v4i){(int)got[0], (int)got[1], (int)p[2 * h + 1][0], (int)p[2 * h + 1][1]};
-          const int n = nb * BN + wn * 128 + j * 32 + 16 * h + 8 * g;
-          const uint32_t off = (live && n < N) ? (rowoff + (uint32_t)n) * 2u : cbytes;
-          __builtin_amdgcn_raw_buffer_store_b128(v, crs, (int)off, 0, 0);
+          v[h] = g == 0 ? (v4i){(int)p[2 * h][0], (int)p[2 * h][1], (int)got[0], (int)got[1]}
+                        : (v4i){(int)got[0], (int)got[1], (int)p[2 * h + 1][0], (int)p[2 * h + 1][1]};
         }
+      };
+      v4i vb[2][2];
+      pack_tile(0, vb[0]);
+#pragma unroll
+      for (int t = 0; t < 8; t++) {
+        const int ii = t >> 2, j = t & 3;
+        {
+          uint8_t* ow = ob + (c32 >> 4) * 8192 + rl * 64;
+#pragma unroll
+          for (int h = 0; h < 2; h++) *reinterpret_cast<v4i*>(ow + (((2 * h + g) ^ (rl & 3)) * 16)) = vb[t & 1][h];
+        }
+        v4i w[2];
+#pragma unroll
+        for (int hs = 0; hs < 2; hs++)
+          w[hs] = *reinterpret_cast<const v4i*>(ob + hs * 8192 + rr * 64 + ((qq ^ (rr & 3)) * 16));
+        if (t + 1 < 8) pack_tile(t + 1, vb[(t + 1) & 1]);
+        const int n = nb * BN + wn * 128 + j * 32 + qq * 8;
+#pragma unroll
+        for (int hs = 0; hs < 2; hs++) {
+          const uint32_t off = (tlv[ii][hs] && n < N) ? (trow[ii][hs] + (uint32_t)n) * 2u : cbytes;
+          __builtin_amdgcn_raw_buffer_store_b128(w[hs], crs, (int)off, 0, 0);
+        }
+      }
+      if (m + 1 < ntiles) {
+        // this wave's staging reads are back (each store waited for its read): the deferred group's activation
+        // parts refill its slots, for the chunk before the group counter's (chunk 2 of the next tile, same stage)
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        const int dc = g_c == 0 ? nchunk - 1 : g_c - 1;
+        const uint32_t so = (uint32_t)(fidx * (int)sizeof(Stage));
+#pragma unroll
+        for (int part = 0; part < 4; part++) dma16s(A, ga[part] + (uint32_t)(dc * KC), la0 + so + part * 512 * 16);
       }
     }
   }
@@ -972,7 +1026,7 @@ int r9k_prefill_launch(long a, long as, long wq, long ws, long c, long sorted_id
       return hipGetLastError() == hipSuccess ? 0 : -6;
     }
   }
-  if (K / KC >= 3 && getenv_flag_off_pf("R9K_PREFILL_PERSIST") == 0) {
+  if (K / KC >= 4 && getenv_flag_off_pf("R9K_PREFILL_PERSIST") == 0) {
     static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(moe_prefill_persistent_kernel),
                                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)SMEM_P);
     if (attr != hipSuccess) return -4;
