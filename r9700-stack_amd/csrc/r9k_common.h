@@ -10,6 +10,9 @@
 namespace r9k {
 
 constexpr int WAVE = 64;
+// Streaming passes (top-k sum, SiLU + quant) switch to non-temporal loads from this many input bytes: prefill-sized
+// inputs (config 3's 134-268 MB) stream past the L2s, decode-sized ones (a few MB) keep plain loads.
+constexpr size_t NT_STREAM_BYTES = size_t(64) << 20;
 
 __device__ __forceinline__ float bf2f(uint16_t u) { return __uint_as_float((uint32_t)u << 16); }
 
@@ -97,8 +100,18 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
 // Chunk c of a row of nvec 16-byte chunks (nvec >= 1), zero past the row. The load always goes out, to an in-range
 // chunk, and the zero is a select after it: a load under a branch is waited for inside that branch, which would
 // serialise a lane's chunk loads instead of keeping them in flight together.
+// NT: a non-temporal load, for passes that stream far more than the L2 holds and never read the row again.
+template <bool NT = false>
 __device__ __forceinline__ uint4 load_chunk_or_zero(const uint4* __restrict__ row, int c, int nvec) {
-  const uint4 t = row[c < nvec ? c : nvec - 1];
+  const uint4* p = row + (c < nvec ? c : nvec - 1);
+  uint4 t;
+  if constexpr (NT) {
+    typedef uint32_t u4v __attribute__((ext_vector_type(4)));
+    const u4v w = __builtin_nontemporal_load(reinterpret_cast<const u4v*>(p));
+    t = make_uint4(w.x, w.y, w.z, w.w);
+  } else {
+    t = *p;
+  }
   return c < nvec ? t : make_uint4(0u, 0u, 0u, 0u);
 }
 
@@ -281,7 +294,7 @@ __device__ __forceinline__ float silu_quant_chunks(const uint4 (&gv)[R], const u
 
 // Loads the lane chunks of one gate_up row for silu_quant_chunks (gate = the first I bf16 values, up = the next I;
 // I % 8 == 0, I <= 512 * R, the row 16-byte aligned).
-template <int R>
+template <int R, bool NT = false>
 __device__ __forceinline__ void load_gate_up_row(const uint16_t* __restrict__ grow, int I, int lane, uint4 (&gv)[R],
                                                  uint4 (&uv)[R]) {
   const int nvec = I / 8;
@@ -290,17 +303,17 @@ __device__ __forceinline__ void load_gate_up_row(const uint16_t* __restrict__ gr
 #pragma unroll
   for (int i = 0; i < R; i++) {
     const int c = lane + i * WAVE;
-    gv[i] = load_chunk_or_zero(gr, c, nvec);
-    uv[i] = load_chunk_or_zero(ur, c, nvec);
+    gv[i] = load_chunk_or_zero<NT>(gr, c, nvec);
+    uv[i] = load_chunk_or_zero<NT>(ur, c, nvec);
   }
 }
 
 // One wave turns one gate_up row into e4m3 codes (the code row 8-byte aligned) and returns its scale.
-template <int R>
+template <int R, bool NT = false>
 __device__ __forceinline__ float silu_quant_row_wave(const uint16_t* __restrict__ grow, int I, uint8_t* qrow,
                                                      int lane) {
   uint4 gv[R], uv[R];
-  load_gate_up_row<R>(grow, I, lane, gv, uv);
+  load_gate_up_row<R, NT>(grow, I, lane, gv, uv);
   return silu_quant_chunks<R>(gv, uv, I / 8, qrow, lane);
 }
 

@@ -24,6 +24,7 @@ constexpr long MAX_WG = 16384;    // 64 workgroups for each of MI355X's 256 CUs;
 
 typedef uint16_t v8u16 __attribute__((ext_vector_type(8)));
 
+template <bool NT>
 __global__ void __launch_bounds__(SUM_WAVES * WAVE) moe_sum_kernel(const uint16_t* __restrict__ down,
                                                                    const uint16_t* __restrict__ shared,
                                                                    uint16_t* __restrict__ out, int M, int topk, int N,
@@ -42,7 +43,11 @@ __global__ void __launch_bounds__(SUM_WAVES * WAVE) moe_sum_kernel(const uint16_
       v8u16 v[BATCH];
 #pragma unroll
       for (int u = 0; u < BATCH; u++)
-        if (j0 + u < topk) v[u] = *reinterpret_cast<const v8u16*>(src + (size_t)(j0 + u) * N);
+        if (j0 + u < topk) {
+          const v8u16* p = reinterpret_cast<const v8u16*>(src + (size_t)(j0 + u) * N);
+          if constexpr (NT) v[u] = __builtin_nontemporal_load(p);
+          else v[u] = *p;
+        }
 #pragma unroll
       for (int u = 0; u < BATCH; u++)
         if (j0 + u < topk) {
@@ -74,7 +79,12 @@ extern "C" int r9k_moe_sum(long down, long shared, long out, int M, int topk, in
   const long items = (long)M * ((N + SEG - 1) / SEG);
   const long want = (items + SUM_WAVES - 1) / SUM_WAVES;
   const int grid = (int)(want < MAX_WG ? want : MAX_WG);
-  hipLaunchKernelGGL(moe_sum_kernel, dim3(grid), dim3(SUM_WAVES * WAVE), 0, (hipStream_t)stream,
-                     (const uint16_t*)down, (const uint16_t*)shared, (uint16_t*)out, M, topk, N, ld_shared, ld_out);
+  // non-temporal loads of the routed rows once they are far larger than the L2s (config 3: 268 MB)
+  if ((size_t)M * (size_t)topk * (size_t)N * 2u >= NT_STREAM_BYTES)
+    hipLaunchKernelGGL(moe_sum_kernel<true>, dim3(grid), dim3(SUM_WAVES * WAVE), 0, (hipStream_t)stream,
+                       (const uint16_t*)down, (const uint16_t*)shared, (uint16_t*)out, M, topk, N, ld_shared, ld_out);
+  else
+    hipLaunchKernelGGL(moe_sum_kernel<false>, dim3(grid), dim3(SUM_WAVES * WAVE), 0, (hipStream_t)stream,
+                       (const uint16_t*)down, (const uint16_t*)shared, (uint16_t*)out, M, topk, N, ld_shared, ld_out);
   return (int)hipGetLastError();
 }

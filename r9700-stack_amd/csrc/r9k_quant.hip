@@ -168,13 +168,14 @@ __global__ void __launch_bounds__(QT) quant_rows_scalar_kernel(const uint16_t* _
 
 
 // One wave per row, R 16-byte chunks of gate and of up per lane (I <= 512 * R), activations kept in registers.
-template <int R>
+// NT: non-temporal row loads (the host sets it for prefill-sized inputs).
+template <int R, bool NT>
 __global__ void __launch_bounds__(WR * WAVE) silu_mul_quant_wave_kernel(const uint16_t* __restrict__ gu,
                                                                         uint8_t* __restrict__ q,
                                                                         float* __restrict__ s, int M, int I) {
   const int row = blockIdx.x * WR + threadIdx.x / WAVE, lane = threadIdx.x % WAVE;
   if (row >= M) return;
-  const float sc = silu_quant_row_wave<R>(gu + (size_t)row * 2 * I, I, q + (size_t)row * I, lane);
+  const float sc = silu_quant_row_wave<R, NT>(gu + (size_t)row * 2 * I, I, q + (size_t)row * I, lane);
   if (lane == 0) s[row] = sc;
 }
 
@@ -295,8 +296,13 @@ extern "C" int r9k_silu_mul_quant_fp8(long gu, long q, long s, int M, int I, lon
   const int R = vec ? wave_chunks(I) : 0;
   const dim3 wgrid((M + WR - 1) / WR), wblk(WR * WAVE);
   const hipStream_t st = (hipStream_t)stream;
-#define SW(RV) hipLaunchKernelGGL(silu_mul_quant_wave_kernel<RV>, wgrid, wblk, 0, st, (const uint16_t*)gu, (uint8_t*)q, \
-                                  (float*)s, M, I)
+  // non-temporal loads once the input is far larger than the L2s (config 3's 134 MB); decode widths keep plain loads
+  const bool nt = (size_t)M * (size_t)I * 4u >= NT_STREAM_BYTES;
+#define SW(RV)                                                                                                      \
+  if (nt) hipLaunchKernelGGL((silu_mul_quant_wave_kernel<RV, true>), wgrid, wblk, 0, st, (const uint16_t*)gu,      \
+                             (uint8_t*)q, (float*)s, M, I);                                                         \
+  else hipLaunchKernelGGL((silu_mul_quant_wave_kernel<RV, false>), wgrid, wblk, 0, st, (const uint16_t*)gu,        \
+                          (uint8_t*)q, (float*)s, M, I)
   if (R == 1) SW(1);
   else if (R == 2) SW(2);
   else if (R == 4) SW(4);
