@@ -85,6 +85,21 @@ def test_quant_rows_fp8_gate(dev):
     assert (gate.cpu() - ref).abs().max().item() <= 2 ** -8        # one bf16 ulp of a value in (0, 1)
 
 
+@pytest.mark.parametrize("M,I", [(65536, 512), (16384, 2048)])
+def test_silu_mul_quant_fp8_streaming_size(dev, M, I):
+    """From 64 MiB of input (config 3's 134 MB gate_up output, config 5's 268 MB at T = 4096) the launch takes
+    non-temporal row loads: its rows equal, bit for bit, the same rows converted from slices small enough for the
+    plain loads (which test_silu_mul_quant_fp8 holds against the oracle)."""
+    g = torch.Generator(device=dev).manual_seed(M + I)
+    gu = (torch.randn(M, 2 * I, generator=g, device=dev) * 2).to(torch.bfloat16)
+    assert gu.numel() * 2 >= 64 << 20
+    q, s = K.silu_mul_quant_fp8(gu)
+    for lo, hi in [(0, 512), (M // 2 - 3, M // 2 + 300), (M - 37, M)]:
+        qs, ss = K.silu_mul_quant_fp8(gu[lo:hi].contiguous())
+        assert torch.equal(q[lo:hi].view(torch.uint8), qs.view(torch.uint8)), (lo, hi)
+        assert torch.equal(s[lo:hi].view(torch.int32), ss.view(torch.int32)), (lo, hi)
+
+
 @pytest.mark.parametrize("M,I,scale", [(37, 320, 2.0), (512, 512, 1.0), (64, 2048, 1.0), (3, 100, 1.0)])
 def test_silu_mul_quant_fp8(dev, M, I, scale):
     g = torch.Generator().manual_seed(M * I)
